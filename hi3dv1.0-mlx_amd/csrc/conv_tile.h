@@ -1,0 +1,71 @@
+// Tile constants and MFMA fragment helpers shared by the gather convolution and the
+// int8 GEMM. All matrix tiles in LDS use one layout: a row of 128 bytes (one K-block)
+// split into eight 16-byte chunks, chunk c of row r stored at position
+// c ^ ((r >> 1) & 7). For a fixed logical chunk, any 16 consecutive rows then fall in
+// 16 distinct 4-bank groups, so the ds_read_b128 fragment reads of the 32x32 MFMAs and
+// the row-wise ds_write_b128 stores are free of bank conflicts.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace hi3d {
+
+constexpr int kTileRows = 128;  // output rows per convolution tile
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ int lds_offset(int row, int chunk) {
+  return row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4);
+}
+
+// One 32-byte K-group of a 32x32 output block: lane l supplies 16 bytes of row
+// (l % 32) from logical chunk (2g + l / 32) for both operands.
+template <typename T>
+struct Mfma;
+
+template <>
+struct Mfma<_Float16> {
+  __device__ __forceinline__ static void run(u32x4 a, u32x4 b, f32x16& c) {
+    c = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+};
+
+template <>
+struct Mfma<__bf16> {
+  __device__ __forceinline__ static void run(u32x4 a, u32x4 b, f32x16& c) {
+    c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0,
+                                                0);
+  }
+};
+
+// fp32: the 16-byte fragment holds 4 consecutive K values; four 32x32x2 MFMAs consume
+// them (both operands use the same K permutation, so the contraction is unchanged).
+template <>
+struct Mfma<float> {
+  __device__ __forceinline__ static void run(u32x4 a, u32x4 b, f32x16& c) {
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(__builtin_bit_cast(float, a.x), __builtin_bit_cast(float, b.x), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(__builtin_bit_cast(float, a.y), __builtin_bit_cast(float, b.y), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(__builtin_bit_cast(float, a.z), __builtin_bit_cast(float, b.z), c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x2f32(__builtin_bit_cast(float, a.w), __builtin_bit_cast(float, b.w), c, 0, 0, 0);
+  }
+};
+
+// Row of accumulator element v of a 32x32 block held by `lane` (column = lane % 32).
+__device__ __forceinline__ int acc_row(int lane, int v) { return ((v >> 2) << 3) + ((lane >> 5) << 2) + (v & 3); }
+
+// XCD-aware block order: the chip deals workgroups round-robin over its 8 XCDs, so
+// block b runs on XCD b % 8. Remap so each XCD walks a contiguous range of work items
+// (neighbouring tiles share gathered rows and weights in that XCD's L2).
+__device__ __forceinline__ int64_t xcd_remap(int64_t b, int64_t total) {
+  const int64_t per = total / 8, rem = total % 8;
+  const int64_t xcd = b % 8, local = b / 8;
+  return xcd * per + (xcd < rem ? xcd : rem) + local;
+}
+
+}  // namespace hi3d

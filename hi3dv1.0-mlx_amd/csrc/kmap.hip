@@ -1,0 +1,677 @@
+// Kernel maps of the sparse convolutions on gfx950.
+//
+//  * hash build + probe -> dense [N, K] neighbour table and per-offset counts
+//    (reference: _voxel_keys / subm_pairs, src/hi3d_mac/torch_backend/sparse_conv.py:109-149;
+//    neighbour_table, src/hi3d_mac/mlx_backend/sparse.py:29-43);
+//  * per-offset pair lists by a stable ballot/prefix compaction
+//    (reference: _PairTable / get_indice_pairs, sparse_conv.py:37-50,264-283);
+//  * the 2x2x2/s2 coarse structure by radix sort + run heads
+//    (reference: downsample_structure, src/hi3d_mac/mlx_backend/sparse.py:217-233);
+//  * the octree child table from the parent table (reference: child_neighbour_table,
+//    src/hi3d_mac/mlx_backend/sparse.py:46-95).
+//
+// The hash is open addressing with linear probing in HBM. A 32-bit key (key space below
+// 2^32 - 1) and its row share one 64-bit slot, so one 64-bit CAS inserts both; wider keys
+// use a 64-bit key array plus a row array. Probing writes each (row, offset) cell of the
+// table exactly once, so the table does not depend on insertion order.
+#include <hipcub/hipcub.hpp>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+
+#include "common.h"
+
+namespace hi3d {
+
+static thread_local std::string g_last_error;
+
+void set_error(const char* fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+}
+
+int fail(int code, const char* fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+namespace {
+
+constexpr uint64_t kEmpty = ~0ull;
+constexpr int kMaxKvol = 343;  // ksize <= 7
+
+// MurmurHash3's 64-bit finaliser: a bijective mix of the packed key.
+__device__ __forceinline__ uint64_t mix64(uint64_t x) {
+  x ^= x >> 33;
+  x *= 0xff51afd7ed558ccdull;
+  x ^= x >> 33;
+  x *= 0xc4ceb9fe1a85ec53ull;
+  x ^= x >> 33;
+  return x;
+}
+
+struct Grid {
+  int32_t sx, sy, sz, batch;
+  __device__ __forceinline__ bool inside(int b, int x, int y, int z) const {
+    return static_cast<unsigned>(b) < static_cast<unsigned>(batch) &&
+           static_cast<unsigned>(x) < static_cast<unsigned>(sx) &&
+           static_cast<unsigned>(y) < static_cast<unsigned>(sy) &&
+           static_cast<unsigned>(z) < static_cast<unsigned>(sz);
+  }
+  __device__ __forceinline__ uint64_t key(int b, int x, int y, int z) const {
+    return ((static_cast<uint64_t>(b) * sx + x) * sy + y) * sz + z;
+  }
+};
+
+__global__ void insert32_kernel(const int4* __restrict__ coords, int64_t n, Grid g,
+                                unsigned long long* __restrict__ slots, uint64_t mask,
+                                int32_t* __restrict__ status) {
+  int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  int4 c = coords[i];
+  if (!g.inside(c.x, c.y, c.z, c.w)) {
+    atomicOr(status, HI3D_MAP_RANGE);
+    return;
+  }
+  uint32_t key = static_cast<uint32_t>(g.key(c.x, c.y, c.z, c.w));
+  unsigned long long packed = (static_cast<unsigned long long>(key) << 32) | static_cast<uint32_t>(i);
+  uint64_t h = mix64(key) & mask;
+  for (uint64_t probe = 0; probe <= mask; ++probe) {
+    unsigned long long prev = atomicCAS(&slots[h], kEmpty, packed);
+    if (prev == kEmpty) return;
+    if (static_cast<uint32_t>(prev >> 32) == key) {
+      atomicOr(status, HI3D_MAP_DUPLICATE);
+      return;
+    }
+    h = (h + 1) & mask;
+  }
+  atomicOr(status, HI3D_MAP_OVERFLOW);
+}
+
+__global__ void insert64_kernel(const int4* __restrict__ coords, int64_t n, Grid g,
+                                unsigned long long* __restrict__ keys, int32_t* __restrict__ vals,
+                                uint64_t mask, int32_t* __restrict__ status) {
+  int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  int4 c = coords[i];
+  if (!g.inside(c.x, c.y, c.z, c.w)) {
+    atomicOr(status, HI3D_MAP_RANGE);
+    return;
+  }
+  unsigned long long key = g.key(c.x, c.y, c.z, c.w);
+  uint64_t h = mix64(key) & mask;
+  for (uint64_t probe = 0; probe <= mask; ++probe) {
+    unsigned long long prev = atomicCAS(&keys[h], kEmpty, key);
+    if (prev == kEmpty) {
+      vals[h] = static_cast<int32_t>(i);
+      return;
+    }
+    if (prev == key) {
+      atomicOr(status, HI3D_MAP_DUPLICATE);
+      return;
+    }
+    h = (h + 1) & mask;
+  }
+  atomicOr(status, HI3D_MAP_OVERFLOW);
+}
+
+__device__ __forceinline__ int32_t lookup32(const unsigned long long* __restrict__ slots,
+                                            uint64_t mask, uint32_t key, int32_t absent) {
+  uint64_t h = mix64(key) & mask;
+  for (uint64_t probe = 0; probe <= mask; ++probe) {
+    unsigned long long s = slots[h];
+    if (s == kEmpty) return absent;
+    if (static_cast<uint32_t>(s >> 32) == key) return static_cast<int32_t>(static_cast<uint32_t>(s));
+    h = (h + 1) & mask;
+  }
+  return absent;
+}
+
+__device__ __forceinline__ int32_t lookup64(const unsigned long long* __restrict__ keys,
+                                            const int32_t* __restrict__ vals, uint64_t mask,
+                                            unsigned long long key, int32_t absent) {
+  uint64_t h = mix64(key) & mask;
+  for (uint64_t probe = 0; probe <= mask; ++probe) {
+    unsigned long long s = keys[h];
+    if (s == kEmpty) return absent;
+    if (s == key) return vals[h];
+    h = (h + 1) & mask;
+  }
+  return absent;
+}
+
+// One block handles kRows rows x kvol offsets; flat (row, offset) order makes the table
+// writes coalesced. Counts are reduced in LDS, then one atomic per offset per block.
+constexpr int kProbeRows = 64;
+
+template <bool kKey64>
+__global__ __launch_bounds__(256) void probe_kernel(const int4* __restrict__ coords, int64_t n,
+                                                    Grid g, int ksize,
+                                                    const unsigned long long* __restrict__ slots,
+                                                    const int32_t* __restrict__ vals, uint64_t mask,
+                                                    int32_t* __restrict__ nbr,
+                                                    int32_t* __restrict__ counts) {
+  __shared__ int32_t cnt[kMaxKvol];
+  const int kvol = ksize * ksize * ksize;
+  const int half = ksize / 2;
+  const int center = kvol / 2;
+  for (int k = threadIdx.x; k < kvol; k += blockDim.x) cnt[k] = 0;
+  __syncthreads();
+  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * kProbeRows;
+  const int rows = static_cast<int>(n - row0 < kProbeRows ? n - row0 : kProbeRows);
+  const int cells = rows * kvol;
+  const int32_t absent = static_cast<int32_t>(n);
+  for (int j = threadIdx.x; j < cells; j += blockDim.x) {
+    const int r = j / kvol;
+    const int k = j - r * kvol;
+    const int64_t o = row0 + r;
+    int32_t found;
+    if (k == center) {
+      found = static_cast<int32_t>(o);
+    } else {
+      int4 c = coords[o];
+      const int dx = k / (ksize * ksize) - half;
+      const int dy = (k / ksize) % ksize - half;
+      const int dz = k % ksize - half;
+      const int x = c.y + dx, y = c.z + dy, z = c.w + dz;
+      if (!g.inside(c.x, x, y, z)) {
+        found = absent;
+      } else if (kKey64) {
+        found = lookup64(slots, vals, mask, g.key(c.x, x, y, z), absent);
+      } else {
+        found = lookup32(slots, mask, static_cast<uint32_t>(g.key(c.x, x, y, z)), absent);
+      }
+    }
+    nbr[o * kvol + k] = found;
+    if (found != absent) atomicAdd(&cnt[k], 1);
+  }
+  __syncthreads();
+  for (int k = threadIdx.x; k < kvol; k += blockDim.x)
+    if (cnt[k]) atomicAdd(&counts[k], cnt[k]);
+}
+
+int64_t default_capacity(int64_t n) {
+  int64_t cap = 64;
+  while (cap < 2 * n) cap <<= 1;
+  return cap;
+}
+
+// ------------------------------------------------------------------ pair lists --
+constexpr int kPairRows = 256;  // rows per block (one per thread)
+
+__global__ __launch_bounds__(256) void pair_count_kernel(const int32_t* __restrict__ nbr, int64_t n,
+                                                         int kvol, int32_t* __restrict__ block_counts,
+                                                         int64_t nblocks) {
+  __shared__ int32_t wave_cnt[4];
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kPairRows + threadIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int k = 0; k < kvol; ++k) {
+    bool present = i < n && nbr[i * kvol + (kvol - 1 - k)] != static_cast<int32_t>(n);
+    uint64_t ballot = __ballot(present);
+    if (lane == 0) wave_cnt[wave] = __popcll(ballot);
+    __syncthreads();
+    if (threadIdx.x == 0)
+      block_counts[static_cast<int64_t>(k) * nblocks + blockIdx.x] =
+          wave_cnt[0] + wave_cnt[1] + wave_cnt[2] + wave_cnt[3];
+    __syncthreads();
+  }
+}
+
+// One block per offset: exclusive scan of that offset's block counts (in place) and the
+// offset's total.
+__global__ __launch_bounds__(1024) void pair_scan_kernel(int32_t* __restrict__ block_counts,
+                                                         int64_t nblocks,
+                                                         int64_t* __restrict__ totals) {
+  typedef hipcub::BlockScan<int64_t, 1024> Scan;
+  __shared__ typename Scan::TempStorage tmp;
+  __shared__ int64_t carry;
+  int32_t* row = block_counts + static_cast<int64_t>(blockIdx.x) * nblocks;
+  if (threadIdx.x == 0) carry = 0;
+  __syncthreads();
+  for (int64_t base = 0; base < nblocks; base += 1024) {
+    int64_t idx = base + threadIdx.x;
+    int64_t v = idx < nblocks ? row[idx] : 0;
+    int64_t excl, agg;
+    Scan(tmp).ExclusiveSum(v, excl, agg);
+    if (idx < nblocks) row[idx] = static_cast<int32_t>(carry + excl);
+    __syncthreads();
+    if (threadIdx.x == 0) carry += agg;
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) totals[blockIdx.x] = carry;
+}
+
+__global__ void pair_offsets_kernel(const int64_t* __restrict__ totals, int kvol,
+                                    int64_t* __restrict__ offsets) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  int64_t acc = 0;
+  for (int k = 0; k < kvol; ++k) {
+    offsets[k] = acc;
+    acc += totals[k];
+  }
+  offsets[kvol] = acc;
+}
+
+__global__ __launch_bounds__(256) void pair_write_kernel(const int32_t* __restrict__ nbr, int64_t n,
+                                                         int kvol,
+                                                         const int32_t* __restrict__ block_offsets,
+                                                         int64_t nblocks,
+                                                         const int64_t* __restrict__ offsets,
+                                                         int32_t* __restrict__ src,
+                                                         int32_t* __restrict__ dst) {
+  __shared__ int32_t wave_cnt[4];
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kPairRows + threadIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  for (int k = 0; k < kvol; ++k) {
+    int32_t j = i < n ? nbr[i * kvol + (kvol - 1 - k)] : static_cast<int32_t>(n);
+    bool present = j != static_cast<int32_t>(n);
+    uint64_t ballot = __ballot(present);
+    if (lane == 0) wave_cnt[wave] = __popcll(ballot);
+    __syncthreads();
+    int before = 0;
+    for (int w = 0; w < wave; ++w) before += wave_cnt[w];
+    // rank of this lane among the present lanes below it in the wave
+    int rank = __popcll(ballot & ((1ull << lane) - 1ull));
+    if (present) {
+      int64_t pos = offsets[k] + block_offsets[static_cast<int64_t>(k) * nblocks + blockIdx.x] + before + rank;
+      src[pos] = static_cast<int32_t>(i);
+      dst[pos] = j;
+    }
+    __syncthreads();
+  }
+}
+
+// ------------------------------------------------------------ stride-2 structure --
+__global__ void half_keys_kernel(const int4* __restrict__ coords, int64_t n, int32_t hx, int32_t hy,
+                                 int32_t hz, unsigned long long* __restrict__ keys,
+                                 int32_t* __restrict__ rows) {
+  int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  int4 c = coords[i];
+  keys[i] = ((static_cast<unsigned long long>(c.x) * hx + (c.y >> 1)) * hy + (c.z >> 1)) * hz + (c.w >> 1);
+  rows[i] = static_cast<int32_t>(i);
+}
+
+__global__ void run_heads_kernel(const unsigned long long* __restrict__ keys, int64_t n,
+                                 int32_t* __restrict__ heads) {
+  int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  heads[i] = (i == 0 || keys[i] != keys[i - 1]) ? 1 : 0;
+}
+
+// After the inclusive scan, ids[i] - 1 is the coarse row of sorted position i.
+__global__ void coarse_emit_kernel(const unsigned long long* __restrict__ keys,
+                                   const int32_t* __restrict__ rows,
+                                   const int32_t* __restrict__ ids, int64_t n, int32_t hx,
+                                   int32_t hy, int32_t hz, const int4* __restrict__ coords,
+                                   int4* __restrict__ low, int32_t* __restrict__ inverse,
+                                   int32_t* __restrict__ counts, uint8_t* __restrict__ slot,
+                                   int64_t* __restrict__ n_low) {
+  int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int32_t c = ids[i] - 1;
+  const int32_t r = rows[i];
+  inverse[r] = c;
+  int4 f = coords[r];
+  slot[r] = static_cast<uint8_t>(((f.y & 1) << 2) | ((f.z & 1) << 1) | (f.w & 1));
+  const bool head = (i == 0) || keys[i] != keys[i - 1];
+  const bool tail = (i == n - 1) || keys[i] != keys[i + 1];
+  if (head) {
+    unsigned long long k = keys[i];
+    int4 l;
+    l.w = static_cast<int>(k % hz);
+    k /= hz;
+    l.z = static_cast<int>(k % hy);
+    k /= hy;
+    l.y = static_cast<int>(k % hx);
+    l.x = static_cast<int>(k / hx);
+    low[c] = l;
+    // run length = position of this run's tail - head + 1, written by the tail below
+  }
+  if (tail) {
+    // find the head by walking back is O(run); instead counts are completed by a
+    // second pass: store the tail position here, the head position at the head.
+    counts[c] = static_cast<int32_t>(i);
+  }
+  if (i == n - 1) *n_low = static_cast<int64_t>(c) + 1;
+}
+
+__global__ void coarse_counts_kernel(const int32_t* __restrict__ ids, int64_t n,
+                                     const unsigned long long* __restrict__ keys,
+                                     int32_t* __restrict__ counts) {
+  int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const bool head = (i == 0) || keys[i] != keys[i - 1];
+  if (head) {
+    const int32_t c = ids[i] - 1;
+    counts[c] = counts[c] - static_cast<int32_t>(i) + 1;  // tail - head + 1
+  }
+}
+
+__global__ void stride2_tables_kernel(const int32_t* __restrict__ inverse,
+                                      const uint8_t* __restrict__ slot, int64_t n, int64_t n_low,
+                                      int32_t* __restrict__ down, int32_t* __restrict__ up) {
+  int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int32_t p = inverse[i];
+  const int s = slot[i];
+  if (down) down[static_cast<int64_t>(p) * 8 + s] = static_cast<int32_t>(i);
+  if (up) {
+    int4 a, b;
+    a.x = s == 0 ? p : static_cast<int32_t>(n_low);
+    a.y = s == 1 ? p : static_cast<int32_t>(n_low);
+    a.z = s == 2 ? p : static_cast<int32_t>(n_low);
+    a.w = s == 3 ? p : static_cast<int32_t>(n_low);
+    b.x = s == 4 ? p : static_cast<int32_t>(n_low);
+    b.y = s == 5 ? p : static_cast<int32_t>(n_low);
+    b.z = s == 6 ? p : static_cast<int32_t>(n_low);
+    b.w = s == 7 ? p : static_cast<int32_t>(n_low);
+    reinterpret_cast<int4*>(up)[i * 2] = a;
+    reinterpret_cast<int4*>(up)[i * 2 + 1] = b;
+  }
+}
+
+// ---------------------------------------------------------------- child table --
+// For child slot s and offset k: parent-neighbourhood offset holding the neighbour
+// (pk) and the neighbour's own slot (ss); same construction as the reference's
+// _child_offset_tables (sparse.py:46-61).
+struct ChildTables {
+  int8_t pk[8][27];
+  int8_t ss[8][27];
+};
+
+ChildTables make_child_tables() {
+  ChildTables t;
+  for (int s = 0; s < 8; ++s) {
+    int bits[3] = {(s >> 2) & 1, (s >> 1) & 1, s & 1};
+    for (int k = 0; k < 27; ++k) {
+      int d[3] = {k / 9 - 1, (k / 3) % 3 - 1, k % 3 - 1};
+      int pd[3], cb[3];
+      for (int a = 0; a < 3; ++a) {
+        int v = bits[a] + d[a];  // in -1..2
+        pd[a] = v >> 1;          // floor division
+        cb[a] = v & 1;
+      }
+      t.pk[s][k] = static_cast<int8_t>((pd[0] + 1) * 9 + (pd[1] + 1) * 3 + (pd[2] + 1));
+      t.ss[s][k] = static_cast<int8_t>(cb[0] * 4 + cb[1] * 2 + cb[2]);
+    }
+  }
+  return t;
+}
+
+__global__ void mask_to_int_kernel(const uint8_t* __restrict__ mask, int64_t m, int32_t* __restrict__ out) {
+  int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= m) return;
+  out[i] = mask[i] ? 1 : 0;
+}
+
+// ids = exclusive scan of the mask: lookup[p*8+s] = child index (or C), plus parent/slot.
+__global__ void child_index_kernel(const uint8_t* __restrict__ mask, const int32_t* __restrict__ excl,
+                                   int64_t m, int32_t* __restrict__ lookup,
+                                   int32_t* __restrict__ parent, int32_t* __restrict__ slot,
+                                   int64_t* __restrict__ n_children) {
+  int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= m) return;
+  const int32_t total = excl[m - 1] + (mask[m - 1] ? 1 : 0);
+  if (i == 0) *n_children = total;
+  if (mask[i]) {
+    const int32_t c = excl[i];
+    lookup[i] = c;
+    parent[c] = static_cast<int32_t>(i >> 3);
+    slot[c] = static_cast<int32_t>(i & 7);
+  } else {
+    lookup[i] = total;
+  }
+  if (i < 8) lookup[m + i] = total;  // target of absent parents (row P)
+}
+
+__global__ void child_table_kernel(const int32_t* __restrict__ parent_table, const int32_t* __restrict__ lookup,
+                                   const int32_t* __restrict__ parent, const int32_t* __restrict__ slot,
+                                   const int64_t* __restrict__ n_children, int64_t cap, ChildTables t,
+                                   int32_t* __restrict__ table) {
+  int64_t j = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t c = j / 27;
+  if (c >= cap || c >= *n_children) return;
+  const int k = static_cast<int>(j - c * 27);
+  const int s = slot[c];
+  const int32_t p = parent[c];
+  const int32_t np = parent_table[static_cast<int64_t>(p) * 27 + t.pk[s][k]];
+  table[j] = lookup[static_cast<int64_t>(np) * 8 + t.ss[s][k]];
+}
+
+}  // namespace
+}  // namespace hi3d
+
+using namespace hi3d;
+
+extern "C" {
+
+const char* hi3d_last_error(void) { return g_last_error.c_str(); }
+
+const char* hi3d_version(void) { return "hi3d_amd 0.1 gfx950"; }
+
+int hi3d_kmap_workspace(int64_t n, int64_t capacity, int32_t key64, int64_t* bytes) {
+  HI3D_REQUIRE(bytes != nullptr, "bytes_host is NULL");
+  HI3D_REQUIRE(n >= 0, "n must be non-negative");
+  int64_t cap = capacity > 0 ? capacity : default_capacity(n);
+  HI3D_REQUIRE((cap & (cap - 1)) == 0, "capacity must be a power of two");
+  *bytes = key64 ? align_up(cap * 8, 256) + cap * 4 + 256 : cap * 8 + 256;
+  return HI3D_OK;
+}
+
+int hi3d_kmap_subm(const int32_t* coords, int64_t n, int32_t sx, int32_t sy, int32_t sz,
+                   int32_t batch_size, int32_t ksize, int64_t capacity, void* workspace,
+                   int64_t workspace_bytes, int32_t* nbr, int32_t* counts, int32_t* status,
+                   void* stream_) {
+  hipStream_t stream = as_stream(stream_);
+  HI3D_REQUIRE(n >= 0, "n must be non-negative");
+  HI3D_REQUIRE(ksize >= 1 && ksize % 2 == 1 && ksize * ksize * ksize <= kMaxKvol,
+               "ksize must be odd and at most 7, got %d", ksize);
+  HI3D_REQUIRE(sx > 0 && sy > 0 && sz > 0 && batch_size > 0, "spatial_shape and batch_size must be positive");
+  HI3D_REQUIRE(n < (int64_t(1) << 31) - 1, "at most 2^31-2 voxels");
+  HI3D_REQUIRE(counts && status && (n == 0 || (coords && nbr && workspace)), "null pointer argument");
+  const int kvol = ksize * ksize * ksize;
+  launch_fill<int32_t>(counts, kvol, 0, stream);
+  launch_fill<int32_t>(status, 1, 0, stream);
+  if (n == 0) {
+    HI3D_LAUNCH_CHECK();
+    return HI3D_OK;
+  }
+  const uint64_t space = static_cast<uint64_t>(batch_size) * sx * sy * sz;
+  const bool key64 = space >= 0xFFFFFFFFull;
+  int64_t cap = capacity > 0 ? capacity : default_capacity(n);
+  int64_t need = 0;
+  int rc = hi3d_kmap_workspace(n, cap, key64, &need);
+  if (rc != HI3D_OK) return rc;
+  HI3D_REQUIRE(workspace_bytes >= need, "workspace too small: %lld < %lld bytes",
+               static_cast<long long>(workspace_bytes), static_cast<long long>(need));
+  Grid g{sx, sy, sz, batch_size};
+  const uint64_t mask = static_cast<uint64_t>(cap - 1);
+  auto* slots = static_cast<unsigned long long*>(workspace);
+  int32_t* vals = key64 ? reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + align_up(cap * 8, 256)) : nullptr;
+  launch_fill<unsigned long long>(slots, cap, kEmpty, stream);
+  const unsigned blocks = static_cast<unsigned>(ceil_div(n, 256));
+  const int4* c4 = reinterpret_cast<const int4*>(coords);
+  if (key64) {
+    hipLaunchKernelGGL(insert64_kernel, dim3(blocks), dim3(256), 0, stream, c4, n, g, slots, vals, mask, status);
+    hipLaunchKernelGGL(probe_kernel<true>, dim3(static_cast<unsigned>(ceil_div(n, kProbeRows))), dim3(256), 0,
+                       stream, c4, n, g, ksize, slots, vals, mask, nbr, counts);
+  } else {
+    hipLaunchKernelGGL(insert32_kernel, dim3(blocks), dim3(256), 0, stream, c4, n, g, slots, mask, status);
+    hipLaunchKernelGGL(probe_kernel<false>, dim3(static_cast<unsigned>(ceil_div(n, kProbeRows))), dim3(256), 0,
+                       stream, c4, n, g, ksize, slots, nullptr, mask, nbr, counts);
+  }
+  HI3D_LAUNCH_CHECK();
+  return HI3D_OK;
+}
+
+int hi3d_kmap_pairs_workspace(int64_t n, int32_t kvol, int64_t* bytes) {
+  HI3D_REQUIRE(bytes != nullptr, "bytes_host is NULL");
+  HI3D_REQUIRE(n >= 0 && kvol > 0, "bad sizes");
+  const int64_t nblocks = std::max<int64_t>(1, ceil_div(n, kPairRows));
+  *bytes = align_up(nblocks * kvol * 4, 256) + align_up(static_cast<int64_t>(kvol) * 8, 256);
+  return HI3D_OK;
+}
+
+int hi3d_kmap_pairs(const int32_t* nbr, int64_t n, int32_t kvol, void* workspace, int64_t workspace_bytes,
+                    int32_t* src, int32_t* dst, int64_t* offsets, void* stream_) {
+  hipStream_t stream = as_stream(stream_);
+  int64_t need = 0;
+  int rc = hi3d_kmap_pairs_workspace(n, kvol, &need);
+  if (rc != HI3D_OK) return rc;
+  HI3D_REQUIRE(offsets != nullptr, "offsets_dev is NULL");
+  if (n == 0) {
+    launch_fill<int64_t>(offsets, kvol + 1, 0, stream);
+    HI3D_LAUNCH_CHECK();
+    return HI3D_OK;
+  }
+  HI3D_REQUIRE(nbr && src && dst && workspace, "null pointer argument");
+  HI3D_REQUIRE(workspace_bytes >= need, "workspace too small");
+  const int64_t nblocks = ceil_div(n, kPairRows);
+  Workspace ws(workspace, workspace_bytes);
+  int32_t* block_counts = ws.take<int32_t>(nblocks * kvol);
+  int64_t* totals = ws.take<int64_t>(kvol);
+  hipLaunchKernelGGL(pair_count_kernel, dim3(static_cast<unsigned>(nblocks)), dim3(256), 0, stream, nbr, n, kvol,
+                     block_counts, nblocks);
+  hipLaunchKernelGGL(pair_scan_kernel, dim3(kvol), dim3(1024), 0, stream, block_counts, nblocks, totals);
+  hipLaunchKernelGGL(pair_offsets_kernel, dim3(1), dim3(64), 0, stream, totals, kvol, offsets);
+  hipLaunchKernelGGL(pair_write_kernel, dim3(static_cast<unsigned>(nblocks)), dim3(256), 0, stream, nbr, n, kvol,
+                     block_counts, nblocks, offsets, src, dst);
+  HI3D_LAUNCH_CHECK();
+  return HI3D_OK;
+}
+
+static size_t downsample_sort_bytes(int64_t n) {
+  size_t sort_bytes = 0, scan_bytes = 0;
+  hipcub::DoubleBuffer<unsigned long long> kb(nullptr, nullptr);
+  hipcub::DoubleBuffer<int32_t> vb(nullptr, nullptr);
+  hipcub::DeviceRadixSort::SortPairs(nullptr, sort_bytes, kb, vb, static_cast<int>(n), 0, 64);
+  hipcub::DeviceScan::InclusiveSum(nullptr, scan_bytes, static_cast<int32_t*>(nullptr),
+                                   static_cast<int32_t*>(nullptr), static_cast<int>(n));
+  return std::max(sort_bytes, scan_bytes);
+}
+
+int hi3d_downsample_workspace(int64_t n, int64_t* bytes) {
+  HI3D_REQUIRE(bytes != nullptr, "bytes_host is NULL");
+  HI3D_REQUIRE(n >= 0 && n < (int64_t(1) << 31) - 1, "bad n");
+  const int64_t m = std::max<int64_t>(n, 1);
+  *bytes = 2 * align_up(m * 8, 256) + 3 * align_up(m * 4, 256) + align_up(static_cast<int64_t>(downsample_sort_bytes(m)), 256) + 256;
+  return HI3D_OK;
+}
+
+int hi3d_downsample_structure(const int32_t* coords, int64_t n, int32_t sx, int32_t sy, int32_t sz,
+                              int32_t batch_size, void* workspace, int64_t workspace_bytes, int32_t* low,
+                              int32_t* inverse, int32_t* counts, uint8_t* slot, int64_t* n_low, void* stream_) {
+  hipStream_t stream = as_stream(stream_);
+  int64_t need = 0;
+  int rc = hi3d_downsample_workspace(n, &need);
+  if (rc != HI3D_OK) return rc;
+  HI3D_REQUIRE(n_low != nullptr, "n_low_dev is NULL");
+  if (n == 0) {
+    launch_fill<int64_t>(n_low, 1, 0, stream);
+    HI3D_LAUNCH_CHECK();
+    return HI3D_OK;
+  }
+  HI3D_REQUIRE(coords && low && inverse && counts && slot && workspace, "null pointer argument");
+  HI3D_REQUIRE(workspace_bytes >= need, "workspace too small");
+  HI3D_REQUIRE(sx > 0 && sy > 0 && sz > 0 && batch_size > 0, "spatial_shape and batch_size must be positive");
+  const int32_t hx = (sx + 1) / 2, hy = (sy + 1) / 2, hz = (sz + 1) / 2;
+  Workspace ws(workspace, workspace_bytes);
+  auto* k0 = ws.take<unsigned long long>(n);
+  auto* k1 = ws.take<unsigned long long>(n);
+  auto* r0 = ws.take<int32_t>(n);
+  auto* r1 = ws.take<int32_t>(n);
+  auto* ids = ws.take<int32_t>(n);
+  size_t temp_bytes = downsample_sort_bytes(n);
+  void* temp = ws.take<char>(static_cast<int64_t>(temp_bytes));
+  const unsigned blocks = static_cast<unsigned>(ceil_div(n, 256));
+  const int4* c4 = reinterpret_cast<const int4*>(coords);
+  hipLaunchKernelGGL(half_keys_kernel, dim3(blocks), dim3(256), 0, stream, c4, n, hx, hy, hz, k0, r0);
+  hipcub::DoubleBuffer<unsigned long long> kb(k0, k1);
+  hipcub::DoubleBuffer<int32_t> vb(r0, r1);
+  const uint64_t space = static_cast<uint64_t>(batch_size) * hx * hy * hz;
+  int end_bit = 1;
+  while (end_bit < 64 && (1ull << end_bit) < space) ++end_bit;
+  HI3D_HIP_CHECK(hipcub::DeviceRadixSort::SortPairs(temp, temp_bytes, kb, vb, static_cast<int>(n), 0, end_bit, stream));
+  const unsigned long long* sk = kb.Current();
+  const int32_t* sr = vb.Current();
+  hipLaunchKernelGGL(run_heads_kernel, dim3(blocks), dim3(256), 0, stream, sk, n, ids);
+  size_t scan_bytes = temp_bytes;
+  HI3D_HIP_CHECK(hipcub::DeviceScan::InclusiveSum(temp, scan_bytes, ids, ids, static_cast<int>(n), stream));
+  hipLaunchKernelGGL(coarse_emit_kernel, dim3(blocks), dim3(256), 0, stream, sk, sr, ids, n, hx, hy, hz, c4,
+                     reinterpret_cast<int4*>(low), inverse, counts, slot, n_low);
+  hipLaunchKernelGGL(coarse_counts_kernel, dim3(blocks), dim3(256), 0, stream, ids, n, sk, counts);
+  HI3D_LAUNCH_CHECK();
+  return HI3D_OK;
+}
+
+int hi3d_stride2_tables(const int32_t* inverse, const uint8_t* slot, int64_t n, int64_t n_low, int32_t* down,
+                        int32_t* up, void* stream_) {
+  hipStream_t stream = as_stream(stream_);
+  HI3D_REQUIRE(n >= 0 && n_low >= 0, "bad sizes");
+  if (n == 0) return HI3D_OK;
+  HI3D_REQUIRE(inverse && slot, "null pointer argument");
+  if (down) launch_fill<int32_t>(down, n_low * 8, static_cast<int32_t>(n), stream);
+  hipLaunchKernelGGL(stride2_tables_kernel, dim3(static_cast<unsigned>(ceil_div(n, 256))), dim3(256), 0, stream,
+                     inverse, slot, n, n_low, down, up);
+  HI3D_LAUNCH_CHECK();
+  return HI3D_OK;
+}
+
+int hi3d_child_table_workspace(int64_t n_parents, int64_t* bytes) {
+  HI3D_REQUIRE(bytes != nullptr, "bytes_host is NULL");
+  HI3D_REQUIRE(n_parents >= 0 && n_parents * 8 < (int64_t(1) << 31) - 16, "bad n_parents");
+  const int64_t m = std::max<int64_t>(n_parents * 8, 1);
+  size_t scan_bytes = 0;
+  hipcub::DeviceScan::ExclusiveSum(nullptr, scan_bytes, static_cast<int32_t*>(nullptr),
+                                   static_cast<int32_t*>(nullptr), static_cast<int>(m));
+  *bytes = 2 * align_up(m * 4, 256) + align_up((m + 8) * 4, 256) + align_up(static_cast<int64_t>(scan_bytes), 256);
+  return HI3D_OK;
+}
+
+int hi3d_child_neighbour_table(const int32_t* parent_table, const uint8_t* mask, int64_t n_parents,
+                               void* workspace, int64_t workspace_bytes, int32_t* table, int32_t* parent,
+                               int32_t* slot, int64_t* n_children, void* stream_) {
+  hipStream_t stream = as_stream(stream_);
+  int64_t need = 0;
+  int rc = hi3d_child_table_workspace(n_parents, &need);
+  if (rc != HI3D_OK) return rc;
+  HI3D_REQUIRE(n_children != nullptr, "n_children_dev is NULL");
+  if (n_parents == 0) {
+    launch_fill<int64_t>(n_children, 1, 0, stream);
+    HI3D_LAUNCH_CHECK();
+    return HI3D_OK;
+  }
+  HI3D_REQUIRE(parent_table && mask && table && parent && slot && workspace, "null pointer argument");
+  HI3D_REQUIRE(workspace_bytes >= need, "workspace too small");
+  const int64_t m = n_parents * 8;
+  Workspace ws(workspace, workspace_bytes);
+  int32_t* flags = ws.take<int32_t>(m);
+  int32_t* excl = ws.take<int32_t>(m);
+  int32_t* lookup = ws.take<int32_t>(m + 8);
+  size_t scan_bytes = 0;
+  hipcub::DeviceScan::ExclusiveSum(nullptr, scan_bytes, flags, excl, static_cast<int>(m));
+  void* temp = ws.take<char>(static_cast<int64_t>(scan_bytes));
+  const unsigned blocks = static_cast<unsigned>(ceil_div(m, 256));
+  hipLaunchKernelGGL(mask_to_int_kernel, dim3(blocks), dim3(256), 0, stream, mask, m, flags);
+  HI3D_HIP_CHECK(hipcub::DeviceScan::ExclusiveSum(temp, scan_bytes, flags, excl, static_cast<int>(m), stream));
+  hipLaunchKernelGGL(child_index_kernel, dim3(blocks), dim3(256), 0, stream, mask, excl, m, lookup, parent, slot,
+                     n_children);
+  static const ChildTables tables = make_child_tables();
+  hipLaunchKernelGGL(child_table_kernel, dim3(static_cast<unsigned>(ceil_div(m * 27, 256))), dim3(256), 0, stream,
+                     parent_table, lookup, parent, slot, n_children, m, tables, table);
+  HI3D_LAUNCH_CHECK();
+  return HI3D_OK;
+}
+
+}  // extern "C"

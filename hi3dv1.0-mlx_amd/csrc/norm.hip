@@ -1,0 +1,200 @@
+// LayerNorm (+ adaLN modulation) row kernel and the adaLN projection, fp16 rows.
+//
+// Reference: layer_norm_modulate (src/hi3d_mac/mlx_backend/kernels.py:162-237),
+// LayerNorm32 (src/sparc3d/nn/norm.py:12-17), the res-block modulation
+// (src/sparc3d/models/transformers/sparc3d_transformer.py:132-144,
+// src/hi3d_mac/mlx_backend/transformer.py:413-424).
+#include "common.h"
+#include "conv_tile.h"
+
+namespace hi3d {
+namespace {
+
+// G lanes per row, CPL 8-element chunks per lane held in registers; fp32 two-pass
+// statistics; y = (x - mean) * inv [* w + b]; h = fp16(y); modulate
+// h = fp16(fp16(h * scale) + shift) (two roundings, no FMA).
+template <int G, int CPL>
+__global__ __launch_bounds__(256) void ln_kernel(const _Float16* __restrict__ x, int64_t rows, int c, float eps,
+                                                 const float* __restrict__ weight, const float* __restrict__ bias,
+                                                 const _Float16* __restrict__ scale,
+                                                 const _Float16* __restrict__ shift, _Float16* __restrict__ out) {
+#pragma clang fp contract(off)
+  constexpr int RPB = 256 / G;  // rows per block
+  const int t = threadIdx.x;
+  const int g = t % G;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + t / G;
+  const bool live = row < rows;
+  const int chunks = c >> 3;
+  const _Float16* xr = x + (live ? row : 0) * c;
+  float v[CPL][8];
+  float sum = 0.0f;
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    const int ch = g + i * G;
+    f16x8 h = {};
+    if (live && ch < chunks) h = *reinterpret_cast<const f16x8*>(xr + ch * 8);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      v[i][e] = static_cast<float>(h[e]);
+      sum += v[i][e];
+    }
+  }
+#pragma unroll
+  for (int d = G / 2; d >= 1; d >>= 1) sum += __shfl_xor(sum, d, 64);
+  const float mean = sum / static_cast<float>(c);
+  float sq = 0.0f;
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    const int ch = g + i * G;
+    if (ch < chunks) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float d = v[i][e] - mean;
+        sq += d * d;
+      }
+    }
+  }
+#pragma unroll
+  for (int d = G / 2; d >= 1; d >>= 1) sq += __shfl_xor(sq, d, 64);
+  const float inv = 1.0f / sqrtf(sq / static_cast<float>(c) + eps);
+  if (!live) return;
+  _Float16* orow = out + row * c;
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    const int ch = g + i * G;
+    if (ch >= chunks) continue;
+    f16x8 o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int col = ch * 8 + e;
+      float y = (v[i][e] - mean) * inv;
+      if (weight != nullptr) y = y * weight[col] + bias[col];
+      _Float16 h = static_cast<_Float16>(y);
+      if (scale != nullptr) {
+        const _Float16 p = static_cast<_Float16>(static_cast<float>(h) * static_cast<float>(scale[col]));
+        h = static_cast<_Float16>(static_cast<float>(p) + static_cast<float>(shift[col]));
+      }
+      o[e] = h;
+    }
+    *reinterpret_cast<f16x8*>(orow + ch * 8) = o;
+  }
+}
+
+// Any width: one wave per row, three passes over the row in global memory.
+__global__ __launch_bounds__(256) void ln_generic_kernel(const _Float16* __restrict__ x, int64_t rows, int c, float eps,
+                                                         const float* __restrict__ weight,
+                                                         const float* __restrict__ bias,
+                                                         const _Float16* __restrict__ scale,
+                                                         const _Float16* __restrict__ shift,
+                                                         _Float16* __restrict__ out) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const _Float16* xr = x + row * c;
+  float sum = 0.0f;
+  for (int i = lane; i < c; i += 64) sum += static_cast<float>(xr[i]);
+  for (int d = 32; d >= 1; d >>= 1) sum += __shfl_xor(sum, d, 64);
+  const float mean = sum / static_cast<float>(c);
+  float sq = 0.0f;
+  for (int i = lane; i < c; i += 64) {
+    const float d = static_cast<float>(xr[i]) - mean;
+    sq += d * d;
+  }
+  for (int d = 32; d >= 1; d >>= 1) sq += __shfl_xor(sq, d, 64);
+  const float inv = 1.0f / sqrtf(sq / static_cast<float>(c) + eps);
+  _Float16* orow = out + row * c;
+  for (int i = lane; i < c; i += 64) {
+    float y = (static_cast<float>(xr[i]) - mean) * inv;
+    if (weight != nullptr) y = y * weight[i] + bias[i];
+    _Float16 h = static_cast<_Float16>(y);
+    if (scale != nullptr) {
+      const _Float16 p = static_cast<_Float16>(static_cast<float>(h) * static_cast<float>(scale[i]));
+      h = static_cast<_Float16>(static_cast<float>(p) + static_cast<float>(shift[i]));
+    }
+    orow[i] = h;
+  }
+}
+
+// One wave per output feature: y = W . cond' + b (fp32), then the fp16 (1 + scale) and
+// shift halves.
+__global__ __launch_bounds__(256) void adaln_kernel(const float* __restrict__ w, const float* __restrict__ b,
+                                                    const float* __restrict__ cond, int n_out, int n_in, int apply_silu,
+                                                    _Float16* __restrict__ scale1p, _Float16* __restrict__ shift) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  const int j = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (j >= n_out) return;
+  const float* wr = w + static_cast<int64_t>(j) * n_in;
+  float acc = 0.0f;
+  for (int i = lane; i < n_in; i += 64) {
+    float ci = cond[i];
+    if (apply_silu) ci = ci / (1.0f + expf(-ci));
+    acc += wr[i] * ci;
+  }
+  for (int d = 32; d >= 1; d >>= 1) acc += __shfl_xor(acc, d, 64);
+  if (lane != 0) return;
+  const float y = acc + (b != nullptr ? b[j] : 0.0f);
+  const int half = n_out / 2;
+  const _Float16 yh = static_cast<_Float16>(y);
+  if (j < half) scale1p[j] = static_cast<_Float16>(1.0f + static_cast<float>(yh));
+  else shift[j - half] = yh;
+}
+
+template <int G, int CPL>
+void launch_ln(const _Float16* x, int64_t rows, int c, float eps, const float* w, const float* b, const _Float16* sc,
+               const _Float16* sh, _Float16* out, hipStream_t stream) {
+  constexpr int RPB = 256 / G;
+  hipLaunchKernelGGL((ln_kernel<G, CPL>), dim3(static_cast<unsigned>(ceil_div(rows, RPB))), dim3(256), 0, stream, x,
+                     rows, c, eps, w, b, sc, sh, out);
+}
+
+}  // namespace
+}  // namespace hi3d
+
+using namespace hi3d;
+
+extern "C" {
+
+int hi3d_layer_norm_modulate(const void* x, int64_t rows, int32_t c, float eps, const float* weight, const float* bias,
+                             const void* scale, const void* shift, void* out, void* stream_) {
+  hipStream_t stream = as_stream(stream_);
+  HI3D_REQUIRE(rows >= 0 && c > 0, "bad sizes");
+  HI3D_REQUIRE((weight == nullptr) == (bias == nullptr), "weight and bias must be given together");
+  HI3D_REQUIRE((scale == nullptr) == (shift == nullptr), "scale and shift must be given together");
+  if (rows == 0) return HI3D_OK;
+  HI3D_REQUIRE(x && out, "null pointer argument");
+  const auto* xh = static_cast<const _Float16*>(x);
+  const auto* sc = static_cast<const _Float16*>(scale);
+  const auto* sh = static_cast<const _Float16*>(shift);
+  auto* o = static_cast<_Float16*>(out);
+  const bool aligned = ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(out)) & 15) == 0;
+  const int chunks = c / 8;
+  if (c % 8 == 0 && aligned && chunks <= 64 * 8) {
+    if (chunks <= 8) launch_ln<8, 1>(xh, rows, c, eps, weight, bias, sc, sh, o, stream);
+    else if (chunks <= 16) launch_ln<16, 1>(xh, rows, c, eps, weight, bias, sc, sh, o, stream);
+    else if (chunks <= 32) launch_ln<32, 1>(xh, rows, c, eps, weight, bias, sc, sh, o, stream);
+    else if (chunks <= 64) launch_ln<64, 1>(xh, rows, c, eps, weight, bias, sc, sh, o, stream);
+    else if (chunks <= 128) launch_ln<64, 2>(xh, rows, c, eps, weight, bias, sc, sh, o, stream);
+    else if (chunks <= 256) launch_ln<64, 4>(xh, rows, c, eps, weight, bias, sc, sh, o, stream);
+    else launch_ln<64, 8>(xh, rows, c, eps, weight, bias, sc, sh, o, stream);
+  } else {
+    hipLaunchKernelGGL(ln_generic_kernel, dim3(static_cast<unsigned>(ceil_div(rows, 4))), dim3(256), 0, stream, xh, rows,
+                       c, eps, weight, bias, sc, sh, o);
+  }
+  HI3D_LAUNCH_CHECK();
+  return HI3D_OK;
+}
+
+int hi3d_adaln_projection(const float* w, const float* b, const float* cond, int32_t n_out, int32_t n_in,
+                          int32_t apply_silu, void* scale1p, void* shift, void* stream_) {
+  hipStream_t stream = as_stream(stream_);
+  HI3D_REQUIRE(n_out > 0 && n_out % 2 == 0 && n_in > 0, "n_out must be even and positive, n_in positive");
+  HI3D_REQUIRE(w && cond && scale1p && shift, "null pointer argument");
+  hipLaunchKernelGGL(adaln_kernel, dim3(static_cast<unsigned>(ceil_div(n_out, 4))), dim3(256), 0, stream, w, b, cond,
+                     n_out, n_in, apply_silu, static_cast<_Float16*>(scale1p), static_cast<_Float16*>(shift));
+  HI3D_LAUNCH_CHECK();
+  return HI3D_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,190 @@
+// Execution plans of the gather-MFMA convolution.
+//
+// The convolution is output-stationary: a tile of kTileRows output rows runs one dense
+// MFMA contraction per kernel offset that is present in at least one of its rows. To
+// keep that union small, output rows are reordered: first by Morton code of their
+// coordinates (spatial locality of the gathered rows), then, inside windows of
+// `window_rows` Morton-ordered rows, by their 27-bit neighbour-presence mask (radix sort
+// is stable, so rows with one mask stay in Morton order). The plan stores per tile the
+// output rows, the transposed gather indices [kvol][kTileRows] (one contiguous run per
+// offset) and the union mask. Output rows are written once each: the "scatter" is a
+// permuted row store, no atomics.
+#include <hipcub/hipcub.hpp>
+
+#include <algorithm>
+
+#include "common.h"
+#include "conv_tile.h"
+
+namespace hi3d {
+namespace {
+
+__device__ __forceinline__ uint64_t spread3(uint32_t v) {
+  // spread the low 19 bits of v to every third bit
+  uint64_t x = v & 0x7ffffu;
+  x = (x | (x << 32)) & 0x001f00000000ffffull;
+  x = (x | (x << 16)) & 0x001f0000ff0000ffull;
+  x = (x | (x << 8)) & 0x100f00f00f00f00full;
+  x = (x | (x << 4)) & 0x10c30c30c30c30c3ull;
+  x = (x | (x << 2)) & 0x1249249249249249ull;
+  return x;
+}
+
+__global__ void morton_kernel(const int4* __restrict__ coords, int64_t n,
+                              unsigned long long* __restrict__ keys, int32_t* __restrict__ rows) {
+  int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  int4 c = coords[i];
+  uint64_t m = (spread3(static_cast<uint32_t>(c.y)) << 2) | (spread3(static_cast<uint32_t>(c.z)) << 1) |
+               spread3(static_cast<uint32_t>(c.w));
+  keys[i] = (static_cast<uint64_t>(static_cast<uint32_t>(c.x) & 0x7f) << 57) | m;
+  rows[i] = static_cast<int32_t>(i);
+}
+
+__global__ void iota_kernel(int32_t* __restrict__ rows, int64_t n) {
+  int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i < n) rows[i] = static_cast<int32_t>(i);
+}
+
+// key = (window << 32) | presence mask, for rows taken in Morton order.
+__global__ void mask_keys_kernel(const int32_t* __restrict__ table, int64_t n_out, int kvol, int64_t n_in,
+                                 const int32_t* __restrict__ order, int64_t window,
+                                 unsigned long long* __restrict__ keys, int32_t* __restrict__ rows) {
+  int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (p >= n_out) return;
+  const int32_t r = order[p];
+  uint32_t mask = 0;
+  if (kvol <= 32) {
+    const int32_t* t = table + static_cast<int64_t>(r) * kvol;
+    for (int k = 0; k < kvol; ++k)
+      if (static_cast<uint32_t>(t[k]) < static_cast<uint64_t>(n_in)) mask |= 1u << k;
+  }
+  const uint64_t w = window > 0 ? static_cast<uint64_t>(p / window) : 0;
+  keys[p] = (w << 32) | mask;
+  rows[p] = r;
+}
+
+// One block of kTileRows threads per tile: output rows, transposed gather indices and
+// the union mask.
+__global__ __launch_bounds__(kTileRows) void tile_kernel(const int32_t* __restrict__ table, int64_t n_out,
+                                                         int kvol, int64_t n_in,
+                                                         const int32_t* __restrict__ order,
+                                                         int32_t* __restrict__ rows,
+                                                         int32_t* __restrict__ gidx,
+                                                         uint32_t* __restrict__ tile_mask) {
+  __shared__ uint32_t wave_mask[kTileRows / 64];
+  const int64_t tile = blockIdx.x;
+  const int r = threadIdx.x;
+  const int64_t p = tile * kTileRows + r;
+  const int32_t row = p < n_out ? order[p] : -1;
+  rows[p] = row;
+  uint32_t mask = 0;
+  int32_t* g = gidx + tile * kvol * kTileRows + r;
+  const int32_t absent = static_cast<int32_t>(n_in);
+  for (int k = 0; k < kvol; ++k) {
+    int32_t v = absent;
+    if (row >= 0) {
+      v = table[static_cast<int64_t>(row) * kvol + k];
+      if (static_cast<uint32_t>(v) >= static_cast<uint64_t>(n_in)) v = absent;
+    }
+    g[k * kTileRows] = v;
+    if (v != absent && k < 32) mask |= 1u << k;
+  }
+  // OR-reduce over the wave, then over the block
+  for (int d = 32; d >= 1; d >>= 1) mask |= __shfl_xor(mask, d, 64);
+  if ((r & 63) == 0) wave_mask[r >> 6] = mask;
+  __syncthreads();
+  if (r == 0) {
+    uint32_t m = 0;
+    for (int w = 0; w < kTileRows / 64; ++w) m |= wave_mask[w];
+    tile_mask[tile] = kvol <= 32 ? m : 0xffffffffu;
+  }
+}
+
+size_t sort_temp_bytes(int64_t n) {
+  size_t bytes = 0;
+  hipcub::DoubleBuffer<unsigned long long> kb(nullptr, nullptr);
+  hipcub::DoubleBuffer<int32_t> vb(nullptr, nullptr);
+  hipcub::DeviceRadixSort::SortPairs(nullptr, bytes, kb, vb, static_cast<int>(std::max<int64_t>(n, 1)), 0, 64);
+  return bytes;
+}
+
+}  // namespace
+}  // namespace hi3d
+
+using namespace hi3d;
+
+extern "C" {
+
+int32_t hi3d_conv_tile_rows(void) { return kTileRows; }
+
+int hi3d_conv_plan_workspace(int64_t n_out, int64_t* bytes) {
+  HI3D_REQUIRE(bytes != nullptr, "bytes_host is NULL");
+  HI3D_REQUIRE(n_out >= 0 && n_out < (int64_t(1) << 31) - 1, "bad n_out");
+  const int64_t m = std::max<int64_t>(n_out, 1);
+  *bytes = 2 * align_up(m * 8, 256) + 2 * align_up(m * 4, 256) + align_up(static_cast<int64_t>(sort_temp_bytes(m)), 256) + 256;
+  return HI3D_OK;
+}
+
+int hi3d_conv_plan(const int32_t* table, int64_t n_out, int32_t kvol, int64_t n_in, const int32_t* coords,
+                   int64_t window_rows, void* workspace, int64_t workspace_bytes, int32_t* rows, int32_t* gidx,
+                   uint32_t* tile_mask, void* stream_) {
+  hipStream_t stream = as_stream(stream_);
+  int64_t need = 0;
+  int rc = hi3d_conv_plan_workspace(n_out, &need);
+  if (rc != HI3D_OK) return rc;
+  HI3D_REQUIRE(kvol >= 1 && kvol <= 1024, "kvol out of range: %d", kvol);
+  HI3D_REQUIRE(n_in >= 0 && n_in < (int64_t(1) << 31) - 1, "bad n_in");
+  if (n_out == 0) return HI3D_OK;
+  HI3D_REQUIRE(table && rows && gidx && tile_mask && workspace, "null pointer argument");
+  HI3D_REQUIRE(workspace_bytes >= need, "workspace too small");
+  Workspace ws(workspace, workspace_bytes);
+  auto* k0 = ws.take<unsigned long long>(n_out);
+  auto* k1 = ws.take<unsigned long long>(n_out);
+  auto* r0 = ws.take<int32_t>(n_out);
+  auto* r1 = ws.take<int32_t>(n_out);
+  size_t temp_bytes = sort_temp_bytes(n_out);
+  void* temp = ws.take<char>(static_cast<int64_t>(temp_bytes));
+  const unsigned blocks = static_cast<unsigned>(ceil_div(n_out, 256));
+  const int n = static_cast<int>(n_out);
+  const int32_t* order = nullptr;
+  if (coords) {
+    hipLaunchKernelGGL(morton_kernel, dim3(blocks), dim3(256), 0, stream, reinterpret_cast<const int4*>(coords),
+                       n_out, k0, r0);
+    hipcub::DoubleBuffer<unsigned long long> kb(k0, k1);
+    hipcub::DoubleBuffer<int32_t> vb(r0, r1);
+    HI3D_HIP_CHECK(hipcub::DeviceRadixSort::SortPairs(temp, temp_bytes, kb, vb, n, 0, 64, stream));
+    order = vb.Current();
+  } else {
+    hipLaunchKernelGGL(iota_kernel, dim3(blocks), dim3(256), 0, stream, r0, n_out);
+    order = r0;
+  }
+  // second key: (window, mask); the sort is stable, so Morton order survives inside
+  int32_t* ord_in = const_cast<int32_t*>(order);
+  int32_t* ord_alt = (ord_in == r0) ? r1 : r0;
+  hipLaunchKernelGGL(mask_keys_kernel, dim3(blocks), dim3(256), 0, stream, table, n_out, kvol, n_in, ord_in,
+                     window_rows, k0, ord_alt);
+  int64_t windows = window_rows > 0 ? ceil_div(n_out, window_rows) : 1;
+  int end_bit = 32;
+  while (end_bit < 64 && (int64_t(1) << (end_bit - 32)) < windows) ++end_bit;
+  const int begin_bit = 0;
+  const int mask_bits = kvol <= 32 ? kvol : 0;
+  const int32_t* final_order = ord_alt;
+  if (mask_bits > 0 || windows > 1) {
+    // mask occupies bits [0, kvol); windows bits [32, end_bit)
+    hipcub::DoubleBuffer<unsigned long long> kb(k0, k1);
+    hipcub::DoubleBuffer<int32_t> vb(ord_alt, ord_in);
+    if (windows > 1 || mask_bits > 0) {
+      const int eb = windows > 1 ? end_bit : std::max(mask_bits, 1);
+      HI3D_HIP_CHECK(hipcub::DeviceRadixSort::SortPairs(temp, temp_bytes, kb, vb, n, begin_bit, eb, stream));
+    }
+    final_order = vb.Current();
+  }
+  const int64_t ntiles = ceil_div(n_out, kTileRows);
+  hipLaunchKernelGGL(tile_kernel, dim3(static_cast<unsigned>(ntiles)), dim3(kTileRows), 0, stream, table, n_out,
+                     kvol, n_in, final_order, rows, gidx, tile_mask);
+  HI3D_LAUNCH_CHECK();
+  return HI3D_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,125 @@
+"""Gather convolutions on the GPU (submanifold, 2x2x2/s2 and its transpose).
+
+``gather_conv`` runs the MFMA kernel over a :class:`~hi3d_amd.kmap.ConvPlan`;
+``gather_conv_simple`` runs the one-thread-per-output kernel straight from a table for
+channel counts and dtypes (float64) the MFMA kernel does not take. Both compute
+
+    out[o] = act(bias + sum_k in[table[o, k]] @ W[:, k, :].T) (+ residual[o])
+
+with ``W`` in spconv's ``[Cout, K, Cin]`` layout (reference:
+src/hi3d_mac/torch_backend/sparse_conv.py:152-195; src/hi3d_mac/mlx_backend/sparse.py:191-214).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from .kmap import ConvPlan
+
+ACTIVATIONS = {None: _lib.ACT_NONE, "none": _lib.ACT_NONE, "silu": _lib.ACT_SILU}
+
+
+def _flat_weight(weight: torch.Tensor, kvol: int) -> torch.Tensor:
+    cout, cin = int(weight.shape[0]), int(weight.shape[-1])
+    w = weight.reshape(cout, -1, cin)
+    if w.shape[1] != kvol:
+        raise ValueError(f"weight has {w.shape[1]} kernel offsets, the map has {kvol}")
+    return w.contiguous()
+
+
+def mfma_supported(dtype: torch.dtype, cin: int, cout: int) -> bool:
+    """Whether the MFMA kernel takes this dtype and channel count (16-byte rows)."""
+    if dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        return False
+    es = torch.empty((), dtype=dtype).element_size()
+    return (cin * es) % 16 == 0 and (cout * es) % 16 == 0
+
+
+def gather_conv(
+    features: torch.Tensor,
+    plan: ConvPlan,
+    weight: torch.Tensor,
+    bias: torch.Tensor | None = None,
+    act: str | None = None,
+    residual: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """MFMA gather convolution; features, weight, bias, residual share one dtype."""
+    device = _lib.require_gpu(features, weight, bias, residual, plan.gidx)
+    dtype = features.dtype
+    if weight.dtype != dtype or (bias is not None and bias.dtype != dtype) or (
+        residual is not None and residual.dtype != dtype
+    ):
+        raise ValueError("features, weight, bias and residual must share one dtype")
+    if features.ndim != 2 or features.shape[0] != plan.n_in:
+        raise ValueError(f"expected features [{plan.n_in}, Cin], got {tuple(features.shape)}")
+    x = features.contiguous()
+    w = _flat_weight(weight, plan.kvol)
+    cin, cout = int(x.shape[1]), int(w.shape[0])
+    if int(w.shape[2]) != cin:
+        raise ValueError(f"weight expects {int(w.shape[2])} input channels, features have {cin}")
+    if not mfma_supported(dtype, cin, cout):
+        raise ValueError(f"MFMA path needs fp16/bf16/fp32 and 16-byte channel rows (dtype {dtype}, {cin}->{cout})")
+    b = None if bias is None else bias.contiguous()
+    r = None if residual is None else residual.contiguous()
+    if r is not None and tuple(r.shape) != (plan.n_out, cout):
+        raise ValueError("residual must have the output's shape")
+    if out is None:
+        out = torch.empty((plan.n_out, cout), dtype=dtype, device=device)
+    _lib.call(
+        "hi3d_gather_conv",
+        _lib.ptr(x), plan.n_in, cin, _lib.ptr(w), _lib.ptr(b), cout, plan.kvol, _lib.ptr(plan.rows),
+        _lib.ptr(plan.gidx), _lib.ptr(plan.tile_mask), plan.n_out, _lib.ptr(r), ACTIVATIONS[act],
+        _lib.DTYPES[dtype], _lib.ptr(out), _lib.stream(device),
+    )
+    return out
+
+
+def gather_conv_simple(
+    features: torch.Tensor,
+    table: torch.Tensor,
+    weight: torch.Tensor,
+    bias: torch.Tensor | None = None,
+    act: str | None = None,
+    residual: torch.Tensor | None = None,
+    n_in: int | None = None,
+) -> torch.Tensor:
+    """The same convolution from a plain table, any channel count, float64 too."""
+    device = _lib.require_gpu(features, table, weight, bias, residual)
+    dtype = features.dtype
+    if dtype not in _lib.DTYPES:
+        raise ValueError(f"unsupported dtype {dtype}")
+    if weight.dtype != dtype or (bias is not None and bias.dtype != dtype):
+        raise ValueError("features, weight and bias must share one dtype")
+    x = features.contiguous()
+    t = table.to(torch.int32).contiguous()
+    kvol = int(t.shape[1])
+    w = _flat_weight(weight, kvol)
+    cin, cout = int(x.shape[1]), int(w.shape[0])
+    n_out = int(t.shape[0])
+    n_in = int(x.shape[0]) if n_in is None else int(n_in)
+    out = torch.empty((n_out, cout), dtype=dtype, device=device)
+    b = None if bias is None else bias.contiguous()
+    r = None if residual is None else residual.to(dtype).contiguous()
+    _lib.call(
+        "hi3d_gather_conv_simple",
+        _lib.ptr(x), n_in, cin, _lib.ptr(w), _lib.ptr(b), cout, kvol, _lib.ptr(t), n_out, _lib.ptr(r),
+        ACTIVATIONS[act], _lib.DTYPES[dtype], _lib.ptr(out), _lib.stream(device),
+    )
+    return out
+
+
+def conv(
+    features: torch.Tensor,
+    plan: ConvPlan,
+    weight: torch.Tensor,
+    bias: torch.Tensor | None = None,
+    act: str | None = None,
+    residual: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Dispatch to the MFMA kernel when it takes the shape, else to the simple kernel."""
+    cin, cout = int(features.shape[1]), int(weight.shape[0])
+    if mfma_supported(features.dtype, cin, cout):
+        return gather_conv(features, plan, weight, bias, act, residual)
+    return gather_conv_simple(features, plan.table, weight, bias, act, residual, n_in=plan.n_in)

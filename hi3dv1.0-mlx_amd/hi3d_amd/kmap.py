@@ -1,0 +1,298 @@
+"""Kernel maps on the GPU: the dense neighbour table, pair lists, stride-2 structure,
+octree child tables and the tile plans the convolution consumes.
+
+Reference functions replaced here:
+  * ``_voxel_keys`` / ``subm_pairs`` (src/hi3d_mac/torch_backend/sparse_conv.py:109-149)
+  * ``neighbour_table`` (src/hi3d_mac/mlx_backend/sparse.py:29-43)
+  * ``_PairTable`` / ``get_indice_pairs`` (sparse_conv.py:37-50,264-283)
+  * ``downsample_structure`` (src/hi3d_mac/mlx_backend/sparse.py:217-233)
+  * ``child_neighbour_table`` (src/hi3d_mac/mlx_backend/sparse.py:46-95)
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import Sequence
+
+import torch
+
+from . import _lib
+
+PLAN_WINDOW_ROWS: int | None = None
+"""Rows per mask-sorting window of a convolution plan; ``None`` picks by size
+(one window up to ``PLAN_GLOBAL_ROWS`` rows, else ``PLAN_LARGE_WINDOW`` rows)."""
+PLAN_GLOBAL_ROWS = 1 << 21
+PLAN_LARGE_WINDOW = 1 << 18
+
+
+def _as_coords(indices: torch.Tensor) -> torch.Tensor:
+    if indices.ndim != 2 or indices.shape[1] != 4:
+        raise ValueError(f"expected coords [N, 4], got {tuple(indices.shape)}")
+    return indices.to(torch.int32).contiguous()
+
+
+@dataclass
+class ConvPlan:
+    """Tile plan of one gather table: output row per tile slot, transposed gather
+    indices per tile and offset, and the offsets present in each tile."""
+
+    rows: torch.Tensor
+    gidx: torch.Tensor
+    tile_mask: torch.Tensor
+    n_out: int
+    n_in: int
+    kvol: int
+    table: torch.Tensor
+
+    @property
+    def ntiles(self) -> int:
+        return int(self.tile_mask.shape[0])
+
+
+def build_plan(
+    table: torch.Tensor, n_in: int, coords: torch.Tensor | None = None, window_rows: int | None = None
+) -> ConvPlan:
+    """Plan a gather convolution over ``table [n_out, kvol]`` (entries >= n_in absent)."""
+    device = _lib.require_gpu(table, coords)
+    table = table.to(torch.int32).contiguous()
+    n_out, kvol = int(table.shape[0]), int(table.shape[1])
+    if coords is not None:
+        coords = _as_coords(coords)
+        if coords.shape[0] != n_out:
+            raise ValueError("plan coordinates must have one row per output row")
+    if window_rows is None:
+        window_rows = PLAN_WINDOW_ROWS
+    if window_rows is None:
+        window_rows = 0 if n_out <= PLAN_GLOBAL_ROWS else PLAN_LARGE_WINDOW
+    t = int(_lib.lib().hi3d_conv_tile_rows())
+    ntiles = (n_out + t - 1) // t
+    rows = torch.empty(ntiles * t, dtype=torch.int32, device=device)
+    gidx = torch.empty(ntiles * kvol * t, dtype=torch.int32, device=device)
+    tile_mask = torch.empty(ntiles, dtype=torch.int32, device=device)
+    ws = _lib.workspace(_lib.query("hi3d_conv_plan_workspace", n_out), device)
+    _lib.call(
+        "hi3d_conv_plan",
+        _lib.ptr(table), n_out, kvol, int(n_in), _lib.ptr(coords), int(window_rows),
+        _lib.ptr(ws), ws.numel(), _lib.ptr(rows), _lib.ptr(gidx), _lib.ptr(tile_mask), _lib.stream(device),
+    )
+    return ConvPlan(rows, gidx, tile_mask, n_out, int(n_in), kvol, table)
+
+
+@dataclass
+class KernelMap:
+    """Submanifold kernel map of one coordinate set (built once, reused by every
+    convolution over the set, like the reference's ``indice_dict`` cache)."""
+
+    indices: torch.Tensor
+    spatial_shape: list[int]
+    batch_size: int
+    ksize: int
+    table: torch.Tensor  # [N, ksize^3] int32, sentinel N
+    counts: torch.Tensor  # [ksize^3] int32 (device)
+    _pairs: tuple | None = field(default=None, repr=False)
+    _plans: dict = field(default_factory=dict, repr=False)
+
+    @property
+    def n(self) -> int:
+        return int(self.table.shape[0])
+
+    @property
+    def kvol(self) -> int:
+        return int(self.table.shape[1])
+
+    def pairs(self) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        """``(src, dst, offsets)``: per-offset lists back to back (list k spans
+        ``offsets[k]:offsets[k+1]``), in spconv's orientation."""
+        if self._pairs is None:
+            self._pairs = pair_lists(self.table)
+        return self._pairs
+
+    def plan(self, window_rows: int | None = None) -> ConvPlan:
+        key = window_rows
+        if key not in self._plans:
+            self._plans[key] = build_plan(self.table, self.n, self.indices, window_rows)
+        return self._plans[key]
+
+
+def build_kernel_map(
+    indices: torch.Tensor,
+    spatial_shape: Sequence[int],
+    batch_size: int | None = None,
+    ksize: int = 3,
+    capacity: int | None = None,
+    check: bool = True,
+) -> KernelMap:
+    """Hash-built submanifold kernel map of ``indices [N, 4]`` ``(batch, x, y, z)``.
+
+    With ``check`` the device status word is read (one sync): duplicate or out-of-range
+    coordinates raise ``ValueError``, a full hash table raises ``RuntimeError``.
+    """
+    coords = _as_coords(indices)
+    device = _lib.require_gpu(coords)
+    sx, sy, sz = (int(v) for v in spatial_shape)
+    n = int(coords.shape[0])
+    if batch_size is None:
+        batch_size = int(coords[:, 0].max()) + 1 if n else 1
+    if ksize % 2 == 0 or ksize < 1:
+        raise ValueError(f"only odd kernel sizes have a submanifold map, got {ksize}")
+    kvol = ksize**3
+    key64 = int(batch_size) * sx * sy * sz >= 0xFFFFFFFF
+    cap = int(capacity or 0)
+    ws = _lib.workspace(_lib.query("hi3d_kmap_workspace", n, cap, int(key64)), device)
+    table = torch.empty((n, kvol), dtype=torch.int32, device=device)
+    counts = torch.empty(kvol, dtype=torch.int32, device=device)
+    status = torch.empty(1, dtype=torch.int32, device=device)
+    _lib.call(
+        "hi3d_kmap_subm",
+        _lib.ptr(coords), n, sx, sy, sz, int(batch_size), int(ksize), cap, _lib.ptr(ws), ws.numel(),
+        _lib.ptr(table), _lib.ptr(counts), _lib.ptr(status), _lib.stream(device),
+    )
+    if check:
+        flags = int(status.item())
+        if flags & _lib.MAP_DUPLICATE:
+            raise ValueError("duplicate coordinates: every active voxel must appear once")
+        if flags & _lib.MAP_RANGE:
+            raise ValueError(f"coordinates outside spatial_shape {[sx, sy, sz]} or batch {batch_size}")
+        if flags & _lib.MAP_OVERFLOW:
+            raise RuntimeError("voxel hash table overflow: capacity too small for the active set")
+    return KernelMap(coords, [sx, sy, sz], int(batch_size), int(ksize), table, counts)
+
+
+def pair_lists(table: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Per-offset ``(src, dst)`` lists from a neighbour table: list k holds
+    ``(i, table[i, kvol-1-k])`` for every row i with that entry present, ascending i."""
+    device = _lib.require_gpu(table)
+    table = table.to(torch.int32).contiguous()
+    n, kvol = int(table.shape[0]), int(table.shape[1])
+    offsets = torch.empty(kvol + 1, dtype=torch.int64, device=device)
+    ws = _lib.workspace(_lib.query("hi3d_kmap_pairs_workspace", n, kvol), device)
+    total_cap = n * kvol
+    src = torch.empty(max(total_cap, 1), dtype=torch.int32, device=device)
+    dst = torch.empty(max(total_cap, 1), dtype=torch.int32, device=device)
+    _lib.call(
+        "hi3d_kmap_pairs",
+        _lib.ptr(table), n, kvol, _lib.ptr(ws), ws.numel(), _lib.ptr(src), _lib.ptr(dst), _lib.ptr(offsets),
+        _lib.stream(device),
+    )
+    total = int(offsets[-1].item())
+    return src[:total], dst[:total], offsets
+
+
+def neighbour_table(coords: torch.Tensor) -> torch.Tensor:
+    """``[N, 27]`` row of each voxel's neighbours (``N`` where absent), for ``[N, 3]``
+    coordinates ``(x, y, z)`` of one batch element (the reference's MLX-side helper)."""
+    if coords.ndim != 2 or coords.shape[1] != 3:
+        raise ValueError(f"expected coords [N, 3], got {tuple(coords.shape)}")
+    _lib.require_gpu(coords)
+    xyz = coords.to(torch.int32)
+    n = int(xyz.shape[0])
+    if n == 0:
+        return torch.empty((0, 27), dtype=torch.int32, device=coords.device)
+    if int(xyz.min()) < 0:
+        raise ValueError("grid coordinates must be non-negative")
+    extent = (xyz.max(dim=0).values + 1).tolist()
+    indices = torch.cat([torch.zeros((n, 1), dtype=torch.int32, device=coords.device), xyz], 1)
+    return build_kernel_map(indices, extent, 1, 3).table
+
+
+@dataclass
+class Stride2Structure:
+    """Coarse set of a 2x2x2/s2 downsampling and its gather tables."""
+
+    low: torch.Tensor  # [Nc, 4] int32 (batch, x, y, z), lexicographic
+    inverse: torch.Tensor  # [Nf] int32
+    counts: torch.Tensor  # [Nc] int32
+    slot: torch.Tensor  # [Nf] uint8
+    down: torch.Tensor  # [Nc, 8] fine child per slot (sentinel Nf)
+    up: torch.Tensor  # [Nf, 8] parent in column slot (sentinel Nc)
+    fine_indices: torch.Tensor
+    spatial_shape: list[int]
+    out_spatial_shape: list[int]
+    _plans: dict = field(default_factory=dict, repr=False)
+
+    @property
+    def n_fine(self) -> int:
+        return int(self.inverse.shape[0])
+
+    @property
+    def n_coarse(self) -> int:
+        return int(self.low.shape[0])
+
+    def down_plan(self) -> ConvPlan:
+        if "down" not in self._plans:
+            self._plans["down"] = build_plan(self.down, self.n_fine, self.low)
+        return self._plans["down"]
+
+    def up_plan(self) -> ConvPlan:
+        if "up" not in self._plans:
+            self._plans["up"] = build_plan(self.up, self.n_coarse, self.fine_indices)
+        return self._plans["up"]
+
+
+def stride2_structure(indices: torch.Tensor, spatial_shape: Sequence[int], batch_size: int | None = None) -> Stride2Structure:
+    """Coarse set, parent/slot maps and gather tables of a 2x2x2 stride-2 convolution."""
+    coords = _as_coords(indices)
+    device = _lib.require_gpu(coords)
+    n = int(coords.shape[0])
+    sx, sy, sz = (int(v) for v in spatial_shape)
+    if batch_size is None:
+        batch_size = int(coords[:, 0].max()) + 1 if n else 1
+    low = torch.empty((max(n, 1), 4), dtype=torch.int32, device=device)
+    inverse = torch.empty(n, dtype=torch.int32, device=device)
+    counts = torch.empty(max(n, 1), dtype=torch.int32, device=device)
+    slot = torch.empty(n, dtype=torch.uint8, device=device)
+    n_low_t = torch.empty(1, dtype=torch.int64, device=device)
+    ws = _lib.workspace(_lib.query("hi3d_downsample_workspace", n), device)
+    stream = _lib.stream(device)
+    _lib.call(
+        "hi3d_downsample_structure",
+        _lib.ptr(coords), n, sx, sy, sz, int(batch_size), _lib.ptr(ws), ws.numel(), _lib.ptr(low),
+        _lib.ptr(inverse), _lib.ptr(counts), _lib.ptr(slot), _lib.ptr(n_low_t), stream,
+    )
+    n_low = int(n_low_t.item())
+    low, counts = low[:n_low], counts[:n_low]
+    down = torch.empty((n_low, 8), dtype=torch.int32, device=device)
+    up = torch.empty((n, 8), dtype=torch.int32, device=device)
+    _lib.call("hi3d_stride2_tables", _lib.ptr(inverse), _lib.ptr(slot), n, n_low, _lib.ptr(down), _lib.ptr(up), stream)
+    out_shape = [(sx + 1) // 2, (sy + 1) // 2, (sz + 1) // 2]
+    return Stride2Structure(low, inverse, counts, slot, down, up, coords, [sx, sy, sz], out_shape)
+
+
+def downsample_structure(coords: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """``(low [Nc, 3], inverse [N], counts [Nc])``: unique ``coords // 2`` in
+    lexicographic ``(x, y, z)`` order, each row's parent, and children per parent."""
+    if coords.ndim != 2 or coords.shape[1] != 3:
+        raise ValueError(f"expected coords [N, 3], got {tuple(coords.shape)}")
+    _lib.require_gpu(coords)
+    xyz = coords.to(torch.int32)
+    n = int(xyz.shape[0])
+    extent = (xyz.max(dim=0).values + 1).tolist() if n else [1, 1, 1]
+    indices = torch.cat([torch.zeros((n, 1), dtype=torch.int32, device=coords.device), xyz], 1)
+    s = stride2_structure(indices, extent, 1)
+    return s.low[:, 1:].contiguous(), s.inverse, s.counts
+
+
+def child_neighbour_table(
+    parent_table: torch.Tensor, child_mask: torch.Tensor
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Children's ``[C, 27]`` table (sentinel C), parent ``[C]`` and slot ``[C]`` from
+    the parent table ``[P, 27]`` (sentinel P) and occupancy ``[P, 8]``, parent-major."""
+    device = _lib.require_gpu(parent_table, child_mask)
+    parent_table = parent_table.to(torch.int32).contiguous()
+    mask = child_mask.to(torch.uint8).contiguous()
+    p = int(parent_table.shape[0])
+    if mask.shape != (p, 8) or parent_table.shape[1] != 27:
+        raise ValueError("expected parent_table [P, 27] and child_mask [P, 8]")
+    cap = max(p * 8, 1)
+    table = torch.empty((cap, 27), dtype=torch.int32, device=device)
+    parent = torch.empty(cap, dtype=torch.int32, device=device)
+    slot = torch.empty(cap, dtype=torch.int32, device=device)
+    n_children = torch.empty(1, dtype=torch.int64, device=device)
+    ws = _lib.workspace(_lib.query("hi3d_child_table_workspace", p), device)
+    _lib.call(
+        "hi3d_child_neighbour_table",
+        _lib.ptr(parent_table), _lib.ptr(mask), p, _lib.ptr(ws), ws.numel(), _lib.ptr(table), _lib.ptr(parent),
+        _lib.ptr(slot), _lib.ptr(n_children), _lib.stream(device),
+    )
+    c = int(n_children.item())
+    return table[:c], parent[:c], slot[:c]

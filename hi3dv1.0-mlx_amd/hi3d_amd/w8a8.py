@@ -1,0 +1,113 @@
+"""W8A8 int8 linear on the GPU: per-token quantisation (signed-H64 rotation or none),
+int8 MFMA GEMM with int32 accumulation and the dequant + bias epilogue fused.
+
+Mirrors src/hi3d_mac/mlx_backend/w8a8.py: ``signs`` :16-18, ``quantize_activation``
+:95-102, ``linear`` :105-119 (same names, argument meaning and ValueErrors). The extra
+``rotation`` argument selects ``"h64"`` (the reference's signed block-Hadamard, default)
+or ``"none"`` (plain per-token symmetric quantisation).
+"""
+
+from __future__ import annotations
+
+from functools import lru_cache
+
+import numpy as np
+import torch
+
+from . import _lib
+
+ROTATIONS = ("h64", "none")
+
+
+@lru_cache(None)
+def _signs_np(width: int) -> np.ndarray:
+    return np.random.default_rng(314159 + width).choice([-1.0, 1.0], width).astype(np.float32)
+
+
+def signs(width: int, device: torch.device | str = "cuda") -> torch.Tensor:
+    """``default_rng(314159 + width).choice([-1., 1.], width)`` as float32."""
+    return _signs_cached(int(width), str(torch.device(device)))
+
+
+@lru_cache(None)
+def _signs_cached(width: int, device: str) -> torch.Tensor:
+    return torch.from_numpy(_signs_np(width)).to(device)
+
+
+def _multiplier(k: int, device, rotation: str, multiplier):
+    if rotation not in ROTATIONS:
+        raise ValueError(f"rotation must be one of {ROTATIONS}, got {rotation!r}")
+    if rotation == "none":
+        return None
+    if multiplier is None:
+        return signs(k, device)
+    m = multiplier.to(device=device, dtype=torch.float32).contiguous()
+    if m.shape != (k,):
+        raise ValueError(f"multiplier must be [{k}]")
+    return m
+
+
+def quantize_activation(x: torch.Tensor, multiplier: torch.Tensor | None = None, rotation: str = "h64"):
+    """``(q int8 [M, K], s float32 [M])`` of fp16 rows ``x [..., K]``."""
+    k = int(x.shape[-1])
+    if rotation == "h64" and k % 64:
+        raise ValueError("signed H64 requires width divisible by 64")
+    if k % 8:
+        raise ValueError("width must be a multiple of 8")
+    device = _lib.require_gpu(x)
+    x2 = x.reshape(-1, k).to(torch.float16).contiguous()
+    m = int(x2.shape[0])
+    mult = _multiplier(k, device, rotation, multiplier)
+    q = torch.empty((m, k), dtype=torch.int8, device=device)
+    s = torch.empty(m, dtype=torch.float32, device=device)
+    _lib.call("hi3d_w8a8_quantize", _lib.ptr(x2), m, k, _lib.ptr(mult), _lib.ptr(q), _lib.ptr(s), _lib.stream(device))
+    return q, s
+
+
+def gemm(
+    q: torch.Tensor,
+    sa: torch.Tensor,
+    w: torch.Tensor,
+    sw: torch.Tensor,
+    bias: torch.Tensor | None,
+    return_acc: bool = False,
+):
+    """Int8 GEMM with fused dequant: ``fp16(((float)acc * sa) * sw + bias)``; with
+    ``return_acc`` also the int32 accumulators."""
+    device = _lib.require_gpu(q, sa, w, sw, bias)
+    m, k = int(q.shape[0]), int(q.shape[1])
+    n = int(w.shape[0])
+    if q.dtype != torch.int8 or w.dtype != torch.int8 or int(w.shape[1]) != k:
+        raise ValueError("q [M, K] and w [N, K] must be int8 with matching K")
+    out = torch.empty((m, n), dtype=torch.float16, device=device)
+    acc = torch.empty((m, n), dtype=torch.int32, device=device) if return_acc else None
+    b = None if bias is None else bias.to(torch.float16).contiguous()
+    _lib.call(
+        "hi3d_w8a8_gemm",
+        _lib.ptr(q.contiguous()), _lib.ptr(sa.contiguous()), _lib.ptr(w.contiguous()), _lib.ptr(sw.contiguous()),
+        _lib.ptr(b), m, n, k, _lib.ptr(out), _lib.ptr(acc), _lib.stream(device),
+    )
+    return (out, acc) if return_acc else out
+
+
+def linear(x, w, sw, bias, tile=(64, 128), multiplier=None, rotation: str = "h64"):
+    """``x [..., K]`` fp16 through the int8 projection ``w [N, K]`` (int8, rows already
+    rotated like the activations) with per-row scales ``sw [N]`` and fp16 ``bias [N]``.
+    ``tile`` is accepted for signature parity; the GPU kernel picks its own tiles."""
+    if w.dtype != torch.int8 or sw.dtype != torch.float32:
+        raise ValueError("W8A8 requires int8 weights and float32 scales")
+    if w.ndim != 2 or x.shape[-1] != w.shape[1] or tuple(sw.shape) != (w.shape[0],) or tuple(bias.shape) != (w.shape[0],):
+        raise ValueError("incompatible W8A8 projection shapes")
+    shape = tuple(x.shape[:-1])
+    n = int(w.shape[0])
+    a, sa = quantize_activation(x, multiplier, rotation)
+    y = gemm(a, sa, w, sw, bias)
+    return y.reshape(*shape, n)
+
+
+def quantize_weight(weight: torch.Tensor, rotation: str = "h64", multiplier: torch.Tensor | None = None):
+    """Offline weight conversion: ``(w int8 [N, K], sw float32 [N])``, symmetric per output
+    row (``maxabs / 127``, round half to even), rows rotated by the same signed H64 as
+    the activations when ``rotation == "h64"`` (format ``hi3d-w8a8-h64``,
+    models/w8a8/manifest.json:10-17). Uses the activation quantiser on the rows."""
+    return quantize_activation(weight.to(torch.float16), multiplier, rotation)

@@ -1,0 +1,229 @@
+/*
+ * hi3d_amd — C ABI of the MI355X (gfx950) sparse-tensor hot path of the Hi3D refiner:
+ * voxel-hash kernel maps, gather-MFMA sparse convolution (submanifold and 2x2x2/s2 with
+ * its transpose), the W8A8 int8 linear and the LayerNorm+adaLN row kernel.
+ *
+ * Conventions
+ *  - Every pointer argument named *_dev is device memory owned by the caller; host
+ *    arrays are named *_host. The library never allocates: scratch comes from a
+ *    caller-provided workspace whose size the matching *_workspace() call reports.
+ *  - Calls are asynchronous on `stream` (a hipStream_t; NULL = default stream) and
+ *    return HI3D_OK or an error code; hi3d_last_error() gives the message of the
+ *    calling thread's last failure. Errors found by kernels (duplicate coordinates,
+ *    hash overflow, out-of-range coordinates) are OR-ed into a caller-provided device
+ *    status word, which the caller reads after the stream has reached that point.
+ *  - Coordinates are int32 [N, 4] rows (batch, x, y, z), as in the reference's
+ *    SparseConvTensor.indices (src/hi3d_mac/torch_backend/sparse_conv.py:78-106).
+ *  - A neighbour table is int32 [N, K] with K = ksize^3 and flat kernel offset
+ *    k = r0*ksize^2 + r1*ksize + r2 (x-major), entry = row of the voxel at
+ *    coords[o] + r - ksize/2, or N when absent
+ *    (src/hi3d_mac/mlx_backend/sparse.py:20-43).
+ *  - Weights use spconv's layout [Cout, K, Cin]
+ *    (src/hi3d_mac/torch_backend/sparse_conv.py:230).
+ */
+#ifndef HI3D_AMD_H
+#define HI3D_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum hi3d_status {
+  HI3D_OK = 0,
+  HI3D_ERR_INVALID = 1,   /* bad argument (shape, dtype, null pointer, small workspace) */
+  HI3D_ERR_HIP = 2,       /* a HIP runtime call or kernel launch failed */
+  HI3D_ERR_UNSUPPORTED = 3
+};
+
+/* Bits of the device status word written by map-building kernels. */
+enum hi3d_map_flags {
+  HI3D_MAP_DUPLICATE = 1, /* two rows share a coordinate */
+  HI3D_MAP_OVERFLOW = 2,  /* the hash table ran out of free slots */
+  HI3D_MAP_RANGE = 4      /* a coordinate lies outside [0, spatial_shape) or the batch */
+};
+
+enum hi3d_dtype { HI3D_F32 = 0, HI3D_F16 = 1, HI3D_BF16 = 2, HI3D_F64 = 3 };
+
+enum hi3d_act { HI3D_ACT_NONE = 0, HI3D_ACT_SILU = 1 };
+
+/* Message of the calling thread's last failed call ("" if none). */
+const char* hi3d_last_error(void);
+
+/* Library version string. */
+const char* hi3d_version(void);
+
+/* ------------------------------------------------------------------ kernel maps -- */
+
+/* Workspace bytes of hi3d_kmap_subm for n voxels; capacity 0 = default (power of two
+ * >= 2n). key64 != 0 when batch*sx*sy*sz >= 2^32 - 1 (64-bit voxel keys). */
+int hi3d_kmap_workspace(int64_t n, int64_t capacity, int32_t key64, int64_t* bytes_host);
+
+/* Submanifold kernel map: inserts every voxel's packed key
+ * ((b*sx + x)*sy + y)*sz + z into an open-addressing hash (linear probing, one CAS per
+ * insert) and probes the ksize^3 neighbourhood of each voxel, writing the dense
+ * neighbour table nbr_dev [n, ksize^3] (sentinel n) and per-offset non-sentinel counts
+ * counts_dev [ksize^3]. Neighbours outside [0, spatial_shape) are absent.
+ * Replaces: _voxel_keys + subm_pairs (src/hi3d_mac/torch_backend/sparse_conv.py:109-149)
+ * and neighbour_table (src/hi3d_mac/mlx_backend/sparse.py:29-43). */
+int hi3d_kmap_subm(const int32_t* coords_dev, int64_t n, int32_t sx, int32_t sy, int32_t sz,
+                   int32_t batch_size, int32_t ksize, int64_t capacity, void* workspace_dev,
+                   int64_t workspace_bytes, int32_t* nbr_dev, int32_t* counts_dev,
+                   int32_t* status_dev, void* stream);
+
+/* Workspace bytes of hi3d_kmap_pairs. */
+int hi3d_kmap_pairs_workspace(int64_t n, int32_t kvol, int64_t* bytes_host);
+
+/* Per-offset pair lists in spconv's orientation: for offset k the pairs
+ * (i, nbr[i, kvol-1-k]) of every row i (ascending) whose entry is present, written
+ * back to back: list k occupies [offsets[k], offsets[k+1]) of src_dev/dst_dev.
+ * offsets_dev [kvol+1] is int64. An input at coords[src] feeds the output at
+ * coords[dst] = coords[src] + ksize/2 - r_k.
+ * Replaces: subm_pairs' (sources, targets) lists and _PairTable / get_indice_pairs
+ * (src/hi3d_mac/torch_backend/sparse_conv.py:37-50,115-149,264-283). */
+int hi3d_kmap_pairs(const int32_t* nbr_dev, int64_t n, int32_t kvol, void* workspace_dev,
+                    int64_t workspace_bytes, int32_t* src_dev, int32_t* dst_dev,
+                    int64_t* offsets_dev, void* stream);
+
+/* Workspace bytes of hi3d_downsample_structure. */
+int hi3d_downsample_workspace(int64_t n, int64_t* bytes_host);
+
+/* 2x2x2 / stride-2 coarse structure: low = sorted unique (b, x>>1, y>>1, z>>1)
+ * (lexicographic), inverse[i] = coarse row of fine row i, counts[c] = children of c,
+ * slot[i] = (x&1)*4 + (y&1)*2 + (z&1). n_low_dev receives the coarse row count (int64).
+ * low_dev must hold n rows of 4 int32 (only the first n_low are written); counts_dev n.
+ * Replaces: downsample_structure (src/hi3d_mac/mlx_backend/sparse.py:217-233) and the
+ * coordinate part of SparseDownsample (src/sparc3d/nn/sparse/spatial.py:34-63). */
+int hi3d_downsample_structure(const int32_t* coords_dev, int64_t n, int32_t sx, int32_t sy,
+                              int32_t sz, int32_t batch_size, void* workspace_dev,
+                              int64_t workspace_bytes, int32_t* low_dev, int32_t* inverse_dev,
+                              int32_t* counts_dev, uint8_t* slot_dev, int64_t* n_low_dev,
+                              void* stream);
+
+/* Gather tables of the strided pair: down_dev [n_low, 8] = fine row of child slot s of
+ * each coarse voxel (sentinel n), up_dev [n, 8] = coarse parent in column slot[i] and
+ * n_low elsewhere. Either output may be NULL.
+ * (No reference function: the reference raises for stride != 1,
+ * src/sparc3d/ops/sparse_backend.py:184-191; the slot order follows
+ * src/hi3d_mac/mlx_backend/sparse.py:46-61.) */
+int hi3d_stride2_tables(const int32_t* inverse_dev, const uint8_t* slot_dev, int64_t n,
+                        int64_t n_low, int32_t* down_dev, int32_t* up_dev, void* stream);
+
+/* Workspace bytes of hi3d_child_neighbour_table. */
+int hi3d_child_table_workspace(int64_t n_parents, int64_t* bytes_host);
+
+/* Octree children's neighbour table from the parent table [P, 27] (sentinel P) and the
+ * child occupancy mask [P, 8] (uint8 0/1), without hashing: child c = (parent p, slot s)
+ * in parent-major, slot-minor order; table_dev [C, 27] (sentinel C), parent_dev [C],
+ * slot_dev [C]. Buffers hold P*8 rows; n_children_dev receives C (int64).
+ * Replaces: child_neighbour_table / _child_offset_tables
+ * (src/hi3d_mac/mlx_backend/sparse.py:46-95). */
+int hi3d_child_neighbour_table(const int32_t* parent_table_dev, const uint8_t* mask_dev,
+                               int64_t n_parents, void* workspace_dev, int64_t workspace_bytes,
+                               int32_t* table_dev, int32_t* parent_dev, int32_t* slot_dev,
+                               int64_t* n_children_dev, void* stream);
+
+/* ------------------------------------------------------------ convolution plans -- */
+
+/* Rows per tile of the gather-MFMA convolution. */
+int32_t hi3d_conv_tile_rows(void);
+
+/* Workspace bytes of hi3d_conv_plan. */
+int hi3d_conv_plan_workspace(int64_t n_out, int64_t* bytes_host);
+
+/* Execution plan of a gather convolution over table_dev [n_out, kvol] (entries >= n_in
+ * are absent): output rows are ordered by Morton code of coords_dev (NULL = row
+ * order), then grouped by their neighbour-presence mask within windows of
+ * window_rows rows (0 = one window), and cut into tiles of hi3d_conv_tile_rows() rows.
+ * Outputs: rows_dev [ntiles*T] (output row per tile slot, -1 past n_out),
+ * gidx_dev [ntiles, kvol, T] (input row per tile slot and offset, n_in if absent) and
+ * tile_mask_dev [ntiles] (offsets present in the tile; kvol <= 32, else all ones).
+ * Built once per coordinate set and reused by every convolution over it, like the
+ * reference's indice_dict cache (src/sparc3d/ops/sparse_backend.py:52-56,124-127). */
+int hi3d_conv_plan(const int32_t* table_dev, int64_t n_out, int32_t kvol, int64_t n_in,
+                   const int32_t* coords_dev, int64_t window_rows, void* workspace_dev,
+                   int64_t workspace_bytes, int32_t* rows_dev, int32_t* gidx_dev,
+                   uint32_t* tile_mask_dev, void* stream);
+
+/* Gather-MFMA convolution: out[o] = act(bias + sum_k in[table[o,k]] . W[:, k, :]^T)
+ * (+ residual[o] after act), fp32 accumulation, every output row written once.
+ * in_dev [n_in, cin], weight_dev [cout, kvol, cin], bias_dev [cout] or NULL,
+ * residual_dev [n_out, cout] or NULL, out_dev [n_out, cout]; all of dtype (F32, F16,
+ * BF16). Requires cin*elem % 16 == 0 and 16-byte aligned pointers.
+ * Replaces: subm_conv / SubMConv3d.forward (src/hi3d_mac/torch_backend/sparse_conv.py:
+ * 152-195,244-247), SubMConv3d._large_forward (src/sparc3d/ops/sparse_backend.py:47-128)
+ * and sparse_conv (src/hi3d_mac/mlx_backend/sparse.py:191-214). */
+int hi3d_gather_conv(const void* in_dev, int64_t n_in, int32_t cin, const void* weight_dev,
+                     const void* bias_dev, int32_t cout, int32_t kvol, const int32_t* rows_dev,
+                     const int32_t* gidx_dev, const uint32_t* tile_mask_dev, int64_t n_out,
+                     const void* residual_dev, int32_t act, int32_t dtype, void* out_dev,
+                     void* stream);
+
+/* The same convolution straight from a table [n_out, kvol], one thread per output
+ * element: any channel count and F64 as well. Used for shapes the MFMA path does not
+ * take (e.g. the reference's C 5->7 float64 case, tests/test_backends.py:32-50). */
+int hi3d_gather_conv_simple(const void* in_dev, int64_t n_in, int32_t cin,
+                            const void* weight_dev, const void* bias_dev, int32_t cout,
+                            int32_t kvol, const int32_t* table_dev, int64_t n_out,
+                            const void* residual_dev, int32_t act, int32_t dtype, void* out_dev,
+                            void* stream);
+
+/* Mean of the present rows per table row: out[o] = sum_k in[table[o,k]] / (count + extra)
+ * over entries < n_in; fp32 (F64: fp64) accumulation. With the stride-2 down table and
+ * extra = 1 this is SparseDownsample's scatter_reduce(mean) onto a zero-initialised
+ * output, which counts the zero as one more element
+ * (src/sparc3d/nn/sparse/spatial.py:53-62). */
+int hi3d_gather_mean(const void* in_dev, int64_t n_in, int32_t c, const int32_t* table_dev,
+                     int32_t kvol, int64_t n_out, int32_t extra, int32_t dtype, void* out_dev,
+                     void* stream);
+
+/* -------------------------------------------------------------------- W8A8 -- */
+
+/* Per-token symmetric int8 quantisation of x_dev [m, k] fp16: with signs_dev [k]
+ * (fp32 +-1) each 64-column block is multiplied by the signs and rotated by the
+ * orthonormal Sylvester-ordered Hadamard H64 (butterflies over column bits 0..5 in that
+ * order, then x0.125); with signs_dev NULL no rotation. s = max(max|v|, 1e-8)/127,
+ * q = clamp(rint(v/s), -127, 127). k % 64 == 0 when rotating.
+ * Replaces: quantize_activation / _QUANT (src/hi3d_mac/mlx_backend/w8a8.py:25-58,95-102). */
+int hi3d_w8a8_quantize(const void* x_dev, int64_t m, int32_t k, const float* signs_dev,
+                       int8_t* q_dev, float* scale_dev, void* stream);
+
+/* out[m, n] = fp16(((float)acc * sa[m]) * sw[n] + (float)bias[n]) with
+ * acc = sum_k q[m,k]*w[n,k] in int32 (int8 MFMA); no FMA contraction in the epilogue.
+ * q_dev [m,k] int8, w_dev [n,k] int8, sa [m], sw [n] fp32, bias [n] fp16 or NULL,
+ * out_dev [m,n] fp16; acc_dev [m,n] int32 optional (NULL = not written).
+ * Requires k % 16 == 0.
+ * Replaces: _GEMM / linear (src/hi3d_mac/mlx_backend/w8a8.py:61-80,105-119). */
+int hi3d_w8a8_gemm(const int8_t* q_dev, const float* sa_dev, const int8_t* w_dev,
+                   const float* sw_dev, const void* bias_dev, int64_t m, int32_t n, int32_t k,
+                   void* out_dev, int32_t* acc_dev, void* stream);
+
+/* ---------------------------------------------------------- LayerNorm + adaLN -- */
+
+/* Row LayerNorm of x_dev [rows, c] fp16 with fp32 two-pass statistics,
+ * y = (x - mean) / sqrt(var + eps) (optionally * weight + bias, fp32 [c]),
+ * h = fp16(y); with scale/shift (fp16 [c]) h = fp16(fp16(h*scale) + shift).
+ * Replaces: layer_norm_modulate (src/hi3d_mac/mlx_backend/kernels.py:162-237) /
+ * LayerNorm32 + modulate (src/sparc3d/nn/norm.py:12-17,
+ * src/sparc3d/models/transformers/sparc3d_transformer.py:140). */
+int hi3d_layer_norm_modulate(const void* x_dev, int64_t rows, int32_t c, float eps,
+                             const float* weight_dev, const float* bias_dev,
+                             const void* scale_dev, const void* shift_dev, void* out_dev,
+                             void* stream);
+
+/* adaLN projection: y = W . (silu(cond) if apply_silu else cond) + b in fp32
+ * (W [n_out, n_in] fp32, cond [n_in], b [n_out] or NULL), then
+ * scale1p_dev = fp16(1 + fp16(y[:n_out/2])) and shift_dev = fp16(y[n_out/2:])
+ * (the chunk order (scale, shift) of _emb_scale_shift,
+ * src/hi3d_mac/mlx_backend/transformer.py:413-416, and the fp16 rounding of (1 + scale),
+ * src/hi3d_mac/mlx_backend/transformer.py:547-548). */
+int hi3d_adaln_projection(const float* w_dev, const float* b_dev, const float* cond_dev,
+                          int32_t n_out, int32_t n_in, int32_t apply_silu, void* scale1p_dev,
+                          void* shift_dev, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HI3D_AMD_H */

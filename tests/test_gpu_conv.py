@@ -1,0 +1,201 @@
+"""Gather convolutions on the GPU against the oracle.
+
+Gates (max|y - y_ref| / rms(y_ref)): fp32 <= 1e-5, fp16 <= 1e-2 (bf16 <= 3e-2, one
+bf16 ulp being 8x an fp16 ulp); float64 (the reference test's C 5->7 case) <= 1e-12
+absolute. Large workloads are checked on sampled output rows against float64 sums.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import GOLDEN
+from oracle import conv as oconv
+from oracle import kmap as okmap
+
+pytestmark = pytest.mark.gpu
+
+GATE = {torch.float32: 1e-5, torch.float16: 1e-2, torch.bfloat16: 3e-2}
+
+
+def _rand_indices(rng, n_side, density, batch=1):
+    rows = []
+    for b in range(batch):
+        xyz = np.argwhere(rng.random((n_side,) * 3) < density)
+        rows.append(np.concatenate([np.full((len(xyz), 1), b), xyz], 1))
+    idx = np.concatenate(rows).astype(np.int32)
+    return idx[rng.permutation(len(idx))]
+
+
+def _case(rng, n, cin, cout, dtype, kvol=27):
+    x = torch.as_tensor(rng.standard_normal((n, cin), dtype=np.float32)).to(dtype)
+    w = torch.as_tensor(rng.standard_normal((cout, kvol, cin), dtype=np.float32) / np.sqrt(kvol * cin)).to(dtype)
+    b = torch.as_tensor(rng.standard_normal(cout, dtype=np.float32) * 0.1).to(dtype)
+    return x, w, b
+
+
+def test_reference_case_float64_golden(cuda):
+    """tests/test_backends.py:32-50 recipe through the spconv API in float64."""
+    from hi3d_amd import spconv
+
+    data = np.load(GOLDEN / "subm_14cube.npz")
+    conv = spconv.SubMConv3d(5, 7, 3, bias=True, indice_key="subm3").double().to(cuda)
+    with torch.no_grad():
+        conv.weight.copy_(torch.as_tensor(data["weight"]))
+        conv.bias.copy_(torch.as_tensor(data["bias"]))
+    x = spconv.SparseConvTensor(torch.as_tensor(data["feats"]).to(cuda), torch.as_tensor(data["indices"]).to(cuda),
+                                [14] * 3, 1)
+    out = conv(x).features.cpu().numpy()
+    assert np.allclose(out, data["out"], atol=1e-12, rtol=1e-12)
+    assert "subm3" in x.indice_dict
+
+
+@pytest.mark.parametrize("dtype,cin,cout", [
+    (torch.float32, 64, 64), (torch.float32, 32, 96), (torch.float16, 128, 128), (torch.float16, 64, 64),
+    (torch.float16, 256, 256), (torch.float16, 64, 320), (torch.float16, 200, 40), (torch.bfloat16, 128, 64),
+])
+def test_mfma_conv_matches_float64(cuda, dtype, cin, cout):
+    from hi3d_amd import conv, kmap
+
+    rng = np.random.default_rng(cin * 1000 + cout)
+    idx = _rand_indices(rng, 24, 0.15, batch=2)
+    km = kmap.build_kernel_map(torch.as_tensor(idx).to(cuda), [24] * 3, 2)
+    x, w, b = _case(rng, len(idx), cin, cout, dtype)
+    y = conv.gather_conv(x.to(cuda), km.plan(), w.to(cuda), b.to(cuda))
+    ref = oconv.gather_conv_f64(x.float().numpy(), km.table.cpu().numpy(), w.float().numpy(), b.float().numpy())
+    assert y.dtype == dtype and y.shape == (len(idx), cout)
+    assert oconv.rel_err(y.float().cpu().numpy(), ref) <= GATE[dtype]
+
+
+def test_epilogue_silu_and_residual(cuda):
+    from hi3d_amd import conv, kmap
+
+    rng = np.random.default_rng(5)
+    idx = _rand_indices(rng, 16, 0.25)
+    km = kmap.build_kernel_map(torch.as_tensor(idx).to(cuda), [16] * 3, 1)
+    x, w, b = _case(rng, len(idx), 64, 64, torch.float16)
+    r = torch.as_tensor(rng.standard_normal((len(idx), 64), dtype=np.float32)).half()
+    t = km.table.cpu().numpy()
+    xf, wf, bf = x.float().numpy(), w.float().numpy(), b.float().numpy()
+    y = conv.gather_conv(x.to(cuda), km.plan(), w.to(cuda), b.to(cuda), act="silu")
+    assert oconv.rel_err(y.float().cpu().numpy(), oconv.gather_conv_f64(xf, t, wf, bf, act="silu")) <= 1e-2
+    y = conv.gather_conv(x.to(cuda), km.plan(), w.to(cuda), b.to(cuda), residual=r.to(cuda))
+    ref = oconv.gather_conv_f64(xf, t, wf, bf, residual=r.float().numpy())
+    assert oconv.rel_err(y.float().cpu().numpy(), ref) <= 1e-2
+
+
+def test_plan_choice_does_not_change_results(cuda):
+    """Rows accumulate the same nonzero K-blocks in the same order under any tiling, so
+    the output is bitwise independent of the plan's window."""
+    from hi3d_amd import conv, kmap
+
+    rng = np.random.default_rng(6)
+    idx = _rand_indices(rng, 32, 0.1)
+    km = kmap.build_kernel_map(torch.as_tensor(idx).to(cuda), [32] * 3, 1)
+    x, w, b = _case(rng, len(idx), 128, 128, torch.float16)
+    x, w, b = x.to(cuda), w.to(cuda), b.to(cuda)
+    outs = [conv.gather_conv(x, kmap.build_plan(km.table, km.n, coords, win), w, b)
+            for coords, win in ((km.indices, 0), (km.indices, 512), (None, 0), (None, 4096))]
+    for o in outs[1:]:
+        assert torch.equal(o, outs[0])
+
+
+def test_unaligned_channels_use_simple_kernel(cuda):
+    from hi3d_amd import conv, kmap
+
+    rng = np.random.default_rng(7)
+    idx = _rand_indices(rng, 12, 0.3)
+    km = kmap.build_kernel_map(torch.as_tensor(idx).to(cuda), [12] * 3, 1)
+    for dtype, cin, cout in ((torch.float16, 12, 20), (torch.float32, 3, 5), (torch.float64, 7, 9)):
+        x, w, b = _case(rng, len(idx), cin, cout, dtype)
+        y = conv.conv(x.to(cuda), km.plan(), w.to(cuda), b.to(cuda))
+        ref = oconv.gather_conv_f64(x.double().numpy(), km.table.cpu().numpy(), w.double().numpy(), b.double().numpy())
+        tol = {torch.float16: 1e-2, torch.float32: 1e-5, torch.float64: 1e-12}[dtype]
+        assert oconv.rel_err(y.double().cpu().numpy(), ref) <= tol
+
+
+def test_workload1_fp32_full(cuda):
+    """128^3 sphere shell, C 64->64 fp32: every output row within 1e-5 of float64."""
+    from hi3d_amd import conv, kmap, workloads
+
+    idx = workloads.coords_for("subm3_c64_fp32")
+    km = kmap.build_kernel_map(torch.as_tensor(idx).to(cuda), [128] * 3, 1)
+    x = workloads.normal((len(idx), 64), 1.0, seed=11)
+    w = workloads.normal((64, 27, 64), 1.0 / np.sqrt(27 * 64), seed=12)
+    y = conv.gather_conv(torch.as_tensor(x).to(cuda), km.plan(), torch.as_tensor(w).to(cuda))
+    ref = oconv.gather_conv_f64(x, km.table.cpu().numpy(), w)
+    assert oconv.rel_err(y.cpu().numpy(), ref) <= 1e-5
+
+
+def test_workload2_fp16_sampled(cuda):
+    from hi3d_amd import conv, kmap, workloads
+
+    idx = workloads.coords_for("subm3_c128_fp16")
+    km = kmap.build_kernel_map(torch.as_tensor(idx).to(cuda), [256] * 3, 1)
+    x = workloads.normal((len(idx), 128), 1.0, seed=21, dtype=np.float16)
+    w = workloads.normal((128, 27, 128), 1.0 / np.sqrt(27 * 128), seed=22, dtype=np.float16)
+    y = conv.gather_conv(torch.as_tensor(x).to(cuda), km.plan(), torch.as_tensor(w).to(cuda))
+    rows = np.random.default_rng(0).choice(len(idx), 4096, replace=False)
+    ref = oconv.gather_conv_f64(x, km.table.cpu().numpy(), w, rows=rows)
+    assert oconv.rel_err(y.float().cpu().numpy()[rows], ref) <= 1e-2
+    assert torch.isfinite(y).all()
+
+
+def test_stride2_golden_float64(cuda):
+    from hi3d_amd import spconv
+
+    data = np.load(GOLDEN / "stride2_12cube.npz")
+    idx = torch.as_tensor(data["indices"]).to(cuda)
+    x = spconv.SparseConvTensor(torch.as_tensor(data["feats"]).to(cuda), idx, [12] * 3, 1)
+    down = spconv.SparseConv3d(6, 10, 2, stride=2, indice_key="s2").double().to(cuda)
+    up = spconv.SparseInverseConv3d(10, 6, 2, indice_key="s2").double().to(cuda)
+    with torch.no_grad():
+        down.weight.copy_(torch.as_tensor(data["weight"]))
+        down.bias.copy_(torch.as_tensor(data["bias"]))
+        up.weight.copy_(torch.as_tensor(data["up_weight"]))
+        up.bias.copy_(torch.as_tensor(data["up_bias"]))
+    y = down(x)
+    assert np.array_equal(y.indices.cpu().numpy(), data["low"]) and y.spatial_shape == [6, 6, 6]
+    assert np.allclose(y.features.cpu().numpy(), data["down_out"], atol=1e-12)
+    z = up(y)
+    assert z.indices is idx and z.spatial_shape == [12, 12, 12]
+    assert np.allclose(z.features.cpu().numpy(), data["up_out"], atol=1e-11)
+
+
+def test_stride2_workload_fp16(cuda):
+    """512^3 shell, fp16: down 64->128 then up 128->64 against float64 gather sums."""
+    from hi3d_amd import conv, kmap, workloads
+
+    idx = workloads.coords_for("down2_up2_c64_c128_fp16")
+    s = kmap.stride2_structure(torch.as_tensor(idx).to(cuda), [512] * 3, 1)
+    x = workloads.normal((len(idx), 64), 1.0, seed=31, dtype=np.float16)
+    wd = workloads.normal((128, 8, 64), 1.0 / np.sqrt(8 * 64), seed=32, dtype=np.float16)
+    wu = workloads.normal((64, 8, 128), 1.0 / np.sqrt(8 * 128), seed=33, dtype=np.float16)
+    y = conv.gather_conv(torch.as_tensor(x).to(cuda), s.down_plan(), torch.as_tensor(wd).to(cuda))
+    z = conv.gather_conv(y, s.up_plan(), torch.as_tensor(wu).to(cuda))
+    down_t, up_t = s.down.cpu().numpy(), s.up.cpu().numpy()
+    rows_c = np.random.default_rng(1).choice(s.n_coarse, 4096, replace=False)
+    ref_y = oconv.gather_conv_f64(x, down_t, wd, rows=rows_c)
+    assert oconv.rel_err(y.float().cpu().numpy()[rows_c], ref_y) <= 1e-2
+    rows_f = np.random.default_rng(2).choice(s.n_fine, 4096, replace=False)
+    ref_z = oconv.gather_conv_f64(y.float().cpu().numpy(), up_t, wu, rows=rows_f)
+    assert oconv.rel_err(z.float().cpu().numpy()[rows_f], ref_z) <= 1e-2
+
+
+def test_gather_mean_pooling(cuda):
+    from hi3d_amd import nn as snn
+
+    rng = np.random.default_rng(8)
+    idx = _rand_indices(rng, 10, 0.4)
+    idx = idx[np.argsort(idx[:, 0], kind="stable")]
+    x = rng.standard_normal((len(idx), 16)).astype(np.float32)
+    t = snn.SparseTensor(torch.as_tensor(x).to(cuda), torch.as_tensor(idx).to(cuda))
+    pooled = snn.SparseDownsample(2)(t)
+    low, inverse, counts, slot, down, up = okmap.stride2_structure(idx)
+    assert np.array_equal(pooled.coords.cpu().numpy(), low)
+    assert np.allclose(pooled.feats.cpu().numpy(), oconv.gather_mean(x, down, 1), atol=1e-6)
+    back = snn.SparseUpsample(2)(pooled)
+    assert torch.equal(back.coords, t.coords)
+    assert np.allclose(back.feats.cpu().numpy(), pooled.feats.cpu().numpy()[inverse])

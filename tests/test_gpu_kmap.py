@@ -1,0 +1,205 @@
+"""Kernel maps on the GPU against the oracle: bit-exact tables, counts and pair lists,
+stride-2 structures and child tables; error paths (duplicates, range, overflow)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import GOLDEN
+from oracle import kmap as okmap
+
+pytestmark = pytest.mark.gpu
+
+
+def _rand_indices(rng, n_side, density, batch=1):
+    rows = []
+    for b in range(batch):
+        xyz = np.argwhere(rng.random((n_side,) * 3) < density)
+        rows.append(np.concatenate([np.full((len(xyz), 1), b), xyz], 1))
+    idx = np.concatenate(rows).astype(np.int32)
+    return idx[rng.permutation(len(idx))]
+
+
+def test_golden_8cube_table_counts_pairs(cuda):
+    from hi3d_amd import kmap
+
+    data = np.load(GOLDEN / "kmap_8cube.npz")
+    km = kmap.build_kernel_map(torch.as_tensor(data["indices"]).to(cuda), [8, 8, 8])
+    assert np.array_equal(km.table.cpu().numpy(), data["table"])
+    assert np.array_equal(km.counts.cpu().numpy(), data["counts"])
+    src, dst, off = km.pairs()
+    assert np.array_equal(off.cpu().numpy(), data["offsets"])
+    assert np.array_equal(src.cpu().numpy(), data["src"])
+    assert np.array_equal(dst.cpu().numpy(), data["dst"])
+
+
+@pytest.mark.parametrize("ksize,batch,n_side,density", [(3, 1, 12, 0.3), (3, 3, 10, 0.5), (1, 2, 6, 0.5), (5, 2, 9, 0.2)])
+def test_random_sets_bit_exact(cuda, ksize, batch, n_side, density):
+    from hi3d_amd import kmap
+
+    rng = np.random.default_rng(100 + ksize + batch)
+    idx = _rand_indices(rng, n_side, density, batch)
+    shape = [n_side, n_side + 1, n_side + 2]
+    km = kmap.build_kernel_map(torch.as_tensor(idx).to(cuda), shape, batch, ksize)
+    ref = okmap.neighbour_table(idx, shape, ksize)
+    assert np.array_equal(km.table.cpu().numpy(), ref)
+    assert np.array_equal(km.counts.cpu().numpy(), (ref != len(idx)).sum(0).astype(np.int32))
+    src, dst, off = km.pairs()
+    rs, rd, ro = okmap.pairs_from_table(ref)
+    assert np.array_equal(off.cpu().numpy(), ro)
+    assert np.array_equal(src.cpu().numpy(), rs) and np.array_equal(dst.cpu().numpy(), rd)
+
+
+def test_64bit_keys(cuda):
+    """batch * sx * sy * sz >= 2^32 selects the 64-bit key hash."""
+    from hi3d_amd import kmap
+
+    rng = np.random.default_rng(7)
+    n = 5000
+    shape = [3000, 3000, 1000]
+    base = rng.integers(0, [2999, 2999, 999], size=(n // 5, 3))
+    pts = np.concatenate([base + d for d in ([0, 0, 0], [1, 0, 0], [0, 1, 0], [0, 0, 1], [1, 1, 1])])
+    pts = np.unique(pts, axis=0)
+    idx = np.concatenate([rng.integers(0, 2, size=(len(pts), 1)), pts], 1).astype(np.int32)
+    idx = np.unique(idx, axis=0)
+    idx = idx[rng.permutation(len(idx))]
+    assert 2 * shape[0] * shape[1] * shape[2] >= 2**32
+    km = kmap.build_kernel_map(torch.as_tensor(idx).to(cuda), shape, 2)
+    assert np.array_equal(km.table.cpu().numpy(), okmap.neighbour_table(idx, shape))
+
+
+def test_errors_duplicate_range_overflow(cuda):
+    from hi3d_amd import kmap
+
+    idx = np.array([[0, 1, 1, 1], [0, 2, 2, 2], [0, 1, 1, 1]], np.int32)
+    with pytest.raises(ValueError, match="duplicate"):
+        kmap.build_kernel_map(torch.as_tensor(idx).to(cuda), [4, 4, 4])
+    idx = np.array([[0, 1, 1, 1], [0, 4, 2, 2]], np.int32)
+    with pytest.raises(ValueError, match="outside"):
+        kmap.build_kernel_map(torch.as_tensor(idx).to(cuda), [4, 4, 4])
+    rng = np.random.default_rng(1)
+    idx = _rand_indices(rng, 8, 0.5)
+    assert len(idx) > 64
+    with pytest.raises(RuntimeError, match="overflow"):
+        kmap.build_kernel_map(torch.as_tensor(idx).to(cuda), [8, 8, 8], capacity=64)
+
+
+def test_empty_and_single(cuda):
+    from hi3d_amd import kmap
+
+    km = kmap.build_kernel_map(torch.zeros((0, 4), dtype=torch.int32, device=cuda), [4, 4, 4], 1)
+    assert km.table.shape == (0, 27) and int(km.counts.sum()) == 0
+    src, dst, off = km.pairs()
+    assert src.numel() == 0 and off.cpu().tolist() == [0] * 28
+    km = kmap.build_kernel_map(torch.tensor([[0, 0, 0, 0]], dtype=torch.int32, device=cuda), [1, 1, 1])
+    t = km.table.cpu().numpy()
+    assert t[0, 13] == 0 and (t == 1).sum() == 26
+
+
+@pytest.mark.parametrize("name", ["subm3_c64_fp32", "subm3_c128_fp16"])
+def test_workload_maps_bit_exact(cuda, name):
+    from hi3d_amd import kmap, workloads
+
+    idx = workloads.coords_for(name)
+    grid = workloads.WORKLOADS[name].grid
+    km = kmap.build_kernel_map(torch.as_tensor(idx).to(cuda), [grid] * 3, 1)
+    ref = okmap.neighbour_table(idx, [grid] * 3)
+    got = km.table.cpu().numpy()
+    assert np.array_equal(got, ref)
+    if name == "subm3_c64_fp32":
+        assert int((ref != len(idx)).sum()) == 474_776
+
+
+def test_large_shell_map_properties(cuda):
+    """The 1024^3 workload (~4.4M voxels): exact on sampled rows, and over all rows the
+    size-independent properties: neighbour coordinates, symmetry, count symmetry."""
+    from hi3d_amd import kmap, workloads
+
+    idx = workloads.coords_for("resblock_c256_fp16", device=cuda)
+    n = len(idx)
+    coords = torch.as_tensor(idx).to(cuda)
+    km = kmap.build_kernel_map(coords, [1024] * 3, 1)
+    table = km.table
+    rows = np.random.default_rng(0).choice(n, 4096, replace=False)
+    assert np.array_equal(table[torch.as_tensor(rows, device=cuda)].cpu().numpy(),
+                          okmap.neighbour_rows(idx, [1024] * 3, rows))
+    offs = torch.as_tensor(okmap.kernel_offsets(3) - 1, device=cuda, dtype=torch.int32)
+    present = table != n
+    for k in range(27):
+        p = present[:, k]
+        nb = table[p, k].long()
+        assert torch.equal(coords[nb, 1:], coords[p, 1:] + offs[k])
+        assert torch.equal(table[nb, 26 - k], torch.nonzero(p).squeeze(1).int())
+    counts = km.counts.cpu().numpy()
+    assert np.array_equal(counts, counts[::-1]) and counts[13] == n
+
+
+def test_stride2_structure(cuda):
+    from hi3d_amd import kmap
+
+    rng = np.random.default_rng(3)
+    idx = _rand_indices(rng, 11, 0.3, batch=2)
+    s = kmap.stride2_structure(torch.as_tensor(idx).to(cuda), [11, 11, 11], 2)
+    low, inverse, counts, slot, down, up = okmap.stride2_structure(idx)
+    assert np.array_equal(s.low.cpu().numpy(), low)
+    assert np.array_equal(s.inverse.cpu().numpy(), inverse)
+    assert np.array_equal(s.counts.cpu().numpy(), counts)
+    assert np.array_equal(s.slot.cpu().numpy(), slot)
+    assert np.array_equal(s.down.cpu().numpy(), down)
+    assert np.array_equal(s.up.cpu().numpy(), up)
+    assert s.out_spatial_shape == [6, 6, 6]
+
+
+def test_stride2_golden_and_workload(cuda):
+    from hi3d_amd import kmap, workloads
+
+    data = np.load(GOLDEN / "stride2_12cube.npz")
+    s = kmap.stride2_structure(torch.as_tensor(data["indices"]).to(cuda), [12, 12, 12])
+    assert np.array_equal(s.low.cpu().numpy(), data["low"])
+    assert np.array_equal(s.inverse.cpu().numpy(), data["inverse"])
+    idx = workloads.coords_for("down2_up2_c64_c128_fp16")
+    s = kmap.stride2_structure(torch.as_tensor(idx).to(cuda), [512] * 3, 1)
+    low, inverse, counts, slot, down, up = okmap.stride2_structure(idx)
+    assert np.array_equal(s.low.cpu().numpy(), low)
+    assert np.array_equal(s.inverse.cpu().numpy(), inverse)
+    assert np.array_equal(s.down.cpu().numpy(), down)
+
+
+def test_mlx_shaped_helpers(cuda):
+    from hi3d_amd import sparse
+
+    data = np.load(GOLDEN / "child_10cube.npz")
+    coords = torch.as_tensor(data["coords"]).to(cuda)
+    table = sparse.neighbour_table(coords)
+    assert np.array_equal(table.cpu().numpy(), okmap.neighbour_table_dense(data["coords"]))
+    ct, parent, slot = sparse.child_neighbour_table(table, torch.as_tensor(data["mask"]).to(cuda))
+    assert np.array_equal(ct.cpu().numpy(), data["table"])
+    assert np.array_equal(parent.cpu().numpy(), data["parent"])
+    assert np.array_equal(slot.cpu().numpy(), data["slot"])
+    low, inv, cnt = sparse.downsample_structure(coords)
+    rl, ri, rc = okmap.downsample_structure(data["coords"])
+    assert np.array_equal(low.cpu().numpy(), rl) and np.array_equal(inv.cpu().numpy(), ri)
+    assert np.array_equal(cnt.cpu().numpy(), rc)
+
+
+def test_plan_covers_every_row_once(cuda):
+    from hi3d_amd import kmap, workloads
+
+    idx = workloads.coords_for("subm3_c128_fp16")
+    km = kmap.build_kernel_map(torch.as_tensor(idx).to(cuda), [256] * 3, 1)
+    for window in (0, 1 << 15):
+        plan = kmap.build_plan(km.table, km.n, km.indices, window)
+        rows = plan.rows.cpu().numpy()
+        valid = rows[rows >= 0]
+        assert np.array_equal(np.sort(valid), np.arange(km.n))
+        gidx = plan.gidx.view(plan.ntiles, 27, 128).cpu().numpy()
+        table = km.table.cpu().numpy()
+        t = np.where(rows.reshape(-1, 128)[:, None, :] >= 0,
+                     table[np.maximum(rows, 0)].reshape(plan.ntiles, 128, 27).transpose(0, 2, 1), km.n)
+        assert np.array_equal(gidx, t)
+        masks = plan.tile_mask.cpu().numpy().astype(np.uint32)
+        present = (gidx != km.n)
+        exp = (present.any(axis=2).astype(np.uint64) << np.arange(27, dtype=np.uint64)).sum(1).astype(np.uint32)
+        assert np.array_equal(masks, exp)

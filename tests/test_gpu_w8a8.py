@@ -1,0 +1,130 @@
+"""W8A8 on the GPU: quantiser codes and scales bit-exact against the oracle (both
+rotations), int32 accumulators bit-exact, the fp16 epilogue bit-exact against the
+unfused float32 formula, and the reference test's tolerance
+(tests/test_w8a8_inference.py:8-20)."""
+
+from __future__ import annotations
+
+import hashlib
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import GOLDEN
+from oracle import w8a8 as ow8a8
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = ((3, 17, 64), (65, 131, 2112), (7, 33, 8448))
+
+
+def _inputs(rows, cols, width):
+    rng = np.random.default_rng(7)
+    x = rng.normal(size=(rows, width)).astype(np.float16)
+    w = rng.integers(-127, 128, size=(cols, width), dtype=np.int8)
+    sw = rng.uniform(0.0001, 0.001, cols).astype(np.float32)
+    bias = rng.normal(0, 0.01, cols).astype(np.float16)
+    return x, w, sw, bias
+
+
+def _sha(a):
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+@pytest.mark.parametrize("rows,cols,width", SHAPES)
+def test_reference_shapes_bit_exact(cuda, rows, cols, width):
+    from hi3d_amd import w8a8
+
+    golden = np.load(GOLDEN / "w8a8.npz")
+    tag = f"{rows}_{cols}_{width}"
+    x, w, sw, bias = _inputs(rows, cols, width)
+    xt = torch.as_tensor(x).to(cuda)
+    q, sa = w8a8.quantize_activation(xt)
+    q, sa = q.cpu().numpy(), sa.cpu().numpy()
+    assert _sha(q) == str(golden[f"q_{tag}"]) and _sha(sa) == str(golden[f"s_{tag}"])
+    out, acc = w8a8.gemm(torch.as_tensor(q).to(cuda), torch.as_tensor(sa).to(cuda), torch.as_tensor(w).to(cuda),
+                         torch.as_tensor(sw).to(cuda), torch.as_tensor(bias).to(cuda), return_acc=True)
+    assert _sha(acc.cpu().numpy()) == str(golden[f"acc_{tag}"])
+    assert _sha(out.cpu().numpy()) == str(golden[f"out_{tag}"])
+    # the reference test's own check (rtol=5e-4, atol=2e-6) through linear()
+    result = w8a8.linear(xt, torch.as_tensor(w).to(cuda), torch.as_tensor(sw).to(cuda),
+                         torch.as_tensor(bias).to(cuda)).float().cpu().numpy()
+    integer = np.asarray(q, np.int64) @ np.asarray(w, np.int64).T
+    expected = integer.astype(np.float32) * sa[:, None] * sw[None, :] + bias.astype(np.float32)
+    assert np.isfinite(result).all()
+    np.testing.assert_allclose(result, expected, rtol=5e-4, atol=2e-6 + 1e-3 * np.abs(expected).max())
+
+
+@pytest.mark.parametrize("rotation", ["h64", "none"])
+def test_quantiser_with_outliers_bit_exact(cuda, rotation):
+    from hi3d_amd import w8a8
+
+    rng = np.random.default_rng(11)
+    x = rng.standard_normal((1000, 1024)).astype(np.float32)
+    out = rng.random(x.shape) < 0.01
+    x[out] *= 20
+    x = x.astype(np.float16)
+    q, s = w8a8.quantize_activation(torch.as_tensor(x).to(cuda), rotation=rotation)
+    rq, rs = ow8a8.quantize_activation(x, rotation=rotation)
+    assert np.array_equal(s.cpu().numpy(), rs)
+    assert np.array_equal(q.cpu().numpy(), rq)
+
+
+def test_zero_rows_and_small_k(cuda):
+    from hi3d_amd import w8a8
+
+    x = np.zeros((5, 64), np.float16)
+    x[2, 7] = -3.5
+    q, s = w8a8.quantize_activation(torch.as_tensor(x).to(cuda), rotation="none")
+    rq, rs = ow8a8.quantize_activation(x, rotation="none")
+    assert np.array_equal(q.cpu().numpy(), rq) and np.array_equal(s.cpu().numpy(), rs)
+    q, s = w8a8.quantize_activation(torch.as_tensor(x).to(cuda))
+    rq, rs = ow8a8.quantize_activation(x)
+    assert np.array_equal(q.cpu().numpy(), rq) and np.array_equal(s.cpu().numpy(), rs)
+
+
+@pytest.mark.parametrize("m,n,k", [(4096, 4096, 1024), (2048, 1024, 4096), (300, 200, 48), (129, 257, 2112)])
+def test_gemm_accumulators_bit_exact(cuda, m, n, k):
+    from hi3d_amd import w8a8
+
+    rng = np.random.default_rng(m + n + k)
+    q = rng.integers(-127, 128, size=(m, k), dtype=np.int8)
+    w = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    sa = rng.uniform(1e-3, 1e-2, m).astype(np.float32)
+    sw = rng.uniform(1e-4, 1e-3, n).astype(np.float32)
+    bias = rng.normal(0, 0.02, n).astype(np.float16)
+    out, acc = w8a8.gemm(*(torch.as_tensor(a).to(cuda) for a in (q, sa, w, sw, bias)), return_acc=True)
+    ref = (q.astype(np.float64) @ w.astype(np.float64).T).astype(np.int64)
+    assert np.array_equal(acc.cpu().numpy().astype(np.int64), ref)
+    assert np.array_equal(out.cpu().numpy(), ow8a8.epilogue(ref.astype(np.int32), sa, sw, bias))
+
+
+def test_workload4_shapes_sampled(cuda):
+    """[65536, 1024] x [4096, 1024]^T and [65536, 4096] x [1024, 4096]^T with 1 % outliers
+    x20: codes, scales and sampled outputs exact against the oracle."""
+    from hi3d_amd import w8a8
+
+    for m, k, n in ((65536, 1024, 4096), (65536, 4096, 1024)):
+        rng = np.random.default_rng(k)
+        x = rng.standard_normal((m, k), dtype=np.float32)
+        x[rng.random((m, k)) < 0.01] *= 20
+        x = x.astype(np.float16)
+        wf = (rng.standard_normal((n, k), dtype=np.float32) / 32).astype(np.float16)
+        bias = (rng.standard_normal(n, dtype=np.float32) * 0.02).astype(np.float16)
+        for rotation in ("h64", "none"):
+            wq, sw = w8a8.quantize_weight(torch.as_tensor(wf).to(cuda), rotation)
+            xt = torch.as_tensor(x).to(cuda)
+            q, sa = w8a8.quantize_activation(xt, rotation=rotation)
+            out = w8a8.gemm(q, sa, wq, sw, torch.as_tensor(bias).to(cuda))
+            rows = np.random.default_rng(5).choice(m, 256, replace=False)
+            rq, rs = ow8a8.quantize_activation(x[rows], rotation=rotation)
+            assert np.array_equal(q[torch.as_tensor(rows).to(cuda)].cpu().numpy(), rq)
+            assert np.array_equal(sa.cpu().numpy()[rows], rs)
+            wqn, swn = wq.cpu().numpy(), sw.cpu().numpy()
+            ref = ow8a8.epilogue(ow8a8.int_gemm(rq, wqn).astype(np.int32), rs, swn, bias)
+            assert np.array_equal(out[torch.as_tensor(rows).to(cuda)].cpu().numpy(), ref)
+            # the int8 product approximates the fp16 projection
+            y = x[rows].astype(np.float32) @ wf.astype(np.float32).T + bias.astype(np.float32)
+            err = np.sqrt(np.mean((ref.astype(np.float32) - y) ** 2) / np.mean(y * y))
+            assert err < 0.15

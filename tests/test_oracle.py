@@ -1,0 +1,358 @@
+"""Pins the CPU oracle itself (no GPU): every oracle function is checked against
+something that does not restate its own formula — the reference tests' dense
+``F.conv3d`` check, brute force on tiny sets, independent constructions, closed forms,
+library routines and the committed golden vectors.
+
+Pinning map (oracle function -> checks here):
+  kmap.subm_pairs / neighbour_table   -> brute_force_table, neighbour_table_dense, the
+                                         layout invariants of tests/test_backends.py:53-67
+  kmap.neighbour_table_dense          -> brute_force_table
+  kmap.pairs_from_table/table_from_pairs -> round trip + subm_pairs lists
+  kmap.stride2_structure / downsample_structure -> brute-force parents and slots
+  kmap.child_neighbour_table          -> dense-grid table of the children
+                                         (tests/test_mlx_kernels.py:79-89)
+  conv.subm_conv_pairs / gather_conv_f64 -> dense F.conv3d (tests/test_backends.py:32-50)
+  conv.dense_down2 / dense_up2        -> explicit per-voxel sums over parents/children
+  conv.gather_mean                    -> scatter_reduce(mean) of PyTorch
+  w8a8.rotate_h64                     -> float64 Hadamard matrix, closed forms (constant
+                                         and one-hot rows), orthonormality
+  w8a8.quantize_activation            -> zero row (s = 1e-8/127), hand-computed rows,
+                                         codes within one step of v/s, |q| <= 127
+  w8a8.int_gemm / epilogue            -> float64 matmul of small integers, the reference
+                                         test's tolerance (tests/test_w8a8_inference.py:20)
+  norm.layer_norm_modulate            -> float64 LayerNorm (torch.nn.functional)
+  norm.adaln_projection / residual_block_f64 -> explicit float64 composition
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from conftest import GOLDEN
+from oracle import conv as oconv
+from oracle import kmap as okmap
+from oracle import norm as onorm
+from oracle import w8a8 as ow8a8
+
+
+def _rand_indices(rng, n_side, density, batch=1):
+    rows = []
+    for b in range(batch):
+        xyz = np.argwhere(rng.random((n_side,) * 3) < density)
+        rows.append(np.concatenate([np.full((len(xyz), 1), b), xyz], 1))
+    idx = np.concatenate(rows).astype(np.int32)
+    return idx
+
+
+# ----------------------------------------------------------------------------- kmap
+
+
+@pytest.mark.parametrize("ksize", [1, 3, 5])
+def test_subm_pairs_matches_brute_force(ksize):
+    rng = np.random.default_rng(0)
+    idx = _rand_indices(rng, 7, 0.3, batch=2)
+    idx = idx[rng.permutation(len(idx))]
+    table = okmap.neighbour_table(idx, [7, 7, 7], ksize)
+    assert np.array_equal(table, okmap.brute_force_table(idx, [7, 7, 7], ksize))
+
+
+def test_dense_grid_table_matches_brute_force():
+    rng = np.random.default_rng(1)
+    idx = _rand_indices(rng, 9, 0.35)
+    idx = idx[rng.permutation(len(idx))]
+    dense = okmap.neighbour_table_dense(idx[:, 1:])
+    assert np.array_equal(dense, okmap.brute_force_table(idx, [9, 9, 9], 3))
+    # the extent-agnostic dense grid agrees with the bounded sort-based map
+    assert np.array_equal(dense, okmap.neighbour_table(idx, [9, 9, 9], 3))
+
+
+def test_pair_layout_invariants():
+    """tests/test_backends.py:53-67: coords[dst] == coords[src] + 1 - r and
+    counts[k] == counts[26 - k]."""
+    data = np.load(GOLDEN / "kmap_8cube.npz")
+    idx = data["indices"]
+    sources, targets, counts = okmap.subm_pairs(idx, [8, 8, 8])
+    coords = idx[:, 1:].astype(np.int64)
+    for k in range(27):
+        r = np.array([k // 9, (k // 3) % 3, k % 3])
+        assert np.array_equal(coords[targets[k]], coords[sources[k]] + 1 - r)
+        assert counts[k] == counts[26 - k]
+        assert np.all(np.diff(sources[k]) > 0)
+
+
+def test_pairs_table_round_trip_and_golden():
+    data = np.load(GOLDEN / "kmap_8cube.npz")
+    idx = data["indices"]
+    sources, targets, counts = okmap.subm_pairs(idx, [8, 8, 8])
+    table = okmap.table_from_pairs(sources, targets, len(idx))
+    assert np.array_equal(table, data["table"])
+    src, dst, off = okmap.pairs_from_table(table)
+    assert np.array_equal(src, data["src"]) and np.array_equal(dst, data["dst"])
+    assert np.array_equal(off, data["offsets"])
+    assert np.array_equal(np.concatenate(sources), src) and np.array_equal(np.concatenate(targets), dst)
+    assert np.array_equal(counts, data["counts"])
+
+
+def test_empty_and_single_voxel_maps():
+    empty = np.zeros((0, 4), np.int32)
+    s, t, c = okmap.subm_pairs(empty, [4, 4, 4])
+    assert c.sum() == 0
+    one = np.array([[0, 0, 0, 0]], np.int32)
+    table = okmap.neighbour_table(one, [1, 1, 1])
+    expected = np.full((1, 27), 1, np.int32)
+    expected[0, 13] = 0
+    assert np.array_equal(table, expected)
+
+
+def test_stride2_structure_matches_brute_force():
+    rng = np.random.default_rng(2)
+    idx = _rand_indices(rng, 9, 0.3, batch=2)
+    idx = idx[rng.permutation(len(idx))]
+    low, inverse, counts, slot, down, up = okmap.stride2_structure(idx)
+    parents = sorted({(int(b), int(x) // 2, int(y) // 2, int(z) // 2) for b, x, y, z in idx})
+    assert [tuple(r) for r in low.tolist()] == parents
+    pos = {p: i for i, p in enumerate(parents)}
+    for i, (b, x, y, z) in enumerate(idx.tolist()):
+        assert inverse[i] == pos[(b, x // 2, y // 2, z // 2)]
+        assert slot[i] == (x & 1) * 4 + (y & 1) * 2 + (z & 1)
+        assert down[inverse[i], slot[i]] == i
+        assert up[i, slot[i]] == inverse[i] and (up[i] == len(low)).sum() == 7
+    assert np.array_equal(counts, np.bincount(inverse, minlength=len(low)))
+    # batch-free restatement of downsample_structure agrees on one batch element
+    one = idx[idx[:, 0] == 0][:, 1:]
+    low3, inv3, cnt3 = okmap.downsample_structure(one)
+    exp = sorted({(x // 2, y // 2, z // 2) for x, y, z in one.tolist()})
+    assert [tuple(r) for r in low3.tolist()] == exp
+    assert np.array_equal(cnt3, np.bincount(inv3, minlength=len(exp)))
+
+
+def test_child_table_matches_dense_grid_of_children():
+    """tests/test_mlx_kernels.py:79-89: the hash-free child table equals the dense-grid
+    table of the children's own coordinates."""
+    data = np.load(GOLDEN / "child_10cube.npz")
+    coords, mask = data["coords"], data["mask"]
+    parent_table = okmap.neighbour_table_dense(coords)
+    table, parent, slot = okmap.child_neighbour_table(parent_table, mask)
+    bits = np.stack([(slot >> 2) & 1, (slot >> 1) & 1, slot & 1], 1)
+    child_coords = coords[parent] * 2 + bits
+    assert np.array_equal(table, okmap.neighbour_table_dense(child_coords))
+    assert np.array_equal(table, data["table"])
+    assert np.array_equal(parent, data["parent"]) and np.array_equal(slot, data["slot"])
+
+
+# ----------------------------------------------------------------------------- conv
+
+
+def test_subm_conv_matches_dense_conv3d_golden():
+    """The reference's own oracle: dense F.conv3d(padding=1) in float64 on the
+    14^3 / density 0.15 / C 5->7 recipe (tests/test_backends.py:32-50)."""
+    data = np.load(GOLDEN / "subm_14cube.npz")
+    idx, feats, w, b = data["indices"], data["feats"], data["weight"], data["bias"]
+    dense = oconv.dense_subm_conv3d(idx, feats, w, b, [14, 14, 14])
+    assert np.array_equal(dense, data["out"])
+    sources, targets, counts = okmap.subm_pairs(idx, [14, 14, 14])
+    pairs_out = oconv.subm_conv_pairs(torch.as_tensor(feats), sources, targets, counts, torch.as_tensor(w),
+                                      torch.as_tensor(b)).numpy()
+    assert np.allclose(pairs_out, dense, atol=1e-12, rtol=1e-12)
+    table = okmap.neighbour_table(idx, [14, 14, 14])
+    assert np.allclose(oconv.gather_conv_f64(feats, table, w, b), dense, atol=1e-12, rtol=1e-12)
+
+
+def test_subm_conv_ksize5_matches_dense():
+    rng = np.random.default_rng(3)
+    idx = _rand_indices(rng, 8, 0.2)
+    x = rng.standard_normal((len(idx), 3))
+    w = rng.standard_normal((4, 5, 5, 5, 3))
+    table = okmap.neighbour_table(idx, [8, 8, 8], 5)
+    dense = oconv.dense_subm_conv3d(idx, x, w, None, [8, 8, 8])
+    assert np.allclose(oconv.gather_conv_f64(x, table, w), dense, atol=1e-11)
+
+
+def test_stride2_dense_equivalents():
+    """down = F.conv3d(stride 2) at the coarse voxels equals the explicit sum over each
+    parent's children; up = F.conv_transpose3d(stride 2) equals W[:, slot] @ y[parent]."""
+    data = np.load(GOLDEN / "stride2_12cube.npz")
+    idx, x, w, b = data["indices"], data["feats"], data["weight"], data["bias"]
+    low, inverse, counts, slot, down, up = okmap.stride2_structure(idx)
+    y = oconv.dense_down2(idx, x, w, b, [12, 12, 12], low)
+    explicit = np.tile(b, (len(low), 1)).astype(np.float64)
+    for i in range(len(idx)):
+        s = slot[i]
+        explicit[inverse[i]] += w[:, s >> 2, (s >> 1) & 1, s & 1, :] @ x[i]
+    assert np.allclose(y, explicit, atol=1e-12)
+    assert np.allclose(oconv.gather_conv_f64(x, down, w.reshape(10, 8, 6), b), y, atol=1e-12)
+    assert np.array_equal(y, data["down_out"])
+    wu, bu = data["up_weight"], data["up_bias"]
+    z = oconv.dense_up2(low, y, wu, bu, [6, 6, 6], idx)
+    explicit_up = np.stack([wu[:, s >> 2, (s >> 1) & 1, s & 1, :] @ y[inverse[i]] + bu for i, s in enumerate(slot)])
+    assert np.allclose(z, explicit_up, atol=1e-11)
+    assert np.allclose(oconv.gather_conv_f64(y, up, wu.reshape(6, 8, 10), bu), z, atol=1e-11)
+    assert np.array_equal(z, data["up_out"])
+
+
+def test_gather_mean_matches_scatter_reduce():
+    rng = np.random.default_rng(4)
+    idx = _rand_indices(rng, 8, 0.4)
+    x = rng.standard_normal((len(idx), 5))
+    low, inverse, counts, slot, down, up = okmap.stride2_structure(idx)
+    ref = torch.zeros(len(low), 5, dtype=torch.float64).scatter_reduce(
+        0, torch.as_tensor(inverse, dtype=torch.long)[:, None].expand(-1, 5), torch.as_tensor(x), reduce="mean"
+    )
+    assert np.allclose(oconv.gather_mean(x, down, extra=1), ref.numpy(), atol=1e-12)
+
+
+def test_rel_err_statistic():
+    ref = np.array([3.0, -4.0])
+    assert oconv.rel_err(ref, ref) == 0
+    assert abs(oconv.rel_err(ref + [0.0, 0.5], ref) - 0.5 / np.sqrt(12.5)) < 1e-15
+
+
+# ----------------------------------------------------------------------------- W8A8
+
+
+def test_signs_golden():
+    data = np.load(GOLDEN / "signs.npz")
+    for key in data.files:
+        k = int(key[1:])
+        s = ow8a8.signs(k)
+        assert s.dtype == np.float32 and np.array_equal(s, data[key])
+        assert set(np.unique(s)) <= {-1.0, 1.0}
+
+
+def test_h64_matches_hadamard_matrix():
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((9, 192)).astype(np.float16)
+    sign = ow8a8.signs(192)
+    got = ow8a8.rotate_h64(x)
+    h = ow8a8.hadamard64()
+    xs = x.astype(np.float64) * sign
+    ref = np.concatenate([xs[:, 64 * j : 64 * j + 64] @ h.T for j in range(3)], 1)
+    assert np.allclose(got, ref, atol=1e-5)
+    # orthonormal: the rotation keeps each 64-block's norm
+    assert np.allclose(np.linalg.norm(got.reshape(9, 3, 64), axis=2), np.linalg.norm(xs.reshape(9, 3, 64), axis=2), rtol=1e-5)
+
+
+def test_h64_closed_forms():
+    ones = np.ones((1, 64), np.float16)
+    mult = np.ones(64, np.float32)
+    got = ow8a8.rotate_h64(ones, mult)
+    expected = np.zeros(64, np.float32)
+    expected[0] = 8.0  # sum of 64 ones / 8
+    assert np.array_equal(got[0], expected)
+    for j in (0, 5, 33, 63):
+        e = np.zeros((1, 64), np.float16)
+        e[0, j] = 1
+        got = ow8a8.rotate_h64(e, mult)[0]
+        p = np.arange(64)
+        want = np.array([(-1.0) ** bin(int(pp) & j).count("1") / 8 for pp in p], np.float32)
+        assert np.array_equal(got, want)
+
+
+def test_quantiser_special_rows():
+    x = np.zeros((2, 64), np.float16)
+    x[1, 3] = 2.0
+    q, s = ow8a8.quantize_activation(x, rotation="none")
+    assert s[0] == np.float32(1e-8) / np.float32(127) and not q[0].any()
+    assert s[1] == np.float32(2.0) / np.float32(127) and q[1, 3] == 127 and (q[1] != 0).sum() == 1
+    # half-way values round to even: 0.5 * 127/63.5 ...
+    x2 = np.array([[127.0, 0.5, 1.5, 2.5, -0.5, -1.5, 0.0, 0.0]], np.float16)
+    q2, s2 = ow8a8.quantize_activation(x2, rotation="none")
+    assert s2[0] == np.float32(1.0)
+    assert q2[0].tolist() == [127, 0, 2, 2, 0, -2, 0, 0]
+
+
+def test_quantiser_codes_within_one_step():
+    rng = np.random.default_rng(6)
+    x = (rng.standard_normal((17, 256)) * 4).astype(np.float16)
+    for rotation in ("h64", "none"):
+        q, s = ow8a8.quantize_activation(x, rotation=rotation)
+        v = ow8a8.rotate_h64(x) if rotation == "h64" else x.astype(np.float32)
+        assert np.all(np.abs(q.astype(np.float64) - v / s[:, None].astype(np.float64)) <= 0.5 + 1e-6)
+        assert np.abs(q).max() == 127 and q.min() >= -127
+        assert np.allclose(s, np.abs(v).max(1) / 127, rtol=1e-7)
+
+
+def test_integer_gemm_and_epilogue():
+    x, w, sw, bias = _w8a8_inputs(65, 131, 2112)
+    q, sa = ow8a8.quantize_activation(x)
+    acc = ow8a8.int_gemm(q, w)
+    assert np.array_equal(acc, (q.astype(np.float64) @ w.astype(np.float64).T).astype(np.int64))
+    out = ow8a8.epilogue(acc.astype(np.int32), sa, sw, bias)
+    expected = acc.astype(np.float32) * sa[:, None] * sw[None, :] + bias.astype(np.float32)
+    np.testing.assert_allclose(out.astype(np.float32), expected, rtol=5e-4, atol=2e-6 + 1e-3 * np.abs(expected).max())
+
+
+def _w8a8_inputs(rows, cols, width):
+    rng = np.random.default_rng(7)
+    x = rng.normal(size=(rows, width)).astype(np.float16)
+    w = rng.integers(-127, 128, size=(cols, width), dtype=np.int8)
+    sw = rng.uniform(0.0001, 0.001, cols).astype(np.float32)
+    bias = rng.normal(0, 0.01, cols).astype(np.float16)
+    return x, w, sw, bias
+
+
+def test_w8a8_golden_digests():
+    import hashlib
+
+    data = np.load(GOLDEN / "w8a8.npz")
+    for rows, cols, width in ((3, 17, 64), (65, 131, 2112), (7, 33, 8448)):
+        x, w, sw, bias = _w8a8_inputs(rows, cols, width)
+        q, sa = ow8a8.quantize_activation(x)
+        tag = f"{rows}_{cols}_{width}"
+        assert hashlib.sha256(q.tobytes()).hexdigest() == str(data[f"q_{tag}"])
+        assert hashlib.sha256(sa.tobytes()).hexdigest() == str(data[f"s_{tag}"])
+
+
+# ----------------------------------------------------------------------------- norm / block
+
+
+def test_layer_norm_matches_float64():
+    rng = np.random.default_rng(8)
+    x = (rng.standard_normal((40, 2112)) * 3 + 0.5).astype(np.float16)
+    got = onorm.layer_norm_modulate(x, 1e-6).astype(np.float64)
+    ref = F.layer_norm(torch.as_tensor(x.astype(np.float64)), (2112,), eps=1e-6).numpy()
+    assert np.abs(got - ref).max() <= 2e-3  # one fp16 ulp at |y| ~ 4
+    scale = (1 + 0.1 * rng.standard_normal(2112)).astype(np.float16)
+    shift = (0.1 * rng.standard_normal(2112)).astype(np.float16)
+    got = onorm.layer_norm_modulate(x, 1e-6, scale=scale, shift=shift).astype(np.float64)
+    want = ref * scale.astype(np.float64) + shift.astype(np.float64)
+    assert np.abs(got - want).max() <= 1e-2
+
+
+def test_layer_norm_golden():
+    import hashlib
+
+    data = np.load(GOLDEN / "layer_norm.npz")
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal((100, 2112)) * 3 + 0.5).astype(np.float16)
+    scale = (1 + 0.1 * rng.standard_normal(2112)).astype(np.float16)
+    shift = (0.1 * rng.standard_normal(2112)).astype(np.float16)
+    got = onorm.layer_norm_modulate(x, 1e-6, scale=scale, shift=shift)
+    assert hashlib.sha256(got.tobytes()).hexdigest() == str(data["mod"])
+
+
+def test_residual_block_composition():
+    rng = np.random.default_rng(9)
+    idx = _rand_indices(rng, 8, 0.3)
+    n, c, d = len(idx), 8, 12
+    x = rng.standard_normal((n, c)).astype(np.float16)
+    cond = rng.standard_normal(d)
+    pw, pb = rng.standard_normal((2 * c, d)) * 0.1, rng.standard_normal(2 * c) * 0.1
+    w1, w2 = rng.standard_normal((c, 3, 3, 3, c)) * 0.1, rng.standard_normal((c, 3, 3, 3, c)) * 0.1
+    b1, b2 = rng.standard_normal(c) * 0.1, rng.standard_normal(c) * 0.1
+    table = okmap.neighbour_table(idx, [8, 8, 8])
+    full = onorm.residual_block_f64(x, table, cond, pw, pb, w1, b1, w2, b2)
+    rows = np.array([0, 3, n - 1])
+    part = onorm.residual_block_f64(x, table, cond, pw, pb, w1, b1, w2, b2, rows=rows)
+    assert np.allclose(full[rows], part, atol=1e-12)
+    # explicit composition through dense conv3d
+    s1p, sh = onorm.adaln_projection(pw, pb, cond)
+    xt = torch.as_tensor(x.astype(np.float64))
+    h = F.layer_norm(xt, (c,), eps=1e-6).numpy() * s1p.astype(np.float64) + sh.astype(np.float64)
+    h1 = oconv.dense_subm_conv3d(idx, h, w1, b1, [8, 8, 8])
+    h1 = h1 / (1 + np.exp(-h1))
+    ref = oconv.dense_subm_conv3d(idx, h1, w2, b2, [8, 8, 8]) + x.astype(np.float64)
+    assert np.allclose(full, ref, atol=1e-10)
