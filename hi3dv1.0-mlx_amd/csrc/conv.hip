@@ -206,6 +206,254 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a) {
   }
 }
 
+// ------------------------------------------------------------------------------------
+// Pipelined variant for kernel volumes up to 27 (3^3 submanifold, 2^3 strided pair).
+//
+// Stages are (present offset, 128-byte K-block) pairs, so every gathered row moves as
+// whole 128-byte lines. Both operands travel global -> LDS by direct-to-LDS 16-byte loads
+// (global_load_lds_dwordx4, no register staging): gathered rows (A) run two stages
+// ahead in a 3-deep ring, weights (B, L2-resident) one stage ahead in a 2-deep ring.
+// Each iteration issues B(s+1) then A(s+2), so waiting until only the newest A group
+// is outstanding completes both A(s) and B(s); the barrier after the wait publishes
+// every wave's part. Absent rows and K padding load from a zero buffer. The tile's
+// gather indices (all offsets, [K][BM]) are copied to LDS once per tile and read into
+// registers once per offset. Fragment reads run two K-groups ahead of the MFMAs.
+// A BM-row tile covers BM / 128 consecutive plan tiles (union of their masks).
+
+__device__ __attribute__((aligned(16))) const uint32_t g_zero16[4] = {0u, 0u, 0u, 0u};
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit counter");
+  // s_waitcnt: vmcnt[3:0] | expcnt[6:4] (7 = no wait) | lgkmcnt[11:8] (15 = no wait) | vmcnt[5:4] at [15:14]
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+__device__ __forceinline__ void lds_dma16(const void* src, char* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(lds_wave_base), 16, 0, 0);
+}
+
+constexpr int kMaxPipelinedKvol = 27;
+
+template <typename T, int BM, int BN, int WGM>
+__global__ __launch_bounds__(256) void conv_pipe_kernel(ConvArgs a) {
+  constexpr int WGN = 4 / WGM;
+  constexpr int WM = BM / WGM, WN = BN / WGN;
+  constexpr int MB = WM / 32, NB = WN / 32;
+  constexpr int A_INS = BM / 32, B_INS = BN / 32;  // 16-byte loads per thread per stage
+  constexpr int A_BYTES = BM * 128, B_BYTES = BN * 128;
+  constexpr int PIPE = 3 * A_BYTES + 2 * B_BYTES;
+  constexpr int EPI = BM * BN * static_cast<int>(sizeof(T));
+  constexpr int REGION = PIPE > EPI ? PIPE : EPI;
+  constexpr int SUB = BM / kTileRows;
+  static_assert(A_INS >= 1 && B_INS >= 1 && MB >= 1 && NB >= 1, "tile shape");
+  __shared__ __attribute__((aligned(16))) char smem[REGION + BM * kMaxPipelinedKvol * 4];
+  char* const ring_a = smem;
+  char* const ring_b = smem + 3 * A_BYTES;
+  int32_t* const gidx = reinterpret_cast<int32_t*>(smem + REGION);
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WGN, wn = wave % WGN;
+  const int64_t item = xcd_remap(blockIdx.x, static_cast<int64_t>(gridDim.x));
+  const int64_t tile = item / a.ny;
+  const int n0 = static_cast<int>(item % a.ny) * BN;
+  const int kvol = a.kvol;
+  const int32_t absent = static_cast<int32_t>(a.n_in);
+
+  uint32_t mask = 0;
+#pragma unroll
+  for (int h = 0; h < SUB; ++h) {
+    const int64_t pt = tile * SUB + h;
+    if (pt < a.ntiles) mask |= a.tile_mask[pt];
+  }
+  mask &= (1u << kvol) - 1u;
+
+  // gather indices of the tile, all offsets: LDS [k][BM]
+  {
+    const int per_k = BM / 4;
+    for (int q = tid; q < kvol * per_k; q += 256) {
+      const int k = q / per_k;
+      const int r = (q - k * per_k) * 4;
+      const int64_t pt = tile * SUB + r / kTileRows;
+      i32x4 v = {absent, absent, absent, absent};
+      if (pt < a.ntiles) v = *reinterpret_cast<const i32x4*>(a.gidx + (pt * kvol + k) * kTileRows + (r % kTileRows));
+      *reinterpret_cast<i32x4*>(gidx + k * BM + r) = v;
+    }
+  }
+  __syncthreads();
+
+  const int row_bytes = a.cin * static_cast<int>(sizeof(T));
+  const int row_chunks = row_bytes >> 4;
+  const int nkb = (row_chunks + 7) >> 3;
+  const int S = __popc(mask) * nkb;
+  const uint64_t n_in = static_cast<uint64_t>(a.n_in);
+  const int lrow = lane >> 3;  // row of this lane within an 8-row load group
+
+  struct Iter {
+    int k, kb;
+    uint32_t rest;
+  };
+  auto first = [&]() {
+    Iter it;
+    it.k = mask ? __builtin_ctz(mask) : 0;
+    it.kb = 0;
+    it.rest = mask & (mask - 1u);
+    return it;
+  };
+  auto advance = [&](Iter& it) {
+    if (++it.kb == nkb) {
+      it.kb = 0;
+      it.k = it.rest ? __builtin_ctz(it.rest) : it.k;
+      it.rest &= it.rest - 1u;
+    }
+  };
+  Iter ia = first(), ib = first();
+  int sa = 0, sb = 0;  // next stage to issue for A / B
+
+  // gather rows of the current A tap, read from LDS once per tap (all K-blocks reuse them)
+  int32_t asrc[A_INS];
+  auto load_asrc = [&]() {
+    const int32_t* g = gidx + ia.k * BM;
+#pragma unroll
+    for (int j = 0; j < A_INS; ++j) asrc[j] = g[(j * 4 + wave) * 8 + lrow];
+  };
+  auto issue_a = [&]() {
+    char* A = ring_a + (sa % 3) * A_BYTES;
+    if (ia.kb == 0) load_asrc();
+#pragma unroll
+    for (int j = 0; j < A_INS; ++j) {
+      const int grp = j * 4 + wave;
+      const int row = grp * 8 + lrow;
+      const int c = (lane & 7) ^ ((row >> 1) & 7);  // logical chunk landing at this lane's slot
+      const int cidx = ia.kb * 8 + c;
+      const int32_t src = asrc[j];
+      const bool ok = cidx < row_chunks && static_cast<uint64_t>(static_cast<uint32_t>(src)) < n_in;
+      const char* real = a.in + static_cast<int64_t>(ok ? src : 0) * row_bytes + cidx * 16;
+      lds_dma16(ok ? static_cast<const void*>(real) : static_cast<const void*>(g_zero16), A + grp * 1024);
+    }
+    advance(ia);
+    ++sa;
+  };
+  auto issue_b = [&]() {
+    char* B = ring_b + (sb % 2) * B_BYTES;
+#pragma unroll
+    for (int j = 0; j < B_INS; ++j) {
+      const int grp = j * 4 + wave;
+      const int row = grp * 8 + lrow;
+      const int c = (lane & 7) ^ ((row >> 1) & 7);
+      const int cidx = ib.kb * 8 + c;
+      const int n = n0 + row;
+      const bool ok = cidx < row_chunks && n < a.cout;
+      const char* real = a.weight + (static_cast<int64_t>(ok ? n : 0) * kvol + ib.k) * row_bytes + cidx * 16;
+      lds_dma16(ok ? static_cast<const void*>(real) : static_cast<const void*>(g_zero16), B + grp * 1024);
+    }
+    advance(ib);
+    ++sb;
+  };
+
+  f32x16 acc[MB][NB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[mb][nb][v] = 0.0f;
+
+  auto compute = [&](int s) {
+    const char* A = ring_a + (s % 3) * A_BYTES;
+    const char* B = ring_b + (s % 2) * B_BYTES;
+    // fragment reads run two K-groups ahead of the MFMAs (at most 12 reads in flight,
+    // within the 4-bit LDS counter), so each K-group waits only for its own reads
+    u32x4 af[4][MB], bf[4][NB];
+    auto frags = [&](int g) {
+      const int c = 2 * g + (lane >> 5);
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+        af[g][mb] = *reinterpret_cast<const u32x4*>(A + lds_offset(wm * WM + mb * 32 + (lane & 31), c));
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+        bf[g][nb] = *reinterpret_cast<const u32x4*>(B + lds_offset(wn * WN + nb * 32 + (lane & 31), c));
+    };
+    auto mma = [&](int g) {
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) Mfma<T>::run(af[g][mb], bf[g][nb], acc[mb][nb]);
+    };
+    frags(0);
+    frags(1);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(0);
+    __builtin_amdgcn_sched_barrier(0);
+    frags(2);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(1);
+    __builtin_amdgcn_sched_barrier(0);
+    frags(3);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(2);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(3);
+  };
+
+  if (S > 0) {
+    issue_b();
+    issue_a();
+    if (S > 1) issue_a();
+  }
+  for (int s = 0; s < S; ++s) {
+    if (s + 1 < S) wait_vmcnt<A_INS>();
+    else wait_vmcnt<0>();
+    __builtin_amdgcn_s_barrier();
+    if (s + 1 < S) issue_b();
+    if (s + 2 < S) issue_a();
+    compute(s);
+  }
+  __syncthreads();
+
+  // epilogue: bias + activation in fp32, round to T, stage the tile in LDS
+  T* C = reinterpret_cast<T*>(smem);
+  const T* bias = static_cast<const T*>(a.bias);
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const int j = wn * WN + nb * 32 + (lane & 31);
+    const int n = n0 + j;
+    const float b = (bias != nullptr && n < a.cout) ? to_f32(bias[n]) : 0.0f;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int i = wm * WM + mb * 32 + acc_row(lane, v);
+        float x = acc[mb][nb][v] + b;
+        if (a.act == HI3D_ACT_SILU) x = silu(x);
+        C[i * BN + j] = static_cast<T>(x);
+      }
+    }
+  }
+  __syncthreads();
+  constexpr int EPC = 16 / static_cast<int>(sizeof(T));
+  constexpr int CPR = BN / EPC;
+  const int64_t out_row_bytes = static_cast<int64_t>(a.cout) * sizeof(T);
+  for (int q = tid; q < BM * CPR; q += 256) {
+    const int i = q / CPR, cc = q - (q / CPR) * CPR;
+    const int64_t pt = tile * SUB + i / kTileRows;
+    if (pt >= a.ntiles) continue;
+    const int32_t orow = a.rows[pt * kTileRows + (i % kTileRows)];
+    const int ncol = n0 + cc * EPC;
+    if (orow < 0 || ncol >= a.cout) continue;
+    u32x4 v = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(C) + (i * BN + cc * EPC) * sizeof(T));
+    const int64_t off = static_cast<int64_t>(orow) * out_row_bytes + static_cast<int64_t>(ncol) * sizeof(T);
+    if (a.residual != nullptr) {
+      u32x4 r = *reinterpret_cast<const u32x4*>(a.residual + off);
+      T* pv = reinterpret_cast<T*>(&v);
+      const T* pr = reinterpret_cast<const T*>(&r);
+#pragma unroll
+      for (int e = 0; e < EPC; ++e) pv[e] = static_cast<T>(to_f32(pv[e]) + to_f32(pr[e]));
+    }
+    *reinterpret_cast<u32x4*>(a.out + off) = v;
+  }
+}
+
 template <typename T, typename Acc>
 __global__ void conv_simple_kernel(const T* __restrict__ in, int64_t n_in, int cin, const T* __restrict__ w,
                                    const T* __restrict__ bias, int cout, int kvol, const int32_t* __restrict__ table,
@@ -239,9 +487,27 @@ int elem_size(int dtype) {
   }
 }
 
+template <typename T, int BM, int BN, int WGM>
+int launch_dma(const ConvArgs& base, hipStream_t stream) {
+  ConvArgs a = base;
+  a.ny = static_cast<int32_t>(ceil_div(a.cout, BN));
+  const int64_t blocks = ceil_div(a.ntiles, BM / kTileRows) * a.ny;
+  if (blocks == 0) return HI3D_OK;
+  HI3D_REQUIRE(blocks < (int64_t(1) << 31), "too many tiles");
+  hipLaunchKernelGGL((conv_pipe_kernel<T, BM, BN, WGM>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
+  HI3D_LAUNCH_CHECK();
+  return HI3D_OK;
+}
+
 template <typename T>
 int launch_mfma(const ConvArgs& base, hipStream_t stream) {
   ConvArgs a = base;
+  if (a.kvol <= kMaxPipelinedKvol) {
+    if (a.cout <= 64) return launch_dma<T, 256, 64, 4>(a, stream);
+    if (sizeof(T) == 4) return launch_dma<T, 128, 128, 2>(a, stream);
+    if (a.cout <= 128) return launch_dma<T, 256, 128, 4>(a, stream);
+    return launch_dma<T, 128, 256, 2>(a, stream);
+  }
   int bn;
   const int cout = a.cout;
   if (cout <= 64) bn = 64;
