@@ -14,6 +14,8 @@
 // registers; stages are double-buffered (global loads of stage s+1 are in flight while
 // stage s computes). The epilogue adds bias, applies SiLU, stages the tile through LDS
 // and writes every output row exactly once with 16-byte stores (plus the residual).
+#include <type_traits>
+
 #include "common.h"
 #include "conv_tile.h"
 
@@ -209,16 +211,19 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a) {
 // ------------------------------------------------------------------------------------
 // Pipelined variant for kernel volumes up to 27 (3^3 submanifold, 2^3 strided pair).
 //
+// 8 waves (two per SIMD) share a BM x BN tile (64 x 64 per wave; 32 x 64 for BN = 64).
 // Stages are (present offset, 128-byte K-block) pairs, so every gathered row moves as
-// whole 128-byte lines. Both operands travel global -> LDS by direct-to-LDS 16-byte loads
-// (global_load_lds_dwordx4, no register staging): gathered rows (A) run two stages
-// ahead in a 3-deep ring, weights (B, L2-resident) one stage ahead in a 2-deep ring.
-// Each iteration issues B(s+1) then A(s+2), so waiting until only the newest A group
-// is outstanding completes both A(s) and B(s); the barrier after the wait publishes
-// every wave's part. Absent rows and K padding load from a zero buffer. The tile's
-// gather indices (all offsets, [K][BM]) are copied to LDS once per tile and read into
-// registers once per offset. Fragment reads run two K-groups ahead of the MFMAs.
-// A BM-row tile covers BM / 128 consecutive plan tiles (union of their masks).
+// whole 128-byte lines. Global loads run three stages ahead into a ring of three
+// register sets (16-byte loads; absent rows and K padding read a zero buffer); after
+// computing stage s from LDS, a thread waits for its stage s+1 loads only (stages s+2
+// and s+3 stay in flight), writes them to the other LDS buffer and joins a barrier. Fragment reads wait
+// on the LDS counter only, never on in-flight global loads, and run two K-groups ahead
+// of the MFMAs. The MFMAs take the weights as their first operand, so each lane's
+// accumulators hold four consecutive output channels of one output row, staged for the
+// epilogue with 8-byte LDS writes. The tile's gather indices (all offsets, [K][BM]) and
+// output rows are copied to LDS once per tile; gather indices are read into registers
+// once per offset. A stage's global loads are issued between its MFMA groups. A BM-row tile
+// covers BM / 128 consecutive plan tiles (union of their masks).
 
 __device__ __attribute__((aligned(16))) const uint32_t g_zero16[4] = {0u, 0u, 0u, 0u};
 
@@ -229,28 +234,30 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
-__device__ __forceinline__ void lds_dma16(const void* src, char* lds_wave_base) {
-  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(lds_wave_base), 16, 0, 0);
-}
+// Wait for this wave's LDS operations only (vmcnt left at its maximum, 63).
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14)); }
 
 constexpr int kMaxPipelinedKvol = 27;
+constexpr int kPipeThreads = 512;
+constexpr int kRing = 3;  // register sets of in-flight global loads
 
 template <typename T, int BM, int BN, int WGM>
-__global__ __launch_bounds__(256) void conv_pipe_kernel(ConvArgs a) {
-  constexpr int WGN = 4 / WGM;
+__global__ __launch_bounds__(kPipeThreads) void conv_pipe_kernel(ConvArgs a) {
+  constexpr int WGN = kPipeThreads / 64 / WGM;
   constexpr int WM = BM / WGM, WN = BN / WGN;
-  constexpr int MB = WM / 32, NB = WN / 32;
-  constexpr int A_INS = BM / 32, B_INS = BN / 32;  // 16-byte loads per thread per stage
+  constexpr int MB = WM / 32, NB = WN / 32;  // 32 x 32 blocks per wave
+  static_assert(MB >= 1 && NB >= 1 && WGM * WGN == kPipeThreads / 64, "wave grid");
+  constexpr int A_INS = BM / 64, B_INS = BN / 64;  // 16-byte loads per thread per stage
+  constexpr int L = A_INS + B_INS;
   constexpr int A_BYTES = BM * 128, B_BYTES = BN * 128;
-  constexpr int PIPE = 3 * A_BYTES + 2 * B_BYTES;
+  constexpr int STAGE = A_BYTES + B_BYTES;
+  constexpr int PIPE = 2 * STAGE;
   constexpr int EPI = BM * BN * static_cast<int>(sizeof(T));
   constexpr int REGION = PIPE > EPI ? PIPE : EPI;
   constexpr int SUB = BM / kTileRows;
-  static_assert(A_INS >= 1 && B_INS >= 1 && MB >= 1 && NB >= 1, "tile shape");
-  __shared__ __attribute__((aligned(16))) char smem[REGION + BM * kMaxPipelinedKvol * 4];
-  char* const ring_a = smem;
-  char* const ring_b = smem + 3 * A_BYTES;
+  __shared__ __attribute__((aligned(16))) char smem[REGION + BM * (kMaxPipelinedKvol + 1) * 4];
   int32_t* const gidx = reinterpret_cast<int32_t*>(smem + REGION);
+  int32_t* const orows = gidx + BM * kMaxPipelinedKvol;  // output row of each tile slot
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WGN, wn = wave % WGN;
@@ -268,10 +275,14 @@ __global__ __launch_bounds__(256) void conv_pipe_kernel(ConvArgs a) {
   }
   mask &= (1u << kvol) - 1u;
 
-  // gather indices of the tile, all offsets: LDS [k][BM]
+  // gather indices of the tile, all offsets: LDS [k][BM]; output rows: LDS [BM]
+  for (int i = tid; i < BM; i += kPipeThreads) {
+    const int64_t pt = tile * SUB + i / kTileRows;
+    orows[i] = pt < a.ntiles ? a.rows[pt * kTileRows + (i % kTileRows)] : -1;
+  }
   {
     const int per_k = BM / 4;
-    for (int q = tid; q < kvol * per_k; q += 256) {
+    for (int q = tid; q < kvol * per_k; q += kPipeThreads) {
       const int k = q / per_k;
       const int r = (q - k * per_k) * 4;
       const int64_t pt = tile * SUB + r / kTileRows;
@@ -287,83 +298,75 @@ __global__ __launch_bounds__(256) void conv_pipe_kernel(ConvArgs a) {
   const int nkb = (row_chunks + 7) >> 3;
   const int S = __popc(mask) * nkb;
   const uint64_t n_in = static_cast<uint64_t>(a.n_in);
-  const int lrow = lane >> 3;  // row of this lane within an 8-row load group
+  const int lrow = tid >> 3, lchunk = tid & 7;  // this thread loads rows lrow + 64 j, chunk lchunk
 
-  struct Iter {
-    int k, kb;
-    uint32_t rest;
-  };
-  auto first = [&]() {
-    Iter it;
-    it.k = mask ? __builtin_ctz(mask) : 0;
-    it.kb = 0;
-    it.rest = mask & (mask - 1u);
-    return it;
-  };
-  auto advance = [&](Iter& it) {
-    if (++it.kb == nkb) {
-      it.kb = 0;
-      it.k = it.rest ? __builtin_ctz(it.rest) : it.k;
-      it.rest &= it.rest - 1u;
-    }
-  };
-  Iter ia = first(), ib = first();
-  int sa = 0, sb = 0;  // next stage to issue for A / B
-
-  // gather rows of the current A tap, read from LDS once per tap (all K-blocks reuse them)
+  int ik = mask ? __builtin_ctz(mask) : 0, ikb = 0;
+  uint32_t irest = mask & (mask - 1u);
   int32_t asrc[A_INS];
-  auto load_asrc = [&]() {
-    const int32_t* g = gidx + ia.k * BM;
+  u32x4 ra[kRing][A_INS], rb[kRing][B_INS];
+
+  auto load_a = [&](const int r) {
+    if (ikb == 0) {
+      const int32_t* g = gidx + ik * BM;
 #pragma unroll
-    for (int j = 0; j < A_INS; ++j) asrc[j] = g[(j * 4 + wave) * 8 + lrow];
-  };
-  auto issue_a = [&]() {
-    char* A = ring_a + (sa % 3) * A_BYTES;
-    if (ia.kb == 0) load_asrc();
+      for (int j = 0; j < A_INS; ++j) asrc[j] = g[lrow + 64 * j];
+    }
+    const int cidx = ikb * 8 + lchunk;
+    const bool cok = cidx < row_chunks;
 #pragma unroll
     for (int j = 0; j < A_INS; ++j) {
-      const int grp = j * 4 + wave;
-      const int row = grp * 8 + lrow;
-      const int c = (lane & 7) ^ ((row >> 1) & 7);  // logical chunk landing at this lane's slot
-      const int cidx = ia.kb * 8 + c;
       const int32_t src = asrc[j];
-      const bool ok = cidx < row_chunks && static_cast<uint64_t>(static_cast<uint32_t>(src)) < n_in;
+      const bool ok = cok && static_cast<uint64_t>(static_cast<uint32_t>(src)) < n_in;
       const char* real = a.in + static_cast<int64_t>(ok ? src : 0) * row_bytes + cidx * 16;
-      lds_dma16(ok ? static_cast<const void*>(real) : static_cast<const void*>(g_zero16), A + grp * 1024);
+      ra[r][j] = *reinterpret_cast<const u32x4*>(ok ? static_cast<const void*>(real) : static_cast<const void*>(g_zero16));
     }
-    advance(ia);
-    ++sa;
   };
-  auto issue_b = [&]() {
-    char* B = ring_b + (sb % 2) * B_BYTES;
+  auto load_b = [&](const int r) {
+    const int cidx = ikb * 8 + lchunk;
+    const bool cok = cidx < row_chunks;
 #pragma unroll
     for (int j = 0; j < B_INS; ++j) {
-      const int grp = j * 4 + wave;
-      const int row = grp * 8 + lrow;
-      const int c = (lane & 7) ^ ((row >> 1) & 7);
-      const int cidx = ib.kb * 8 + c;
-      const int n = n0 + row;
-      const bool ok = cidx < row_chunks && n < a.cout;
-      const char* real = a.weight + (static_cast<int64_t>(ok ? n : 0) * kvol + ib.k) * row_bytes + cidx * 16;
-      lds_dma16(ok ? static_cast<const void*>(real) : static_cast<const void*>(g_zero16), B + grp * 1024);
+      const int n = n0 + lrow + 64 * j;
+      const bool ok = cok && n < a.cout;
+      const char* real = a.weight + (static_cast<int64_t>(ok ? n : 0) * kvol + ik) * row_bytes + cidx * 16;
+      rb[r][j] = *reinterpret_cast<const u32x4*>(ok ? static_cast<const void*>(real) : static_cast<const void*>(g_zero16));
     }
-    advance(ib);
-    ++sb;
+    if (++ikb == nkb) {
+      ikb = 0;
+      ik = irest ? __builtin_ctz(irest) : ik;
+      irest &= irest - 1u;
+    }
+  };
+  auto store = [&](const int r, const int buf) {
+    char* A = smem + buf * STAGE;
+    char* B = A + A_BYTES;
+#pragma unroll
+    for (int j = 0; j < A_INS; ++j) *reinterpret_cast<u32x4*>(A + lds_offset(lrow + 64 * j, lchunk)) = ra[r][j];
+#pragma unroll
+    for (int j = 0; j < B_INS; ++j) *reinterpret_cast<u32x4*>(B + lds_offset(lrow + 64 * j, lchunk)) = rb[r][j];
   };
 
-  f32x16 acc[MB][NB];
+  // acc[nb][mb]: channels block nb (MFMA rows) x output-row block mb (MFMA columns)
+  f32x16 acc[NB][MB];
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb)
+  for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
+    for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) acc[mb][nb][v] = 0.0f;
+      for (int v = 0; v < 16; ++v) acc[nb][mb][v] = 0.0f;
 
-  auto compute = [&](int s) {
-    const char* A = ring_a + (s % 3) * A_BYTES;
-    const char* B = ring_b + (s % 2) * B_BYTES;
-    // fragment reads run two K-groups ahead of the MFMAs (at most 12 reads in flight,
-    // within the 4-bit LDS counter), so each K-group waits only for its own reads
+  auto load = [&](const int r) {
+    load_a(r);
+    load_b(r);
+  };
+
+  // compute stage `buf` from LDS; with `issue` set, the global loads of the next stage
+  // for register set `next` (a compile-time constant) are issued between the MFMA groups
+  // so a stalled load issue overlaps MFMAs already in flight
+  auto compute = [&](const int buf, auto nc, const bool issue) {
+    constexpr int next = decltype(nc)::value;
+    const char* A = smem + buf * STAGE;
+    const char* B = A + A_BYTES;
     u32x4 af[4][MB], bf[4][NB];
     auto frags = [&](int g) {
       const int c = 2 * g + (lane >> 5);
@@ -376,18 +379,22 @@ __global__ __launch_bounds__(256) void conv_pipe_kernel(ConvArgs a) {
     };
     auto mma = [&](int g) {
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb)
+      for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) Mfma<T>::run(af[g][mb], bf[g][nb], acc[mb][nb]);
+        for (int mb = 0; mb < MB; ++mb) Mfma<T>::run(bf[g][nb], af[g][mb], acc[nb][mb]);
     };
     frags(0);
     frags(1);
     __builtin_amdgcn_sched_barrier(0);
     mma(0);
     __builtin_amdgcn_sched_barrier(0);
+    if (issue) load_a(next);
+    __builtin_amdgcn_sched_barrier(0);
     frags(2);
     __builtin_amdgcn_sched_barrier(0);
     mma(1);
+    __builtin_amdgcn_sched_barrier(0);
+    if (issue) load_b(next);
     __builtin_amdgcn_sched_barrier(0);
     frags(3);
     __builtin_amdgcn_sched_barrier(0);
@@ -396,37 +403,86 @@ __global__ __launch_bounds__(256) void conv_pipe_kernel(ConvArgs a) {
     mma(3);
   };
 
-  if (S > 0) {
-    issue_b();
-    issue_a();
-    if (S > 1) issue_a();
-  }
-  for (int s = 0; s < S; ++s) {
-    if (s + 1 < S) wait_vmcnt<A_INS>();
-    else wait_vmcnt<0>();
+  // one pipeline step; R = s % kRing and the LDS buffer s & 1 are compile-time
+  // constants (the loop is unrolled by 2 * kRing) so every register set stays in
+  // registers. Stage s+kRing is loaded into the set that held stage s; stages
+  // s+1 .. s+kRing are in flight while stage s computes.
+  auto step = [&](int s, auto rc, auto bc) {
+    constexpr int R = decltype(rc)::value, BUF = decltype(bc)::value;
+    constexpr int RN = (R + 1) % kRing;
+    compute(BUF, rc, s + kRing < S);
+    if (s + 1 < S) {
+      const int newer = (S - 2 - s) < (kRing - 1) ? (S - 2 - s) : (kRing - 1);  // stages issued after s+1
+      if (newer >= 2) wait_vmcnt<2 * L>();
+      else if (newer == 1) wait_vmcnt<L>();
+      else wait_vmcnt<0>();
+      __builtin_amdgcn_sched_barrier(0);
+      store(RN, 1 - BUF);
+      wait_lgkm0();
+    }
     __builtin_amdgcn_s_barrier();
-    if (s + 1 < S) issue_b();
-    if (s + 2 < S) issue_a();
-    compute(s);
+  };
+  if (S > 0) {
+#pragma unroll
+    for (int r = 0; r < kRing; ++r)
+      if (r < S) load(r);
+    const int newer = (S - 1) < (kRing - 1) ? (S - 1) : (kRing - 1);
+    if (newer >= 2) wait_vmcnt<2 * L>();
+    else if (newer == 1) wait_vmcnt<L>();
+    else wait_vmcnt<0>();
+    store(0, 0);
+    wait_lgkm0();
+    __builtin_amdgcn_s_barrier();
+  }
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  static_assert(kRing == 3, "the unrolled loop below is written for three register sets");
+  for (int s = 0; s < S; s += 6) {
+    step(s, I0{}, I0{});
+    if (s + 1 < S) step(s + 1, I1{}, I1{});
+    if (s + 2 < S) step(s + 2, I2{}, I0{});
+    if (s + 3 < S) step(s + 3, I0{}, I1{});
+    if (s + 4 < S) step(s + 4, I1{}, I0{});
+    if (s + 5 < S) step(s + 5, I2{}, I1{});
   }
   __syncthreads();
 
-  // epilogue: bias + activation in fp32, round to T, stage the tile in LDS
+  // epilogue: bias + activation in fp32, round to T; lane (l % 32) of block (nb, mb)
+  // holds output row wm*WM + mb*32 + l%32 and channels wn*WN + nb*32 + 8*(v/4) +
+  // 4*(l/32) + v%4: four consecutive channels per 8-byte LDS write
   T* C = reinterpret_cast<T*>(smem);
   const T* bias = static_cast<const T*>(a.bias);
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
-    const int j = wn * WN + nb * 32 + (lane & 31);
-    const int n = n0 + j;
-    const float b = (bias != nullptr && n < a.cout) ? to_f32(bias[n]) : 0.0f;
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
+    for (int q = 0; q < 4; ++q) {
+      const int j0 = wn * WN + nb * 32 + 8 * q + 4 * (lane >> 5);
+      float b[4];
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int i = wm * WM + mb * 32 + acc_row(lane, v);
-        float x = acc[mb][nb][v] + b;
-        if (a.act == HI3D_ACT_SILU) x = silu(x);
-        C[i * BN + j] = static_cast<T>(x);
+      for (int e = 0; e < 4; ++e) {
+        const int n = n0 + j0 + e;
+        b[e] = (bias != nullptr && n < a.cout) ? to_f32(bias[n]) : 0.0f;
+      }
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        const int i = wm * WM + mb * 32 + (lane & 31);
+        T h[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float x = acc[nb][mb][4 * q + e] + b[e];
+          if (a.act == HI3D_ACT_SILU) x = silu(x);
+          h[e] = static_cast<T>(x);
+        }
+        if constexpr (sizeof(T) == 2) {
+          uint2 packed;
+          __builtin_memcpy(&packed, h, 8);
+          *reinterpret_cast<uint2*>(C + i * BN + j0) = packed;
+        } else {
+          u32x4 packed;
+          __builtin_memcpy(&packed, h, 16);
+          *reinterpret_cast<u32x4*>(C + i * BN + j0) = packed;
+        }
       }
     }
   }
@@ -434,11 +490,9 @@ __global__ __launch_bounds__(256) void conv_pipe_kernel(ConvArgs a) {
   constexpr int EPC = 16 / static_cast<int>(sizeof(T));
   constexpr int CPR = BN / EPC;
   const int64_t out_row_bytes = static_cast<int64_t>(a.cout) * sizeof(T);
-  for (int q = tid; q < BM * CPR; q += 256) {
+  for (int q = tid; q < BM * CPR; q += kPipeThreads) {
     const int i = q / CPR, cc = q - (q / CPR) * CPR;
-    const int64_t pt = tile * SUB + i / kTileRows;
-    if (pt >= a.ntiles) continue;
-    const int32_t orow = a.rows[pt * kTileRows + (i % kTileRows)];
+    const int32_t orow = orows[i];
     const int ncol = n0 + cc * EPC;
     if (orow < 0 || ncol >= a.cout) continue;
     u32x4 v = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(C) + (i * BN + cc * EPC) * sizeof(T));
@@ -488,13 +542,13 @@ int elem_size(int dtype) {
 }
 
 template <typename T, int BM, int BN, int WGM>
-int launch_dma(const ConvArgs& base, hipStream_t stream) {
+int launch_pipe(const ConvArgs& base, hipStream_t stream) {
   ConvArgs a = base;
   a.ny = static_cast<int32_t>(ceil_div(a.cout, BN));
   const int64_t blocks = ceil_div(a.ntiles, BM / kTileRows) * a.ny;
   if (blocks == 0) return HI3D_OK;
   HI3D_REQUIRE(blocks < (int64_t(1) << 31), "too many tiles");
-  hipLaunchKernelGGL((conv_pipe_kernel<T, BM, BN, WGM>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
+  hipLaunchKernelGGL((conv_pipe_kernel<T, BM, BN, WGM>), dim3(static_cast<unsigned>(blocks)), dim3(kPipeThreads), 0, stream, a);
   HI3D_LAUNCH_CHECK();
   return HI3D_OK;
 }
@@ -503,10 +557,9 @@ template <typename T>
 int launch_mfma(const ConvArgs& base, hipStream_t stream) {
   ConvArgs a = base;
   if (a.kvol <= kMaxPipelinedKvol) {
-    if (a.cout <= 64) return launch_dma<T, 256, 64, 4>(a, stream);
-    if (sizeof(T) == 4) return launch_dma<T, 128, 128, 2>(a, stream);
-    if (a.cout <= 128) return launch_dma<T, 256, 128, 4>(a, stream);
-    return launch_dma<T, 128, 256, 2>(a, stream);
+    if (a.cout <= 64) return launch_pipe<T, 256, 64, 8>(a, stream);
+    if (a.cout <= 128) return launch_pipe<T, 256, 128, 4>(a, stream);
+    return launch_pipe<T, 128, 256, 2>(a, stream);
   }
   int bn;
   const int cout = a.cout;
