@@ -34,6 +34,24 @@ PEAK_FP32_TFLOPS = 157.3
 PEAK_INT8_TOPS = 5000.0
 PEAK_HBM_GBS = 8000.0
 
+# Headline kernel (fp16, Cout 128 selects the 256x128 tile) and the counter summary that
+# holds its measured HBM traffic per launch: FETCH_SIZE and WRITE_SIZE per dispatch from
+# two rocprofv3 --pmc runs of this script, each scaled by the factor the same counter
+# reads for a plain device copy of known size (`--copy-probe`).
+HEADLINE_KERNEL = "conv_pipe_kernel<_Float16,256,128,4>"
+TRAFFIC_SUMMARY = ROOT / "profiles" / "conv_pipe_subm3_c128_fp16_traffic.txt"
+
+
+def measured_traffic():
+    """HBM bytes per headline-kernel launch from the committed counter summary, or None."""
+    try:
+        for line in TRAFFIC_SUMMARY.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch"):
+                return float(line.split("=", 1)[1])
+    except (OSError, ValueError):
+        pass
+    return None
+
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
@@ -322,8 +340,10 @@ def main() -> int:
             "peak": PEAK_FP16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": achieved / PEAK_FP16_TFLOPS,
-            "traffic": None,
-            "kernel": "conv_mfma_kernel<_Float16,128>",
+            "traffic": measured_traffic(),
+            "traffic_source": TRAFFIC_SUMMARY.name,
+            "alg_bytes": head["conv_alg_bytes"],
+            "kernel": HEADLINE_KERNEL,
             "kernel_ms": head["conv_kernel_ms"],
         },
         "cpu_baseline": cpu,

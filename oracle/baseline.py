@@ -98,7 +98,7 @@ def time_subm_conv(indices: np.ndarray, spatial_shape, cin: int, cout: int, seed
     n = int(idx.shape[0])
     rng = np.random.default_rng(seed)
     feats = torch.as_tensor(rng.standard_normal((n, cin), dtype=np.float32))
-    weight = torch.as_tensor(rng.standard_normal((cout, 3, 3, 3, cin), dtype=np.float32) / np.sqrt(27 * cin))
+    weight = torch.as_tensor((rng.standard_normal((cout, 3, 3, 3, cin)) / np.sqrt(27 * cin)).astype(np.float32))
     t0 = time.perf_counter()
     pairs = kernel_map(idx, spatial_shape)
     t_map = time.perf_counter() - t0

@@ -356,3 +356,21 @@ def test_residual_block_composition():
     h1 = h1 / (1 + np.exp(-h1))
     ref = oconv.dense_subm_conv3d(idx, h1, w2, b2, [8, 8, 8]) + x.astype(np.float64)
     assert np.allclose(full, ref, atol=1e-10)
+
+
+def test_cpu_baseline_runs_on_a_sample():
+    """The timed CPU baseline (reference CPU fallback) runs and its conv equals the
+    float64 gather sum over the same pairs."""
+    from oracle import baseline
+
+    rng = np.random.default_rng(4)
+    idx = _rand_indices(rng, 10, 0.3)
+    r = baseline.time_subm_conv(idx, [10] * 3, 8, 6, repeats=1, max_rows=200, threads=1)
+    assert r["rows"] == 200 and r["conv_s"] > 0 and r["torch_threads"] >= 1
+    feats = rng.standard_normal((len(idx), 8)).astype(np.float32)
+    weight = (rng.standard_normal((6, 3, 3, 3, 8)) / 10).astype(np.float32)
+    pairs = baseline.kernel_map(torch.as_tensor(idx), [10] * 3)
+    got = baseline.subm_conv(torch.as_tensor(feats), *pairs, torch.as_tensor(weight), None).numpy()
+    table = okmap.neighbour_table(idx, [10] * 3)
+    ref = oconv.gather_conv_f64(feats, table, weight.reshape(6, 27, 8))
+    assert oconv.rel_err(got, ref) <= 1e-5
