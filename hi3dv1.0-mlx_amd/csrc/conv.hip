@@ -227,16 +227,6 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a) {
 
 __device__ __attribute__((aligned(16))) const uint32_t g_zero16[4] = {0u, 0u, 0u, 0u};
 
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit counter");
-  // s_waitcnt: vmcnt[3:0] | expcnt[6:4] (7 = no wait) | lgkmcnt[11:8] (15 = no wait) | vmcnt[5:4] at [15:14]
-  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
-
-// Wait for this wave's LDS operations only (vmcnt left at its maximum, 63).
-__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14)); }
-
 constexpr int kMaxPipelinedKvol = 27;
 constexpr int kPipeThreads = 512;
 constexpr int kRing = 3;  // register sets of in-flight global loads

@@ -64,6 +64,32 @@ struct Mfma<float> {
 // Row of accumulator element v of a 32x32 block held by `lane` (column = lane % 32).
 __device__ __forceinline__ int acc_row(int lane, int v) { return ((v >> 2) << 3) + ((lane >> 5) << 2) + (v & 3); }
 
+// s_waitcnt with only the vector-memory counter limited to N outstanding operations
+// (fields: vmcnt[3:0], expcnt[6:4] = 7, lgkmcnt[11:8] = 15, vmcnt[5:4] at bits 15:14).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit counter");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Wait for this wave's LDS operations only (vmcnt left at its maximum, 63).
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14)); }
+
+// Workgroup barrier without the implicit drain of outstanding global loads that
+// __syncthreads() performs; the empty asm statements keep the compiler from moving
+// memory accesses across it. Callers wait for their own operations first.
+__device__ __forceinline__ void raw_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// 16-byte direct-to-LDS load (global_load_lds_dwordx4): lane l's 16 bytes land at
+// lds_wave_base + 16 l. The LDS base must be the same for the whole wave.
+__device__ __forceinline__ void lds_dma16(const void* src, char* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(lds_wave_base), 16, 0, 0);
+}
+
 // XCD-aware block order: the chip deals workgroups round-robin over its 8 XCDs, so
 // block b runs on XCD b % 8. Remap so each XCD walks a contiguous range of work items
 // (neighbouring tiles share gathered rows and weights in that XCD's L2).

@@ -3,6 +3,8 @@
 //
 // Reference: src/hi3d_mac/mlx_backend/w8a8.py — signs :16-18, _QUANT :25-58,
 // _GEMM :61-80, quantize_activation :95-102, linear :105-119.
+#include <type_traits>
+
 #include "common.h"
 #include "conv_tile.h"
 
@@ -102,140 +104,539 @@ __global__ __launch_bounds__(256) void quant_kernel(const _Float16* __restrict__
 }
 
 // -------------------------------------------------------------------- GEMM --
-// C[m, n] = sum_k A[m, k] * W[n, k] on int8 MFMA 32x32x32 with int32 accumulators.
-// Workgroup tile BM x BN, 4 waves in a 2x2 grid, K-blocks of 128 bytes double-buffered
-// through LDS in the shared swizzled layout.
-template <int BM, int BN>
-__global__ __launch_bounds__(256) void w8a8_gemm_kernel(const int8_t* __restrict__ qa, const float* __restrict__ sa,
-                                                        const int8_t* __restrict__ w, const float* __restrict__ sw,
-                                                        const _Float16* __restrict__ bias, int64_t m, int n, int k,
-                                                        _Float16* __restrict__ out, int32_t* __restrict__ acc_out,
-                                                        int64_t mtiles, int ntiles) {
-#pragma clang fp contract(off)
-  constexpr int WM = BM / 2, WN = BN / 2;
-  constexpr int MB = WM / 32, NB = WN / 32;
-  constexpr int A_BYTES = BM * 128, B_BYTES = BN * 128;
-  constexpr int STAGE = A_BYTES + B_BYTES;
-  constexpr int PIPE = 2 * STAGE;
-  constexpr int EPI = BM * BN * 2;
-  constexpr int SMEM = PIPE > EPI ? PIPE : EPI;
-  constexpr int AL = BM / 32, BL = BN / 32;
-  __shared__ __attribute__((aligned(16))) char smem[SMEM];
+// out[m, n] = fp16(((float)acc[m, n] * sa[m]) * sw[n] + (float)bias[n]) with the exact
+// int32 acc[m, n] = sum_k q[m, k] * w[n, k].
+//
+// Workgroup tile: 256 tokens x 256 channels, 4 waves, each owning 128 channels x 128
+// tokens as 4 x 4 blocks of v_mfma_i32_32x32x32_i8 with the weights as the first operand
+// (a lane's accumulators then hold four consecutive channels of one token). K advances
+// in 64-byte stages through a 4-deep LDS ring filled by direct-to-LDS 16-byte loads
+// issued three stages ahead. Rows are 64 bytes with chunk c of row r stored at
+// c ^ (((r >> 1) ^ (r >> 3)) & 3): the 16-byte fragment reads of 8 or 16 consecutive
+// rows then touch distinct banks. One barrier per stage, between the two K-groups of the
+// stage: before it the wave multiplies K-group 0 while its K-group 1 fragments load;
+// after it, it issues the loads three stages ahead (into the buffer every wave has
+// finished reading) and reads the next stage's K-group 0 while K-group 1 multiplies.
+constexpr int kGemmBM = 256, kGemmBN = 256, kGemmRing = 4;
+constexpr int kGemmStageA = kGemmBM * 64, kGemmStage = kGemmStageA + kGemmBN * 64;
+constexpr int kGemmLoads = 8;  // direct-to-LDS loads per wave per stage
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  // column tiles innermost: consecutive items share the A rows (L2 reuse in one XCD)
+__device__ __attribute__((aligned(16))) const uint32_t g_zero_chunk[4] = {0u, 0u, 0u, 0u};
+
+__device__ __forceinline__ int lds_off64(int row, int chunk) {
+  return row * 64 + ((chunk ^ (((row >> 1) ^ (row >> 3)) & 3)) << 4);
+}
+
+template <bool kDump, bool kTail>
+__global__ __launch_bounds__(256, 1) void w8a8_gemm_kernel(const int8_t* __restrict__ qa, const float* __restrict__ sa,
+                                                           const int8_t* __restrict__ w, const float* __restrict__ sw,
+                                                           const _Float16* __restrict__ bias, int64_t m, int n, int k,
+                                                           _Float16* __restrict__ out, int32_t* __restrict__ acc_out,
+                                                           int ntiles) {
+#pragma clang fp contract(off)
+  constexpr int BM = kGemmBM, BN = kGemmBN, NS = kGemmRing;
+  constexpr int RING = NS * kGemmStage;
+  constexpr int EPI = BM * BN * 2;
+  static_assert(EPI <= RING, "the epilogue tile reuses the ring");
+  __shared__ __attribute__((aligned(16))) char smem[RING + (BM + BN) * 4 + BN * 2];
+  float* const s_sa = reinterpret_cast<float*>(smem + RING);
+  float* const s_sw = s_sa + BM;
+  _Float16* const s_bias = reinterpret_cast<_Float16*>(s_sw + BN);
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wn = wave >> 1, wm = wave & 1;
+  // channel tiles innermost: the workgroups an XCD runs together share their token rows
   const int64_t item = xcd_remap(blockIdx.x, static_cast<int64_t>(gridDim.x));
   const int64_t mt = item / ntiles;
   const int nt = static_cast<int>(item - mt * ntiles);
   const int64_t m0 = mt * BM;
   const int n0 = nt * BN;
 
-  const int chunks = k >> 4;
-  const int S = (chunks + 7) >> 3;
-  const int ld_row = tid >> 3, ld_chunk = tid & 7;
-  const u32x4 zero = {0u, 0u, 0u, 0u};
-  u32x4 ra[AL], rb[BL];
-  int ls = 0;
-  auto load = [&]() {
-    const int c = ls * 8 + ld_chunk;
-    const bool cok = c < chunks;
-#pragma unroll
-    for (int i = 0; i < AL; ++i) {
-      const int64_t r = m0 + ld_row + 32 * i;
-      ra[i] = (cok && r < m) ? *reinterpret_cast<const u32x4*>(qa + r * k + c * 16) : zero;
-    }
-#pragma unroll
-    for (int j = 0; j < BL; ++j) {
-      const int r = n0 + ld_row + 32 * j;
-      rb[j] = (cok && r < n) ? *reinterpret_cast<const u32x4*>(w + static_cast<int64_t>(r) * k + c * 16) : zero;
-    }
-    ++ls;
-  };
-  auto store = [&](int buf) {
-    char* A = smem + buf * STAGE;
-    char* B = A + A_BYTES;
-#pragma unroll
-    for (int i = 0; i < AL; ++i) *reinterpret_cast<u32x4*>(A + lds_offset(ld_row + 32 * i, ld_chunk)) = ra[i];
-#pragma unroll
-    for (int j = 0; j < BL; ++j) *reinterpret_cast<u32x4*>(B + lds_offset(ld_row + 32 * j, ld_chunk)) = rb[j];
-  };
-  i32x16 acc[MB][NB];
-#pragma unroll
-  for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[mb][nb][v] = 0;
-  auto compute = [&](int buf) {
-    const char* A = smem + buf * STAGE;
-    const char* B = A + A_BYTES;
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int c = 2 * g + (lane >> 5);
-      u32x4 af[MB], bf[NB];
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb)
-        af[mb] = *reinterpret_cast<const u32x4*>(A + lds_offset(wm * WM + mb * 32 + (lane & 31), c));
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb)
-        bf[nb] = *reinterpret_cast<const u32x4*>(B + lds_offset(wn * WN + nb * 32 + (lane & 31), c));
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-          acc[mb][nb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, af[mb]),
-                                                               __builtin_bit_cast(i32x4, bf[nb]), acc[mb][nb], 0, 0, 0);
-    }
-  };
-  if (S > 0) {
-    load();
-    store(0);
-    __syncthreads();
-    for (int s = 0; s < S; ++s) {
-      const bool more = s + 1 < S;
-      if (more) load();
-      compute(s & 1);
-      if (more) store((s + 1) & 1);
-      __syncthreads();
-    }
+  for (int i = tid; i < BM; i += 256) s_sa[i] = m0 + i < m ? sa[m0 + i] : 0.0f;
+  for (int j = tid; j < BN; j += 256) {
+    const bool ok = n0 + j < n;
+    s_sw[j] = ok ? sw[n0 + j] : 0.0f;
+    s_bias[j] = (ok && bias != nullptr) ? bias[n0 + j] : static_cast<_Float16>(0.0f);
   }
-  // epilogue: fp16(((float)acc * sa) * sw + (float)bias), staged in LDS for 16-byte stores
+
+  // load j (0..3) of this wave covers ring rows (4j + wave) * 16 .. +15; lane l fills row
+  // + l / 4 at physical chunk l % 4, i.e. logical chunk (l % 4) ^ swizzle(row). Rows past
+  // the matrix edge re-read the last row (their results are never stored). Sources are
+  // a workgroup-uniform tile base plus a 32-bit per-lane offset (row * k + chunk), so
+  // without a K tail (kTail false: k % 64 == 0) a load needs no per-lane arithmetic.
+  const int S = (k + 63) >> 6;
+  const int8_t* const a_tile = qa + m0 * k;
+  const int8_t* const b_tile = w + static_cast<int64_t>(n0) * k;
+  uint32_t aoff[4], boff[4];
+  int coff[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int r = (4 * j + wave) * 16 + (lane >> 2);
+    const int c = (lane & 3) ^ (((r >> 1) ^ (r >> 3)) & 3);
+    coff[j] = c * 16;
+    const int ar = m0 + r < m ? r : static_cast<int>(m - 1 - m0);
+    const int br = n0 + r < n ? r : n - 1 - n0;
+    aoff[j] = static_cast<uint32_t>(ar) * static_cast<uint32_t>(k) + coff[j];
+    boff[j] = static_cast<uint32_t>(br) * static_cast<uint32_t>(k) + coff[j];
+  }
+  auto issue_one = [&](int s, int j) {  // load j of stage s: 0..3 tokens, 4..7 channels
+    char* base = smem + (s % NS) * kGemmStage + (j < 4 ? 0 : kGemmStageA) + (4 * (j & 3) + wave) * 1024;
+    const int kb = s * 64;
+    const int8_t* src = (j < 4 ? a_tile : b_tile) + kb + (j < 4 ? aoff[j & 3] : boff[j & 3]);
+    if (kTail) {
+      const bool ok = kb + coff[j & 3] < k;
+      lds_dma16(ok ? static_cast<const void*>(src) : static_cast<const void*>(g_zero_chunk), base);
+    } else {
+      lds_dma16(src, base);
+    }
+  };
+  auto issue = [&](int s) {
+#pragma unroll
+    for (int j = 0; j < kGemmLoads; ++j) issue_one(s, j);
+  };
+
+  i32x16 acc[4][4];  // [channel block][token block]
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[nb][mb][v] = 0;
+  u32x4 fw[2][4], fq[2][4];  // fragments of K-group 0 / 1
+  // fragment read i of K-group G of stage s: 0..3 channel blocks, 4..7 token blocks
+  auto frag_one = [&](int s, auto gc, int i) {
+    constexpr int G = decltype(gc)::value;
+    const char* A = smem + (s % NS) * kGemmStage;
+    const int c = 2 * G + (lane >> 5);
+    if (i < 4)
+      fw[G][i] = *reinterpret_cast<const u32x4*>(A + kGemmStageA + lds_off64(wn * 128 + i * 32 + (lane & 31), c));
+    else
+      fq[G][i - 4] = *reinterpret_cast<const u32x4*>(A + lds_off64(wm * 128 + (i - 4) * 32 + (lane & 31), c));
+  };
+  auto frags = [&](int s, auto gc) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) frag_one(s, gc, i);
+  };
+  // MFMA i of K-group G: channel block i / 4, token block i % 4
+  auto mma_one = [&](auto gc, int i) {
+    constexpr int G = decltype(gc)::value;
+    acc[i >> 2][i & 3] = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, fw[G][i >> 2]),
+                                                             __builtin_bit_cast(i32x4, fq[G][i & 3]), acc[i >> 2][i & 3],
+                                                             0, 0, 0);
+  };
+  auto mma = [&](auto gc) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) mma_one(gc, i);
+  };
+  using G0 = std::integral_constant<int, 0>;
+  using G1 = std::integral_constant<int, 1>;
+
+  // Loads of stage s + 3 are spread over two half-stages to keep the vector memory path
+  // busy without bursts: channel rows (loads 4..7) during the second half of stage s,
+  // token rows (loads 0..3) during the first half of stage s + 1. Either way every wave
+  // has passed the barrier of stage s, so the buffer of stage s - 1 is free.
+  //
+  // First half of stage s: K-group 0 MFMAs; after each of the first eight one K-group 1
+  // fragment read, after every other one of the last eight (with `dma`) one token-row
+  // load of stage s + 2.
+  auto half0 = [&](int s, bool dma) {
+    wait_lgkm0();  // K-group 0 fragments (read during the previous K-group 1 MFMAs) are in
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      mma_one(G0{}, i);
+      __builtin_amdgcn_sched_barrier(0);
+      if (i < 8) {
+        frag_one(s, G1{}, i);
+      } else if (dma && (i & 1)) {
+        issue_one(s + NS - 2, (i - 8) >> 1);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  // Second half: K-group 1 MFMAs; after each of the first eight one K-group 0 fragment
+  // read of stage s + 1, after every other one of the last eight (with `dma`) one
+  // channel-row load of stage s + 3.
+  auto half1 = [&](int s, bool dma) {
+    wait_lgkm0();  // K-group 1 fragments (read during the K-group 0 MFMAs) are in
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      mma_one(G1{}, i);
+      __builtin_amdgcn_sched_barrier(0);
+      if (i < 8) {
+        frag_one(s + 1, G0{}, i);
+      } else if (dma && (i & 1)) {
+        issue_one(s + NS - 1, 4 + ((i - 8) >> 1));
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  // Barrier of stage s: this wave's part of stage s + 1 has landed (loads issued later:
+  // stage s + 2, i.e. kGemmLoads of them while it exists) and every wave is done reading
+  // stage s - 1.
+  auto sync = [&](int s) {
+    if (s + 2 < S) wait_vmcnt<kGemmLoads>();
+    else wait_vmcnt<0>();
+    raw_barrier();
+  };
+
+  // prologue: stages 0..2 in full
+#pragma unroll
+  for (int s = 0; s < NS - 1; ++s)
+    if (s < S) issue(s);
+  if (S > 2) wait_vmcnt<2 * kGemmLoads>();
+  else if (S > 1) wait_vmcnt<kGemmLoads>();
+  else wait_vmcnt<0>();
+  raw_barrier();
+  frags(0, G0{});
+  int s = 0;
+  if (S > 1) {  // stage 0: its first half has no token rows to load (stage 2 is loaded)
+    half0(0, false);
+    sync(0);
+    half1(0, NS - 1 < S);
+    s = 1;
+  }
+  for (; s + NS - 1 < S; ++s) {  // steady state: both halves load
+    half0(s, true);
+    sync(s);
+    half1(s, true);
+  }
+  if (s + NS - 2 < S && s + 1 < S) {  // token rows of the last stage remain
+    half0(s, true);
+    sync(s);
+    half1(s, false);
+    ++s;
+  }
+  for (; s + 1 < S; ++s) {  // nothing left to load
+    half0(s, false);
+    sync(s);
+    half1(s, false);
+  }
+  if (S > 0) {  // the final stage
+    wait_lgkm0();
+    frags(S - 1, G1{});
+    mma(G0{});
+    mma(G1{});
+  }
+
+  // epilogue: channels wn*128 + nb*32 + 8*(v/4) + 4*(l/32) + v%4, token wm*128 + mb*32 + l%32
+  if (kDump) {
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb) {
+        const int64_t row = m0 + wm * 128 + mb * 32 + (lane & 31);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int col = n0 + wn * 128 + nb * 32 + 8 * q + 4 * (lane >> 5);
+          if (row >= m) continue;
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (col + e < n) acc_out[row * n + col + e] = acc[nb][mb][4 * q + e];
+        }
+      }
+  }
+  wait_vmcnt<0>();
+  __syncthreads();  // every wave is done with the ring: it becomes the output tile
   _Float16* C = reinterpret_cast<_Float16*>(smem);
+  constexpr int CROW = BN * 2;  // bytes per output row in LDS; 16-byte chunks swizzled by row
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    const int j = wn * WN + nb * 32 + (lane & 31);
-    const int col = n0 + j;
-    const bool cok = col < n;
-    const float swc = cok ? sw[col] : 0.0f;
-    const float bc = (cok && bias != nullptr) ? static_cast<float>(bias[col]) : 0.0f;
+  for (int mb = 0; mb < 4; ++mb) {
+    const int i = wm * 128 + mb * 32 + (lane & 31);
+    const float sar = s_sa[i];
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
+    for (int nb = 0; nb < 4; ++nb) {
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int i = wm * WM + mb * 32 + acc_row(lane, v);
-        const int64_t row = m0 + i;
-        const float sar = row < m ? sa[row] : 0.0f;
-        const float prod = static_cast<float>(acc[mb][nb][v]) * sar;
-        const float y = prod * swc + bc;
-        C[i * BN + j] = static_cast<_Float16>(y);
-        if (acc_out != nullptr && cok && row < m) acc_out[row * n + col] = acc[mb][nb][v];
+      for (int q = 0; q < 4; ++q) {
+        const int j0 = wn * 128 + nb * 32 + 8 * q + 4 * (lane >> 5);
+        _Float16 h[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float prod = static_cast<float>(acc[nb][mb][4 * q + e]) * sar;
+          h[e] = static_cast<_Float16>(prod * s_sw[j0 + e] + static_cast<float>(s_bias[j0 + e]));
+        }
+        const int chunk = (j0 >> 3) ^ (i & 31);
+        *reinterpret_cast<uint2*>(reinterpret_cast<char*>(C) + i * CROW + chunk * 16 + (j0 & 4) * 2) =
+            __builtin_bit_cast(uint2, h);
       }
     }
   }
   __syncthreads();
-  constexpr int CPR = BN / 8;
+  constexpr int CPR = BN / 8;  // 16-byte chunks per row
+  const bool vec = (n & 7) == 0;
   for (int q = tid; q < BM * CPR; q += 256) {
-    const int i = q / CPR, cc = q - (q / CPR) * CPR;
+    const int i = q / CPR, cc = q % CPR;
     const int64_t row = m0 + i;
     const int col = n0 + cc * 8;
     if (row >= m || col >= n) continue;
-    const u32x4 v = *reinterpret_cast<const u32x4*>(C + i * BN + cc * 8);
-    if (col + 8 <= n && (n & 7) == 0) {
+    const u32x4 v = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(C) + i * CROW + ((cc ^ (i & 31)) * 16));
+    if (vec) {
       *reinterpret_cast<u32x4*>(out + row * n + col) = v;
     } else {
       const _Float16* pv = reinterpret_cast<const _Float16*>(&v);
       for (int e = 0; e < 8 && col + e < n; ++e) out[row * n + col + e] = pv[e];
+    }
+  }
+}
+
+// Persistent variant for full tiles (m, n >= 256, n % 8 == 0, k % 64 == 0, k >= 256): one
+// workgroup per CU walks a list of tiles while the stage pipeline above runs on without a
+// break: the next tile's first stages load during the current tile's last ones, and the
+// per-tile work around the K loop shrinks to the epilogue.
+//  * Tiles: the last tile of each dimension is moved back to end at m (n), so every tile
+//    is full and in bounds; where tiles overlap, both compute and store the same bits.
+//  * Work list: the chip deals workgroups round-robin over its 8 XCDs; each XCD's
+//    workgroups take a contiguous range of tiles (channel tiles innermost), so the tiles
+//    an XCD runs together share their token rows in its L2.
+//  * Scales: sa / sw / bias of a tile arrive by three 4-byte direct-to-LDS loads per wave
+//    at the tile's first stage, into one of two LDS slots.
+//  * Epilogue: after the last MFMAs of a tile, the ring buffer of that stage (free: every
+//    wave is past its reads) stages the int32 accumulators in eight 32-token chunks,
+//    written straight from the accumulator registers by the two waves holding those
+//    tokens; every thread then converts one fixed 8-channel group of 4 rows per chunk
+//    (dequant + bias, fp16) and stores it as one 16-byte row chunk. The stores drain while
+//    the next tile computes.
+//  * Counting: every wave issues the same number of vector memory operations (no
+//    predicated loads or stores), so the vmcnt waits are exact: at the barrier of stage g
+//    the operations issued after stage g + 1's last load are stage g + 2's loads (8) and,
+//    at a tile's first stage, the previous tile's 32 stores and this tile's 3 scale loads.
+constexpr int kGemmScale = kGemmBM * 4 + kGemmBN * 4 + kGemmBN * 2;  // sa, sw, bias of one tile
+constexpr int kGemmStores = 32;                                       // epilogue stores per wave
+constexpr int kGemmScaleLoads = 3;                                    // scale loads per wave per tile
+
+__device__ __attribute__((aligned(16))) const uint32_t g_zero_bias[kGemmBN / 2] = {};
+
+__device__ __forceinline__ void lds_dma4(const void* src, char* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(lds_wave_base), 4, 0, 0);
+}
+
+__global__ __launch_bounds__(256, 1) void w8a8_gemm_persistent_kernel(
+    const int8_t* __restrict__ qa, const float* __restrict__ sa, const int8_t* __restrict__ w,
+    const float* __restrict__ sw, const _Float16* __restrict__ bias, int64_t m, int n, int k,
+    _Float16* __restrict__ out, int ntiles_n, int64_t total) {
+#pragma clang fp contract(off)
+  constexpr int NS = kGemmRing;
+  constexpr int RING = NS * kGemmStage;
+  __shared__ __attribute__((aligned(16))) char smem[RING + 2 * kGemmScale];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wn = wave >> 1, wm = wave & 1;
+
+  // this workgroup's tiles: lo + L + i * P_x within the XCD's range [lo, hi)
+  const int P = static_cast<int>(gridDim.x);
+  const int x = static_cast<int>(blockIdx.x) & 7, L = static_cast<int>(blockIdx.x) >> 3;
+  const int Px = P / 8 + (x < P % 8 ? 1 : 0);
+  const int64_t per = total / 8, rem = total % 8;
+  const int64_t lo = x * per + (x < rem ? x : rem);
+  const int64_t hi = lo + per + (x < rem ? 1 : 0);
+  const int64_t mine = hi - lo > L ? (hi - lo - L + Px - 1) / Px : 0;
+  const int S = k >> 6;
+  const int64_t G = mine * S;
+  if (G == 0) return;
+  auto origin = [&](int64_t t, int64_t& m0, int& n0) {
+    const int64_t item = lo + L + t * Px;
+    const int64_t mt = item / ntiles_n;
+    const int nt = static_cast<int>(item - mt * ntiles_n);
+    m0 = mt * kGemmBM < m - kGemmBM ? mt * kGemmBM : m - kGemmBM;
+    n0 = nt * kGemmBN < n - kGemmBN ? nt * kGemmBN : n - kGemmBN;
+  };
+
+  // per-lane source offsets inside a tile (see the non-persistent kernel for the layout)
+  uint32_t roff[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int r = (4 * j + wave) * 16 + (lane >> 2);
+    const int c = (lane & 3) ^ (((r >> 1) ^ (r >> 3)) & 3);
+    roff[j] = static_cast<uint32_t>(r) * static_cast<uint32_t>(k) + c * 16;
+  }
+  // load cursors: the next stage whose token (A) / channel (B) rows are to be issued
+  struct Cursor {
+    int64_t t;
+    int s, slot;
+    const int8_t* base;  // tile rows + 64 s
+  };
+  auto cursor_at_tile = [&](Cursor& c, bool tokens) {
+    int64_t m0;
+    int n0;
+    origin(c.t, m0, n0);
+    c.base = tokens ? qa + m0 * k : w + static_cast<int64_t>(n0) * k;
+  };
+  auto advance = [&](Cursor& c, bool tokens) {
+    c.slot = (c.slot + 1) & (NS - 1);
+    if (++c.s == S) {
+      c.s = 0;
+      ++c.t;
+      if (c.t < mine) cursor_at_tile(c, tokens);
+    } else {
+      c.base += 64;
+    }
+  };
+  Cursor ct{0, 0, 0, nullptr}, cc{0, 0, 0, nullptr};
+  cursor_at_tile(ct, true);
+  cursor_at_tile(cc, false);
+  auto issue_tokens = [&](int j) {  // load j (0..3) of the token cursor's stage
+    lds_dma16(ct.base + roff[j], smem + ct.slot * kGemmStage + (4 * j + wave) * 1024);
+  };
+  auto issue_channels = [&](int j) {
+    lds_dma16(cc.base + roff[j], smem + cc.slot * kGemmStage + kGemmStageA + (4 * j + wave) * 1024);
+  };
+  auto issue_scales = [&](int64_t t) {
+    int64_t m0;
+    int n0;
+    origin(t, m0, n0);
+    char* region = smem + RING + (t & 1) * kGemmScale;
+    lds_dma4(sa + m0 + wave * 64 + lane, region + wave * 256);
+    lds_dma4(sw + n0 + wave * 64 + lane, region + kGemmBM * 4 + wave * 256);
+    const uint32_t* b = bias != nullptr ? reinterpret_cast<const uint32_t*>(bias + n0) : g_zero_bias;
+    lds_dma4(b + (wave & 1) * 64 + lane, region + (kGemmBM + kGemmBN) * 4 + (wave & 1) * 256);
+  };
+
+  i32x16 acc[4][4];
+  u32x4 fw[2][4], fq[2][4];
+  auto frag_one = [&](int slot, auto gc, int i) {
+    constexpr int Gk = decltype(gc)::value;
+    const char* A = smem + slot * kGemmStage;
+    const int c = 2 * Gk + (lane >> 5);
+    if (i < 4)
+      fw[Gk][i] = *reinterpret_cast<const u32x4*>(A + kGemmStageA + lds_off64(wn * 128 + i * 32 + (lane & 31), c));
+    else
+      fq[Gk][i - 4] = *reinterpret_cast<const u32x4*>(A + lds_off64(wm * 128 + (i - 4) * 32 + (lane & 31), c));
+  };
+  const i32x16 zero16 = {};
+  auto mma_one = [&](auto gc, int i, auto fc) {  // fc: first K-group of a tile (zero accumulators)
+    constexpr int Gk = decltype(gc)::value;
+    constexpr bool kFirst = decltype(fc)::value;
+    acc[i >> 2][i & 3] = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, fw[Gk][i >> 2]),
+                                                             __builtin_bit_cast(i32x4, fq[Gk][i & 3]),
+                                                             kFirst ? zero16 : acc[i >> 2][i & 3], 0, 0, 0);
+  };
+  // first half of a stage: K-group 0 MFMAs, K-group 1 fragment reads, token-row loads
+  auto half0 = [&](auto fc, int slot, bool tok) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      mma_one(std::integral_constant<int, 0>{}, i, fc);
+      __builtin_amdgcn_sched_barrier(0);
+      if (i < 8) {
+        frag_one(slot, std::integral_constant<int, 1>{}, i);
+      } else if (tok && (i & 1)) {
+        issue_tokens((i - 8) >> 1);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  using G0 = std::integral_constant<int, 0>;
+  using G1 = std::integral_constant<int, 1>;
+
+  // prologue: tile 0's scales, then stages 0..2 in full
+  issue_scales(0);
+#pragma unroll
+  for (int st = 0; st < NS - 1; ++st) {
+    if (st < G) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) issue_tokens(j);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) issue_channels(j);
+      advance(ct, true);
+      advance(cc, false);
+    }
+  }
+  wait_vmcnt<2 * kGemmLoads>();  // G >= S >= 4: stages 1 and 2 may stay in flight
+  raw_barrier();
+#pragma unroll
+  for (int i = 0; i < 8; ++i) frag_one(0, G0{}, i);
+
+  int s = 0;  // stage of the current tile
+  int64_t t = 0;
+  for (int64_t g = 0; g < G; ++g) {
+    const int slot = static_cast<int>(g & (NS - 1));
+    const bool first = s == 0;
+    const bool tok = g >= 1 && g + 2 < G;  // token rows of stage g + 2
+    // first half: K-group 0 MFMAs (zero accumulators at a tile's first stage), K-group 1
+    // fragment reads, token-row loads of stage g + 2 and, at a tile's first stage, its scales
+    wait_lgkm0();
+    if (first && g > 0) issue_scales(t);
+    __builtin_amdgcn_sched_barrier(0);
+    if (first) half0(std::true_type{}, slot, tok);
+    else half0(std::false_type{}, slot, tok);
+    if (tok) advance(ct, true);
+    if (g + 1 < G) {
+      if (g + 2 >= G) wait_vmcnt<0>();
+      else if (first && g > 0) wait_vmcnt<kGemmLoads + kGemmStores + kGemmScaleLoads>();
+      else wait_vmcnt<kGemmLoads>();
+      raw_barrier();
+    }
+    // second half: K-group 1 MFMAs, K-group 0 fragment reads of stage g + 1, channel-row
+    // loads of stage g + 3
+    const bool chn = g + 3 < G;
+    const bool nxt = g + 1 < G;
+    wait_lgkm0();
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      mma_one(G1{}, i, std::false_type{});
+      __builtin_amdgcn_sched_barrier(0);
+      if (i < 8) {
+        if (nxt) frag_one((slot + 1) & (NS - 1), G0{}, i);
+      } else if (chn && (i & 1)) {
+        issue_channels((i - 8) >> 1);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (chn) advance(cc, false);
+
+    if (++s == S) {  // epilogue of tile t
+      s = 0;
+      if (!nxt) raw_barrier();  // the final stage has no barrier of its own
+      int64_t m0;
+      int n0;
+      origin(t, m0, n0);
+      const char* region = smem + RING + (t & 1) * kGemmScale;
+      const float* s_sa = reinterpret_cast<const float*>(region);
+      const float* s_sw = s_sa + kGemmBM;
+      const _Float16* s_bias = reinterpret_cast<const _Float16*>(s_sw + kGemmBN);
+      char* stg = smem + slot * kGemmStage;
+      // read-back role: this thread converts channels cb .. cb + 7 of rows tid / 32 + 8 i
+      const int grp = tid & 31, cb = grp * 8;
+      const f32x4 sw0 = *reinterpret_cast<const f32x4*>(s_sw + cb);
+      const f32x4 sw1 = *reinterpret_cast<const f32x4*>(s_sw + cb + 4);
+      const f16x8 bv = *reinterpret_cast<const f16x8*>(s_bias + cb);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {  // tokens 32 c .. 32 c + 31 = block mb = c % 4 of the waves with wm = c / 4
+        if (wm == (c >> 2)) {
+          const int row = lane & 31;
+#pragma unroll
+          for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const int ch = wn * 32 + nb * 8 + 2 * q + (lane >> 5);  // 4-channel group
+              const i32x4 v = {acc[nb][c & 3][4 * q], acc[nb][c & 3][4 * q + 1], acc[nb][c & 3][4 * q + 2],
+                               acc[nb][c & 3][4 * q + 3]};
+              *reinterpret_cast<i32x4*>(stg + row * 1024 + ((ch ^ row) << 4)) = v;
+            }
+        }
+        wait_lgkm0();
+        raw_barrier();
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int row = (tid >> 5) + 8 * i;
+          const float sar = s_sa[c * 32 + row];
+          const i32x4 lo = *reinterpret_cast<const i32x4*>(stg + row * 1024 + (((2 * grp) ^ row) << 4));
+          const i32x4 hi = *reinterpret_cast<const i32x4*>(stg + row * 1024 + (((2 * grp + 1) ^ row) << 4));
+          f16x8 y;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            y[e] = static_cast<_Float16>((static_cast<float>(lo[e]) * sar) * sw0[e] + static_cast<float>(bv[e]));
+            y[e + 4] = static_cast<_Float16>((static_cast<float>(hi[e]) * sar) * sw1[e] + static_cast<float>(bv[e + 4]));
+          }
+          *reinterpret_cast<f16x8*>(out + (m0 + 32 * c + row) * n + n0 + cb) = y;
+        }
+        wait_lgkm0();
+        raw_barrier();
+      }
+      ++t;
     }
   }
 }
@@ -286,14 +687,44 @@ int hi3d_w8a8_gemm(const int8_t* q, const float* sa, const int8_t* w, const floa
   HI3D_REQUIRE(q && sa && w && sw && out, "null pointer argument");
   HI3D_REQUIRE(((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(out)) & 15) == 0,
                "q, w and out must be 16-byte aligned");
-  constexpr int BM = 128, BN = 256;
-  const int64_t mtiles = ceil_div(m, BM);
-  const int ntiles = static_cast<int>(ceil_div(n, BN));
+  const int64_t mtiles = ceil_div(m, kGemmBM);
+  const int ntiles = static_cast<int>(ceil_div(n, kGemmBN));
   const int64_t blocks = mtiles * ntiles;
   HI3D_REQUIRE(blocks < (int64_t(1) << 31), "problem too large");
-  hipLaunchKernelGGL((w8a8_gemm_kernel<BM, BN>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, q, sa, w,
-                     sw, static_cast<const _Float16*>(bias), m, n, k, static_cast<_Float16*>(out), acc_out, mtiles,
-                     ntiles);
+  const _Float16* b = static_cast<const _Float16*>(bias);
+  _Float16* o = static_cast<_Float16*>(out);
+  // per-lane source offsets within a 256-row tile are 32-bit
+  // The persistent kernel removes the per-tile load latency and overlaps tiles; its stage
+  // loop is slower than the one-tile kernel's, so it pays off for short K loops only
+  // (measured: K = 1024 faster, K = 4096 slower).
+  if (acc_out == nullptr && k % 64 == 0 && k >= 4 * 64 && k < 32 * 64 && m >= kGemmBM && n >= kGemmBN && n % 8 == 0 &&
+      static_cast<int64_t>(kGemmBM) * k < (int64_t(1) << 32) && (reinterpret_cast<uintptr_t>(sa) & 3) == 0 &&
+      (reinterpret_cast<uintptr_t>(sw) & 3) == 0 && (reinterpret_cast<uintptr_t>(bias) & 3) == 0) {
+    const int cus = compute_units();
+    HI3D_REQUIRE(cus > 0, "cannot query the compute unit count");
+    const int64_t workers = blocks < cus ? blocks : cus;
+    hipLaunchKernelGGL(w8a8_gemm_persistent_kernel, dim3(static_cast<unsigned>(workers)), dim3(256), 0, stream, q, sa,
+                       w, sw, b, m, n, k, o, ntiles, blocks);
+    HI3D_LAUNCH_CHECK();
+    return HI3D_OK;
+  }
+  HI3D_REQUIRE(static_cast<int64_t>(kGemmBM) * k < (int64_t(1) << 32), "k too large");
+  const dim3 grid(static_cast<unsigned>(blocks));
+  if (k % 64 == 0) {
+    if (acc_out)
+      hipLaunchKernelGGL((w8a8_gemm_kernel<true, false>), grid, dim3(256), 0, stream, q, sa, w, sw, b, m, n, k, o, acc_out,
+                         ntiles);
+    else
+      hipLaunchKernelGGL((w8a8_gemm_kernel<false, false>), grid, dim3(256), 0, stream, q, sa, w, sw, b, m, n, k, o,
+                         acc_out, ntiles);
+  } else {
+    if (acc_out)
+      hipLaunchKernelGGL((w8a8_gemm_kernel<true, true>), grid, dim3(256), 0, stream, q, sa, w, sw, b, m, n, k, o, acc_out,
+                         ntiles);
+    else
+      hipLaunchKernelGGL((w8a8_gemm_kernel<false, true>), grid, dim3(256), 0, stream, q, sa, w, sw, b, m, n, k, o,
+                         acc_out, ntiles);
+  }
   HI3D_LAUNCH_CHECK();
   return HI3D_OK;
 }

@@ -128,3 +128,31 @@ def test_workload4_shapes_sampled(cuda):
             y = x[rows].astype(np.float32) @ wf.astype(np.float32).T + bias.astype(np.float32)
             err = np.sqrt(np.mean((ref.astype(np.float32) - y) ** 2) / np.mean(y * y))
             assert err < 0.15
+
+
+@pytest.mark.parametrize("m,n,k,with_bias", [(1000, 520, 320, True), (4096, 4096, 1024, True), (300, 264, 1984, False),
+                                             (256, 256, 256, True), (2600, 1032, 1536, True), (1000, 520, 4096, True),
+                                             (600, 300, 2112, False)])
+def test_gemm_full_output_bit_exact(cuda, m, n, k, with_bias):
+    """Every output bit-equal to the oracle on both fused-output paths: the persistent
+    full-tile kernel (m, n >= 256, n % 8 == 0, k % 64 == 0, 256 <= k < 2048) and the
+    one-tile kernel (here k >= 2048), including ragged edges (the persistent kernel moves
+    the last tile of each dimension back so it overlaps its neighbour) and a missing
+    bias; both also equal the accumulator-dump variant's output."""
+    from hi3d_amd import w8a8
+
+    rng = np.random.default_rng(m * 7 + n * 3 + k)
+    q = rng.integers(-127, 128, size=(m, k), dtype=np.int8)
+    w = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+    sa = rng.uniform(1e-3, 1e-2, m).astype(np.float32)
+    sw = rng.uniform(1e-4, 1e-3, n).astype(np.float32)
+    bias = rng.normal(0, 0.02, n).astype(np.float16)
+    dev = [torch.as_tensor(a).to(cuda) for a in (q, sa, w, sw, bias)]
+    bias_t = dev[4] if with_bias else None
+    out = w8a8.gemm(dev[0], dev[1], dev[2], dev[3], bias_t)
+    ref_acc = (q.astype(np.float64) @ w.astype(np.float64).T).astype(np.int64).astype(np.int32)
+    ref = ow8a8.epilogue(ref_acc, sa, sw, bias if with_bias else np.zeros(n, np.float16))
+    got = out.cpu().numpy()
+    assert np.array_equal(got, ref), int((got != ref).sum())
+    out2, _ = w8a8.gemm(dev[0], dev[1], dev[2], dev[3], bias_t, return_acc=True)
+    assert torch.equal(out, out2)
