@@ -34,12 +34,12 @@ PEAK_FP32_TFLOPS = 157.3
 PEAK_INT8_TOPS = 5000.0
 PEAK_HBM_GBS = 8000.0
 
-# Headline kernel (fp16, Cout 128 selects the 256x128 tile) and the counter summary that
+# Headline kernel (fp16, Cout 128: the 384-row ring kernel) and the counter summary that
 # holds its measured HBM traffic per launch: FETCH_SIZE and WRITE_SIZE per dispatch from
 # two rocprofv3 --pmc runs of this script, each scaled by the factor the same counter
 # reads for a plain device copy of known size (`--copy-probe`).
-HEADLINE_KERNEL = "conv_pipe_kernel<_Float16,256,128,4>"
-TRAFFIC_SUMMARY = ROOT / "profiles" / "conv_pipe_subm3_c128_fp16_traffic.txt"
+HEADLINE_KERNEL = "conv_ring_kernel<_Float16>"
+TRAFFIC_SUMMARY = ROOT / "profiles" / "conv_ring_subm3_c128_fp16_traffic.txt"
 
 
 def measured_traffic():

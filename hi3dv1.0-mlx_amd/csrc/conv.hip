@@ -531,6 +531,330 @@ int elem_size(int dtype) {
   }
 }
 
+// ------------------------------------------------------------- ring kernel --
+// Gather convolution for fp16 / bf16 with Cout a multiple of 128, 256..512-byte input
+// rows (4..8 steps of 64 bytes per offset) and at most 27 offsets: the submanifold
+// 3x3x3 layers of 128 and 256 channels.
+//  * Tile: 384 output rows (three plan tiles, union of their offset masks) x 128 output
+//    channels, 4 waves; wave w owns rows 96 w .. 96 w + 95 and all 128 channels as 4 x 3
+//    blocks of 32x32x16 MFMAs with the weights as the first operand.
+//  * Stages: (present offset, 64-byte K step). A stage is 384 gathered rows + 128 weight
+//    rows of 64 bytes (32 KB) in a 4-deep LDS ring, filled by direct-to-LDS 16-byte loads
+//    issued three stages ahead: per wave 6 gathered-row and 2 weight-row loads per stage,
+//    half in the second half of stage s (cursor X) and half in the first half of stage
+//    s + 1 (cursor Y), each load after one MFMA. Rows use the 64-byte swizzled layout of
+//    the int8 GEMM; absent neighbours load from a zero row.
+//  * Gather indices: the tile's 384 indices of an offset reach a two-slot LDS ring by
+//    direct-to-LDS loads (2 per wave; waves 2 and 3 repeat one), issued when cursor X
+//    enters the previous offset; each cursor turns its three rows' indices into source
+//    addresses once per offset.
+//  * One barrier per stage, between its two K-groups. Every wave issues the same loads,
+//    so the vmcnt waits are exact: at the barrier of stage s the operations issued after
+//    stage s + 1's last load are stage s + 2's 8 loads plus 2 index loads when stage
+//    s + 2 begins an offset that has a successor.
+//  * Epilogue: bias + activation in fp32, round to T; each wave stages its own 96 rows
+//    in LDS and writes them as 16-byte row chunks to the tile's output rows, adding the
+//    residual.
+constexpr int kRingBM = 384;
+constexpr int kRingSub = kRingBM / kTileRows;
+constexpr int kRingStageA = kRingBM * 64;
+constexpr int kRingStage = kRingStageA + 128 * 64;
+constexpr int kRingDepth = 4;
+constexpr int kRingLoads = 8;
+constexpr int kRingIdxLoads = 2;
+constexpr int kRingMaxRowBytes = 512;
+
+__device__ __attribute__((aligned(16))) const uint32_t g_zero_row[kRingMaxRowBytes / 4] = {};
+
+__device__ __forceinline__ void lds_dma4(const void* src, char* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(lds_wave_base), 4, 0, 0);
+}
+
+__device__ __forceinline__ int ring_off(int row, int chunk) {
+  return row * 64 + ((chunk ^ (((row >> 1) ^ (row >> 3)) & 3)) << 4);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256, 1) void conv_ring_kernel(ConvArgs a) {
+  constexpr int NS = kRingDepth, BM = kRingBM;
+  constexpr int RING = NS * kRingStage;
+  constexpr int IDX = BM * 4;
+  __shared__ __attribute__((aligned(16))) char smem[RING + 2 * IDX];
+  char* const idx_ring = smem + RING;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t item = xcd_remap(blockIdx.x, static_cast<int64_t>(gridDim.x));
+  const int64_t tile = item / a.ny;
+  const int n0 = static_cast<int>(item - tile * a.ny) * 128;
+  const int kvol = a.kvol;
+  uint32_t mask = 0;
+#pragma unroll
+  for (int h = 0; h < kRingSub; ++h) {
+    const int64_t pt = tile * kRingSub + h;
+    if (pt < a.ntiles) mask |= a.tile_mask[pt];
+  }
+  mask &= (1u << kvol) - 1u;
+  const int rb = a.cin * static_cast<int>(sizeof(T));
+  const int KB = rb >> 6;
+  const int taps = __popc(mask);
+  const int S = taps * KB;
+  const uint64_t n_in = static_cast<uint64_t>(a.n_in);
+
+  // load geometry: load j of this wave covers ring rows (wave + 4 j) * 16 + lane / 4, at
+  // physical chunk lane % 4, i.e. logical chunk `lc` (the swizzle repeats every 64 rows)
+  const int lrow = lane >> 2;
+  const int r0 = wave * 16 + lrow;
+  const int coff = ((lane & 3) ^ (((r0 >> 1) ^ (r0 >> 3)) & 3)) * 16;
+  const char* wrow[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+    wrow[j] = a.weight + static_cast<int64_t>(n0 + r0 + 64 * j) * kvol * rb + coff;
+  const char* const zrow = reinterpret_cast<const char*>(g_zero_row) + coff;
+
+  // gather-index loads of offset k into slot `slot`: load i of 6 covers rows 64 i .. +63
+  // (plan tile i / 2, clamped to the plan); wave w issues loads w and (w + 4, or w again)
+  auto issue_idx = [&](int k, int slot) {
+#pragma unroll
+    for (int u = 0; u < kRingIdxLoads; ++u) {
+      const int i = u == 0 ? wave : (wave + 4 < 6 ? wave + 4 : wave);
+      int64_t pt = tile * kRingSub + (i >> 1);
+      if (pt >= a.ntiles) pt = a.ntiles - 1;
+      const int32_t* src = a.gidx + (pt * kvol + k) * kTileRows + (i & 1) * 64 + lane;
+      lds_dma4(src, idx_ring + slot * IDX + i * 256);
+    }
+  };
+
+  // load cursors over the stage stream (present offsets in increasing order, K steps
+  // inside); X issues gathered loads 0..2 + weight load 0, Y gathered loads 3..5 +
+  // weight load 1
+  struct Cursor {
+    uint32_t rest;  // offsets after the current one
+    int k, kb, ord, slot;
+    const char* src[3];  // gathered-row sources of this cursor's loads at step 0
+  };
+  auto enter_offset = [&](Cursor& c, int jbase) {
+    const int32_t* gi = reinterpret_cast<const int32_t*>(idx_ring + (c.ord & 1) * IDX);
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      const int32_t g = gi[r0 + 64 * (jbase + j)];
+      const bool ok = static_cast<uint64_t>(static_cast<uint32_t>(g)) < n_in;
+      c.src[j] = ok ? a.in + static_cast<int64_t>(g) * rb + coff : zrow;
+    }
+  };
+  auto start = [&](Cursor& c) {
+    c.k = mask ? __builtin_ctz(mask) : 0;
+    c.rest = mask & (mask - 1u);
+    c.kb = 0;
+    c.ord = 0;
+    c.slot = 0;
+  };
+  // advance to the next stage; returns true when it enters a new offset
+  auto advance = [&](Cursor& c) {
+    c.slot = (c.slot + 1) & (NS - 1);
+    if (++c.kb == KB) {
+      c.kb = 0;
+      c.k = c.rest ? __builtin_ctz(c.rest) : c.k;
+      c.rest &= c.rest - 1u;
+      ++c.ord;
+      return true;
+    }
+    return false;
+  };
+  auto issue_x = [&](Cursor& c, int u) {  // u = 0..3
+    char* st = smem + c.slot * kRingStage;
+    if (u < 3) {
+      lds_dma16(c.src[u] + c.kb * 64, st + (wave + 4 * u) * 1024);
+    } else {
+      lds_dma16(wrow[0] + c.k * rb + c.kb * 64, st + kRingStageA + wave * 1024);
+    }
+  };
+  auto issue_y = [&](Cursor& c, int u) {
+    char* st = smem + c.slot * kRingStage;
+    if (u < 3) {
+      lds_dma16(c.src[u] + c.kb * 64, st + (wave + 4 * (3 + u)) * 1024);
+    } else {
+      lds_dma16(wrow[1] + c.k * rb + c.kb * 64, st + kRingStageA + (wave + 4) * 1024);
+    }
+  };
+
+  f32x16 acc[4][3];
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb)
+#pragma unroll
+    for (int mb = 0; mb < 3; ++mb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[nb][mb][v] = 0.0f;
+  u32x4 fa[2][3], fb[2][4];
+  auto frag_one = [&](int slot, auto gc, int i) {  // i: 0..3 weight blocks, 4..6 row blocks
+    constexpr int Gk = decltype(gc)::value;
+    const char* st = smem + slot * kRingStage;
+    const int c = 2 * Gk + (lane >> 5);
+    if (i < 4)
+      fb[Gk][i] = *reinterpret_cast<const u32x4*>(st + kRingStageA + ring_off(i * 32 + (lane & 31), c));
+    else
+      fa[Gk][i - 4] = *reinterpret_cast<const u32x4*>(st + ring_off(wave * 96 + (i - 4) * 32 + (lane & 31), c));
+  };
+  auto mma_one = [&](auto gc, int i) {  // i = nb * 3 + mb
+    constexpr int Gk = decltype(gc)::value;
+    Mfma<T>::run(fb[Gk][i / 3], fa[Gk][i % 3], acc[i / 3][i % 3]);
+  };
+  using G0 = std::integral_constant<int, 0>;
+  using G1 = std::integral_constant<int, 1>;
+
+  if (S > 0) {
+    Cursor cx, cy;
+    start(cx);
+    start(cy);
+    // prologue: offset 0's indices; then stages 0..2 in full
+    issue_idx(cx.k, 0);
+    wait_vmcnt<0>();
+    raw_barrier();
+    enter_offset(cx, 0);
+    enter_offset(cy, 3);
+    if (taps > 1) issue_idx(cx.rest ? __builtin_ctz(cx.rest) : 0, 1);
+#pragma unroll
+    for (int st = 0; st < NS - 1; ++st) {
+      if (st < S) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) issue_x(cx, u);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) issue_y(cy, u);
+        advance(cx);  // offsets span KB >= 4 steps: no offset change inside the prologue
+        advance(cy);
+      }
+    }
+    if (S > 2) wait_vmcnt<2 * kRingLoads>();
+    else if (S > 1) wait_vmcnt<kRingLoads>();
+    else wait_vmcnt<0>();
+    raw_barrier();
+#pragma unroll
+    for (int i = 0; i < 7; ++i) frag_one(0, G0{}, i);
+
+    bool idx_pending = false;  // index loads were issued with stage s + 2's X loads
+    for (int s = 0; s < S; ++s) {
+      const int slot = s & (NS - 1);
+      const bool yload = s >= 1 && s + 2 < S;  // Y part of stage s + 2
+      const bool xload = s + 3 < S;            // X part of stage s + 3
+      const bool next = s + 1 < S;
+      // first half: K-group 0 MFMAs, K-group 1 fragment reads, Y loads of stage s + 2
+      wait_lgkm0();
+      if (yload && cy.kb == 0) {
+        enter_offset(cy, 3);
+        wait_lgkm0();
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < 12; ++i) {
+        mma_one(G0{}, i);
+        __builtin_amdgcn_sched_barrier(0);
+        if (i < 7) {
+          frag_one(slot, G1{}, i);
+        } else if (i < 11 && yload) {
+          issue_y(cy, i - 7);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (yload) advance(cy);
+      if (next) {
+        if (s + 2 >= S) wait_vmcnt<0>();
+        else if (idx_pending) wait_vmcnt<kRingLoads + kRingIdxLoads>();
+        else wait_vmcnt<kRingLoads>();
+        raw_barrier();
+      }
+      // second half: K-group 1 MFMAs, K-group 0 fragment reads of stage s + 1, X loads of
+      // stage s + 3 (entering a new offset first: its sources, and the next offset's indices)
+      idx_pending = false;
+      wait_lgkm0();
+      if (xload && cx.kb == 0) {
+        enter_offset(cx, 0);
+        if (cx.rest) {
+          issue_idx(__builtin_ctz(cx.rest), (cx.ord + 1) & 1);
+          idx_pending = true;
+        }
+        wait_lgkm0();
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < 12; ++i) {
+        mma_one(G1{}, i);
+        __builtin_amdgcn_sched_barrier(0);
+        if (i < 7) {
+          if (next) frag_one((slot + 1) & (NS - 1), G0{}, i);
+        } else if (i < 11 && xload) {
+          issue_x(cx, i - 7);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      if (xload) advance(cx);
+    }
+  }
+
+  // epilogue
+  wait_vmcnt<0>();
+  __syncthreads();
+  const T* bias = static_cast<const T*>(a.bias);
+  char* stg = smem + wave * (96 * 256);
+#pragma unroll
+  for (int nb = 0; nb < 4; ++nb) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int j0 = nb * 32 + 8 * q + 4 * (lane >> 5);
+      float b[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) b[e] = bias != nullptr ? to_f32(bias[n0 + j0 + e]) : 0.0f;
+#pragma unroll
+      for (int mb = 0; mb < 3; ++mb) {
+        const int row = mb * 32 + (lane & 31);
+        T h[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float x = acc[nb][mb][4 * q + e] + b[e];
+          if (a.act == HI3D_ACT_SILU) x = silu(x);
+          h[e] = static_cast<T>(x);
+        }
+        uint2 packed;
+        __builtin_memcpy(&packed, h, 8);
+        *reinterpret_cast<uint2*>(stg + row * 256 + (((j0 >> 3) ^ (row & 15)) << 4) + (j0 & 4) * 2) = packed;
+      }
+    }
+  }
+  wait_lgkm0();
+  const int64_t out_row_bytes = static_cast<int64_t>(a.cout) * sizeof(T);
+#pragma unroll 4
+  for (int i = 0; i < 24; ++i) {
+    const int row = (lane >> 4) + 4 * i;  // 0..95 within this wave's rows
+    const int chunk = lane & 15;
+    const int tr = wave * 96 + row;
+    const int64_t pt = tile * kRingSub + tr / kTileRows;
+    if (pt >= a.ntiles) continue;
+    const int32_t orow = a.rows[pt * kTileRows + (tr % kTileRows)];
+    if (orow < 0) continue;
+    u32x4 v = *reinterpret_cast<const u32x4*>(stg + row * 256 + ((chunk ^ (row & 15)) << 4));
+    const int64_t off = static_cast<int64_t>(orow) * out_row_bytes + static_cast<int64_t>(n0 + chunk * 8) * sizeof(T);
+    if (a.residual != nullptr) {
+      const u32x4 r = *reinterpret_cast<const u32x4*>(a.residual + off);
+      T* pv = reinterpret_cast<T*>(&v);
+      const T* pr = reinterpret_cast<const T*>(&r);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) pv[e] = static_cast<T>(to_f32(pv[e]) + to_f32(pr[e]));
+    }
+    *reinterpret_cast<u32x4*>(a.out + off) = v;
+  }
+}
+
+template <typename T>
+int launch_ring(const ConvArgs& base, hipStream_t stream) {
+  ConvArgs a = base;
+  a.ny = a.cout / 128;
+  const int64_t blocks = ceil_div(a.ntiles, kRingSub) * a.ny;
+  if (blocks == 0) return HI3D_OK;
+  HI3D_REQUIRE(blocks < (int64_t(1) << 31), "too many tiles");
+  hipLaunchKernelGGL((conv_ring_kernel<T>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
+  HI3D_LAUNCH_CHECK();
+  return HI3D_OK;
+}
+
 template <typename T, int BM, int BN, int WGM>
 int launch_pipe(const ConvArgs& base, hipStream_t stream) {
   ConvArgs a = base;
@@ -546,6 +870,11 @@ int launch_pipe(const ConvArgs& base, hipStream_t stream) {
 template <typename T>
 int launch_mfma(const ConvArgs& base, hipStream_t stream) {
   ConvArgs a = base;
+  if constexpr (sizeof(T) == 2) {
+    const int rb = a.cin * static_cast<int>(sizeof(T));
+    if (a.kvol <= kMaxPipelinedKvol && a.cout % 128 == 0 && rb % 64 == 0 && rb >= 4 * 64 && rb <= kRingMaxRowBytes)
+      return launch_ring<T>(a, stream);
+  }
   if (a.kvol <= kMaxPipelinedKvol) {
     if (a.cout <= 64) return launch_pipe<T, 256, 64, 8>(a, stream);
     if (a.cout <= 128) return launch_pipe<T, 256, 128, 4>(a, stream);

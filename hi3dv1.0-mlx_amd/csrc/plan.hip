@@ -19,6 +19,10 @@
 namespace hi3d {
 namespace {
 
+constexpr int kHaloRows = 256;   // output rows per halo tile
+constexpr int kHaloMax = 768;    // halo slots per tile (the last one always absent)
+constexpr int kHaloKvol = 27;    // 3x3x3 submanifold maps only
+
 __device__ __forceinline__ uint64_t spread3(uint32_t v) {
   // spread the low 19 bits of v to every third bit
   uint64_t x = v & 0x7ffffu;
@@ -98,6 +102,87 @@ __global__ __launch_bounds__(kTileRows) void tile_kernel(const int32_t* __restri
     uint32_t m = 0;
     for (int w = 0; w < kTileRows / 64; ++w) m |= wave_mask[w];
     tile_mask[tile] = kvol <= 32 ? m : 0xffffffffu;
+  }
+}
+
+// Halo plans (27-offset submanifold maps): tiles of kHaloRows output rows in Morton
+// order. Per tile: its output rows, the sorted unique input rows its offsets touch (the
+// halo, padded with the absent id n_in; at most kHaloMax - 1 used so that the last slot
+// always reads as a zero row), each (row, offset)'s position in the halo (0xffff when
+// absent) laid out [row][32] (offsets 0..26), and per 32-row block the 27-bit mask of
+// offsets present in any of its rows. A tile whose halo does not fit sets *overflow.
+__global__ __launch_bounds__(kHaloRows) void halo_tile_kernel(const int32_t* __restrict__ table, int64_t n_out,
+                                                              int64_t n_in, const int32_t* __restrict__ order,
+                                                              int key_bits, int32_t* __restrict__ rows,
+                                                              int32_t* __restrict__ halo, int32_t* __restrict__ hcount,
+                                                              uint16_t* __restrict__ loff, uint32_t* __restrict__ bmask,
+                                                              int32_t* __restrict__ overflow) {
+  using Sort = hipcub::BlockRadixSort<uint32_t, kHaloRows, kHaloKvol, uint32_t>;
+  using Scan = hipcub::BlockScan<int, kHaloRows>;
+  __shared__ union {
+    typename Sort::TempStorage sort;
+    typename Scan::TempStorage scan;
+  } tmp;
+  __shared__ uint32_t sorted[kHaloRows * kHaloKvol];
+  const int64_t tile = blockIdx.x;
+  const int r = threadIdx.x;
+  const int64_t p = tile * kHaloRows + r;
+  const int32_t row = p < n_out ? order[p] : -1;
+  rows[p] = row;
+  const uint32_t absent = static_cast<uint32_t>(n_in);
+  uint32_t keys[kHaloKvol], vals[kHaloKvol];
+  uint32_t mask = 0;
+#pragma unroll
+  for (int k = 0; k < kHaloKvol; ++k) {
+    uint32_t v = absent;
+    if (row >= 0) {
+      const uint32_t t = static_cast<uint32_t>(table[static_cast<int64_t>(row) * kHaloKvol + k]);
+      if (t < absent) {
+        v = t;
+        mask |= 1u << k;
+      }
+    }
+    keys[k] = v;
+    vals[k] = static_cast<uint32_t>(r * 32 + k);  // position in the [row][32] layout
+  }
+  // 32-row block masks
+#pragma unroll
+  for (int d = 16; d >= 1; d >>= 1) mask |= __shfl_xor(mask, d, 64);
+  if ((r & 31) == 0) bmask[tile * (kHaloRows / 32) + (r >> 5)] = mask;
+  Sort(tmp.sort).Sort(keys, vals, 0, key_bits);  // blocked: thread r holds sorted ranks r*27 .. r*27+26
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < kHaloKvol; ++i) sorted[r * kHaloKvol + i] = keys[i];
+  __syncthreads();
+  int heads = 0;
+#pragma unroll
+  for (int i = 0; i < kHaloKvol; ++i) {
+    const int pos = r * kHaloKvol + i;
+    const uint32_t prev = pos > 0 ? sorted[pos - 1] : 0xffffffffu;
+    heads += (keys[i] < absent && keys[i] != prev) ? 1 : 0;
+  }
+  int base = 0, total = 0;
+  Scan(tmp.scan).ExclusiveSum(heads, base, total);
+  uint16_t* lt = loff + tile * kHaloRows * 32;
+  int32_t* ht = halo + tile * kHaloMax;
+  int run = base - 1;  // halo position of the current run
+#pragma unroll
+  for (int i = 0; i < kHaloKvol; ++i) {
+    const int pos = r * kHaloKvol + i;
+    const uint32_t prev = pos > 0 ? sorted[pos - 1] : 0xffffffffu;
+    const bool present = keys[i] < absent;
+    if (present && keys[i] != prev) {
+      ++run;
+      if (run < kHaloMax - 1) ht[run] = static_cast<int32_t>(keys[i]);
+    }
+    lt[vals[i]] = (present && run < kHaloMax - 1) ? static_cast<uint16_t>(run) : static_cast<uint16_t>(0xffff);
+  }
+  // unused positions of the [row][32] layout and of the halo
+  for (int k = kHaloKvol; k < 32; ++k) lt[r * 32 + k] = 0xffff;
+  for (int i = total + r; i < kHaloMax; i += kHaloRows) ht[i] = static_cast<int32_t>(absent);
+  if (r == 0) {
+    hcount[tile] = total < kHaloMax - 1 ? total : kHaloMax - 1;
+    if (total > kHaloMax - 1) atomicOr(overflow, 1);
   }
 }
 
@@ -186,5 +271,55 @@ int hi3d_conv_plan(const int32_t* table, int64_t n_out, int32_t kvol, int64_t n_
   HI3D_LAUNCH_CHECK();
   return HI3D_OK;
 }
+
+
+int hi3d_halo_plan_workspace(int64_t n_out, int64_t* bytes) {
+  return hi3d_conv_plan_workspace(n_out, bytes);
+}
+
+int hi3d_halo_plan(const int32_t* table, int64_t n_out, int32_t kvol, int64_t n_in, const int32_t* coords,
+                   void* workspace, int64_t workspace_bytes, int32_t* rows, int32_t* halo, int32_t* hcount,
+                   uint16_t* loff, uint32_t* bmask, int32_t* overflow, void* stream_) {
+  hipStream_t stream = as_stream(stream_);
+  int64_t need = 0;
+  int rc = hi3d_halo_plan_workspace(n_out, &need);
+  if (rc != HI3D_OK) return rc;
+  HI3D_REQUIRE(kvol == kHaloKvol, "halo plans cover 27-offset maps (got %d offsets)", kvol);
+  HI3D_REQUIRE(n_in >= 0 && n_in < (int64_t(1) << 31) - 1, "bad n_in");
+  HI3D_REQUIRE(overflow != nullptr, "null pointer argument");
+  launch_fill(overflow, 1, int32_t(0), stream);
+  if (n_out == 0) return HI3D_OK;
+  HI3D_REQUIRE(table && rows && halo && hcount && loff && bmask && workspace, "null pointer argument");
+  HI3D_REQUIRE(workspace_bytes >= need, "workspace too small");
+  Workspace ws(workspace, workspace_bytes);
+  auto* k0 = ws.take<unsigned long long>(n_out);
+  auto* k1 = ws.take<unsigned long long>(n_out);
+  auto* r0 = ws.take<int32_t>(n_out);
+  auto* r1 = ws.take<int32_t>(n_out);
+  size_t temp_bytes = sort_temp_bytes(n_out);
+  void* temp = ws.take<char>(static_cast<int64_t>(temp_bytes));
+  const unsigned blocks = static_cast<unsigned>(ceil_div(n_out, 256));
+  const int32_t* order = r0;
+  if (coords) {
+    hipLaunchKernelGGL(morton_kernel, dim3(blocks), dim3(256), 0, stream, reinterpret_cast<const int4*>(coords),
+                       n_out, k0, r0);
+    hipcub::DoubleBuffer<unsigned long long> kb(k0, k1);
+    hipcub::DoubleBuffer<int32_t> vb(r0, r1);
+    HI3D_HIP_CHECK(hipcub::DeviceRadixSort::SortPairs(temp, temp_bytes, kb, vb, static_cast<int>(n_out), 0, 64, stream));
+    order = vb.Current();
+  } else {
+    hipLaunchKernelGGL(iota_kernel, dim3(blocks), dim3(256), 0, stream, r0, n_out);
+  }
+  int key_bits = 1;
+  while (key_bits < 32 && (int64_t(1) << key_bits) <= n_in) ++key_bits;
+  const int64_t ntiles = ceil_div(n_out, kHaloRows);
+  hipLaunchKernelGGL(halo_tile_kernel, dim3(static_cast<unsigned>(ntiles)), dim3(kHaloRows), 0, stream, table, n_out,
+                     n_in, order, key_bits, rows, halo, hcount, loff, bmask, overflow);
+  HI3D_LAUNCH_CHECK();
+  return HI3D_OK;
+}
+
+int32_t hi3d_halo_tile_rows(void) { return kHaloRows; }
+int32_t hi3d_halo_capacity(void) { return kHaloMax; }
 
 }  // extern "C"

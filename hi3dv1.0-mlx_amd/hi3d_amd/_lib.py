@@ -47,12 +47,18 @@ _SIGNATURES = {
     "hi3d_gather_conv": [_p, _i64, _i32, _p, _p, _i32, _i32, _p, _p, _p, _i64, _p, _i32, _i32, _p, _p],
     "hi3d_gather_conv_simple": [_p, _i64, _i32, _p, _p, _i32, _i32, _p, _i64, _p, _i32, _i32, _p, _p],
     "hi3d_gather_mean": [_p, _i64, _i32, _p, _i32, _i64, _i32, _i32, _p, _p],
+    "hi3d_halo_tile_rows": [],
+    "hi3d_halo_capacity": [],
+    "hi3d_halo_plan_workspace": [_i64, _p],
+    "hi3d_halo_plan": [_p, _i64, _i32, _i64, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _p],
+    "hi3d_halo_conv": [_p, _i64, _i32, _p, _p, _i32, _p, _p, _p, _i64, _p, _i32, _i32, _p, _p],
     "hi3d_w8a8_quantize": [_p, _i64, _i32, _p, _p, _p, _p],
     "hi3d_w8a8_gemm": [_p, _p, _p, _p, _p, _i64, _i32, _i32, _p, _p, _p],
     "hi3d_layer_norm_modulate": [_p, _i64, _i32, _f32, _p, _p, _p, _p, _p, _p],
     "hi3d_adaln_projection": [_p, _p, _p, _i32, _i32, _i32, _p, _p, _p],
 }
-_RESTYPES = {"hi3d_last_error": ctypes.c_char_p, "hi3d_version": ctypes.c_char_p, "hi3d_conv_tile_rows": _i32}
+_RESTYPES = {"hi3d_last_error": ctypes.c_char_p, "hi3d_version": ctypes.c_char_p, "hi3d_conv_tile_rows": _i32,
+             "hi3d_halo_tile_rows": _i32, "hi3d_halo_capacity": _i32}
 
 _LIB: ctypes.CDLL | None = None
 

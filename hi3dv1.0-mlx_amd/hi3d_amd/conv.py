@@ -19,6 +19,21 @@ from .kmap import ConvPlan
 
 ACTIVATIONS = {None: _lib.ACT_NONE, "none": _lib.ACT_NONE, "silu": _lib.ACT_SILU}
 
+HALO = False
+"""Use the halo convolution (3x3x3 submanifold maps, fp16/bf16, Cout % 128 == 0,
+256..512-byte input rows) whenever the plan has a halo plan. Off by default: on the
+ellipsoid-shell workloads it matches the tile-plan kernel at 128 channels and trails it
+at 256 (a Morton tile computes every offset for every row, 33-47 % of them on absent
+neighbours, and its halo reads conflict in LDS banks)."""
+
+
+def halo_supported(dtype: torch.dtype, cin: int, cout: int, kvol: int) -> bool:
+    """Whether the halo kernel takes this convolution."""
+    if dtype not in (torch.float16, torch.bfloat16) or kvol != 27:
+        return False
+    rb = cin * 2
+    return cout % 128 == 0 and rb % 64 == 0 and 256 <= rb <= 512
+
 
 def _flat_weight(weight: torch.Tensor, kvol: int) -> torch.Tensor:
     cout, cin = int(weight.shape[0]), int(weight.shape[-1])
@@ -67,6 +82,15 @@ def gather_conv(
         raise ValueError("residual must have the output's shape")
     if out is None:
         out = torch.empty((plan.n_out, cout), dtype=dtype, device=device)
+    hp = plan.halo() if HALO and halo_supported(dtype, cin, cout, plan.kvol) else None
+    if hp is not None:
+        _lib.call(
+            "hi3d_halo_conv",
+            _lib.ptr(x), plan.n_in, cin, _lib.ptr(w), _lib.ptr(b), cout, _lib.ptr(hp.rows), _lib.ptr(hp.halo),
+            _lib.ptr(hp.loff), hp.ntiles, _lib.ptr(r), ACTIVATIONS[act], _lib.DTYPES[dtype], _lib.ptr(out),
+            _lib.stream(device),
+        )
+        return out
     _lib.call(
         "hi3d_gather_conv",
         _lib.ptr(x), plan.n_in, cin, _lib.ptr(w), _lib.ptr(b), cout, plan.kvol, _lib.ptr(plan.rows),

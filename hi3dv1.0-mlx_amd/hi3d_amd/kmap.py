@@ -20,8 +20,11 @@ from . import _lib
 
 PLAN_WINDOW_ROWS: int | None = None
 """Rows per mask-sorting window of a convolution plan; ``None`` picks by size
-(one window up to ``PLAN_GLOBAL_ROWS`` rows, else ``PLAN_LARGE_WINDOW`` rows)."""
+(``PLAN_SMALL_WINDOW`` rows up to ``PLAN_GLOBAL_ROWS`` rows, else ``PLAN_LARGE_WINDOW``).
+Measured on the 543k-voxel C128 shells: one global window 0.60 ms, 16k-64k-row windows
+0.53 ms; on the 4.4M-voxel C256 shells 2^18-row windows are best."""
 PLAN_GLOBAL_ROWS = 1 << 21
+PLAN_SMALL_WINDOW = 1 << 16
 PLAN_LARGE_WINDOW = 1 << 18
 
 
@@ -32,9 +35,62 @@ def _as_coords(indices: torch.Tensor) -> torch.Tensor:
 
 
 @dataclass
+class HaloPlan:
+    """Halo plan of a 27-offset submanifold table: tiles of 256 output rows in Morton
+    order, each with the sorted unique input rows its offsets touch (the halo) and every
+    (row, offset)'s position in it; the halo convolution gathers each tile's halo into
+    LDS once per K step."""
+
+    rows: torch.Tensor  # [ntiles * 256] output row per slot, -1 for padding
+    halo: torch.Tensor  # [ntiles, 768] input rows, n_in where unused
+    hcount: torch.Tensor  # [ntiles]
+    loff: torch.Tensor  # [ntiles * 256, 32] int16 halo positions (offsets 0..26), -1 absent
+    bmask: torch.Tensor  # [ntiles * 8] offsets present per 32-row block
+    n_out: int
+    n_in: int
+
+    @property
+    def ntiles(self) -> int:
+        return int(self.hcount.shape[0])
+
+
+def build_halo_plan(table: torch.Tensor, n_in: int, coords: torch.Tensor | None = None) -> HaloPlan | None:
+    """Halo plan of ``table [n_out, 27]``, or None when a tile's halo exceeds the
+    kernel's capacity (callers then use the tile plan)."""
+    device = _lib.require_gpu(table, coords)
+    table = table.to(torch.int32).contiguous()
+    n_out, kvol = int(table.shape[0]), int(table.shape[1])
+    if kvol != 27:
+        raise ValueError(f"halo plans cover 27-offset maps, got {kvol} offsets")
+    if coords is not None:
+        coords = _as_coords(coords)
+        if coords.shape[0] != n_out:
+            raise ValueError("plan coordinates must have one row per output row")
+    L = _lib.lib()
+    t, cap = int(L.hi3d_halo_tile_rows()), int(L.hi3d_halo_capacity())
+    ntiles = (n_out + t - 1) // t
+    rows = torch.empty(ntiles * t, dtype=torch.int32, device=device)
+    halo = torch.empty((ntiles, cap), dtype=torch.int32, device=device)
+    hcount = torch.empty(ntiles, dtype=torch.int32, device=device)
+    loff = torch.empty((ntiles * t, 32), dtype=torch.int16, device=device)
+    bmask = torch.empty(ntiles * (t // 32), dtype=torch.int32, device=device)
+    overflow = torch.empty(1, dtype=torch.int32, device=device)
+    ws = _lib.workspace(_lib.query("hi3d_halo_plan_workspace", n_out), device)
+    _lib.call(
+        "hi3d_halo_plan",
+        _lib.ptr(table), n_out, kvol, int(n_in), _lib.ptr(coords), _lib.ptr(ws), ws.numel(), _lib.ptr(rows),
+        _lib.ptr(halo), _lib.ptr(hcount), _lib.ptr(loff), _lib.ptr(bmask), _lib.ptr(overflow), _lib.stream(device),
+    )
+    if int(overflow.item()) != 0:
+        return None
+    return HaloPlan(rows, halo, hcount, loff, bmask, n_out, int(n_in))
+
+
+@dataclass
 class ConvPlan:
     """Tile plan of one gather table: output row per tile slot, transposed gather
-    indices per tile and offset, and the offsets present in each tile."""
+    indices per tile and offset, and the offsets present in each tile. For 27-offset
+    submanifold tables it also builds (once, on request) the halo plan."""
 
     rows: torch.Tensor
     gidx: torch.Tensor
@@ -43,10 +99,20 @@ class ConvPlan:
     n_in: int
     kvol: int
     table: torch.Tensor
+    coords: torch.Tensor | None = None
+    _halo: list = field(default_factory=list, repr=False)
 
     @property
     def ntiles(self) -> int:
         return int(self.tile_mask.shape[0])
+
+    def halo(self) -> HaloPlan | None:
+        """The halo plan (None when the table is not a 27-offset map over its own rows
+        or a tile's halo does not fit)."""
+        if not self._halo:
+            ok = self.kvol == 27 and self.n_out == self.n_in
+            self._halo.append(build_halo_plan(self.table, self.n_in, self.coords) if ok else None)
+        return self._halo[0]
 
 
 def build_plan(
@@ -63,7 +129,7 @@ def build_plan(
     if window_rows is None:
         window_rows = PLAN_WINDOW_ROWS
     if window_rows is None:
-        window_rows = 0 if n_out <= PLAN_GLOBAL_ROWS else PLAN_LARGE_WINDOW
+        window_rows = PLAN_SMALL_WINDOW if n_out <= PLAN_GLOBAL_ROWS else PLAN_LARGE_WINDOW
     t = int(_lib.lib().hi3d_conv_tile_rows())
     ntiles = (n_out + t - 1) // t
     rows = torch.empty(ntiles * t, dtype=torch.int32, device=device)
@@ -75,7 +141,7 @@ def build_plan(
         _lib.ptr(table), n_out, kvol, int(n_in), _lib.ptr(coords), int(window_rows),
         _lib.ptr(ws), ws.numel(), _lib.ptr(rows), _lib.ptr(gidx), _lib.ptr(tile_mask), _lib.stream(device),
     )
-    return ConvPlan(rows, gidx, tile_mask, n_out, int(n_in), kvol, table)
+    return ConvPlan(rows, gidx, tile_mask, n_out, int(n_in), kvol, table, coords)
 
 
 @dataclass

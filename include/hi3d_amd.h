@@ -178,6 +178,40 @@ int hi3d_gather_mean(const void* in_dev, int64_t n_in, int32_t c, const int32_t*
                      int32_t kvol, int64_t n_out, int32_t extra, int32_t dtype, void* out_dev,
                      void* stream);
 
+/* Output rows per halo tile (256) and halo rows per tile (768, the last always absent). */
+int32_t hi3d_halo_tile_rows(void);
+int32_t hi3d_halo_capacity(void);
+
+/* Workspace bytes of hi3d_halo_plan. */
+int hi3d_halo_plan_workspace(int64_t n_out, int64_t* bytes_host);
+
+/* Halo plan of a 27-offset submanifold table_dev [n_out, 27] (entries >= n_in absent):
+ * output rows in Morton order of coords_dev (NULL = row order), cut into tiles of
+ * hi3d_halo_tile_rows() rows. Per tile: rows_dev [ntiles*256] (output row per slot, -1
+ * past n_out), halo_dev [ntiles, 768] (sorted unique input rows touched by the tile,
+ * n_in where unused), hcount_dev [ntiles], loff_dev [ntiles*256, 32] (halo position of
+ * each (row, offset) for offsets 0..26, 0xffff if absent) and bmask_dev [ntiles*8]
+ * (offsets present per 32-row block). *overflow_dev is set when a tile touches more
+ * than 767 input rows (the plan is then unusable and the tile plan is used instead).
+ * Same role as hi3d_conv_plan: built once per coordinate set and cached with the map
+ * (src/sparc3d/ops/sparse_backend.py:52-56,124-127). */
+int hi3d_halo_plan(const int32_t* table_dev, int64_t n_out, int32_t kvol, int64_t n_in,
+                   const int32_t* coords_dev, void* workspace_dev, int64_t workspace_bytes,
+                   int32_t* rows_dev, int32_t* halo_dev, int32_t* hcount_dev, uint16_t* loff_dev,
+                   uint32_t* bmask_dev, int32_t* overflow_dev, void* stream);
+
+/* The submanifold 3x3x3 convolution of hi3d_gather_conv over a halo plan: each tile's
+ * halo is gathered into LDS once per 64-byte K step and shared by all 27 offsets. fp16
+ * or bf16, cout a multiple of 128, cin*2 in 256..512 in steps of 64, 16-byte aligned
+ * pointers. Same arguments and results as hi3d_gather_conv (fp32 accumulation).
+ * Replaces: subm_conv / SubMConv3d.forward (src/hi3d_mac/torch_backend/sparse_conv.py:
+ * 152-195,244-247) and sparse_conv (src/hi3d_mac/mlx_backend/sparse.py:191-214). */
+int hi3d_halo_conv(const void* in_dev, int64_t n_in, int32_t cin, const void* weight_dev,
+                   const void* bias_dev, int32_t cout, const int32_t* rows_dev,
+                   const int32_t* halo_dev, const uint16_t* loff_dev, int64_t ntiles,
+                   const void* residual_dev, int32_t act, int32_t dtype, void* out_dev,
+                   void* stream);
+
 /* -------------------------------------------------------------------- W8A8 -- */
 
 /* Per-token symmetric int8 quantisation of x_dev [m, k] fp16: with signs_dev [k]

@@ -86,9 +86,103 @@ def test_epilogue_silu_and_residual(cuda):
     assert oconv.rel_err(y.float().cpu().numpy(), ref) <= 1e-2
 
 
+@pytest.mark.parametrize("dtype,cin,cout,density,act,res", [
+    (torch.bfloat16, 128, 256, 0.15, None, False), (torch.float16, 160, 128, 0.15, "silu", True),
+    (torch.float16, 256, 128, 0.3, "silu", False), (torch.float16, 128, 128, 0.004, None, True),
+])
+def test_ring_kernel_variants(cuda, dtype, cin, cout, density, act, res):
+    """The 384-row ring kernel's paths (fp16/bf16, Cout a multiple of 128, 256..512-byte
+    rows): two output-column tiles, five K steps per offset, SiLU and residual in its
+    epilogue, and isolated voxels (tiles whose only offset is the centre)."""
+    from hi3d_amd import conv, kmap
+
+    rng = np.random.default_rng(cin * 7 + cout + int(density * 1000))
+    idx = _rand_indices(rng, 24, density, batch=2)
+    km = kmap.build_kernel_map(torch.as_tensor(idx).to(cuda), [24] * 3, 2)
+    x, w, b = _case(rng, len(idx), cin, cout, dtype)
+    r = torch.as_tensor(rng.standard_normal((len(idx), cout), dtype=np.float32)).to(dtype) if res else None
+    y = conv.gather_conv(x.to(cuda), km.plan(), w.to(cuda), b.to(cuda), act=act,
+                         residual=None if r is None else r.to(cuda))
+    ref = oconv.gather_conv_f64(x.float().numpy(), km.table.cpu().numpy(), w.float().numpy(), b.float().numpy(),
+                                act=act, residual=None if r is None else r.float().numpy())
+    assert oconv.rel_err(y.float().cpu().numpy(), ref) <= GATE[dtype]
+
+
+def test_halo_plan_resolves_the_table(cuda):
+    """Halo plan kernel, exact: every (row, offset) of every tile resolves through its
+    halo position to the table's input row (absent stays absent), each halo is sorted
+    and unique with the unused tail (and always the last slot) absent, each output row
+    appears once, and the 32-row block masks are the OR of the rows' presence."""
+    from hi3d_amd import kmap
+
+    rng = np.random.default_rng(17)
+    idx = _rand_indices(rng, 28, 0.12, batch=2)
+    km = kmap.build_kernel_map(torch.as_tensor(idx).to(cuda), [28] * 3, 2)
+    hp = km.plan().halo()
+    assert hp is not None
+    n = km.n
+    table = km.table.cpu().numpy()
+    rows = hp.rows.cpu().numpy().reshape(hp.ntiles, 256)
+    halo = hp.halo.cpu().numpy()
+    hcount = hp.hcount.cpu().numpy()
+    loff = hp.loff.cpu().numpy().view(np.uint16).reshape(hp.ntiles, 256, 32)
+    bmask = hp.bmask.cpu().numpy().view(np.uint32).reshape(hp.ntiles, 8)
+    assert np.array_equal(np.sort(rows[rows >= 0]), np.arange(n))
+    for t in range(hp.ntiles):
+        h = halo[t]
+        c = int(hcount[t])
+        assert np.all(np.diff(h[:c]) > 0) and np.all(h[c:] == n) and h[-1] == n
+        for r in range(256):
+            o = rows[t, r]
+            want = table[o] if o >= 0 else np.full(27, n)
+            got = np.where(loff[t, r, :27] == 0xFFFF, n, h[np.minimum(loff[t, r, :27], 767)])
+            assert np.array_equal(got, np.where(want < n, want, n)), (t, r)
+            assert np.all(loff[t, r, 27:] == 0xFFFF)
+        for b in range(8):
+            sub = [rows[t, r] for r in range(32 * b, 32 * b + 32) if rows[t, r] >= 0]
+            m = 0
+            for o in sub:
+                for k in range(27):
+                    if table[o, k] < n:
+                        m |= 1 << k
+            assert bmask[t, b] == m
+
+
+@pytest.mark.parametrize("dtype,cin,cout,density,act,res", [
+    (torch.float16, 128, 128, 0.15, None, False), (torch.bfloat16, 256, 256, 0.2, "silu", True),
+    (torch.float16, 192, 384, 0.05, None, True), (torch.float16, 128, 128, 0.004, "silu", False),
+])
+def test_halo_conv_matches_float64_and_tile_plan(cuda, dtype, cin, cout, density, act, res):
+    """The halo convolution (fp16/bf16, Cout % 128 == 0, 256..512-byte rows) against
+    the float64 oracle, and against the tile-plan kernels on the same inputs."""
+    from hi3d_amd import conv, kmap
+
+    rng = np.random.default_rng(cin + cout * 3 + int(density * 1000))
+    idx = _rand_indices(rng, 24, density, batch=2)
+    km = kmap.build_kernel_map(torch.as_tensor(idx).to(cuda), [24] * 3, 2)
+    plan = km.plan()
+    assert plan.halo() is not None
+    x, w, b = _case(rng, len(idx), cin, cout, dtype)
+    r = torch.as_tensor(rng.standard_normal((len(idx), cout), dtype=np.float32)).to(dtype) if res else None
+    args = (x.to(cuda), plan, w.to(cuda), b.to(cuda), act, None if r is None else r.to(cuda))
+    conv.HALO = True
+    try:
+        y = conv.gather_conv(*args)
+    finally:
+        conv.HALO = False
+    ref = oconv.gather_conv_f64(x.float().numpy(), km.table.cpu().numpy(), w.float().numpy(), b.float().numpy(),
+                                act=act, residual=None if r is None else r.float().numpy())
+    assert oconv.rel_err(y.float().cpu().numpy(), ref) <= GATE[dtype]
+    y2 = conv.gather_conv(*args)
+    assert oconv.rel_err(y.float().cpu().numpy(), y2.float().cpu().numpy().astype(np.float64)) <= GATE[dtype]
+
+
 def test_plan_choice_does_not_change_results(cuda):
-    """Rows accumulate the same nonzero K-blocks in the same order under any tiling, so
-    the output is bitwise independent of the plan's window."""
+    """Within a kernel family the output is bitwise independent of the plan: the tile-plan
+    kernels accumulate each row's present (offset, K-block) products in the same order
+    under any tiling or window, and the halo kernel accumulates (K step, offset) in the
+    same order in every halo tile. The two families sum in different orders and agree
+    to the fp16 gate."""
     from hi3d_amd import conv, kmap
 
     rng = np.random.default_rng(6)
@@ -96,10 +190,20 @@ def test_plan_choice_does_not_change_results(cuda):
     km = kmap.build_kernel_map(torch.as_tensor(idx).to(cuda), [32] * 3, 1)
     x, w, b = _case(rng, len(idx), 128, 128, torch.float16)
     x, w, b = x.to(cuda), w.to(cuda), b.to(cuda)
-    outs = [conv.gather_conv(x, kmap.build_plan(km.table, km.n, coords, win), w, b)
-            for coords, win in ((km.indices, 0), (km.indices, 512), (None, 0), (None, 4096))]
+    plans = [kmap.build_plan(km.table, km.n, coords, win)
+             for coords, win in ((km.indices, 0), (km.indices, 512), (None, 0), (None, 4096))]
+    outs = [conv.gather_conv(x, p, w, b) for p in plans]
     for o in outs[1:]:
         assert torch.equal(o, outs[0])
+    conv.HALO = True
+    try:
+        halo_outs = [conv.gather_conv(x, p, w, b) for p in plans if p.halo() is not None]
+    finally:
+        conv.HALO = False
+    assert halo_outs, "the Morton-ordered plan has a halo plan"
+    for o in halo_outs[1:]:
+        assert torch.equal(o, halo_outs[0])
+    assert oconv.rel_err(halo_outs[0].float().cpu().numpy(), outs[0].float().cpu().numpy().astype(np.float64)) <= 1e-2
 
 
 def test_unaligned_channels_use_simple_kernel(cuda):
