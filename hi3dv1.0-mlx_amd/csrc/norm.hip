@@ -10,73 +10,95 @@
 namespace hi3d {
 namespace {
 
-// G lanes per row, CPL 8-element chunks per lane held in registers; fp32 two-pass
-// statistics; y = (x - mean) * inv [* w + b]; h = fp16(y); modulate
-// h = fp16(fp16(h * scale) + shift) (two roundings, no FMA).
-template <int G, int CPL>
+// G lanes per row, CPL 8-element chunks per lane (chunk g + i G), held in registers;
+// fp32 two-pass statistics; y = (x - mean) * inv [* w + b]; h = fp16(y); modulate
+// h = fp16(fp16(h * scale) + shift) (two roundings, no FMA). The per-channel vectors of a
+// lane's chunks are loaded once; blocks stride over groups of 256 / G rows.
+template <int G, int CPL, bool kAffine, bool kModulate>
 __global__ __launch_bounds__(256) void ln_kernel(const _Float16* __restrict__ x, int64_t rows, int c, float eps,
                                                  const float* __restrict__ weight, const float* __restrict__ bias,
                                                  const _Float16* __restrict__ scale,
                                                  const _Float16* __restrict__ shift, _Float16* __restrict__ out) {
 #pragma clang fp contract(off)
-  constexpr int RPB = 256 / G;  // rows per block
+  constexpr int RPB = 256 / G;  // rows per block per step
   const int t = threadIdx.x;
   const int g = t % G;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * RPB + t / G;
-  const bool live = row < rows;
   const int chunks = c >> 3;
-  const _Float16* xr = x + (live ? row : 0) * c;
-  float v[CPL][8];
-  float sum = 0.0f;
+  constexpr bool affine = kAffine, modulate = kModulate;
+  f32x4 wv[kAffine ? CPL : 1][2], bv[kAffine ? CPL : 1][2];
+  f16x8 sv[kModulate ? CPL : 1], hv[kModulate ? CPL : 1];
 #pragma unroll
   for (int i = 0; i < CPL; ++i) {
     const int ch = g + i * G;
-    f16x8 h = {};
-    if (live && ch < chunks) h = *reinterpret_cast<const f16x8*>(xr + ch * 8);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      v[i][e] = static_cast<float>(h[e]);
-      sum += v[i][e];
+    const bool ok = ch < chunks;
+    if constexpr (affine) {
+      if (!ok) continue;
+      wv[i][0] = *reinterpret_cast<const f32x4*>(weight + ch * 8);
+      wv[i][1] = *reinterpret_cast<const f32x4*>(weight + ch * 8 + 4);
+      bv[i][0] = *reinterpret_cast<const f32x4*>(bias + ch * 8);
+      bv[i][1] = *reinterpret_cast<const f32x4*>(bias + ch * 8 + 4);
+    }
+    if constexpr (modulate) {
+      if (!ok) continue;
+      sv[i] = *reinterpret_cast<const f16x8*>(scale + ch * 8);
+      hv[i] = *reinterpret_cast<const f16x8*>(shift + ch * 8);
     }
   }
+  for (int64_t base = static_cast<int64_t>(blockIdx.x) * RPB; base < rows; base += static_cast<int64_t>(gridDim.x) * RPB) {
+    const int64_t row = base + t / G;
+    const bool live = row < rows;
+    const _Float16* xr = x + (live ? row : 0) * c;
+    float v[CPL][8];
+    float sum = 0.0f;
 #pragma unroll
-  for (int d = G / 2; d >= 1; d >>= 1) sum += __shfl_xor(sum, d, 64);
-  const float mean = sum / static_cast<float>(c);
-  float sq = 0.0f;
-#pragma unroll
-  for (int i = 0; i < CPL; ++i) {
-    const int ch = g + i * G;
-    if (ch < chunks) {
+    for (int i = 0; i < CPL; ++i) {
+      const int ch = g + i * G;
+      f16x8 h = {};
+      if (live && ch < chunks) h = *reinterpret_cast<const f16x8*>(xr + ch * 8);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float d = v[i][e] - mean;
-        sq += d * d;
+        v[i][e] = static_cast<float>(h[e]);
+        sum += v[i][e];
       }
     }
-  }
 #pragma unroll
-  for (int d = G / 2; d >= 1; d >>= 1) sq += __shfl_xor(sq, d, 64);
-  const float inv = 1.0f / sqrtf(sq / static_cast<float>(c) + eps);
-  if (!live) return;
-  _Float16* orow = out + row * c;
+    for (int d = G / 2; d >= 1; d >>= 1) sum += __shfl_xor(sum, d, 64);
+    const float mean = sum / static_cast<float>(c);
+    float sq = 0.0f;
 #pragma unroll
-  for (int i = 0; i < CPL; ++i) {
-    const int ch = g + i * G;
-    if (ch >= chunks) continue;
-    f16x8 o;
+    for (int i = 0; i < CPL; ++i) {
+      const int ch = g + i * G;
+      if (ch < chunks) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int col = ch * 8 + e;
-      float y = (v[i][e] - mean) * inv;
-      if (weight != nullptr) y = y * weight[col] + bias[col];
-      _Float16 h = static_cast<_Float16>(y);
-      if (scale != nullptr) {
-        const _Float16 p = static_cast<_Float16>(static_cast<float>(h) * static_cast<float>(scale[col]));
-        h = static_cast<_Float16>(static_cast<float>(p) + static_cast<float>(shift[col]));
+        for (int e = 0; e < 8; ++e) {
+          const float d = v[i][e] - mean;
+          sq += d * d;
+        }
       }
-      o[e] = h;
     }
-    *reinterpret_cast<f16x8*>(orow + ch * 8) = o;
+#pragma unroll
+    for (int d = G / 2; d >= 1; d >>= 1) sq += __shfl_xor(sq, d, 64);
+    const float inv = 1.0f / sqrtf(sq / static_cast<float>(c) + eps);
+    if (!live) continue;
+    _Float16* orow = out + row * c;
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) {
+      const int ch = g + i * G;
+      if (ch >= chunks) continue;
+      f16x8 o;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float y = (v[i][e] - mean) * inv;
+        if constexpr (affine) y = y * wv[i][e >> 2][e & 3] + bv[i][e >> 2][e & 3];
+        _Float16 h = static_cast<_Float16>(y);
+        if constexpr (modulate) {
+          const _Float16 p = static_cast<_Float16>(static_cast<float>(h) * static_cast<float>(sv[i][e]));
+          h = static_cast<_Float16>(static_cast<float>(p) + static_cast<float>(hv[i][e]));
+        }
+        o[e] = h;
+      }
+      *reinterpret_cast<f16x8*>(orow + ch * 8) = o;
+    }
   }
 }
 
@@ -145,8 +167,18 @@ template <int G, int CPL>
 void launch_ln(const _Float16* x, int64_t rows, int c, float eps, const float* w, const float* b, const _Float16* sc,
                const _Float16* sh, _Float16* out, hipStream_t stream) {
   constexpr int RPB = 256 / G;
-  hipLaunchKernelGGL((ln_kernel<G, CPL>), dim3(static_cast<unsigned>(ceil_div(rows, RPB))), dim3(256), 0, stream, x,
-                     rows, c, eps, w, b, sc, sh, out);
+  const int64_t groups = ceil_div(rows, RPB);
+  const int cus = compute_units();
+  const int64_t cap = static_cast<int64_t>(cus > 0 ? cus : 256) * 16;  // a few strides per block
+  const dim3 grid(static_cast<unsigned>(groups < cap ? groups : cap));
+  if (w != nullptr && sc != nullptr)
+    hipLaunchKernelGGL((ln_kernel<G, CPL, true, true>), grid, dim3(256), 0, stream, x, rows, c, eps, w, b, sc, sh, out);
+  else if (w != nullptr)
+    hipLaunchKernelGGL((ln_kernel<G, CPL, true, false>), grid, dim3(256), 0, stream, x, rows, c, eps, w, b, sc, sh, out);
+  else if (sc != nullptr)
+    hipLaunchKernelGGL((ln_kernel<G, CPL, false, true>), grid, dim3(256), 0, stream, x, rows, c, eps, w, b, sc, sh, out);
+  else
+    hipLaunchKernelGGL((ln_kernel<G, CPL, false, false>), grid, dim3(256), 0, stream, x, rows, c, eps, w, b, sc, sh, out);
 }
 
 }  // namespace
@@ -168,14 +200,17 @@ int hi3d_layer_norm_modulate(const void* x, int64_t rows, int32_t c, float eps, 
   const auto* sc = static_cast<const _Float16*>(scale);
   const auto* sh = static_cast<const _Float16*>(shift);
   auto* o = static_cast<_Float16*>(out);
-  const bool aligned = ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(out)) & 15) == 0;
+  const uintptr_t vec = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(out) |
+                        reinterpret_cast<uintptr_t>(weight) | reinterpret_cast<uintptr_t>(bias) |
+                        reinterpret_cast<uintptr_t>(scale) | reinterpret_cast<uintptr_t>(shift);
   const int chunks = c / 8;
-  if (c % 8 == 0 && aligned && chunks <= 64 * 8) {
-    if (chunks <= 8) launch_ln<8, 1>(xh, rows, c, eps, weight, bias, sc, sh, o, stream);
-    else if (chunks <= 16) launch_ln<16, 1>(xh, rows, c, eps, weight, bias, sc, sh, o, stream);
-    else if (chunks <= 32) launch_ln<32, 1>(xh, rows, c, eps, weight, bias, sc, sh, o, stream);
-    else if (chunks <= 64) launch_ln<64, 1>(xh, rows, c, eps, weight, bias, sc, sh, o, stream);
-    else if (chunks <= 128) launch_ln<64, 2>(xh, rows, c, eps, weight, bias, sc, sh, o, stream);
+  if (c % 8 == 0 && (vec & 15) == 0 && chunks <= 64 * 8) {
+    if (chunks <= 4) launch_ln<4, 1>(xh, rows, c, eps, weight, bias, sc, sh, o, stream);
+    else if (chunks <= 8) launch_ln<8, 1>(xh, rows, c, eps, weight, bias, sc, sh, o, stream);
+    else if (chunks <= 16) launch_ln<8, 2>(xh, rows, c, eps, weight, bias, sc, sh, o, stream);
+    else if (chunks <= 32) launch_ln<8, 4>(xh, rows, c, eps, weight, bias, sc, sh, o, stream);
+    else if (chunks <= 64) launch_ln<16, 4>(xh, rows, c, eps, weight, bias, sc, sh, o, stream);
+    else if (chunks <= 128) launch_ln<32, 4>(xh, rows, c, eps, weight, bias, sc, sh, o, stream);
     else if (chunks <= 256) launch_ln<64, 4>(xh, rows, c, eps, weight, bias, sc, sh, o, stream);
     else launch_ln<64, 8>(xh, rows, c, eps, weight, bias, sc, sh, o, stream);
   } else {
