@@ -535,30 +535,41 @@ int elem_size(int dtype) {
 // Gather convolution for fp16 / bf16 with Cout a multiple of 128, 256..512-byte input
 // rows (4..8 steps of 64 bytes per offset) and at most 27 offsets: the submanifold
 // 3x3x3 layers of 128 and 256 channels.
-//  * Tile: 384 output rows (three plan tiles, union of their offset masks) x 128 output
-//    channels, 4 waves; wave w owns rows 96 w .. 96 w + 95 and all 128 channels as 4 x 3
-//    blocks of 32x32x16 MFMAs with the weights as the first operand.
-//  * Stages: (present offset, 64-byte K step). A stage is 384 gathered rows + 128 weight
+//  * Tile: BM output rows (the union of BM / 128 plan tiles' offset masks) x BN output
+//    channels, 4 waves; wave w owns rows w BM / 4 .. and all BN channels as blocks of
+//    32x32x16 MFMAs with the weights as the first operand. BN = 128 takes BM = 384
+//    (4 x 3 blocks per wave), BN = 256 (Cout a multiple of 256) takes BM = 256 (8 x 2
+//    blocks per wave, half the gathered bytes per flop of the 128-channel tile).
+//  * Stages: (present offset, 64-byte K step). A stage is BM gathered rows + BN weight
 //    rows of 64 bytes (32 KB) in a 4-deep LDS ring, filled by direct-to-LDS 16-byte loads
-//    issued three stages ahead: per wave 6 gathered-row and 2 weight-row loads per stage,
-//    half in the second half of stage s (cursor X) and half in the first half of stage
-//    s + 1 (cursor Y), each load after one MFMA. Rows use the 64-byte swizzled layout of
-//    the int8 GEMM; absent neighbours load from a zero row.
-//  * Gather indices: the tile's 384 indices of an offset reach a two-slot LDS ring by
-//    direct-to-LDS loads (2 per wave; waves 2 and 3 repeat one), issued when cursor X
-//    enters the previous offset; each cursor turns its three rows' indices into source
-//    addresses once per offset.
+//    issued three stages ahead: per wave 8 loads per stage (BM / 64 gathered-row and
+//    BN / 64 weight-row loads), half in the second half of stage s (cursor X) and half in
+//    the first half of stage s + 1 (cursor Y), each load after one MFMA. Rows use the
+//    64-byte swizzled layout of the int8 GEMM; absent neighbours load from a zero row.
+//  * Gather indices: the tile's BM indices of an offset reach a two-slot LDS ring by
+//    direct-to-LDS loads (2 per wave, some repeated), issued when cursor X enters the
+//    previous offset; each cursor turns its rows' indices into source addresses once per
+//    offset.
 //  * One barrier per stage, between its two K-groups. Every wave issues the same loads,
 //    so the vmcnt waits are exact: at the barrier of stage s the operations issued after
 //    stage s + 1's last load are stage s + 2's 8 loads plus 2 index loads when stage
 //    s + 2 begins an offset that has a successor.
-//  * Epilogue: bias + activation in fp32, round to T; each wave stages its own 96 rows
-//    in LDS and writes them as 16-byte row chunks to the tile's output rows, adding the
+//  * Epilogue: bias + activation in fp32, round to T; each wave stages its own rows in
+//    LDS and writes them as 16-byte row chunks to the tile's output rows, adding the
 //    residual.
-constexpr int kRingBM = 384;
-constexpr int kRingSub = kRingBM / kTileRows;
-constexpr int kRingStageA = kRingBM * 64;
-constexpr int kRingStage = kRingStageA + 128 * 64;
+template <int BN>
+struct RingShape {
+  static constexpr int BM = BN == 128 ? 384 : 256;
+  static constexpr int SUB = BM / kTileRows;  // plan tiles per tile
+  static constexpr int MB = BM / 4 / 32;      // row blocks per wave
+  static constexpr int NB = BN / 32;          // channel blocks per wave
+  static constexpr int AX = BM / 128;         // gathered-row loads per cursor (X or Y)
+  static constexpr int BX = BN / 128;         // weight-row loads per cursor
+  static constexpr int STAGE_A = BM * 64;
+  static constexpr int STAGE = STAGE_A + BN * 64;
+  static constexpr int IDX = BM * 4;
+  static constexpr int NIDX = BM / 64;        // gather-index loads of one offset
+};
 constexpr int kRingDepth = 4;
 constexpr int kRingLoads = 8;
 constexpr int kRingIdxLoads = 2;
@@ -574,11 +585,13 @@ __device__ __forceinline__ int ring_off(int row, int chunk) {
   return row * 64 + ((chunk ^ (((row >> 1) ^ (row >> 3)) & 3)) << 4);
 }
 
-template <typename T>
+template <typename T, int BN>
 __global__ __launch_bounds__(256, 1) void conv_ring_kernel(ConvArgs a) {
-  constexpr int NS = kRingDepth, BM = kRingBM;
+  using Sh = RingShape<BN>;
+  constexpr int NS = kRingDepth, BM = Sh::BM, MB = Sh::MB, NB = Sh::NB, AX = Sh::AX, BX = Sh::BX;
+  constexpr int kRingSub = Sh::SUB, kRingStageA = Sh::STAGE_A, kRingStage = Sh::STAGE, IDX = Sh::IDX;
   constexpr int RING = NS * kRingStage;
-  constexpr int IDX = BM * 4;
+  static_assert(AX + BX == 4 && kRingStage == 32768, "stage shape");
   __shared__ __attribute__((aligned(16))) char smem[RING + 2 * IDX];
   char* const idx_ring = smem + RING;
 
@@ -586,7 +599,7 @@ __global__ __launch_bounds__(256, 1) void conv_ring_kernel(ConvArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t item = xcd_remap(blockIdx.x, static_cast<int64_t>(gridDim.x));
   const int64_t tile = item / a.ny;
-  const int n0 = static_cast<int>(item - tile * a.ny) * 128;
+  const int n0 = static_cast<int>(item - tile * a.ny) * BN;
   const int kvol = a.kvol;
   uint32_t mask = 0;
 #pragma unroll
@@ -606,18 +619,18 @@ __global__ __launch_bounds__(256, 1) void conv_ring_kernel(ConvArgs a) {
   const int lrow = lane >> 2;
   const int r0 = wave * 16 + lrow;
   const int coff = ((lane & 3) ^ (((r0 >> 1) ^ (r0 >> 3)) & 3)) * 16;
-  const char* wrow[2];
+  const char* wrow[2 * BX];
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
+  for (int j = 0; j < 2 * BX; ++j)
     wrow[j] = a.weight + static_cast<int64_t>(n0 + r0 + 64 * j) * kvol * rb + coff;
   const char* const zrow = reinterpret_cast<const char*>(g_zero_row) + coff;
 
-  // gather-index loads of offset k into slot `slot`: load i of 6 covers rows 64 i .. +63
+  // gather-index loads of offset k into slot `slot`: load i of NIDX covers rows 64 i .. +63
   // (plan tile i / 2, clamped to the plan); wave w issues loads w and (w + 4, or w again)
   auto issue_idx = [&](int k, int slot) {
 #pragma unroll
     for (int u = 0; u < kRingIdxLoads; ++u) {
-      const int i = u == 0 ? wave : (wave + 4 < 6 ? wave + 4 : wave);
+      const int i = u == 0 ? wave : (wave + 4 < Sh::NIDX ? wave + 4 : wave);
       int64_t pt = tile * kRingSub + (i >> 1);
       if (pt >= a.ntiles) pt = a.ntiles - 1;
       const int32_t* src = a.gidx + (pt * kvol + k) * kTileRows + (i & 1) * 64 + lane;
@@ -626,17 +639,16 @@ __global__ __launch_bounds__(256, 1) void conv_ring_kernel(ConvArgs a) {
   };
 
   // load cursors over the stage stream (present offsets in increasing order, K steps
-  // inside); X issues gathered loads 0..2 + weight load 0, Y gathered loads 3..5 +
-  // weight load 1
+  // inside); X issues gathered loads 0..AX-1 + weight loads 0..BX-1, Y the rest
   struct Cursor {
     uint32_t rest;  // offsets after the current one
     int k, kb, ord, slot;
-    const char* src[3];  // gathered-row sources of this cursor's loads at step 0
+    const char* src[AX];  // gathered-row sources of this cursor's loads at step 0
   };
   auto enter_offset = [&](Cursor& c, int jbase) {
     const int32_t* gi = reinterpret_cast<const int32_t*>(idx_ring + (c.ord & 1) * IDX);
 #pragma unroll
-    for (int j = 0; j < 3; ++j) {
+    for (int j = 0; j < AX; ++j) {
       const int32_t g = gi[r0 + 64 * (jbase + j)];
       const bool ok = static_cast<uint64_t>(static_cast<uint32_t>(g)) < n_in;
       c.src[j] = ok ? a.in + static_cast<int64_t>(g) * rb + coff : zrow;
@@ -663,41 +675,44 @@ __global__ __launch_bounds__(256, 1) void conv_ring_kernel(ConvArgs a) {
   };
   auto issue_x = [&](Cursor& c, int u) {  // u = 0..3
     char* st = smem + c.slot * kRingStage;
-    if (u < 3) {
+    if (u < AX) {
       lds_dma16(c.src[u] + c.kb * 64, st + (wave + 4 * u) * 1024);
     } else {
-      lds_dma16(wrow[0] + c.k * rb + c.kb * 64, st + kRingStageA + wave * 1024);
+      lds_dma16(wrow[u - AX] + c.k * rb + c.kb * 64, st + kRingStageA + (wave + 4 * (u - AX)) * 1024);
     }
   };
   auto issue_y = [&](Cursor& c, int u) {
     char* st = smem + c.slot * kRingStage;
-    if (u < 3) {
-      lds_dma16(c.src[u] + c.kb * 64, st + (wave + 4 * (3 + u)) * 1024);
+    if (u < AX) {
+      lds_dma16(c.src[u] + c.kb * 64, st + (wave + 4 * (AX + u)) * 1024);
     } else {
-      lds_dma16(wrow[1] + c.k * rb + c.kb * 64, st + kRingStageA + (wave + 4) * 1024);
+      lds_dma16(wrow[BX + u - AX] + c.k * rb + c.kb * 64, st + kRingStageA + (wave + 4 * (BX + u - AX)) * 1024);
     }
   };
 
-  f32x16 acc[4][3];
+  f32x16 acc[NB][MB];
 #pragma unroll
-  for (int nb = 0; nb < 4; ++nb)
+  for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-    for (int mb = 0; mb < 3; ++mb)
+    for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[nb][mb][v] = 0.0f;
-  u32x4 fa[2][3], fb[2][4];
-  auto frag_one = [&](int slot, auto gc, int i) {  // i: 0..3 weight blocks, 4..6 row blocks
+  constexpr int NF = NB + MB;        // fragment reads per K-group
+  constexpr int NM = NB * MB;        // MFMAs per K-group
+  u32x4 fa[2][MB], fb[2][NB];
+  auto frag_one = [&](int slot, auto gc, int i) {  // i: 0..NB-1 weight blocks, then row blocks
     constexpr int Gk = decltype(gc)::value;
     const char* st = smem + slot * kRingStage;
     const int c = 2 * Gk + (lane >> 5);
-    if (i < 4)
+    if (i < NB)
       fb[Gk][i] = *reinterpret_cast<const u32x4*>(st + kRingStageA + ring_off(i * 32 + (lane & 31), c));
     else
-      fa[Gk][i - 4] = *reinterpret_cast<const u32x4*>(st + ring_off(wave * 96 + (i - 4) * 32 + (lane & 31), c));
+      fa[Gk][i - NB] =
+          *reinterpret_cast<const u32x4*>(st + ring_off(wave * (MB * 32) + (i - NB) * 32 + (lane & 31), c));
   };
-  auto mma_one = [&](auto gc, int i) {  // i = nb * 3 + mb
+  auto mma_one = [&](auto gc, int i) {  // i = nb * MB + mb
     constexpr int Gk = decltype(gc)::value;
-    Mfma<T>::run(fb[Gk][i / 3], fa[Gk][i % 3], acc[i / 3][i % 3]);
+    Mfma<T>::run(fb[Gk][i / MB], fa[Gk][i % MB], acc[i / MB][i % MB]);
   };
   using G0 = std::integral_constant<int, 0>;
   using G1 = std::integral_constant<int, 1>;
@@ -711,7 +726,7 @@ __global__ __launch_bounds__(256, 1) void conv_ring_kernel(ConvArgs a) {
     wait_vmcnt<0>();
     raw_barrier();
     enter_offset(cx, 0);
-    enter_offset(cy, 3);
+    enter_offset(cy, AX);
     if (taps > 1) issue_idx(cx.rest ? __builtin_ctz(cx.rest) : 0, 1);
 #pragma unroll
     for (int st = 0; st < NS - 1; ++st) {
@@ -729,7 +744,7 @@ __global__ __launch_bounds__(256, 1) void conv_ring_kernel(ConvArgs a) {
     else wait_vmcnt<0>();
     raw_barrier();
 #pragma unroll
-    for (int i = 0; i < 7; ++i) frag_one(0, G0{}, i);
+    for (int i = 0; i < NF; ++i) frag_one(0, G0{}, i);
 
     bool idx_pending = false;  // index loads were issued with stage s + 2's X loads
     for (int s = 0; s < S; ++s) {
@@ -740,18 +755,18 @@ __global__ __launch_bounds__(256, 1) void conv_ring_kernel(ConvArgs a) {
       // first half: K-group 0 MFMAs, K-group 1 fragment reads, Y loads of stage s + 2
       wait_lgkm0();
       if (yload && cy.kb == 0) {
-        enter_offset(cy, 3);
+        enter_offset(cy, AX);
         wait_lgkm0();
       }
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int i = 0; i < 12; ++i) {
+      for (int i = 0; i < NM; ++i) {
         mma_one(G0{}, i);
         __builtin_amdgcn_sched_barrier(0);
-        if (i < 7) {
+        if (i < NF) {
           frag_one(slot, G1{}, i);
-        } else if (i < 11 && yload) {
-          issue_y(cy, i - 7);
+        } else if (i < NF + 4 && yload) {
+          issue_y(cy, i - NF);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -776,13 +791,13 @@ __global__ __launch_bounds__(256, 1) void conv_ring_kernel(ConvArgs a) {
       }
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int i = 0; i < 12; ++i) {
+      for (int i = 0; i < NM; ++i) {
         mma_one(G1{}, i);
         __builtin_amdgcn_sched_barrier(0);
-        if (i < 7) {
+        if (i < NF) {
           if (next) frag_one((slot + 1) & (NS - 1), G0{}, i);
-        } else if (i < 11 && xload) {
-          issue_x(cx, i - 7);
+        } else if (i < NF + 4 && xload) {
+          issue_x(cx, i - NF);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -794,9 +809,11 @@ __global__ __launch_bounds__(256, 1) void conv_ring_kernel(ConvArgs a) {
   wait_vmcnt<0>();
   __syncthreads();
   const T* bias = static_cast<const T*>(a.bias);
-  char* stg = smem + wave * (96 * 256);
+  constexpr int ROWB = BN * 2;     // staged row bytes
+  constexpr int CPR = BN / 8;      // 16-byte chunks per staged row
+  char* stg = smem + wave * (MB * 32 * ROWB);
 #pragma unroll
-  for (int nb = 0; nb < 4; ++nb) {
+  for (int nb = 0; nb < NB; ++nb) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const int j0 = nb * 32 + 8 * q + 4 * (lane >> 5);
@@ -804,7 +821,7 @@ __global__ __launch_bounds__(256, 1) void conv_ring_kernel(ConvArgs a) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) b[e] = bias != nullptr ? to_f32(bias[n0 + j0 + e]) : 0.0f;
 #pragma unroll
-      for (int mb = 0; mb < 3; ++mb) {
+      for (int mb = 0; mb < MB; ++mb) {
         const int row = mb * 32 + (lane & 31);
         T h[4];
 #pragma unroll
@@ -815,22 +832,22 @@ __global__ __launch_bounds__(256, 1) void conv_ring_kernel(ConvArgs a) {
         }
         uint2 packed;
         __builtin_memcpy(&packed, h, 8);
-        *reinterpret_cast<uint2*>(stg + row * 256 + (((j0 >> 3) ^ (row & 15)) << 4) + (j0 & 4) * 2) = packed;
+        *reinterpret_cast<uint2*>(stg + row * ROWB + (((j0 >> 3) ^ (row & (CPR - 1))) << 4) + (j0 & 4) * 2) = packed;
       }
     }
   }
   wait_lgkm0();
   const int64_t out_row_bytes = static_cast<int64_t>(a.cout) * sizeof(T);
 #pragma unroll 4
-  for (int i = 0; i < 24; ++i) {
-    const int row = (lane >> 4) + 4 * i;  // 0..95 within this wave's rows
-    const int chunk = lane & 15;
-    const int tr = wave * 96 + row;
+  for (int i = 0; i < MB * 32 * CPR / 64; ++i) {
+    const int row = lane / CPR + (64 / CPR) * i;  // within this wave's MB * 32 rows
+    const int chunk = lane % CPR;
+    const int tr = wave * (MB * 32) + row;
     const int64_t pt = tile * kRingSub + tr / kTileRows;
     if (pt >= a.ntiles) continue;
     const int32_t orow = a.rows[pt * kTileRows + (tr % kTileRows)];
     if (orow < 0) continue;
-    u32x4 v = *reinterpret_cast<const u32x4*>(stg + row * 256 + ((chunk ^ (row & 15)) << 4));
+    u32x4 v = *reinterpret_cast<const u32x4*>(stg + row * ROWB + ((chunk ^ (row & (CPR - 1))) << 4));
     const int64_t off = static_cast<int64_t>(orow) * out_row_bytes + static_cast<int64_t>(n0 + chunk * 8) * sizeof(T);
     if (a.residual != nullptr) {
       const u32x4 r = *reinterpret_cast<const u32x4*>(a.residual + off);
@@ -843,14 +860,14 @@ __global__ __launch_bounds__(256, 1) void conv_ring_kernel(ConvArgs a) {
   }
 }
 
-template <typename T>
+template <typename T, int BN>
 int launch_ring(const ConvArgs& base, hipStream_t stream) {
   ConvArgs a = base;
-  a.ny = a.cout / 128;
-  const int64_t blocks = ceil_div(a.ntiles, kRingSub) * a.ny;
+  a.ny = a.cout / BN;
+  const int64_t blocks = ceil_div(a.ntiles, RingShape<BN>::SUB) * a.ny;
   if (blocks == 0) return HI3D_OK;
   HI3D_REQUIRE(blocks < (int64_t(1) << 31), "too many tiles");
-  hipLaunchKernelGGL((conv_ring_kernel<T>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
+  hipLaunchKernelGGL((conv_ring_kernel<T, BN>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
   HI3D_LAUNCH_CHECK();
   return HI3D_OK;
 }
@@ -873,7 +890,7 @@ int launch_mfma(const ConvArgs& base, hipStream_t stream) {
   if constexpr (sizeof(T) == 2) {
     const int rb = a.cin * static_cast<int>(sizeof(T));
     if (a.kvol <= kMaxPipelinedKvol && a.cout % 128 == 0 && rb % 64 == 0 && rb >= 4 * 64 && rb <= kRingMaxRowBytes)
-      return launch_ring<T>(a, stream);
+      return a.cout % 256 == 0 ? launch_ring<T, 256>(a, stream) : launch_ring<T, 128>(a, stream);
   }
   if (a.kvol <= kMaxPipelinedKvol) {
     if (a.cout <= 64) return launch_pipe<T, 256, 64, 8>(a, stream);

@@ -89,10 +89,13 @@ def test_epilogue_silu_and_residual(cuda):
 @pytest.mark.parametrize("dtype,cin,cout,density,act,res", [
     (torch.bfloat16, 128, 256, 0.15, None, False), (torch.float16, 160, 128, 0.15, "silu", True),
     (torch.float16, 256, 128, 0.3, "silu", False), (torch.float16, 128, 128, 0.004, None, True),
+    (torch.float16, 256, 256, 0.2, "silu", True), (torch.bfloat16, 192, 512, 0.1, None, True),
+    (torch.float16, 256, 256, 0.004, None, False),
 ])
 def test_ring_kernel_variants(cuda, dtype, cin, cout, density, act, res):
-    """The 384-row ring kernel's paths (fp16/bf16, Cout a multiple of 128, 256..512-byte
-    rows): two output-column tiles, five K steps per offset, SiLU and residual in its
+    """The ring kernel's paths (fp16/bf16, Cout a multiple of 128, 256..512-byte rows):
+    384 x 128 tiles (Cout 128) and 256 x 256 tiles (Cout a multiple of 256), several
+    output-column tiles, five and six K steps per offset, SiLU and residual in the
     epilogue, and isolated voxels (tiles whose only offset is the centre)."""
     from hi3d_amd import conv, kmap
 
