@@ -15,6 +15,7 @@
 // stage s computes). The epilogue adds bias, applies SiLU, stages the tile through LDS
 // and writes every output row exactly once with 16-byte stores (plus the residual).
 #include <type_traits>
+#include <utility>
 
 #include "common.h"
 #include "conv_tile.h"
@@ -536,43 +537,47 @@ int elem_size(int dtype) {
 // rows (4..8 steps of 64 bytes per offset) and at most 27 offsets: the submanifold
 // 3x3x3 layers of 128 and 256 channels.
 //  * Tile: BM output rows (the union of BM / 128 plan tiles' offset masks) x BN output
-//    channels, 4 waves; wave w owns rows w BM / 4 .. and all BN channels as blocks of
-//    32x32x16 MFMAs with the weights as the first operand. BN = 128 takes BM = 384
-//    (4 x 3 blocks per wave), BN = 256 (Cout a multiple of 256) takes BM = 256 (8 x 2
-//    blocks per wave, half the gathered bytes per flop of the 128-channel tile).
+//    channels. NW waves (two per SIMD at NW = 8) form a 4 x NW / 4 grid; each owns
+//    BM / 4 rows x 4 BN / NW channels as blocks of 32x32x16 MFMAs with the weights as the
+//    first operand. BN = 128 takes BM = 384; BN = 256 (Cout a multiple of 256) takes
+//    BM = 256, half the gathered bytes per flop of the 128-channel tile.
 //  * Stages: (present offset, 64-byte K step). A stage is BM gathered rows + BN weight
 //    rows of 64 bytes (32 KB) in a 4-deep LDS ring, filled by direct-to-LDS 16-byte loads
-//    issued three stages ahead: per wave 8 loads per stage (BM / 64 gathered-row and
-//    BN / 64 weight-row loads), half in the second half of stage s (cursor X) and half in
-//    the first half of stage s + 1 (cursor Y), each load after one MFMA. Rows use the
-//    64-byte swizzled layout of the int8 GEMM; absent neighbours load from a zero row.
+//    issued three stages ahead: per wave L = (BM + BN) / (16 NW) loads per stage, half in
+//    the second half of stage s (cursor X) and half in the first half of stage s + 1
+//    (cursor Y), each after one MFMA. Rows use the 64-byte swizzled layout of the int8
+//    GEMM; absent neighbours load from a zero row.
 //  * Gather indices: the tile's BM indices of an offset reach a two-slot LDS ring by
-//    direct-to-LDS loads (2 per wave, some repeated), issued when cursor X enters the
-//    previous offset; each cursor turns its rows' indices into source addresses once per
-//    offset.
+//    direct-to-LDS loads (some repeated so that every wave issues the same number),
+//    issued when cursor X enters the previous offset; each cursor turns its rows'
+//    indices into source addresses once per offset. The tile's output rows arrive the
+//    same way at the start.
 //  * One barrier per stage, between its two K-groups. Every wave issues the same loads,
 //    so the vmcnt waits are exact: at the barrier of stage s the operations issued after
-//    stage s + 1's last load are stage s + 2's 8 loads plus 2 index loads when stage
+//    stage s + 1's last load are stage s + 2's L loads plus the index loads when stage
 //    s + 2 begins an offset that has a successor.
-//  * Epilogue: bias + activation in fp32, round to T; each wave stages its own rows in
-//    LDS and writes them as 16-byte row chunks to the tile's output rows, adding the
+//  * Epilogue: bias + activation in fp32, round to T; each wave stages its own block in
+//    LDS and writes it as 16-byte row chunks to the tile's output rows, adding the
 //    residual.
-template <int BN>
+// Tile shapes: BN = 128 takes BM = 384 rows, BN = 256 takes 256 rows (32 KB stages);
+// NW waves form a 4 x NW / 4 grid over rows x channels.
+template <int BN, int NW>
 struct RingShape {
   static constexpr int BM = BN == 128 ? 384 : 256;
   static constexpr int SUB = BM / kTileRows;  // plan tiles per tile
-  static constexpr int MB = BM / 4 / 32;      // row blocks per wave
-  static constexpr int NB = BN / 32;          // channel blocks per wave
-  static constexpr int AX = BM / 128;         // gathered-row loads per cursor (X or Y)
-  static constexpr int BX = BN / 128;         // weight-row loads per cursor
+  static constexpr int WM = 4, WN = NW / 4;   // wave grid
+  static constexpr int MB = BM / WM / 32;     // row blocks per wave
+  static constexpr int NB = BN / WN / 32;     // channel blocks per wave
+  static constexpr int LA = BM / (16 * NW);   // gathered-row loads per wave and stage
+  static constexpr int LB = BN / (16 * NW);   // weight-row loads per wave and stage
+  static constexpr int L = LA + LB;
   static constexpr int STAGE_A = BM * 64;
   static constexpr int STAGE = STAGE_A + BN * 64;
   static constexpr int IDX = BM * 4;
-  static constexpr int NIDX = BM / 64;        // gather-index loads of one offset
+  static constexpr int NIDX = BM / 64;        // 64-entry index loads of one offset
+  static constexpr int IDXL = (NIDX + NW - 1) / NW;  // index loads per wave
 };
 constexpr int kRingDepth = 4;
-constexpr int kRingLoads = 8;
-constexpr int kRingIdxLoads = 2;
 constexpr int kRingMaxRowBytes = 512;
 
 __device__ __attribute__((aligned(16))) const uint32_t g_zero_row[kRingMaxRowBytes / 4] = {};
@@ -581,30 +586,43 @@ __device__ __forceinline__ void lds_dma4(const void* src, char* lds_wave_base) {
   __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(lds_wave_base), 4, 0, 0);
 }
 
+// source address of gathered row g (rows outside [0, n_in) read the zero row); the
+// address is made opaque before the select so that it stays a v_cndmask, not a branch
+__device__ __forceinline__ const char* gather_src(const char* in, int32_t g, uint64_t n_in, int rb, int coff,
+                                                  const char* zrow) {
+  const bool ok = static_cast<uint64_t>(static_cast<uint32_t>(g)) < n_in;
+  uint64_t pin = reinterpret_cast<uint64_t>(in) + static_cast<uint64_t>(static_cast<int64_t>(g) * rb + coff);
+  asm volatile("" : "+v"(pin));
+  return ok ? reinterpret_cast<const char*>(pin) : zrow;
+}
+
 __device__ __forceinline__ int ring_off(int row, int chunk) {
   return row * 64 + ((chunk ^ (((row >> 1) ^ (row >> 3)) & 3)) << 4);
 }
 
-template <typename T, int BN>
-__global__ __launch_bounds__(256, 1) void conv_ring_kernel(ConvArgs a) {
-  using Sh = RingShape<BN>;
-  constexpr int NS = kRingDepth, BM = Sh::BM, MB = Sh::MB, NB = Sh::NB, AX = Sh::AX, BX = Sh::BX;
-  constexpr int kRingSub = Sh::SUB, kRingStageA = Sh::STAGE_A, kRingStage = Sh::STAGE, IDX = Sh::IDX;
-  constexpr int RING = NS * kRingStage;
-  static_assert(AX + BX == 4 && kRingStage == 32768, "stage shape");
-  __shared__ __attribute__((aligned(16))) char smem[RING + 2 * IDX];
+template <typename T, int BN, int NW>
+__global__ __launch_bounds__(NW * 64, 1) void conv_ring_kernel(ConvArgs a) {
+  using Sh = RingShape<BN, NW>;
+  constexpr int NS = kRingDepth, BM = Sh::BM, MB = Sh::MB, NB = Sh::NB, LA = Sh::LA, L = Sh::L;
+  constexpr int SUB = Sh::SUB, STAGE_A = Sh::STAGE_A, STAGE = Sh::STAGE, IDX = Sh::IDX;
+  constexpr int IDXL = Sh::IDXL, LX = L / 2;  // cursor X issues loads 0..LX-1, Y the rest
+  constexpr int RING = NS * STAGE;
+  static_assert(STAGE == 32768 && L % 2 == 0 && LA * 16 * NW == BM, "stage shape");
+  __shared__ __attribute__((aligned(16))) char smem[RING + 3 * IDX];
   char* const idx_ring = smem + RING;
+  char* const rows_lds = idx_ring + 2 * IDX;  // the tile's output rows
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave % Sh::WM, wn = wave / Sh::WM;
   const int64_t item = xcd_remap(blockIdx.x, static_cast<int64_t>(gridDim.x));
   const int64_t tile = item / a.ny;
   const int n0 = static_cast<int>(item - tile * a.ny) * BN;
   const int kvol = a.kvol;
   uint32_t mask = 0;
 #pragma unroll
-  for (int h = 0; h < kRingSub; ++h) {
-    const int64_t pt = tile * kRingSub + h;
+  for (int h = 0; h < SUB; ++h) {
+    const int64_t pt = tile * SUB + h;
     if (pt < a.ntiles) mask |= a.tile_mask[pt];
   }
   mask &= (1u << kvol) - 1u;
@@ -614,46 +632,59 @@ __global__ __launch_bounds__(256, 1) void conv_ring_kernel(ConvArgs a) {
   const int S = taps * KB;
   const uint64_t n_in = static_cast<uint64_t>(a.n_in);
 
-  // load geometry: load j of this wave covers ring rows (wave + 4 j) * 16 + lane / 4, at
-  // physical chunk lane % 4, i.e. logical chunk `lc` (the swizzle repeats every 64 rows)
-  const int lrow = lane >> 2;
-  const int r0 = wave * 16 + lrow;
+  // load u of this wave covers stage rows (wave + NW u) * 16 + lane / 4 (gathered rows for
+  // u < LA, weight rows for u - LA after), at physical chunk lane % 4, i.e. logical chunk
+  // `coff` / 16 (the swizzle repeats every 64 rows)
+  const int r0 = wave * 16 + (lane >> 2);
   const int coff = ((lane & 3) ^ (((r0 >> 1) ^ (r0 >> 3)) & 3)) * 16;
-  const char* wrow[2 * BX];
+  const char* wrow[Sh::LB];
 #pragma unroll
-  for (int j = 0; j < 2 * BX; ++j)
-    wrow[j] = a.weight + static_cast<int64_t>(n0 + r0 + 64 * j) * kvol * rb + coff;
+  for (int j = 0; j < Sh::LB; ++j)
+    wrow[j] = a.weight + static_cast<int64_t>(n0 + r0 + 16 * NW * j) * kvol * rb + coff;
   const char* const zrow = reinterpret_cast<const char*>(g_zero_row) + coff;
 
-  // gather-index loads of offset k into slot `slot`: load i of NIDX covers rows 64 i .. +63
-  // (plan tile i / 2, clamped to the plan); wave w issues loads w and (w + 4, or w again)
+  // 64-entry index loads: load i of NIDX covers rows 64 i .. +63 (plan tile i / 2, clamped
+  // to the plan); wave w issues loads w, w + NW, ... (repeating its first beyond NIDX)
+  auto idx_load = [&](const int32_t* base, int64_t stride, int u) {
+    int i = wave + NW * u;
+    if (i >= Sh::NIDX) i = wave < Sh::NIDX ? wave : Sh::NIDX - 1;
+    int64_t pt = tile * SUB + (i >> 1);
+    if (pt >= a.ntiles) pt = a.ntiles - 1;
+    return std::pair<const int32_t*, int>(base + pt * stride + (i & 1) * 64 + lane, i * 256);
+  };
   auto issue_idx = [&](int k, int slot) {
 #pragma unroll
-    for (int u = 0; u < kRingIdxLoads; ++u) {
-      const int i = u == 0 ? wave : (wave + 4 < Sh::NIDX ? wave + 4 : wave);
-      int64_t pt = tile * kRingSub + (i >> 1);
-      if (pt >= a.ntiles) pt = a.ntiles - 1;
-      const int32_t* src = a.gidx + (pt * kvol + k) * kTileRows + (i & 1) * 64 + lane;
-      lds_dma4(src, idx_ring + slot * IDX + i * 256);
+    for (int u = 0; u < IDXL; ++u) {
+      auto [src, off] = idx_load(a.gidx + k * kTileRows, static_cast<int64_t>(kvol) * kTileRows, u);
+      lds_dma4(src, idx_ring + slot * IDX + off);
     }
   };
+  // the tile's output rows reach LDS at the start (complete by the first wait)
+#pragma unroll
+  for (int u = 0; u < IDXL; ++u) {
+    auto [src, off] = idx_load(a.rows, kTileRows, u);
+    lds_dma4(src, rows_lds + off);
+  }
 
   // load cursors over the stage stream (present offsets in increasing order, K steps
-  // inside); X issues gathered loads 0..AX-1 + weight loads 0..BX-1, Y the rest
+  // inside); X issues loads 0..LX-1 of a stage, Y loads LX..L-1
   struct Cursor {
     uint32_t rest;  // offsets after the current one
     int k, kb, ord, slot;
-    const char* src[AX];  // gathered-row sources of this cursor's loads at step 0
+    const char* src[LA];  // gathered-row sources of this cursor's loads at step 0
   };
-  auto enter_offset = [&](Cursor& c, int jbase) {
+  auto enter_offset = [&](Cursor& c, auto yc) {
+    constexpr bool Y = decltype(yc)::value;
+    constexpr int U0 = Y ? LX : 0, U1 = Y ? (LA < L ? LA : L) : (LA < LX ? LA : LX);
     const int32_t* gi = reinterpret_cast<const int32_t*>(idx_ring + (c.ord & 1) * IDX);
+    int32_t g[LA];
 #pragma unroll
-    for (int j = 0; j < AX; ++j) {
-      const int32_t g = gi[r0 + 64 * (jbase + j)];
-      const bool ok = static_cast<uint64_t>(static_cast<uint32_t>(g)) < n_in;
-      c.src[j] = ok ? a.in + static_cast<int64_t>(g) * rb + coff : zrow;
-    }
+    for (int u = U0; u < U1; ++u) g[u] = gi[r0 + 16 * NW * u];
+#pragma unroll
+    for (int u = U0; u < U1; ++u) c.src[u] = gather_src(a.in, g[u], n_in, rb, coff, zrow);
   };
+  using XC = std::false_type;
+  using YC = std::true_type;
   auto start = [&](Cursor& c) {
     c.k = mask ? __builtin_ctz(mask) : 0;
     c.rest = mask & (mask - 1u);
@@ -673,21 +704,12 @@ __global__ __launch_bounds__(256, 1) void conv_ring_kernel(ConvArgs a) {
     }
     return false;
   };
-  auto issue_x = [&](Cursor& c, int u) {  // u = 0..3
-    char* st = smem + c.slot * kRingStage;
-    if (u < AX) {
-      lds_dma16(c.src[u] + c.kb * 64, st + (wave + 4 * u) * 1024);
-    } else {
-      lds_dma16(wrow[u - AX] + c.k * rb + c.kb * 64, st + kRingStageA + (wave + 4 * (u - AX)) * 1024);
-    }
-  };
-  auto issue_y = [&](Cursor& c, int u) {
-    char* st = smem + c.slot * kRingStage;
-    if (u < AX) {
-      lds_dma16(c.src[u] + c.kb * 64, st + (wave + 4 * (AX + u)) * 1024);
-    } else {
-      lds_dma16(wrow[BX + u - AX] + c.k * rb + c.kb * 64, st + kRingStageA + (wave + 4 * (BX + u - AX)) * 1024);
-    }
+  auto issue = [&](Cursor& c, int u) {  // load u of the cursor's current stage
+    char* st = smem + c.slot * STAGE;
+    if (u < LA)
+      lds_dma16(c.src[u] + c.kb * 64, st + (wave + NW * u) * 1024);
+    else
+      lds_dma16(wrow[u - LA] + c.k * rb + c.kb * 64, st + STAGE_A + (wave + NW * (u - LA)) * 1024);
   };
 
   f32x16 acc[NB][MB];
@@ -697,18 +719,19 @@ __global__ __launch_bounds__(256, 1) void conv_ring_kernel(ConvArgs a) {
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[nb][mb][v] = 0.0f;
-  constexpr int NF = NB + MB;        // fragment reads per K-group
-  constexpr int NM = NB * MB;        // MFMAs per K-group
+  constexpr int NF = NB + MB;  // fragment reads per K-group
+  constexpr int NM = NB * MB;  // MFMAs per K-group
+  static_assert(NM >= NF && NM >= LX, "slots");
   u32x4 fa[2][MB], fb[2][NB];
-  auto frag_one = [&](int slot, auto gc, int i) {  // i: 0..NB-1 weight blocks, then row blocks
+  auto frag_one = [&](int slot, auto gc, int i) {  // i: weight blocks, then row blocks
     constexpr int Gk = decltype(gc)::value;
-    const char* st = smem + slot * kRingStage;
+    const char* st = smem + slot * STAGE;
     const int c = 2 * Gk + (lane >> 5);
     if (i < NB)
-      fb[Gk][i] = *reinterpret_cast<const u32x4*>(st + kRingStageA + ring_off(i * 32 + (lane & 31), c));
+      fb[Gk][i] = *reinterpret_cast<const u32x4*>(st + STAGE_A + ring_off(wn * NB * 32 + i * 32 + (lane & 31), c));
     else
       fa[Gk][i - NB] =
-          *reinterpret_cast<const u32x4*>(st + ring_off(wave * (MB * 32) + (i - NB) * 32 + (lane & 31), c));
+          *reinterpret_cast<const u32x4*>(st + ring_off(wm * (MB * 32) + (i - NB) * 32 + (lane & 31), c));
   };
   auto mma_one = [&](auto gc, int i) {  // i = nb * MB + mb
     constexpr int Gk = decltype(gc)::value;
@@ -725,22 +748,22 @@ __global__ __launch_bounds__(256, 1) void conv_ring_kernel(ConvArgs a) {
     issue_idx(cx.k, 0);
     wait_vmcnt<0>();
     raw_barrier();
-    enter_offset(cx, 0);
-    enter_offset(cy, AX);
+    enter_offset(cx, XC{});
+    enter_offset(cy, YC{});
     if (taps > 1) issue_idx(cx.rest ? __builtin_ctz(cx.rest) : 0, 1);
 #pragma unroll
     for (int st = 0; st < NS - 1; ++st) {
       if (st < S) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) issue_x(cx, u);
+        for (int u = 0; u < LX; ++u) issue(cx, u);
 #pragma unroll
-        for (int u = 0; u < 4; ++u) issue_y(cy, u);
+        for (int u = LX; u < L; ++u) issue(cy, u);
         advance(cx);  // offsets span KB >= 4 steps: no offset change inside the prologue
         advance(cy);
       }
     }
-    if (S > 2) wait_vmcnt<2 * kRingLoads>();
-    else if (S > 1) wait_vmcnt<kRingLoads>();
+    if (S > 2) wait_vmcnt<2 * L>();
+    else if (S > 1) wait_vmcnt<L>();
     else wait_vmcnt<0>();
     raw_barrier();
 #pragma unroll
@@ -755,7 +778,7 @@ __global__ __launch_bounds__(256, 1) void conv_ring_kernel(ConvArgs a) {
       // first half: K-group 0 MFMAs, K-group 1 fragment reads, Y loads of stage s + 2
       wait_lgkm0();
       if (yload && cy.kb == 0) {
-        enter_offset(cy, AX);
+        enter_offset(cy, YC{});
         wait_lgkm0();
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -763,18 +786,15 @@ __global__ __launch_bounds__(256, 1) void conv_ring_kernel(ConvArgs a) {
       for (int i = 0; i < NM; ++i) {
         mma_one(G0{}, i);
         __builtin_amdgcn_sched_barrier(0);
-        if (i < NF) {
-          frag_one(slot, G1{}, i);
-        } else if (i < NF + 4 && yload) {
-          issue_y(cy, i - NF);
-        }
+        if (i < NF) frag_one(slot, G1{}, i);
+        if (i >= NM - (L - LX) && yload) issue(cy, LX + i - (NM - (L - LX)));
         __builtin_amdgcn_sched_barrier(0);
       }
       if (yload) advance(cy);
       if (next) {
         if (s + 2 >= S) wait_vmcnt<0>();
-        else if (idx_pending) wait_vmcnt<kRingLoads + kRingIdxLoads>();
-        else wait_vmcnt<kRingLoads>();
+        else if (idx_pending) wait_vmcnt<L + IDXL>();
+        else wait_vmcnt<L>();
         raw_barrier();
       }
       // second half: K-group 1 MFMAs, K-group 0 fragment reads of stage s + 1, X loads of
@@ -782,7 +802,7 @@ __global__ __launch_bounds__(256, 1) void conv_ring_kernel(ConvArgs a) {
       idx_pending = false;
       wait_lgkm0();
       if (xload && cx.kb == 0) {
-        enter_offset(cx, 0);
+        enter_offset(cx, XC{});
         if (cx.rest) {
           issue_idx(__builtin_ctz(cx.rest), (cx.ord + 1) & 1);
           idx_pending = true;
@@ -794,24 +814,22 @@ __global__ __launch_bounds__(256, 1) void conv_ring_kernel(ConvArgs a) {
       for (int i = 0; i < NM; ++i) {
         mma_one(G1{}, i);
         __builtin_amdgcn_sched_barrier(0);
-        if (i < NF) {
-          if (next) frag_one((slot + 1) & (NS - 1), G0{}, i);
-        } else if (i < NF + 4 && xload) {
-          issue_x(cx, i - NF);
-        }
+        if (i < NF && next) frag_one((slot + 1) & (NS - 1), G0{}, i);
+        if (i >= NM - LX && xload) issue(cx, i - (NM - LX));
         __builtin_amdgcn_sched_barrier(0);
       }
       if (xload) advance(cx);
     }
   }
 
-  // epilogue
+  // epilogue: each wave stages its (MB * 32) x (NB * 32) block
   wait_vmcnt<0>();
   __syncthreads();
   const T* bias = static_cast<const T*>(a.bias);
-  constexpr int ROWB = BN * 2;     // staged row bytes
-  constexpr int CPR = BN / 8;      // 16-byte chunks per staged row
+  constexpr int ROWB = NB * 64;  // staged row bytes
+  constexpr int CPR = NB * 4;    // 16-byte chunks per staged row
   char* stg = smem + wave * (MB * 32 * ROWB);
+  const int cb = n0 + wn * NB * 32;
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
 #pragma unroll
@@ -819,7 +837,7 @@ __global__ __launch_bounds__(256, 1) void conv_ring_kernel(ConvArgs a) {
       const int j0 = nb * 32 + 8 * q + 4 * (lane >> 5);
       float b[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) b[e] = bias != nullptr ? to_f32(bias[n0 + j0 + e]) : 0.0f;
+      for (int e = 0; e < 4; ++e) b[e] = bias != nullptr ? to_f32(bias[cb + j0 + e]) : 0.0f;
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) {
         const int row = mb * 32 + (lane & 31);
@@ -842,13 +860,13 @@ __global__ __launch_bounds__(256, 1) void conv_ring_kernel(ConvArgs a) {
   for (int i = 0; i < MB * 32 * CPR / 64; ++i) {
     const int row = lane / CPR + (64 / CPR) * i;  // within this wave's MB * 32 rows
     const int chunk = lane % CPR;
-    const int tr = wave * (MB * 32) + row;
-    const int64_t pt = tile * kRingSub + tr / kTileRows;
+    const int tr = wm * (MB * 32) + row;
+    const int64_t pt = tile * SUB + tr / kTileRows;
     if (pt >= a.ntiles) continue;
-    const int32_t orow = a.rows[pt * kTileRows + (tr % kTileRows)];
+    const int32_t orow = reinterpret_cast<const int32_t*>(rows_lds)[tr];
     if (orow < 0) continue;
     u32x4 v = *reinterpret_cast<const u32x4*>(stg + row * ROWB + ((chunk ^ (row & (CPR - 1))) << 4));
-    const int64_t off = static_cast<int64_t>(orow) * out_row_bytes + static_cast<int64_t>(n0 + chunk * 8) * sizeof(T);
+    const int64_t off = static_cast<int64_t>(orow) * out_row_bytes + static_cast<int64_t>(cb + chunk * 8) * sizeof(T);
     if (a.residual != nullptr) {
       const u32x4 r = *reinterpret_cast<const u32x4*>(a.residual + off);
       T* pv = reinterpret_cast<T*>(&v);
@@ -860,14 +878,309 @@ __global__ __launch_bounds__(256, 1) void conv_ring_kernel(ConvArgs a) {
   }
 }
 
-template <typename T, int BN>
+template <typename T, int BN, int NW>
 int launch_ring(const ConvArgs& base, hipStream_t stream) {
   ConvArgs a = base;
   a.ny = a.cout / BN;
-  const int64_t blocks = ceil_div(a.ntiles, RingShape<BN>::SUB) * a.ny;
+  const int64_t blocks = ceil_div(a.ntiles, RingShape<BN, NW>::SUB) * a.ny;
   if (blocks == 0) return HI3D_OK;
   HI3D_REQUIRE(blocks < (int64_t(1) << 31), "too many tiles");
-  hipLaunchKernelGGL((conv_ring_kernel<T, BN>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, stream, a);
+  hipLaunchKernelGGL((conv_ring_kernel<T, BN, NW>), dim3(static_cast<unsigned>(blocks)), dim3(NW * 64), 0, stream, a);
+  HI3D_LAUNCH_CHECK();
+  return HI3D_OK;
+}
+
+// ------------------------------------------------------ wide-step ring kernel --
+// The ring kernel's scheme with 128-byte K steps: each gathered row is fetched as one
+// 128-byte request per stage instead of two 64-byte ones, halving the gather requests
+// per flop (L2-resident gathers: ~24 TB/s with 128-byte rows against ~15 TB/s with
+// 64-byte rows). Stages of (BM + BN) x 128 bytes = 48 KB sit in a 3-deep ring.
+//  * Tile: BN = 128 takes BM = 256 rows, BN = 256 takes BM = 128 rows; NW waves form a
+//    BM / 64 x NW / (BM / 64) grid, each owning 64 rows x its channels as 2 x NB blocks
+//    of 32x32x16 MFMAs, four K-groups of 16 elements per stage.
+//  * Loads: per wave L = (BM + BN) / (8 NW) direct-to-LDS 16-byte loads per stage
+//    (8 lanes per 128-byte row), all for stage s + 2, issued in K-groups 0..2 of stage
+//    s, L / 3 after the last MFMAs of each. Stage s + 2 reuses the slot of stage s - 1,
+//    whose last fragment reads precede the barrier of stage s - 1.
+//  * One barrier per stage, before K-group 3 (whose fragment reads are stage s + 1's
+//    K-group 0): the wait before it leaves exactly stage s + 2's L loads in flight,
+//    plus the next offset's index load when one was issued in stage s.
+//  * Rows use the 128-byte XOR swizzle (chunk c of row r at c ^ ((r >> 1) & 7)), so the
+//    fragment reads are conflict-free; gather indices and the epilogue follow the ring
+//    kernel.
+template <int BN, int NW>
+struct WideShape {
+  static constexpr int BM = BN == 128 ? 256 : 128;
+  static constexpr int WM = BM / 64;         // waves across rows (64 rows each)
+  static constexpr int WN = NW / WM;         // waves across channels
+  static constexpr int NB = BN / WN / 32;    // channel blocks per wave
+  static constexpr int SUB = BM / kTileRows;
+  static constexpr int LA = BM / (8 * NW);   // gathered-row loads per wave and stage
+  static constexpr int LB = BN / (8 * NW);   // weight-row loads per wave and stage
+  static constexpr int L = LA + LB;
+  static constexpr int STAGE_A = BM * 128;
+  static constexpr int STAGE = STAGE_A + BN * 128;
+  static constexpr int IDX = BM * 4;
+};
+constexpr int kWideDepth = 3;
+
+__device__ __forceinline__ int wide_off(int row, int chunk) { return row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4); }
+
+template <typename T, int BN, int NW>
+__global__ __launch_bounds__(NW * 64, 1) void conv_wide_kernel(ConvArgs a) {
+  using Sh = WideShape<BN, NW>;
+  constexpr int NS = kWideDepth, BM = Sh::BM, LA = Sh::LA, LB = Sh::LB, SUB = Sh::SUB, L = Sh::L;
+  constexpr int STAGE = Sh::STAGE, STAGE_A = Sh::STAGE_A, IDX = Sh::IDX;
+  constexpr int MB = 2, NB = Sh::NB, NF = MB + NB, NM = MB * NB, KG = 4, LG = L / (KG - 1);
+  static_assert(STAGE == 49152 && LG * (KG - 1) == L && LG <= NM && LA * 8 * NW == BM, "stage shape");
+  __shared__ __attribute__((aligned(16))) char smem[NS * STAGE + 3 * IDX];
+  char* const idx_ring = smem + NS * STAGE;
+  char* const rows_lds = idx_ring + 2 * IDX;  // the tile's output rows
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave % Sh::WM, wn = wave / Sh::WM;
+  const int64_t item = xcd_remap(blockIdx.x, static_cast<int64_t>(gridDim.x));
+  const int64_t tile = item / a.ny;
+  const int n0 = static_cast<int>(item - tile * a.ny) * BN;
+  const int kvol = a.kvol;
+  uint32_t mask = 0;
+#pragma unroll
+  for (int h = 0; h < SUB; ++h) {
+    const int64_t pt = tile * SUB + h;
+    if (pt < a.ntiles) mask |= a.tile_mask[pt];
+  }
+  mask &= (1u << kvol) - 1u;
+  const int rb = a.cin * static_cast<int>(sizeof(T));
+  const int KB = rb >> 7;
+  const int taps = __popc(mask);
+  const int S = taps * KB;
+  const uint64_t n_in = static_cast<uint64_t>(a.n_in);
+
+  // load j of this wave covers rows (wave + NW j) * 8 + lane / 8 at physical chunk
+  // lane % 8, i.e. logical chunk coff / 16 (the swizzle repeats every 16 rows)
+  const int r0 = wave * 8 + (lane >> 3);
+  const int coff = ((lane & 7) ^ ((r0 >> 1) & 7)) * 16;
+  const char* wrow[LB];
+#pragma unroll
+  for (int j = 0; j < LB; ++j)
+    wrow[j] = a.weight + static_cast<int64_t>(n0 + r0 + 8 * NW * j) * kvol * rb + coff;
+  const char* const zrow = reinterpret_cast<const char*>(g_zero_row) + coff;
+
+  // gather indices of offset k into slot `slot`: load `wave` of BM / 64 covers rows
+  // 64 wave .. +63 (waves beyond BM / 64 repeat the last one)
+  auto issue_idx = [&](int k, int slot) {
+    const int i = wave < BM / 64 ? wave : BM / 64 - 1;
+    int64_t pt = tile * SUB + (i >> 1);
+    if (pt >= a.ntiles) pt = a.ntiles - 1;
+    lds_dma4(a.gidx + (pt * kvol + k) * kTileRows + (i & 1) * 64 + lane, idx_ring + slot * IDX + i * 256);
+  };
+
+  {  // the tile's output rows reach LDS at the start (complete by the first wait)
+    const int i = wave < BM / 64 ? wave : BM / 64 - 1;
+    int64_t pt = tile * SUB + (i >> 1);
+    if (pt >= a.ntiles) pt = a.ntiles - 1;
+    lds_dma4(a.rows + pt * kTileRows + (i & 1) * 64 + lane, rows_lds + i * 256);
+  }
+
+  uint32_t rest;  // offsets after the current one of the load cursor
+  int ck, ckb, cord;
+  const char* src[LA];
+  auto enter_offset = [&]() {
+    const int32_t* gi = reinterpret_cast<const int32_t*>(idx_ring + (cord & 1) * IDX);
+    int32_t g[LA];
+#pragma unroll
+    for (int j = 0; j < LA; ++j) g[j] = gi[r0 + 8 * NW * j];
+#pragma unroll
+    for (int j = 0; j < LA; ++j) src[j] = gather_src(a.in, g[j], n_in, rb, coff, zrow);
+  };
+  auto advance = [&]() {
+    if (++ckb == KB) {
+      ckb = 0;
+      ck = rest ? __builtin_ctz(rest) : ck;
+      rest &= rest - 1u;
+      ++cord;
+    }
+  };
+  auto issue_load = [&](int slot, int u) {  // u = 0..L-1: LA gathered, then LB weight loads
+    char* st = smem + slot * STAGE;
+    if (u < LA)
+      lds_dma16(src[u] + ckb * 128, st + (wave + NW * u) * 1024);
+    else
+      lds_dma16(wrow[u - LA] + ck * rb + ckb * 128, st + STAGE_A + (wave + NW * (u - LA)) * 1024);
+  };
+
+  f32x16 acc[NB][MB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[nb][mb][v] = 0.0f;
+  u32x4 fa[2][MB], fb[2][NB];
+  auto frag_one = [&](int slot, auto gc, int i) {  // K-group G of the stage in `slot`
+    constexpr int G = decltype(gc)::value;
+    const char* st = smem + slot * STAGE;
+    const int c = 2 * G + (lane >> 5);
+    if (i < NB)
+      fb[G & 1][i] = *reinterpret_cast<const u32x4*>(st + STAGE_A + wide_off(wn * NB * 32 + i * 32 + (lane & 31), c));
+    else
+      fa[G & 1][i - NB] = *reinterpret_cast<const u32x4*>(st + wide_off(wm * 64 + (i - NB) * 32 + (lane & 31), c));
+  };
+  auto mma_one = [&](auto gc, int i) {  // i = nb * MB + mb
+    constexpr int G = decltype(gc)::value;
+    Mfma<T>::run(fb[G & 1][i / MB], fa[G & 1][i % MB], acc[i / MB][i % MB]);
+  };
+  using G0 = std::integral_constant<int, 0>;
+  using G1 = std::integral_constant<int, 1>;
+  using G2 = std::integral_constant<int, 2>;
+  using G3 = std::integral_constant<int, 3>;
+
+  if (S > 0) {
+    ck = mask ? __builtin_ctz(mask) : 0;
+    rest = mask & (mask - 1u);
+    ckb = 0;
+    cord = 0;
+    issue_idx(ck, 0);
+    wait_vmcnt<0>();
+    raw_barrier();
+    enter_offset();
+    bool idx_pending = false;
+    if (taps > 1) {
+      issue_idx(__builtin_ctz(rest), 1);
+      idx_pending = true;
+    }
+    // prologue: stages 0 and 1 (one offset: KB >= 2)
+#pragma unroll
+    for (int st = 0; st < NS - 1; ++st) {
+      if (st < S) {
+#pragma unroll
+        for (int u = 0; u < L; ++u) issue_load(st, u);
+        advance();
+      }
+    }
+    if (S > 1) wait_vmcnt<L>();
+    else wait_vmcnt<0>();
+    raw_barrier();
+#pragma unroll
+    for (int i = 0; i < NF; ++i) frag_one(0, G0{}, i);
+
+    int slot = 0;
+    for (int s = 0; s < S; ++s) {
+      const int lslot = slot == 0 ? NS - 1 : slot - 1;  // slot of stage s + 2
+      const bool load = s + 2 < S;
+      const bool next = s + 1 < S;
+      const bool pend = idx_pending;  // index load issued in an earlier stage
+      idx_pending = false;
+      if (load && ckb == 0) {
+        wait_lgkm0();
+        enter_offset();
+        if (rest) {
+          issue_idx(__builtin_ctz(rest), (cord + 1) & 1);
+          idx_pending = true;
+        }
+      }
+      auto group = [&](auto gc) {
+        constexpr int G = decltype(gc)::value;
+        wait_lgkm0();
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < NM; ++i) {
+          mma_one(gc, i);
+          __builtin_amdgcn_sched_barrier(0);
+          if (i < NF) {
+            if constexpr (G < KG - 1)
+              frag_one(slot, std::integral_constant<int, G + 1>{}, i);
+            else if (next)
+              frag_one(slot + 1 == NS ? 0 : slot + 1, G0{}, i);
+          }
+          if constexpr (G < KG - 1) {
+            if (i >= NM - LG && load) issue_load(lslot, G * LG + i - (NM - LG));
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      };
+      group(G0{});
+      group(G1{});
+      group(G2{});
+      if (load) advance();
+      if (next) {
+        // in flight after stage s + 1's loads: stage s + 2's loads and this stage's
+        // index load; an older index load must be complete
+        (void)pend;
+        if (!load) wait_vmcnt<0>();
+        else if (idx_pending) wait_vmcnt<L + 1>();
+        else wait_vmcnt<L>();
+        raw_barrier();
+      }
+      group(G3{});
+      slot = slot + 1 == NS ? 0 : slot + 1;
+    }
+  }
+
+  // epilogue: each wave stages its 64 x (NB * 32) block
+  wait_vmcnt<0>();
+  __syncthreads();
+  const T* bias = static_cast<const T*>(a.bias);
+  constexpr int ROWB = NB * 64, CPR = NB * 4;
+  char* stg = smem + wave * (64 * ROWB);
+  const int cb = n0 + wn * NB * 32;
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int j0 = nb * 32 + 8 * q + 4 * (lane >> 5);
+      float b[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) b[e] = bias != nullptr ? to_f32(bias[cb + j0 + e]) : 0.0f;
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        const int row = mb * 32 + (lane & 31);
+        T h[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float x = acc[nb][mb][4 * q + e] + b[e];
+          if (a.act == HI3D_ACT_SILU) x = silu(x);
+          h[e] = static_cast<T>(x);
+        }
+        uint2 packed;
+        __builtin_memcpy(&packed, h, 8);
+        *reinterpret_cast<uint2*>(stg + row * ROWB + (((j0 >> 3) ^ (row & (CPR - 1))) << 4) + (j0 & 4) * 2) = packed;
+      }
+    }
+  }
+  wait_lgkm0();
+  const int64_t out_row_bytes = static_cast<int64_t>(a.cout) * sizeof(T);
+#pragma unroll 4
+  for (int i = 0; i < CPR; ++i) {
+    const int row = lane / CPR + (64 / CPR) * i;  // 0..63 within this wave's rows
+    const int chunk = lane % CPR;
+    const int tr = wm * 64 + row;
+    const int64_t pt = tile * SUB + tr / kTileRows;
+    if (pt >= a.ntiles) continue;
+    const int32_t orow = reinterpret_cast<const int32_t*>(rows_lds)[tr];
+    if (orow < 0) continue;
+    u32x4 v = *reinterpret_cast<const u32x4*>(stg + row * ROWB + ((chunk ^ (row & (CPR - 1))) << 4));
+    const int64_t off = static_cast<int64_t>(orow) * out_row_bytes + static_cast<int64_t>(cb + chunk * 8) * sizeof(T);
+    if (a.residual != nullptr) {
+      const u32x4 r = *reinterpret_cast<const u32x4*>(a.residual + off);
+      T* pv = reinterpret_cast<T*>(&v);
+      const T* pr = reinterpret_cast<const T*>(&r);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) pv[e] = static_cast<T>(to_f32(pv[e]) + to_f32(pr[e]));
+    }
+    *reinterpret_cast<u32x4*>(a.out + off) = v;
+  }
+}
+
+template <typename T, int BN, int NW>
+int launch_wide(const ConvArgs& base, hipStream_t stream) {
+  ConvArgs a = base;
+  a.ny = a.cout / BN;
+  const int64_t blocks = ceil_div(a.ntiles, WideShape<BN, NW>::SUB) * a.ny;
+  if (blocks == 0) return HI3D_OK;
+  HI3D_REQUIRE(blocks < (int64_t(1) << 31), "too many tiles");
+  hipLaunchKernelGGL((conv_wide_kernel<T, BN, NW>), dim3(static_cast<unsigned>(blocks)), dim3(NW * 64), 0, stream, a);
   HI3D_LAUNCH_CHECK();
   return HI3D_OK;
 }
@@ -890,7 +1203,13 @@ int launch_mfma(const ConvArgs& base, hipStream_t stream) {
   if constexpr (sizeof(T) == 2) {
     const int rb = a.cin * static_cast<int>(sizeof(T));
     if (a.kvol <= kMaxPipelinedKvol && a.cout % 128 == 0 && rb % 64 == 0 && rb >= 4 * 64 && rb <= kRingMaxRowBytes)
-      return a.cout % 256 == 0 ? launch_ring<T, 256>(a, stream) : launch_ring<T, 128>(a, stream);
+    {
+      // 8 waves throughout; 128-byte K steps for 128-channel tiles, whose gathers are the
+      // larger share of their loads (measured: C128 0.46 vs 0.49 ms, C256 8.8 vs 8.9 ms)
+      if (a.cout % 256 == 0) return launch_ring<T, 256, 8>(a, stream);
+      if (rb % 128 == 0) return launch_wide<T, 128, 8>(a, stream);
+      return launch_ring<T, 128, 8>(a, stream);
+    }
   }
   if (a.kvol <= kMaxPipelinedKvol) {
     if (a.cout <= 64) return launch_pipe<T, 256, 64, 8>(a, stream);

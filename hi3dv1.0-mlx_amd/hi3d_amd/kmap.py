@@ -21,10 +21,12 @@ from . import _lib
 PLAN_WINDOW_ROWS: int | None = None
 """Rows per mask-sorting window of a convolution plan; ``None`` picks by size
 (``PLAN_SMALL_WINDOW`` rows up to ``PLAN_GLOBAL_ROWS`` rows, else ``PLAN_LARGE_WINDOW``).
-Measured on the 543k-voxel C128 shells: one global window 0.60 ms, 16k-64k-row windows
-0.53 ms; on the 4.4M-voxel C256 shells 2^18-row windows are best."""
+Measured with the 8-wave kernels: on the 543k-voxel C128 shells 2^18..2^20-row windows
+0.444-0.454 ms against 0.455-0.462 ms at 2^16 (smaller windows keep gathers in L2 but
+group fewer rows of equal offset masks); on the 4.4M-voxel C256 shells 2^18 is best
+(7.99 ms, 8.10-8.17 ms at 2^19..2^20, 8.18-8.22 ms at 2^17)."""
 PLAN_GLOBAL_ROWS = 1 << 21
-PLAN_SMALL_WINDOW = 1 << 16
+PLAN_SMALL_WINDOW = 1 << 18
 PLAN_LARGE_WINDOW = 1 << 18
 
 

@@ -93,10 +93,11 @@ def test_epilogue_silu_and_residual(cuda):
     (torch.float16, 256, 256, 0.004, None, False),
 ])
 def test_ring_kernel_variants(cuda, dtype, cin, cout, density, act, res):
-    """The ring kernel's paths (fp16/bf16, Cout a multiple of 128, 256..512-byte rows):
-    384 x 128 tiles (Cout 128) and 256 x 256 tiles (Cout a multiple of 256), several
-    output-column tiles, five and six K steps per offset, SiLU and residual in the
-    epilogue, and isolated voxels (tiles whose only offset is the centre)."""
+    """The ring kernels (fp16/bf16, Cout a multiple of 128, 256..512-byte rows): 256 x 256
+    tiles of 64-byte K steps (Cout a multiple of 256), 256 x 128 tiles of 128-byte K steps
+    (rows a multiple of 128 bytes) and 384 x 128 tiles of 64-byte steps (320-byte rows),
+    several output-column tiles, two to eight K steps per offset, SiLU and residual in
+    the epilogue, and isolated voxels (tiles whose only offset is the centre)."""
     from hi3d_amd import conv, kmap
 
     rng = np.random.default_rng(cin * 7 + cout + int(density * 1000))
