@@ -39,7 +39,7 @@ PEAK_HBM_GBS = 8000.0
 # two rocprofv3 --pmc runs of this script, each scaled by the factor the same counter
 # reads for a plain device copy of known size (`--copy-probe`).
 HEADLINE_KERNEL = "conv_wide_kernel<_Float16, 128, 8>"
-TRAFFIC_SUMMARY = ROOT / "profiles" / "conv_ring_subm3_c128_fp16_traffic.txt"
+TRAFFIC_SUMMARY = ROOT / "profiles" / "conv_wide_subm3_c128_fp16_traffic.txt"
 
 
 def measured_traffic():
