@@ -12,94 +12,212 @@ namespace hi3d {
 namespace {
 
 // ------------------------------------------------------------------ quantiser --
-// One wave per row. Pass p covers columns [512p, 512p + 512): lane l holds the 8
-// consecutive columns 512p + 8l .. +7, i.e. positions 8(l%8) .. +7 of 64-column block
-// 8p + l/8. Hadamard butterflies run over position bits 0..5 in increasing order, the
-// same order as the reference's lane shuffles (bits 0..4) followed by its u/v combine
-// (bit 5), so every intermediate value is the same IEEE fp32 operation:
-//   pair (L, H) differing in bit d -> (L + H, L - H); the last stage also scales by 1/8.
-// Position bits 0..2 live in registers, bits 3..5 are lane bits 0..2 (xor shuffles).
-template <int NP, bool kRotate>
+// One wave per row, grid-stride over rows, the next row's fp16 data loaded while the
+// current one is computed. Pass p covers columns [1024p, 1024p + 1024): lane l holds the
+// 16 consecutive columns 1024p + 16l .. +15, i.e. positions 16(l%4) .. +15 of 64-column
+// block 16p + l/4. Hadamard butterflies run over position bits 0..5 in increasing
+// order, the same order as the reference's lane shuffles (bits 0..4) followed by its
+// u/v combine (bit 5):  pair (L, H) differing in bit d -> (L + H, L - H).
+// Bits 0..3 live in registers, bits 4 and 5 are lane bits 0 and 1 (quad DPP moves).
+// The reference scales the last stage by 1/8; here the values stay unscaled (8x theirs,
+// exactly: scaling by a power of two commutes with rounding away from the subnormal
+// range) and the 1/8 moves into the scale: s = fl(max(8 max|v|, 8e-8) / 127) / 8 is
+// the reference's s, and v / (8 s) is the reference's quotient, the same real number.
+// Quantisation divides with the compiler's own correctly rounded f32 division
+// sequence, its reciprocal refinement hoisted per row (t = 8 s, r = rcp(t) refined):
+//   q = v r, e = v - t q, q1 = q + e r, e1 = v - t q1, v / t = q1 + e1 r   (fma each)
+// The division's pre-scaling (v_div_scale) and fix-up only act when the quotient is
+// below 2^-126 or v below 2^-103 (t is at least 8e-8 / 127 and |v| / t at most 127),
+// where both round to 0; rows with a non-finite scale use the full division.
+// The multipliers (signs) sit in LDS, loaded once per workgroup.
+constexpr int kQuantCols = 1024;  // columns per pass
+
+__device__ __forceinline__ float dpp_xor1(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
+}
+__device__ __forceinline__ float dpp_xor2(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, true));
+}
+
+template <int NP, bool kRotate, bool kFull>
 __global__ __launch_bounds__(256) void quant_kernel(const _Float16* __restrict__ x, int64_t m, int k,
                                                     const float* __restrict__ signs, int8_t* __restrict__ q,
                                                     float* __restrict__ scale) {
 #pragma clang fp contract(off)
+  extern __shared__ __attribute__((aligned(16))) float mult[];  // k multipliers when rotating
+  constexpr bool kHold = NP <= 8;      // row held in registers (else recomputed)
+  constexpr bool kPrefetch = NP <= 4;  // and the next row's loads in flight meanwhile
   const int lane = threadIdx.x & 63;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (row >= m) return;
-  const _Float16* xr = x + row * k;
-  float v[NP][8];
-  float maximum = 0.0f;
-#pragma unroll
-  for (int p = 0; p < NP; ++p) {
-    const int c0 = p * 512 + lane * 8;
-    const bool ok = c0 < k;
-    f16x8 h = {};
-    if (ok) h = *reinterpret_cast<const f16x8*>(xr + c0);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) v[p][e] = static_cast<float>(h[e]);
-    if (kRotate) {
-      if (ok) {
-        const float4 s0 = *reinterpret_cast<const float4*>(signs + c0);
-        const float4 s1 = *reinterpret_cast<const float4*>(signs + c0 + 4);
-        v[p][0] *= s0.x; v[p][1] *= s0.y; v[p][2] *= s0.z; v[p][3] *= s0.w;
-        v[p][4] *= s1.x; v[p][5] *= s1.y; v[p][6] *= s1.z; v[p][7] *= s1.w;
-      }
-      // position bits 0, 1, 2 (in registers)
-#pragma unroll
-      for (int d = 1; d < 8; d <<= 1) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          if (e & d) continue;
-          const float lo = v[p][e], hi = v[p][e + d];
-          v[p][e] = lo + hi;
-          v[p][e + d] = lo - hi;
-        }
-      }
-      // position bits 3, 4 (lane bits 0, 1)
-#pragma unroll
-      for (int d = 1; d < 4; d <<= 1) {
-        const bool upper = (lane & d) != 0;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float other = __shfl_xor(v[p][e], d, 64);
-          v[p][e] = upper ? other - v[p][e] : v[p][e] + other;
-        }
-      }
-      // position bit 5 (lane bit 2) with the 1/8 normalisation
-      {
-        const bool upper = (lane & 4) != 0;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float other = __shfl_xor(v[p][e], 4, 64);
-          v[p][e] = upper ? (other - v[p][e]) * 0.125f : (v[p][e] + other) * 0.125f;
-        }
-      }
-    }
-    if (ok) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) maximum = fmaxf(maximum, fabsf(v[p][e]));
-    }
+  const int64_t first = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * 4;
+  if constexpr (kRotate) {
+    for (int i = threadIdx.x * 4; i < k; i += 1024)
+      *reinterpret_cast<float4*>(mult + i) = *reinterpret_cast<const float4*>(signs + i);
+    __syncthreads();
   }
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) maximum = fmaxf(maximum, __shfl_xor(maximum, d, 64));
-  const float s = fmaxf(maximum, 1e-8f) / 127.0f;
-  if (lane == 0) scale[row] = s;
-  int8_t* qr = q + row * k;
-#pragma unroll
-  for (int p = 0; p < NP; ++p) {
-    const int c0 = p * 512 + lane * 8;
-    if (c0 >= k) continue;
-    uint32_t lo = 0, hi = 0;
+  const float up1 = (lane & 1) ? -1.0f : 1.0f, up2 = (lane & 2) ? -1.0f : 1.0f;
+  // loads are unconditional (straight-line code keeps the wait counts exact): chunks
+  // past k load column 0 of the row and are zeroed where used (kFull: k % 1024 == 0)
+  using Raw = f16x8[2];
+  auto load_raw = [&](int64_t row, int p, Raw& h) {
+    const _Float16* xr = x + row * k;
+    const int c0 = p * kQuantCols + lane * 16;
+    h[0] = *reinterpret_cast<const f16x8*>(xr + (kFull || c0 < k ? c0 : 0));
+    h[1] = *reinterpret_cast<const f16x8*>(xr + (kFull || c0 + 8 < k ? c0 + 8 : 0));
+  };
+  // this lane's 16 values of pass p, rotated (unscaled) when kRotate; zeros past k
+  auto rotate = [&](int p, const Raw& h, float (&v)[16]) {
+    const int c0 = p * kQuantCols + lane * 16;
+    const bool ok0 = kFull || c0 < k, ok1 = kFull || c0 + 8 < k;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      float r = __builtin_rintf(v[p][e] / s);
-      r = fminf(fmaxf(r, -127.0f), 127.0f);
-      const uint32_t b = static_cast<uint32_t>(static_cast<int32_t>(r)) & 0xffu;
-      if (e < 4) lo |= b << (8 * e);
-      else hi |= b << (8 * (e - 4));
+      v[e] = ok0 ? static_cast<float>(h[0][e]) : 0.0f;
+      v[e + 8] = ok1 ? static_cast<float>(h[1][e]) : 0.0f;
     }
-    *reinterpret_cast<uint2*>(qr + c0) = make_uint2(lo, hi);
+    if constexpr (kRotate) {
+      if (kFull || c0 < k) {
+#pragma unroll
+        for (int e4 = 0; e4 < 4; ++e4) {
+          const float4 t = *reinterpret_cast<const float4*>(mult + c0 + 4 * e4);
+          v[4 * e4 + 0] *= t.x;
+          v[4 * e4 + 1] *= t.y;
+          v[4 * e4 + 2] *= t.z;
+          v[4 * e4 + 3] *= t.w;
+        }
+      }
+      // position bits 0..3 (in registers)
+#pragma unroll
+      for (int d = 1; d < 16; d <<= 1) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          if (e & d) continue;
+          const float lo = v[e], hi = v[e + d];
+          v[e] = lo + hi;
+          v[e + d] = lo - hi;
+        }
+      }
+      // position bit 4 (lane bit 0): lower lane L + H, upper lane L - H = L + (-H)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) v[e] = dpp_xor1(v[e]) + v[e] * up1;
+      // position bit 5 (lane bit 1)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) v[e] = dpp_xor2(v[e]) + v[e] * up2;
+    }
+  };
+  // quantise and store pass p
+  auto store_pass = [&](int8_t* qr, int p, float (&v)[16], float t, float r, bool fast) {
+    if (fast) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const float a = v[e];
+        const float q0 = a * r;
+        const float q1 = __builtin_fmaf(__builtin_fmaf(-t, q0, a), r, q0);
+        v[e] = __builtin_fmaf(__builtin_fmaf(-t, q1, a), r, q1);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) v[e] = v[e] / t;
+    }
+    const int c0 = p * kQuantCols + lane * 16;
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint32_t packed = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float rr = fminf(fmaxf(__builtin_rintf(v[4 * j + e]), -127.0f), 127.0f);
+        packed |= (static_cast<uint32_t>(static_cast<int32_t>(rr)) & 0xffu) << (8 * e);
+      }
+      w[j] = packed;
+    }
+    if (c0 + 8 < k) *reinterpret_cast<uint4*>(qr + c0) = make_uint4(w[0], w[1], w[2], w[3]);
+    else if (c0 < k) *reinterpret_cast<uint2*>(qr + c0) = make_uint2(w[0], w[1]);
+  };
+  // the row's scale (written out) and the divisor of its values
+  auto finish_scale = [&](int64_t row, float maximum, float& t, float& r, bool& fast) {
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) maximum = fmaxf(maximum, __shfl_xor(maximum, d, 64));
+    if constexpr (kRotate) {
+      t = fmaxf(maximum, 1e-8f * 8.0f) / 127.0f;  // 8 s
+      if (lane == 0) scale[row] = t * 0.125f;
+    } else {
+      t = fmaxf(maximum, 1e-8f) / 127.0f;
+      if (lane == 0) scale[row] = t;
+    }
+    fast = __builtin_isfinite(t);
+    const float r0 = __builtin_amdgcn_rcpf(t);
+    r = __builtin_fmaf(__builtin_fmaf(-t, r0, 1.0f), r0, r0);
+  };
+
+  if constexpr (kHold) {
+    // rows alternate between two register buffers: while one row is computed, the
+    // next one's loads are in flight
+    auto process = [&](int64_t row, Raw (&cur)[NP]) {
+      float v[NP][16];
+      float maximum = 0.0f;
+      // columns past k hold zeros (whole 64-column blocks when rotating), which leave
+      // the maximum of absolute values unchanged
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        rotate(p, cur[p], v[p]);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) maximum = fmaxf(maximum, fabsf(v[p][e]));
+      }
+      float t, r;
+      bool fast;
+      finish_scale(row, maximum, t, r, fast);
+      int8_t* qr = q + row * k;
+#pragma unroll
+      for (int p = 0; p < NP; ++p) store_pass(qr, p, v[p], t, r, fast);
+    };
+    auto load_row = [&](int64_t row, Raw (&buf)[NP]) {  // rows past m load row m - 1
+      const int64_t rr = row < m ? row : m - 1;
+#pragma unroll
+      for (int p = 0; p < NP; ++p) load_raw(rr, p, buf[p]);
+    };
+    if constexpr (kPrefetch) {
+      Raw a[NP], b[NP];
+      load_row(first, a);
+      for (int64_t row = first; row < m; row += 2 * stride) {
+        load_row(row + stride, b);
+        process(row, a);
+        if (row + stride >= m) break;
+        load_row(row + 2 * stride, a);
+        process(row + stride, b);
+      }
+    } else {
+      for (int64_t row = first; row < m; row += stride) {
+        Raw a[NP];
+        load_row(row, a);
+        process(row, a);
+      }
+    }
+  } else {
+    // wide rows: a first pass for the maximum, a second that recomputes and stores
+    for (int64_t row = first; row < m; row += stride) {
+      float maximum = 0.0f;
+#pragma unroll 1
+      for (int p = 0; p < NP; ++p) {
+        Raw h;
+        float v[16];
+        load_raw(row, p, h);
+        rotate(p, h, v);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) maximum = fmaxf(maximum, fabsf(v[e]));
+      }
+      float t, r;
+      bool fast;
+      finish_scale(row, maximum, t, r, fast);
+      int8_t* qr = q + row * k;
+#pragma unroll 1
+      for (int p = 0; p < NP; ++p) {
+        Raw h;
+        float v[16];
+        load_raw(row, p, h);
+        rotate(p, h, v);
+        store_pass(qr, p, v, t, r, fast);
+      }
+    }
   }
 }
 
@@ -643,9 +761,15 @@ __global__ __launch_bounds__(256, 1) void w8a8_gemm_persistent_kernel(
 
 template <int NP>
 void launch_quant(const _Float16* x, int64_t m, int k, const float* signs, int8_t* q, float* s, hipStream_t stream) {
-  const dim3 grid(static_cast<unsigned>(ceil_div(m, 4)));
-  if (signs) hipLaunchKernelGGL((quant_kernel<NP, true>), grid, dim3(256), 0, stream, x, m, k, signs, q, s);
-  else hipLaunchKernelGGL((quant_kernel<NP, false>), grid, dim3(256), 0, stream, x, m, k, signs, q, s);
+  const dim3 grid(static_cast<unsigned>(std::min<int64_t>(ceil_div(m, 4), int64_t(compute_units()) * 8)));
+  const size_t lds = static_cast<size_t>(k) * sizeof(float);
+  if (k % kQuantCols == 0) {
+    if (signs) hipLaunchKernelGGL((quant_kernel<NP, true, true>), grid, dim3(256), lds, stream, x, m, k, signs, q, s);
+    else hipLaunchKernelGGL((quant_kernel<NP, false, true>), grid, dim3(256), 0, stream, x, m, k, signs, q, s);
+  } else {
+    if (signs) hipLaunchKernelGGL((quant_kernel<NP, true, false>), grid, dim3(256), lds, stream, x, m, k, signs, q, s);
+    else hipLaunchKernelGGL((quant_kernel<NP, false, false>), grid, dim3(256), 0, stream, x, m, k, signs, q, s);
+  }
 }
 
 }  // namespace
@@ -667,13 +791,13 @@ int hi3d_w8a8_quantize(const void* x, int64_t m, int32_t k, const float* signs, 
   HI3D_REQUIRE((reinterpret_cast<uintptr_t>(x) & 15) == 0 && (reinterpret_cast<uintptr_t>(q) & 7) == 0,
                "x must be 16-byte and q 8-byte aligned");
   const _Float16* xh = static_cast<const _Float16*>(x);
-  const int passes = (k + 511) / 512;
+  if (signs) HI3D_REQUIRE((reinterpret_cast<uintptr_t>(signs) & 15) == 0, "multipliers must be 16-byte aligned");
+  const int passes = (k + kQuantCols - 1) / kQuantCols;
   if (passes <= 1) launch_quant<1>(xh, m, k, signs, q, scale, stream);
   else if (passes <= 2) launch_quant<2>(xh, m, k, signs, q, scale, stream);
   else if (passes <= 4) launch_quant<4>(xh, m, k, signs, q, scale, stream);
   else if (passes <= 8) launch_quant<8>(xh, m, k, signs, q, scale, stream);
-  else if (passes <= 16) launch_quant<16>(xh, m, k, signs, q, scale, stream);
-  else launch_quant<32>(xh, m, k, signs, q, scale, stream);
+  else launch_quant<16>(xh, m, k, signs, q, scale, stream);
   HI3D_LAUNCH_CHECK();
   return HI3D_OK;
 }

@@ -44,6 +44,8 @@ def _multiplier(k: int, device, rotation: str, multiplier):
     m = multiplier.to(device=device, dtype=torch.float32).contiguous()
     if m.shape != (k,):
         raise ValueError(f"multiplier must be [{k}]")
+    if m.data_ptr() % 16:  # the kernel reads multipliers as 16-byte vectors
+        m = m.clone()
     return m
 
 

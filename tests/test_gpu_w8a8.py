@@ -71,6 +71,35 @@ def test_quantiser_with_outliers_bit_exact(cuda, rotation):
     assert np.array_equal(q.cpu().numpy(), rq)
 
 
+@pytest.mark.parametrize("m,k,rotation,custom", [
+    (3000, 2048, "h64", False), (700, 8192, "h64", False), (700, 8192, "none", False),
+    (513, 72, "none", False), (5000, 4096, "h64", True), (4099, 1024, "none", False),
+])
+def test_quantiser_paths_bit_exact(cuda, m, k, rotation, custom):
+    """Every quantiser path against the oracle: one to eight 1024-column passes held in
+    registers (with the next row prefetched up to four), widths that end inside a pass,
+    more rows than waves, and a general float multiplier instead of the signs. Rows mix
+    magnitudes from fp16 subnormals to 6e4, all-zero rows and one-hot rows, so the
+    division by the row scale meets tiny and exact quotients."""
+    from hi3d_amd import w8a8
+
+    rng = np.random.default_rng(m + k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    mag = np.float32(10.0) ** rng.uniform(-7, 4.7, size=(m, 1)).astype(np.float32)
+    x = x * mag
+    x[::17] = 0.0
+    x[5::23] = 0.0
+    x[5::23, 3] = -2.5
+    x[rng.random(x.shape) < 0.002] *= 50
+    x = np.clip(x, -60000, 60000).astype(np.float16)
+    mult = rng.standard_normal(k).astype(np.float32) if custom else None
+    xt = torch.as_tensor(x).to(cuda)
+    q, s = w8a8.quantize_activation(xt, None if mult is None else torch.as_tensor(mult).to(cuda), rotation=rotation)
+    rq, rs = ow8a8.quantize_activation(x, mult, rotation=rotation)
+    assert np.array_equal(s.cpu().numpy(), rs)
+    assert np.array_equal(q.cpu().numpy(), rq)
+
+
 def test_zero_rows_and_small_k(cuda):
     from hi3d_amd import w8a8
 
