@@ -933,9 +933,10 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_wide_kernel(ConvArgs a) {
   constexpr int STAGE = Sh::STAGE, STAGE_A = Sh::STAGE_A, IDX = Sh::IDX;
   constexpr int MB = 2, NB = Sh::NB, NF = MB + NB, NM = MB * NB, KG = 4, LG = L / (KG - 1);
   static_assert(STAGE == 49152 && LG * (KG - 1) == L && LG <= NM && LA * 8 * NW == BM, "stage shape");
-  __shared__ __attribute__((aligned(16))) char smem[NS * STAGE + 3 * IDX];
+  __shared__ __attribute__((aligned(16))) char smem[NS * STAGE + 3 * IDX + 256];
   char* const idx_ring = smem + NS * STAGE;
   char* const rows_lds = idx_ring + 2 * IDX;  // the tile's output rows
+  char* const idx_dummy = rows_lds + IDX;     // target of the index DMA of stages entering no offset
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1036,7 +1037,61 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_wide_kernel(ConvArgs a) {
   using G2 = std::integral_constant<int, 2>;
   using G3 = std::integral_constant<int, 3>;
 
-  if (S > 0) {
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  // Stage s of the stream in ring slot SL = s % 3. MODE 0: a steady stage (loads stage
+  // s + 2, stage s + 1 follows); 1: stage S - 2 (no loads); 2: stage S - 1 (no loads,
+  // nothing follows). A steady stage issues exactly one index DMA (the next offset's
+  // indices when stage s + 2 begins an offset, else a dummy) and then its L loads, so
+  // the wait before its barrier is always L + 1.
+  auto stage = [&](int SL, auto modec) {
+    constexpr int MODE = decltype(modec)::value;
+    const int LS = SL == 0 ? NS - 1 : SL - 1, NSL = SL == NS - 1 ? 0 : SL + 1;
+    if constexpr (MODE == 0) {
+      if (ckb == 0) {
+        wait_lgkm0();
+        enter_offset();
+        issue_idx(rest ? __builtin_ctz(rest) : ck, (cord + 1) & 1);
+      } else {
+        lds_dma4(a.gidx + lane, idx_dummy);
+      }
+    }
+    auto group = [&](auto gc) {
+      constexpr int G = decltype(gc)::value;
+      wait_lgkm0();
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < NM; ++i) {
+        mma_one(gc, i);
+        __builtin_amdgcn_sched_barrier(0);
+        if (i < NF) {
+          if constexpr (G < KG - 1)
+            frag_one(SL, std::integral_constant<int, G + 1>{}, i);
+          else if constexpr (MODE != 2)
+            frag_one(NSL, G0{}, i);
+        }
+        if constexpr (G < KG - 1 && MODE == 0) {
+          if (i >= NM - LG) issue_load(LS, G * LG + i - (NM - LG));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
+    group(G0{});
+    group(G1{});
+    group(G2{});
+    if constexpr (MODE == 0) {
+      advance();
+      wait_vmcnt<L + 1>();
+      raw_barrier();
+    } else if constexpr (MODE == 1) {
+      wait_vmcnt<0>();
+      raw_barrier();
+    }
+    group(G3{});
+  };
+
+  if (S > 0) {  // S = taps * KB >= 2
     ck = mask ? __builtin_ctz(mask) : 0;
     rest = mask & (mask - 1u);
     ckb = 0;
@@ -1045,77 +1100,28 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_wide_kernel(ConvArgs a) {
     wait_vmcnt<0>();
     raw_barrier();
     enter_offset();
-    bool idx_pending = false;
-    if (taps > 1) {
-      issue_idx(__builtin_ctz(rest), 1);
-      idx_pending = true;
-    }
-    // prologue: stages 0 and 1 (one offset: KB >= 2)
+    // prologue: the next offset's indices (offset 0's again without a successor), then
+    // stages 0 and 1 (one offset: KB >= 2)
+    issue_idx(rest ? __builtin_ctz(rest) : ck, 1);
 #pragma unroll
     for (int st = 0; st < NS - 1; ++st) {
-      if (st < S) {
 #pragma unroll
-        for (int u = 0; u < L; ++u) issue_load(st, u);
-        advance();
-      }
+      for (int u = 0; u < L; ++u) issue_load(st, u);
+      advance();
     }
-    if (S > 1) wait_vmcnt<L>();
-    else wait_vmcnt<0>();
+    wait_vmcnt<L>();
     raw_barrier();
 #pragma unroll
     for (int i = 0; i < NF; ++i) frag_one(0, G0{}, i);
 
     int slot = 0;
-    for (int s = 0; s < S; ++s) {
-      const int lslot = slot == 0 ? NS - 1 : slot - 1;  // slot of stage s + 2
-      const bool load = s + 2 < S;
-      const bool next = s + 1 < S;
-      const bool pend = idx_pending;  // index load issued in an earlier stage
-      idx_pending = false;
-      if (load && ckb == 0) {
-        wait_lgkm0();
-        enter_offset();
-        if (rest) {
-          issue_idx(__builtin_ctz(rest), (cord + 1) & 1);
-          idx_pending = true;
-        }
-      }
-      auto group = [&](auto gc) {
-        constexpr int G = decltype(gc)::value;
-        wait_lgkm0();
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int i = 0; i < NM; ++i) {
-          mma_one(gc, i);
-          __builtin_amdgcn_sched_barrier(0);
-          if (i < NF) {
-            if constexpr (G < KG - 1)
-              frag_one(slot, std::integral_constant<int, G + 1>{}, i);
-            else if (next)
-              frag_one(slot + 1 == NS ? 0 : slot + 1, G0{}, i);
-          }
-          if constexpr (G < KG - 1) {
-            if (i >= NM - LG && load) issue_load(lslot, G * LG + i - (NM - LG));
-          }
-          __builtin_amdgcn_sched_barrier(0);
-        }
-      };
-      group(G0{});
-      group(G1{});
-      group(G2{});
-      if (load) advance();
-      if (next) {
-        // in flight after stage s + 1's loads: stage s + 2's loads and this stage's
-        // index load; an older index load must be complete
-        (void)pend;
-        if (!load) wait_vmcnt<0>();
-        else if (idx_pending) wait_vmcnt<L + 1>();
-        else wait_vmcnt<L>();
-        raw_barrier();
-      }
-      group(G3{});
-      slot = slot + 1 == NS ? 0 : slot + 1;
+    for (int s = 0; s + 2 < S; ++s) {
+      stage(slot, I0{});
+      slot = slot == NS - 1 ? 0 : slot + 1;
     }
+    // the last two stages, S - 2 and S - 1
+    stage(slot, I1{});
+    stage(slot == NS - 1 ? 0 : slot + 1, I2{});
   }
 
   // epilogue: each wave stages its 64 x (NB * 32) block
