@@ -608,9 +608,10 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_ring_kernel(ConvArgs a) {
   constexpr int IDXL = Sh::IDXL, LX = L / 2;  // cursor X issues loads 0..LX-1, Y the rest
   constexpr int RING = NS * STAGE;
   static_assert(STAGE == 32768 && L % 2 == 0 && LA * 16 * NW == BM, "stage shape");
-  __shared__ __attribute__((aligned(16))) char smem[RING + 3 * IDX];
+  __shared__ __attribute__((aligned(16))) char smem[RING + 3 * IDX + 256];
   char* const idx_ring = smem + RING;
   char* const rows_lds = idx_ring + 2 * IDX;  // the tile's output rows
+  char* const idx_dummy = rows_lds + IDX;     // target of the index DMAs of stages entering no offset
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -740,7 +741,80 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_ring_kernel(ConvArgs a) {
   using G0 = std::integral_constant<int, 0>;
   using G1 = std::integral_constant<int, 1>;
 
-  if (S > 0) {
+  // Stage s of the stream. MODE 0: s = 0 (its Y loads were part of the prologue); 1: a
+  // steady stage (Y loads of stage s + 2, X loads of stage s + 3); 2: s = S - 3 (Y loads
+  // only); 3: s = S - 2 (no loads); 4: s = S - 1 (nothing follows). The second half of
+  // modes 0 and 1 issues exactly IDXL index DMAs (the next offset's indices when cursor
+  // X enters an offset, else dummies) before its X loads, so the wait before a steady
+  // barrier is always L + IDXL.
+  auto stage = [&](Cursor& cx, Cursor& cy, int slot, auto modec) {
+    constexpr int MODE = decltype(modec)::value;
+    constexpr bool yload = MODE == 1 || MODE == 2, xload = MODE <= 1, next = MODE != 4;
+    // first half: K-group 0 MFMAs, K-group 1 fragment reads, Y loads of stage s + 2
+    wait_lgkm0();
+    if constexpr (yload) {
+      if (cy.kb == 0) {
+        enter_offset(cy, YC{});
+        wait_lgkm0();
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < NM; ++i) {
+      mma_one(G0{}, i);
+      __builtin_amdgcn_sched_barrier(0);
+      if (i < NF) frag_one(slot, G1{}, i);
+      if constexpr (yload) {
+        if (i >= NM - (L - LX)) issue(cy, LX + i - (NM - (L - LX)));
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (yload) advance(cy);
+    if constexpr (MODE == 0) wait_vmcnt<L>();
+    else if constexpr (MODE <= 2) wait_vmcnt<L + IDXL>();
+    else if constexpr (MODE == 3) wait_vmcnt<0>();
+    if constexpr (next) raw_barrier();
+    // second half: K-group 1 MFMAs, K-group 0 fragment reads of stage s + 1, X loads of
+    // stage s + 3 (entering a new offset first: its sources, and the next offset's indices)
+    wait_lgkm0();
+    if constexpr (xload) {
+      if (cx.kb == 0) {
+        enter_offset(cx, XC{});
+        if (cx.rest) {
+          issue_idx(__builtin_ctz(cx.rest), (cx.ord + 1) & 1);
+        } else {
+#pragma unroll
+          for (int u = 0; u < IDXL; ++u) lds_dma4(a.gidx + lane, idx_dummy);
+        }
+        wait_lgkm0();
+      } else {
+#pragma unroll
+        for (int u = 0; u < IDXL; ++u) lds_dma4(a.gidx + lane, idx_dummy);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const int nslot = (slot + 1) & (NS - 1);
+#pragma unroll
+    for (int i = 0; i < NM; ++i) {
+      mma_one(G1{}, i);
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (next) {
+        if (i < NF) frag_one(nslot, G0{}, i);
+      }
+      if constexpr (xload) {
+        if (i >= NM - LX) issue(cx, i - (NM - LX));
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (xload) advance(cx);
+  };
+  using M0 = std::integral_constant<int, 0>;
+  using M1 = std::integral_constant<int, 1>;
+  using M2 = std::integral_constant<int, 2>;
+  using M3 = std::integral_constant<int, 3>;
+  using M4 = std::integral_constant<int, 4>;
+
+  if (S > 0) {  // S = taps * KB >= 4
     Cursor cx, cy;
     start(cx);
     start(cy);
@@ -753,73 +827,27 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_ring_kernel(ConvArgs a) {
     if (taps > 1) issue_idx(cx.rest ? __builtin_ctz(cx.rest) : 0, 1);
 #pragma unroll
     for (int st = 0; st < NS - 1; ++st) {
-      if (st < S) {
 #pragma unroll
-        for (int u = 0; u < LX; ++u) issue(cx, u);
+      for (int u = 0; u < LX; ++u) issue(cx, u);
 #pragma unroll
-        for (int u = LX; u < L; ++u) issue(cy, u);
-        advance(cx);  // offsets span KB >= 4 steps: no offset change inside the prologue
-        advance(cy);
-      }
+      for (int u = LX; u < L; ++u) issue(cy, u);
+      advance(cx);  // offsets span KB >= 4 steps: no offset change inside the prologue
+      advance(cy);
     }
-    if (S > 2) wait_vmcnt<2 * L>();
-    else if (S > 1) wait_vmcnt<L>();
-    else wait_vmcnt<0>();
+    wait_vmcnt<2 * L>();
     raw_barrier();
 #pragma unroll
     for (int i = 0; i < NF; ++i) frag_one(0, G0{}, i);
 
-    bool idx_pending = false;  // index loads were issued with stage s + 2's X loads
-    for (int s = 0; s < S; ++s) {
-      const int slot = s & (NS - 1);
-      const bool yload = s >= 1 && s + 2 < S;  // Y part of stage s + 2
-      const bool xload = s + 3 < S;            // X part of stage s + 3
-      const bool next = s + 1 < S;
-      // first half: K-group 0 MFMAs, K-group 1 fragment reads, Y loads of stage s + 2
-      wait_lgkm0();
-      if (yload && cy.kb == 0) {
-        enter_offset(cy, YC{});
-        wait_lgkm0();
-      }
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int i = 0; i < NM; ++i) {
-        mma_one(G0{}, i);
-        __builtin_amdgcn_sched_barrier(0);
-        if (i < NF) frag_one(slot, G1{}, i);
-        if (i >= NM - (L - LX) && yload) issue(cy, LX + i - (NM - (L - LX)));
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      if (yload) advance(cy);
-      if (next) {
-        if (s + 2 >= S) wait_vmcnt<0>();
-        else if (idx_pending) wait_vmcnt<L + IDXL>();
-        else wait_vmcnt<L>();
-        raw_barrier();
-      }
-      // second half: K-group 1 MFMAs, K-group 0 fragment reads of stage s + 1, X loads of
-      // stage s + 3 (entering a new offset first: its sources, and the next offset's indices)
-      idx_pending = false;
-      wait_lgkm0();
-      if (xload && cx.kb == 0) {
-        enter_offset(cx, XC{});
-        if (cx.rest) {
-          issue_idx(__builtin_ctz(cx.rest), (cx.ord + 1) & 1);
-          idx_pending = true;
-        }
-        wait_lgkm0();
-      }
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int i = 0; i < NM; ++i) {
-        mma_one(G1{}, i);
-        __builtin_amdgcn_sched_barrier(0);
-        if (i < NF && next) frag_one((slot + 1) & (NS - 1), G0{}, i);
-        if (i >= NM - LX && xload) issue(cx, i - (NM - LX));
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      if (xload) advance(cx);
+    stage(cx, cy, 0, M0{});
+    int slot = 1;
+    for (int s = 1; s + 3 < S; ++s) {
+      stage(cx, cy, slot, M1{});
+      slot = (slot + 1) & (NS - 1);
     }
+    stage(cx, cy, slot, M2{});
+    stage(cx, cy, (slot + 1) & (NS - 1), M3{});
+    stage(cx, cy, (slot + 2) & (NS - 1), M4{});
   }
 
   // epilogue: each wave stages its (MB * 32) x (NB * 32) block
