@@ -561,9 +561,9 @@ int elem_size(int dtype) {
 //    residual.
 // Tile shapes: BN = 128 takes BM = 384 rows, BN = 256 takes 256 rows (32 KB stages);
 // NW waves form a 4 x NW / 4 grid over rows x channels.
-template <int BN, int NW>
+template <int BN, int NW, int BMv = (BN == 128 ? 384 : 256)>
 struct RingShape {
-  static constexpr int BM = BN == 128 ? 384 : 256;
+  static constexpr int BM = BMv;
   static constexpr int SUB = BM / kTileRows;  // plan tiles per tile
   static constexpr int WM = 4, WN = NW / 4;   // wave grid
   static constexpr int MB = BM / WM / 32;     // row blocks per wave
@@ -600,14 +600,14 @@ __device__ __forceinline__ int ring_off(int row, int chunk) {
   return row * 64 + ((chunk ^ (((row >> 1) ^ (row >> 3)) & 3)) << 4);
 }
 
-template <typename T, int BN, int NW>
+template <typename T, int BN, int NW, int BMv>
 __global__ __launch_bounds__(NW * 64, 1) void conv_ring_kernel(ConvArgs a) {
-  using Sh = RingShape<BN, NW>;
+  using Sh = RingShape<BN, NW, BMv>;
   constexpr int NS = kRingDepth, BM = Sh::BM, MB = Sh::MB, NB = Sh::NB, LA = Sh::LA, L = Sh::L;
   constexpr int SUB = Sh::SUB, STAGE_A = Sh::STAGE_A, STAGE = Sh::STAGE, IDX = Sh::IDX;
   constexpr int IDXL = Sh::IDXL, LX = L / 2;  // cursor X issues loads 0..LX-1, Y the rest
   constexpr int RING = NS * STAGE;
-  static_assert(STAGE == 32768 && L % 2 == 0 && LA * 16 * NW == BM, "stage shape");
+  static_assert(STAGE % 1024 == 0 && LA * 16 * NW == BM && Sh::LB * 16 * NW == BN, "stage shape");
   __shared__ __attribute__((aligned(16))) char smem[RING + 3 * IDX + 256];
   char* const idx_ring = smem + RING;
   char* const rows_lds = idx_ring + 2 * IDX;  // the tile's output rows
@@ -722,7 +722,7 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_ring_kernel(ConvArgs a) {
       for (int v = 0; v < 16; ++v) acc[nb][mb][v] = 0.0f;
   constexpr int NF = NB + MB;  // fragment reads per K-group
   constexpr int NM = NB * MB;  // MFMAs per K-group
-  static_assert(NM >= NF && NM >= LX, "slots");
+  static_assert(NM >= L - LX && NM >= LX, "slots");
   u32x4 fa[2][MB], fb[2][NB];
   auto frag_one = [&](int slot, auto gc, int i) {  // i: weight blocks, then row blocks
     constexpr int Gk = decltype(gc)::value;
@@ -744,9 +744,10 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_ring_kernel(ConvArgs a) {
   // Stage s of the stream. MODE 0: s = 0 (its Y loads were part of the prologue); 1: a
   // steady stage (Y loads of stage s + 2, X loads of stage s + 3); 2: s = S - 3 (Y loads
   // only); 3: s = S - 2 (no loads); 4: s = S - 1 (nothing follows). The second half of
-  // modes 0 and 1 issues exactly IDXL index DMAs (the next offset's indices when cursor
-  // X enters an offset, else dummies) before its X loads, so the wait before a steady
-  // barrier is always L + IDXL.
+  // modes 0 and 1, and the end of the prologue, issue exactly IDXL index DMAs (the next
+  // offset's indices when cursor X has entered an offset, else dummies) before the X
+  // loads, so the wait before the barriers of modes 0..2 is always L + IDXL (at most
+  // one set of index DMAs older than the loads it waits for is then left in flight).
   auto stage = [&](Cursor& cx, Cursor& cy, int slot, auto modec) {
     constexpr int MODE = decltype(modec)::value;
     constexpr bool yload = MODE == 1 || MODE == 2, xload = MODE <= 1, next = MODE != 4;
@@ -763,15 +764,15 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_ring_kernel(ConvArgs a) {
     for (int i = 0; i < NM; ++i) {
       mma_one(G0{}, i);
       __builtin_amdgcn_sched_barrier(0);
-      if (i < NF) frag_one(slot, G1{}, i);
+#pragma unroll
+      for (int f = i * NF / NM; f < (i + 1) * NF / NM; ++f) frag_one(slot, G1{}, f);
       if constexpr (yload) {
         if (i >= NM - (L - LX)) issue(cy, LX + i - (NM - (L - LX)));
       }
       __builtin_amdgcn_sched_barrier(0);
     }
     if constexpr (yload) advance(cy);
-    if constexpr (MODE == 0) wait_vmcnt<L>();
-    else if constexpr (MODE <= 2) wait_vmcnt<L + IDXL>();
+    if constexpr (MODE <= 2) wait_vmcnt<L + IDXL>();
     else if constexpr (MODE == 3) wait_vmcnt<0>();
     if constexpr (next) raw_barrier();
     // second half: K-group 1 MFMAs, K-group 0 fragment reads of stage s + 1, X loads of
@@ -799,7 +800,8 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_ring_kernel(ConvArgs a) {
       mma_one(G1{}, i);
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (next) {
-        if (i < NF) frag_one(nslot, G0{}, i);
+#pragma unroll
+        for (int f = i * NF / NM; f < (i + 1) * NF / NM; ++f) frag_one(nslot, G0{}, f);
       }
       if constexpr (xload) {
         if (i >= NM - LX) issue(cx, i - (NM - LX));
@@ -814,40 +816,66 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_ring_kernel(ConvArgs a) {
   using M3 = std::integral_constant<int, 3>;
   using M4 = std::integral_constant<int, 4>;
 
-  if (S > 0) {  // S = taps * KB >= 4
+  if (S > 0) {  // S = taps * KB, KB >= 2
     Cursor cx, cy;
     start(cx);
     start(cy);
-    // prologue: offset 0's indices; then stages 0..2 in full
+    // prologue: the first two offsets' indices; then stages 0..2 (those that exist),
+    // entering the second offset on the way when KB < 3
     issue_idx(cx.k, 0);
+    if (taps > 1) issue_idx(__builtin_ctz(cx.rest), 1);
     wait_vmcnt<0>();
     raw_barrier();
     enter_offset(cx, XC{});
     enter_offset(cy, YC{});
-    if (taps > 1) issue_idx(cx.rest ? __builtin_ctz(cx.rest) : 0, 1);
+    bool x_entered = false;
 #pragma unroll
     for (int st = 0; st < NS - 1; ++st) {
+      if (st < S) {
 #pragma unroll
-      for (int u = 0; u < LX; ++u) issue(cx, u);
+        for (int u = 0; u < LX; ++u) issue(cx, u);
 #pragma unroll
-      for (int u = LX; u < L; ++u) issue(cy, u);
-      advance(cx);  // offsets span KB >= 4 steps: no offset change inside the prologue
-      advance(cy);
+        for (int u = LX; u < L; ++u) issue(cy, u);
+        // (stage 3 and later enter their offsets in the stage loop)
+        if (advance(cx) && st + 1 < NS - 1 && st + 1 < S) {
+          enter_offset(cx, XC{});
+          x_entered = true;
+        }
+        if (advance(cy) && st + 1 < NS - 1 && st + 1 < S) enter_offset(cy, YC{});
+      }
     }
-    wait_vmcnt<2 * L>();
-    raw_barrier();
+    if (S >= 4) {
+      // the offset after the one cursor X entered in the prologue (else dummies): the
+      // steady-state rule, issued after the prologue's loads
+      if (x_entered && cx.rest) {
+        issue_idx(__builtin_ctz(cx.rest), (cx.ord + 1) & 1);
+      } else {
 #pragma unroll
-    for (int i = 0; i < NF; ++i) frag_one(0, G0{}, i);
+        for (int u = 0; u < IDXL; ++u) lds_dma4(a.gidx + lane, idx_dummy);
+      }
+      wait_vmcnt<2 * L + IDXL>();
+      raw_barrier();
+#pragma unroll
+      for (int i = 0; i < NF; ++i) frag_one(0, G0{}, i);
 
-    stage(cx, cy, 0, M0{});
-    int slot = 1;
-    for (int s = 1; s + 3 < S; ++s) {
-      stage(cx, cy, slot, M1{});
-      slot = (slot + 1) & (NS - 1);
+      stage(cx, cy, 0, M0{});
+      int slot = 1;
+      for (int s = 1; s + 3 < S; ++s) {
+        stage(cx, cy, slot, M1{});
+        slot = (slot + 1) & (NS - 1);
+      }
+      stage(cx, cy, slot, M2{});
+      stage(cx, cy, (slot + 1) & (NS - 1), M3{});
+      stage(cx, cy, (slot + 2) & (NS - 1), M4{});
+    } else {
+      // two or three stages: all of them are in the ring
+      wait_vmcnt<0>();
+      raw_barrier();
+#pragma unroll
+      for (int i = 0; i < NF; ++i) frag_one(0, G0{}, i);
+      for (int s = 0; s + 1 < S; ++s) stage(cx, cy, s, M3{});
+      stage(cx, cy, S - 1, M4{});
     }
-    stage(cx, cy, slot, M2{});
-    stage(cx, cy, (slot + 1) & (NS - 1), M3{});
-    stage(cx, cy, (slot + 2) & (NS - 1), M4{});
   }
 
   // epilogue: each wave stages its (MB * 32) x (NB * 32) block
@@ -906,14 +934,14 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_ring_kernel(ConvArgs a) {
   }
 }
 
-template <typename T, int BN, int NW>
+template <typename T, int BN, int NW, int BM = RingShape<BN, NW>::BM>
 int launch_ring(const ConvArgs& base, hipStream_t stream) {
   ConvArgs a = base;
   a.ny = a.cout / BN;
-  const int64_t blocks = ceil_div(a.ntiles, RingShape<BN, NW>::SUB) * a.ny;
+  const int64_t blocks = ceil_div(a.ntiles, RingShape<BN, NW, BM>::SUB) * a.ny;
   if (blocks == 0) return HI3D_OK;
   HI3D_REQUIRE(blocks < (int64_t(1) << 31), "too many tiles");
-  hipLaunchKernelGGL((conv_ring_kernel<T, BN, NW>), dim3(static_cast<unsigned>(blocks)), dim3(NW * 64), 0, stream, a);
+  hipLaunchKernelGGL((conv_ring_kernel<T, BN, NW, BM>), dim3(static_cast<unsigned>(blocks)), dim3(NW * 64), 0, stream, a);
   HI3D_LAUNCH_CHECK();
   return HI3D_OK;
 }
@@ -1236,11 +1264,16 @@ int launch_mfma(const ConvArgs& base, hipStream_t stream) {
   ConvArgs a = base;
   if constexpr (sizeof(T) == 2) {
     const int rb = a.cin * static_cast<int>(sizeof(T));
-    if (a.kvol <= kMaxPipelinedKvol && a.cout % 128 == 0 && rb % 64 == 0 && rb >= 4 * 64 && rb <= kRingMaxRowBytes)
-    {
-      // 8 waves throughout; 128-byte K steps for 128-channel tiles, whose gathers are the
-      // larger share of their loads (measured: C128 0.46 vs 0.49 ms, C256 8.8 vs 8.9 ms)
-      if (a.cout % 256 == 0) return launch_ring<T, 256, 8>(a, stream);
+    const bool ring_rows = rb % 64 == 0 && rb >= 4 * 64 && rb <= kRingMaxRowBytes;
+    const bool few = a.kvol <= 8 && (rb == 128 || rb == 256) && (a.cout == 64 || a.cout == 128);
+    // 8 waves for the large tiles; 128-byte K steps for 128-channel tiles, whose gathers
+    // are the larger share of their loads (measured: C128 0.46 vs 0.49 ms, C256 8.8 vs
+    // 8.9 ms)
+    if (a.kvol <= kMaxPipelinedKvol && ring_rows && a.cout % 256 == 0) return launch_ring<T, 256, 8>(a, stream);
+    // few-offset tables (the strided pair): 128-row tiles in a 48..64 KB ring, so that two
+    // or three workgroups share a CU and cover each other's tile start and end
+    if (few) return a.cout == 64 ? launch_ring<T, 64, 4, 128>(a, stream) : launch_ring<T, 128, 4, 128>(a, stream);
+    if (a.kvol <= kMaxPipelinedKvol && ring_rows && a.cout % 128 == 0) {
       if (rb % 128 == 0) return launch_wide<T, 128, 8>(a, stream);
       return launch_ring<T, 128, 8>(a, stream);
     }
