@@ -631,20 +631,6 @@ __global__ __launch_bounds__(256, 1) void w8a8_gemm_persistent_kernel(
                                                              __builtin_bit_cast(i32x4, fq[Gk][i & 3]),
                                                              kFirst ? zero16 : acc[i >> 2][i & 3], 0, 0, 0);
   };
-  // first half of a stage: K-group 0 MFMAs, K-group 1 fragment reads, token-row loads
-  auto half0 = [&](auto fc, int slot, bool tok) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      mma_one(std::integral_constant<int, 0>{}, i, fc);
-      __builtin_amdgcn_sched_barrier(0);
-      if (i < 8) {
-        frag_one(slot, std::integral_constant<int, 1>{}, i);
-      } else if (tok && (i & 1)) {
-        issue_tokens((i - 8) >> 1);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-  };
   using G0 = std::integral_constant<int, 0>;
   using G1 = std::integral_constant<int, 1>;
 
@@ -652,14 +638,12 @@ __global__ __launch_bounds__(256, 1) void w8a8_gemm_persistent_kernel(
   issue_scales(0);
 #pragma unroll
   for (int st = 0; st < NS - 1; ++st) {
-    if (st < G) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) issue_tokens(j);
+    for (int j = 0; j < 4; ++j) issue_tokens(j);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) issue_channels(j);
-      advance(ct, true);
-      advance(cc, false);
-    }
+    for (int j = 0; j < 4; ++j) issue_channels(j);
+    advance(ct, true);
+    advance(cc, false);
   }
   wait_vmcnt<2 * kGemmLoads>();  // G >= S >= 4: stages 1 and 2 may stay in flight
   raw_barrier();
@@ -668,28 +652,47 @@ __global__ __launch_bounds__(256, 1) void w8a8_gemm_persistent_kernel(
 
   int s = 0;  // stage of the current tile
   int64_t t = 0;
-  for (int64_t g = 0; g < G; ++g) {
+  // Stage g of the stream. MODE 0: g = 0 (its token rows were part of the prologue);
+  // 1: steady (token rows of stage g + 2, channel rows of stage g + 3); 2: g = G - 3
+  // (token rows only); 3: g = G - 2 (no loads); 4: g = G - 1 (nothing follows). `first`
+  // marks a tile's first stage: zero accumulators, the tile's scales, and the previous
+  // tile's epilogue stores still in flight at the barrier.
+  auto stage = [&](int64_t g, auto modec) {
+    constexpr int MODE = decltype(modec)::value;
+    constexpr bool tok = MODE == 1 || MODE == 2, chn = MODE <= 1, nxt = MODE != 4;
     const int slot = static_cast<int>(g & (NS - 1));
     const bool first = s == 0;
-    const bool tok = g >= 1 && g + 2 < G;  // token rows of stage g + 2
     // first half: K-group 0 MFMAs (zero accumulators at a tile's first stage), K-group 1
     // fragment reads, token-row loads of stage g + 2 and, at a tile's first stage, its scales
     wait_lgkm0();
     if (first && g > 0) issue_scales(t);
     __builtin_amdgcn_sched_barrier(0);
-    if (first) half0(std::true_type{}, slot, tok);
-    else half0(std::false_type{}, slot, tok);
-    if (tok) advance(ct, true);
-    if (g + 1 < G) {
-      if (g + 2 >= G) wait_vmcnt<0>();
-      else if (first && g > 0) wait_vmcnt<kGemmLoads + kGemmStores + kGemmScaleLoads>();
+    auto half0 = [&](auto fc) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        mma_one(G0{}, i, fc);
+        __builtin_amdgcn_sched_barrier(0);
+        if (i < 8) {
+          frag_one(slot, G1{}, i);
+        } else if constexpr (tok) {
+          if (i & 1) issue_tokens((i - 8) >> 1);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
+    if (first) half0(std::true_type{});
+    else half0(std::false_type{});
+    if constexpr (tok) advance(ct, true);
+    if constexpr (MODE == 3) {
+      wait_vmcnt<0>();
+      raw_barrier();
+    } else if constexpr (nxt) {
+      if (first && g > 0) wait_vmcnt<kGemmLoads + kGemmStores + kGemmScaleLoads>();
       else wait_vmcnt<kGemmLoads>();
       raw_barrier();
     }
     // second half: K-group 1 MFMAs, K-group 0 fragment reads of stage g + 1, channel-row
     // loads of stage g + 3
-    const bool chn = g + 3 < G;
-    const bool nxt = g + 1 < G;
     wait_lgkm0();
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -697,17 +700,17 @@ __global__ __launch_bounds__(256, 1) void w8a8_gemm_persistent_kernel(
       mma_one(G1{}, i, std::false_type{});
       __builtin_amdgcn_sched_barrier(0);
       if (i < 8) {
-        if (nxt) frag_one((slot + 1) & (NS - 1), G0{}, i);
-      } else if (chn && (i & 1)) {
-        issue_channels((i - 8) >> 1);
+        if constexpr (nxt) frag_one((slot + 1) & (NS - 1), G0{}, i);
+      } else if constexpr (chn) {
+        if (i & 1) issue_channels((i - 8) >> 1);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-    if (chn) advance(cc, false);
+    if constexpr (chn) advance(cc, false);
 
     if (++s == S) {  // epilogue of tile t
       s = 0;
-      if (!nxt) raw_barrier();  // the final stage has no barrier of its own
+      if constexpr (!nxt) raw_barrier();  // the final stage has no barrier of its own
       int64_t m0;
       int n0;
       origin(t, m0, n0);
@@ -756,7 +759,17 @@ __global__ __launch_bounds__(256, 1) void w8a8_gemm_persistent_kernel(
       }
       ++t;
     }
-  }
+  };
+  using M0 = std::integral_constant<int, 0>;
+  using M1 = std::integral_constant<int, 1>;
+  using M2 = std::integral_constant<int, 2>;
+  using M3 = std::integral_constant<int, 3>;
+  using M4 = std::integral_constant<int, 4>;
+  stage(0, M0{});
+  for (int64_t g = 1; g + 3 < G; ++g) stage(g, M1{});
+  stage(G - 3, M2{});
+  stage(G - 2, M3{});
+  stage(G - 1, M4{});
 }
 
 template <int NP>
