@@ -882,8 +882,11 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_ring_kernel(ConvArgs a) {
   wait_vmcnt<0>();
   __syncthreads();
   const T* bias = static_cast<const T*>(a.bias);
-  constexpr int ROWB = NB * 64;  // staged row bytes
-  constexpr int CPR = NB * 4;    // 16-byte chunks per staged row
+  constexpr int ES = static_cast<int>(sizeof(T));
+  constexpr int EPC = 16 / ES;          // elements per 16-byte chunk
+  constexpr int ROWB = NB * 32 * ES;    // staged row bytes
+  constexpr int CPR = ROWB / 16;        // 16-byte chunks per staged row
+  using Quad = std::conditional_t<ES == 2, uint2, u32x4>;  // a lane's 4 consecutive channels
   char* stg = smem + wave * (MB * 32 * ROWB);
   const int cb = n0 + wn * NB * 32;
 #pragma unroll
@@ -904,14 +907,15 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_ring_kernel(ConvArgs a) {
           if (a.act == HI3D_ACT_SILU) x = silu(x);
           h[e] = static_cast<T>(x);
         }
-        uint2 packed;
-        __builtin_memcpy(&packed, h, 8);
-        *reinterpret_cast<uint2*>(stg + row * ROWB + (((j0 >> 3) ^ (row & (CPR - 1))) << 4) + (j0 & 4) * 2) = packed;
+        Quad packed;
+        __builtin_memcpy(&packed, h, sizeof(Quad));
+        const int byte = j0 * ES;  // 16-byte chunk byte / 16, offset byte % 16 inside it
+        *reinterpret_cast<Quad*>(stg + row * ROWB + (((byte >> 4) ^ (row & (CPR - 1))) << 4) + (byte & 15)) = packed;
       }
     }
   }
   wait_lgkm0();
-  const int64_t out_row_bytes = static_cast<int64_t>(a.cout) * sizeof(T);
+  const int64_t out_row_bytes = static_cast<int64_t>(a.cout) * ES;
 #pragma unroll 4
   for (int i = 0; i < MB * 32 * CPR / 64; ++i) {
     const int row = lane / CPR + (64 / CPR) * i;  // within this wave's MB * 32 rows
@@ -922,13 +926,13 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_ring_kernel(ConvArgs a) {
     const int32_t orow = reinterpret_cast<const int32_t*>(rows_lds)[tr];
     if (orow < 0) continue;
     u32x4 v = *reinterpret_cast<const u32x4*>(stg + row * ROWB + ((chunk ^ (row & (CPR - 1))) << 4));
-    const int64_t off = static_cast<int64_t>(orow) * out_row_bytes + static_cast<int64_t>(cb + chunk * 8) * sizeof(T);
+    const int64_t off = static_cast<int64_t>(orow) * out_row_bytes + static_cast<int64_t>(cb + chunk * EPC) * ES;
     if (a.residual != nullptr) {
       const u32x4 r = *reinterpret_cast<const u32x4*>(a.residual + off);
       T* pv = reinterpret_cast<T*>(&v);
       const T* pr = reinterpret_cast<const T*>(&r);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) pv[e] = static_cast<T>(to_f32(pv[e]) + to_f32(pr[e]));
+      for (int e = 0; e < EPC; ++e) pv[e] = static_cast<T>(to_f32(pv[e]) + to_f32(pr[e]));
     }
     *reinterpret_cast<u32x4*>(a.out + off) = v;
   }
@@ -989,6 +993,7 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_wide_kernel(ConvArgs a) {
   constexpr int STAGE = Sh::STAGE, STAGE_A = Sh::STAGE_A, IDX = Sh::IDX;
   constexpr int MB = 2, NB = Sh::NB, NF = MB + NB, NM = MB * NB, KG = 4, LG = L / (KG - 1);
   static_assert(STAGE == 49152 && LG * (KG - 1) == L && LG <= NM && LA * 8 * NW == BM, "stage shape");
+  static_assert(sizeof(T) == 2, "16-bit elements (the epilogue packs four channels into 8 bytes)");
   __shared__ __attribute__((aligned(16))) char smem[NS * STAGE + 3 * IDX + 256];
   char* const idx_ring = smem + NS * STAGE;
   char* const rows_lds = idx_ring + 2 * IDX;  // the tile's output rows
@@ -1277,6 +1282,13 @@ int launch_mfma(const ConvArgs& base, hipStream_t stream) {
       if (rb % 128 == 0) return launch_wide<T, 128, 8>(a, stream);
       return launch_ring<T, 128, 8>(a, stream);
     }
+  }
+  if constexpr (sizeof(T) == 4) {
+    // fp32 (four 32x32x2 MFMAs per fragment): 128-row tiles so that small sets still
+    // spread over every CU (the 45k-voxel C64 shell makes 353 of them)
+    const int rb = a.cin * 4;
+    if (a.kvol <= kMaxPipelinedKvol && (rb == 256 || rb == 512) && (a.cout == 64 || a.cout == 128))
+      return a.cout == 64 ? launch_ring<T, 64, 4, 128>(a, stream) : launch_ring<T, 128, 4, 128>(a, stream);
   }
   if (a.kvol <= kMaxPipelinedKvol) {
     if (a.cout <= 64) return launch_pipe<T, 256, 64, 8>(a, stream);
