@@ -235,6 +235,43 @@ def bench_block(steps: int, warmup: int):
     }
 
 
+def bench_vae(steps: int, warmup: int):
+    """VAE decoder residual block (GroupNorm + swish -> conv, twice, + shortcut) at C64
+    fp16 on the 512^3 fine shells, with its kernels timed apart."""
+    import numpy as np
+    import torch
+
+    from hi3d_amd import kernels, sparse, vae, workloads
+
+    dev = torch.device("cuda:0")
+    idx = workloads.coords_for("down2_up2_c64_c128_fp16", device=dev)
+    level = sparse.Level.from_coords(torch.as_tensor(idx[:, 1:]).to(dev))
+    n, c = level.n, 64
+    x = torch.as_tensor(workloads.normal((n, c), 1.0, 61, np.float16)).to(dev)
+    p = {}
+    for i, name in enumerate(("v.block.0", "v.block.3")):
+        p[f"{name}.weights"] = torch.as_tensor(1.0 + workloads.normal((1, c), 0.1, 62 + i)).to(dev)
+        p[f"{name}.bias"] = torch.as_tensor(workloads.normal((1, c), 0.1, 64 + i)).to(dev)
+    for i, name in enumerate(("v.block.2", "v.block.5")):
+        p[f"{name}.weight"] = torch.as_tensor(workloads.normal((27 * c, c), 1.0 / np.sqrt(27 * c), 66 + i, np.float16)).to(dev)
+        p[f"{name}.bias"] = torch.as_tensor(workloads.normal((c,), 0.02, 68 + i, np.float16)).to(dev)
+    _, st = timed(lambda: vae.group_stats(x), steps, warmup)
+    mean, inv = vae.group_stats(x)
+    _, sw = timed(lambda: kernels.group_norm_swish(x, mean, inv, p["v.block.0.weights"], p["v.block.0.bias"],
+                                                   torch.float16), steps, warmup)
+    b_wall, b_ev = timed(lambda: vae.resnet(x, level, p, "v"), max(3, steps // 5), max(1, warmup // 2))
+    return {
+        "workload": "vae_resnet_c64_fp16",
+        "voxels": n,
+        "block_ms": b_wall,
+        "group_stats_ms": st,
+        "group_stats_gbs": n * c * 2 / (st * 1e-3) / 1e9,
+        "gn_swish_ms": sw,
+        "gn_swish_gbs": 2 * n * c * 2 / (sw * 1e-3) / 1e9,
+        "voxels_per_s": n / (b_wall * 1e-3),
+    }
+
+
 def cpu_baseline(name: str, grid: int, cin: int, cout: int, max_rows: int | None):
     import torch
 
@@ -298,6 +335,8 @@ def main() -> int:
         extra["w8a8_linear"] = bench_w8a8(max(10, args.steps // 2), max(3, args.warmup // 2))
         log("workload 5: residual block C256 fp16, 1024^3 shells")
         extra["resblock_c256_fp16"] = bench_block(max(10, args.steps // 2), max(2, args.warmup // 2))
+        log("VAE decoder residual block C64 fp16, 512^3 fine shells")
+        extra["vae_resnet_c64_fp16"] = bench_vae(max(10, args.steps // 2), max(2, args.warmup // 2))
     cpu = None
     if not args.no_cpu:
         log("CPU baseline (reference CPU fallback, oracle port)")

@@ -56,6 +56,10 @@ _SIGNATURES = {
     "hi3d_w8a8_gemm": [_p, _p, _p, _p, _p, _i64, _i32, _i32, _p, _p, _p],
     "hi3d_layer_norm_modulate": [_p, _i64, _i32, _f32, _p, _p, _p, _p, _p, _p],
     "hi3d_adaln_projection": [_p, _p, _p, _i32, _i32, _i32, _p, _p, _p],
+    "hi3d_group_stats_workspace": [_i64, _i32, _p],
+    "hi3d_group_stats": [_p, _i32, _i64, _i32, _i32, _f32, _p, _i64, _p, _p, _p],
+    "hi3d_gn_swish": [_p, _i32, _i64, _i32, _p, _p, _p, _p, _p, _i32, _p],
+    "hi3d_gather_gn_swish": [_p, _i32, _i64, _i32, _p, _i64, _p, _p, _p, _p, _p, _i32, _p],
 }
 _RESTYPES = {"hi3d_last_error": ctypes.c_char_p, "hi3d_version": ctypes.c_char_p, "hi3d_conv_tile_rows": _i32,
              "hi3d_halo_tile_rows": _i32, "hi3d_halo_capacity": _i32}

@@ -1,8 +1,9 @@
-"""Fused row kernels: LayerNorm (+ adaLN modulation) and the adaLN projection.
+"""Fused row kernels: LayerNorm (+ adaLN modulation), the adaLN projection, and the
+VAE convolution prologue's GroupNorm + swish.
 
 Mirrors ``layer_norm_modulate`` (src/hi3d_mac/mlx_backend/kernels.py:162-237): fp16 rows,
 fp32 two-pass statistics, optional fp32 affine, optional fp16 ``h * scale + shift``
-with two fp16 roundings.
+with two fp16 roundings; and ``gather_group_norm_swish`` (kernels.py:240-296).
 """
 
 from __future__ import annotations
@@ -70,3 +71,54 @@ def adaln_projection(
         _lib.stream(device),
     )
     return scale1p, shift
+
+
+def _vec(v: torch.Tensor, c: int, device: torch.device, what: str) -> torch.Tensor:
+    out = v.to(device=device, dtype=torch.float32).reshape(-1).contiguous()
+    if out.numel() != c:
+        raise ValueError(f"{what} must hold {c} values")
+    return out.clone() if out.data_ptr() % 16 else out
+
+
+def _rows(x: torch.Tensor) -> torch.Tensor:
+    if x.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        raise ValueError(f"unsupported dtype {x.dtype}")
+    if x.dim() != 2:
+        raise ValueError("x must be [n, C]")
+    if x.shape[1] % 8 or x.shape[1] > 2048:
+        raise ValueError("channels must be a multiple of 8, at most 2048")
+    xc = x.contiguous()
+    return xc.clone() if xc.data_ptr() % 16 else xc
+
+
+def group_norm_swish(x: torch.Tensor, mean: torch.Tensor, inv: torch.Tensor, weight: torch.Tensor,
+                     bias: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """``u * sigmoid(u)`` with ``u = (x - mean) * inv * weight + bias`` in float32, per
+    channel, for every row of ``x [n, C]``, returned in ``dtype``: the activation the
+    reference applies while gathering (kernels.py:240-258), once per row."""
+    device = _lib.require_gpu(x)
+    xc = _rows(x)
+    n, c = int(xc.shape[0]), int(xc.shape[1])
+    vecs = [_vec(v, c, device, k) for v, k in ((mean, "mean"), (inv, "inv"), (weight, "weight"), (bias, "bias"))]
+    out = torch.empty((n, c), dtype=dtype, device=device)
+    _lib.call("hi3d_gn_swish", _lib.ptr(xc), _lib.DTYPES[xc.dtype], n, c, *[_lib.ptr(v) for v in vecs],
+              _lib.ptr(out), _lib.DTYPES[dtype], _lib.stream(device))
+    return out
+
+
+def gather_group_norm_swish(x: torch.Tensor, table: torch.Tensor, mean: torch.Tensor, inv: torch.Tensor,
+                            weight: torch.Tensor, bias: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """Convolution input block ``swish(GN(x))[table]`` ``[rows, kvol * C]`` in ``dtype``,
+    zeros where ``table`` holds ``n`` (absent), as ``gather_group_norm_swish``
+    (src/hi3d_mac/mlx_backend/kernels.py:261-296)."""
+    device = _lib.require_gpu(x, table)
+    xc = _rows(x)
+    n, c = int(xc.shape[0]), int(xc.shape[1])
+    t = table.to(torch.int32).contiguous()
+    rows = int(t.shape[0])
+    kvol = int(t.shape[1]) if t.dim() == 2 else 1
+    vecs = [_vec(v, c, device, k) for v, k in ((mean, "mean"), (inv, "inv"), (weight, "weight"), (bias, "bias"))]
+    out = torch.empty((rows, kvol * c), dtype=dtype, device=device)
+    _lib.call("hi3d_gather_gn_swish", _lib.ptr(xc), _lib.DTYPES[xc.dtype], n, c, _lib.ptr(t), rows * kvol,
+              *[_lib.ptr(v) for v in vecs], _lib.ptr(out), _lib.DTYPES[dtype], _lib.stream(device))
+    return out

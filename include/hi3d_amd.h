@@ -233,6 +233,39 @@ int hi3d_w8a8_gemm(const int8_t* q_dev, const float* sa_dev, const int8_t* w_dev
                    const float* sw_dev, const void* bias_dev, int64_t m, int32_t n, int32_t k,
                    void* out_dev, int32_t* acc_dev, void* stream);
 
+/* ------------------------------------------------- VAE GroupNorm + swish -- */
+
+/* Workspace bytes of hi3d_group_stats (per-block partial column sums). */
+int hi3d_group_stats_workspace(int64_t n, int32_t c, int64_t* bytes_host);
+
+/* GroupNorm statistics of x_dev [n, c] (F16 / BF16 / F32, c % 8 == 0, c <= 2048, rows
+ * 16-byte aligned) over `groups` groups of c / groups consecutive channels: per
+ * channel fp32 sums of x and x^2, then per group mean = S1 / (n w + eps),
+ * var = S2 / (n w + eps) - mean^2, inv = 1 / sqrt(var + eps), written per channel to
+ * mean_dev / inv_dev [c] fp32. Replaces SparconvVAEDecoderMLX.group_stats
+ * (src/hi3d_mac/mlx_backend/vae.py:141-164). */
+int hi3d_group_stats(const void* x_dev, int32_t dtype, int64_t n, int32_t c, int32_t groups, float eps,
+                     void* workspace_dev, int64_t workspace_bytes, float* mean_dev, float* inv_dev,
+                     void* stream);
+
+/* out_dev [n, c] (out_dtype) = u * sigmoid(u) with u = ((x - mean) * inv) * weight + bias in
+ * fp32 per channel (mean, inv, weight, bias fp32 [c], 16-byte aligned) and the sigmoid in
+ * the reference's form e = 1 / (1 + exp(|u|)), u < 0 ? e : 1 - e. The activation that
+ * conv_gn_swish applies while gathering (src/hi3d_mac/mlx_backend/vae.py:166-192,
+ * kernels.py:240-258), computed once per row here: the convolution then gathers it. */
+int hi3d_gn_swish(const void* x_dev, int32_t dtype, int64_t n, int32_t c, const float* mean_dev,
+                  const float* inv_dev, const float* weight_dev, const float* bias_dev, void* out_dev,
+                  int32_t out_dtype, void* stream);
+
+/* The same activation gathered through a table: out_dev [entries, c] row j is the
+ * activated row table_dev[j], zeros where table_dev[j] is outside [0, n); with a
+ * [rows, kvol] table this is the [rows, kvol c] block of gather_group_norm_swish
+ * (src/hi3d_mac/mlx_backend/kernels.py:261-296). */
+int hi3d_gather_gn_swish(const void* x_dev, int32_t dtype, int64_t n, int32_t c,
+                         const int32_t* table_dev, int64_t entries, const float* mean_dev,
+                         const float* inv_dev, const float* weight_dev, const float* bias_dev,
+                         void* out_dev, int32_t out_dtype, void* stream);
+
 /* ---------------------------------------------------------- LayerNorm + adaLN -- */
 
 /* Row LayerNorm of x_dev [rows, c] fp16 with fp32 two-pass statistics,

@@ -374,3 +374,46 @@ def test_cpu_baseline_runs_on_a_sample():
     table = okmap.neighbour_table(idx, [10] * 3)
     ref = oconv.gather_conv_f64(feats, table, weight.reshape(6, 27, 8))
     assert oconv.rel_err(got, ref) <= 1e-5
+
+
+def test_vae_group_stats_oracle_against_numpy_moments():
+    """group_stats_f64 against per-group numpy mean / variance of the consecutive-channel
+    groups (the divisor n w + eps differs from n w by 1e-6 / (n w)); group counts of
+    PointGroupNorm (vae.py:152)."""
+    from oracle import vae as ovae
+
+    assert [ovae.groups_for(c) for c in (32, 64, 96, 128, 256, 512)] == [8, 16, 24, 32, 32, 32]
+    rng = np.random.default_rng(21)
+    for c in (64, 256):
+        x = rng.normal(0.7, 2.0, (1500, c))
+        mean, inv = ovae.group_stats_f64(x)
+        g = ovae.groups_for(c)
+        w = c // g
+        for k in range(g):
+            blk = x[:, k * w:(k + 1) * w]
+            assert np.allclose(mean[k * w:(k + 1) * w], blk.mean(), rtol=1e-9, atol=0)
+            assert np.allclose(inv[k * w:(k + 1) * w], 1 / np.sqrt(blk.var() + 1e-6), rtol=1e-8, atol=0)
+
+
+def test_vae_swish_form_and_gathered_block():
+    """The reference's sigmoid form equals the textbook u / (1 + exp(-u)); swish(0) = 0,
+    swish(u) -> u for large u and -> 0 for very negative u; the gathered block puts the
+    activation of row table[o, k] at columns k C .. k C + C - 1 and zeros for absent."""
+    from oracle import vae as ovae
+
+    u = np.linspace(-60.0, 60.0, 2401)
+    assert np.allclose(ovae.swish_reference_form(u), u / (1.0 + np.exp(-u)), rtol=1e-12, atol=1e-300)
+    assert ovae.swish_reference_form(np.array([0.0]))[0] == 0.0
+    assert abs(ovae.swish_reference_form(np.array([40.0]))[0] - 40.0) < 1e-12
+    assert abs(ovae.swish_reference_form(np.array([-40.0]))[0]) < 1e-15
+    rng = np.random.default_rng(22)
+    n, c = 11, 8
+    x = rng.normal(size=(n, c))
+    mean, inv, w, b = rng.normal(size=c), rng.uniform(0.5, 2, c), rng.normal(size=c), rng.normal(size=c)
+    table = rng.integers(0, n + 1, (5, 3))
+    blk = ovae.gather_group_norm_swish(x, table, mean, inv, w, b)
+    for o in range(5):
+        for k in range(3):
+            r = table[o, k]
+            want = np.zeros(c) if r == n else ovae.swish_reference_form(((x[r] - mean) * inv) * w + b)
+            assert np.array_equal(blk[o, k * c:(k + 1) * c], want)
