@@ -1,10 +1,13 @@
-"""VAE decoder convolution prologue: GroupNorm statistics, GroupNorm + swish, and the
-residual block built from them.
+"""VAE decoder convolution prologue (GroupNorm statistics, GroupNorm + swish, the
+residual block built from them) and octree upsampling (occupancy logits, child map,
+child projection).
 
-Mirrors ``SparconvVAEDecoderMLX.group_stats`` / ``conv_gn_swish`` / ``resnet``
-(src/hi3d_mac/mlx_backend/vae.py:141-218) as functions of explicit tensors: ``level`` is
-a :class:`hi3d_amd.sparse.Level`, convolution weights use the MLX GEMM layout
-``[27 * Cin, Cout]`` (``sparse.conv_weight``), GroupNorm affines are ``[1, C]``.
+Mirrors ``SparconvVAEDecoderMLX.group_stats`` / ``conv_gn_swish`` / ``resnet`` /
+``children`` / ``occupancy`` and the upsampling step of ``__call__``
+(src/hi3d_mac/mlx_backend/vae.py:141-244,270-271,316-327) as functions of explicit
+tensors: ``level`` is a :class:`hi3d_amd.sparse.Level`, convolution weights use the MLX
+GEMM layout ``[27 * Cin, Cout]`` (``sparse.conv_weight``), GroupNorm affines are
+``[1, C]``, parameter dictionaries use the reference's names.
 
 The reference activates each gathered neighbour row while building the GEMM input
 block. Here the activation runs once per row (``swish(GN(x))`` ``[n, C]``) and the
@@ -18,10 +21,12 @@ import torch
 
 from . import _lib
 from . import conv as _conv
+from . import kmap as _kmap
 from .kernels import gather_group_norm_swish, group_norm_swish
-from .sparse import Level
+from .sparse import Level, child_neighbour_table
 
-__all__ = ["groups_for", "group_stats", "group_norm_swish", "gather_group_norm_swish", "conv_gn_swish", "resnet"]
+__all__ = ["groups_for", "group_stats", "group_norm_swish", "gather_group_norm_swish", "conv_gn_swish", "resnet",
+           "child_plan", "children", "occupancy", "upsample"]
 
 
 def groups_for(c: int) -> int:
@@ -93,3 +98,72 @@ def resnet(x: torch.Tensor, level: Level, params: dict, name: str, eps: float = 
     return conv_gn_swish(h, level, p[f"{name}.block.3.weights"], p[f"{name}.block.3.bias"],
                          p[f"{name}.block.5.weight"], p[f"{name}.block.5.bias"], out=h.dtype,
                          residual=shortcut, eps=eps)
+
+
+def child_plan(parent: torch.Tensor, slot: torch.Tensor, n_parents: int) -> _kmap.ConvPlan:
+    """Gather plan of the child projection over ``n_parents`` parent rows: table
+    ``[C, 8]`` holding child ``i``'s parent in column ``slot[i]`` (absent elsewhere), rows
+    grouped by slot in child order, so every 128-row tile but the (at most seven) tiles
+    that straddle two slots multiplies by one slot's matrix only."""
+    device = _lib.require_gpu(parent, slot)
+    n = int(parent.shape[0])
+    if slot.shape[0] != n:
+        raise ValueError("parent and slot must have one entry per child")
+    par = parent.to(torch.int32).contiguous()
+    sl = slot.to(torch.uint8).contiguous()
+    up = torch.empty((n, 8), dtype=torch.int32, device=device)
+    if n:
+        _lib.call("hi3d_stride2_tables", _lib.ptr(par), _lib.ptr(sl), n, int(n_parents), None, _lib.ptr(up),
+                  _lib.stream(device))
+    return _kmap.build_plan(up, int(n_parents), None, window_rows=0)
+
+
+def children(x: torch.Tensor, parent: torch.Tensor, slot: torch.Tensor, weight: torch.Tensor,
+             out: torch.dtype | None = None, plan: _kmap.ConvPlan | None = None) -> torch.Tensor:
+    """``SerializedUnpooling`` features of the kept children (vae.py:220-244): child
+    ``(p, s)`` is ``x[p] @ weight[s*C:(s+1)*C].T``, row ``p * 8 + s`` of the full
+    projection ``(x @ weight.T).reshape(-1, C)`` for ``weight [8C, C]``, in child order.
+    Only the kept children are computed (one slot matrix per child, fp32 accumulation,
+    result rounded to ``weight.dtype`` and then to ``out``)."""
+    _lib.require_gpu(x, parent, slot, weight)
+    if x.dim() != 2:
+        raise ValueError("x must be [P, C]")
+    p, c = int(x.shape[0]), int(x.shape[1])
+    if tuple(weight.shape) != (8 * c, c):
+        raise ValueError(f"weight must be [8C, C] = [{8 * c}, {c}], got {tuple(weight.shape)}")
+    out = weight.dtype if out is None else out
+    n = int(parent.shape[0])
+    if n == 0:
+        return torch.empty((0, c), dtype=out, device=x.device)
+    if plan is None:
+        plan = child_plan(parent, slot, p)
+    w = weight.reshape(8, c, c).permute(1, 0, 2).contiguous()  # [C_out, slot, C_in]
+    y = _conv.conv(x.to(weight.dtype).contiguous(), plan, w, None)
+    return y if y.dtype == out else y.to(out)
+
+
+def occupancy(x: torch.Tensor, level: Level, params: dict, name: str, eps: float = 1e-6) -> torch.Tensor:
+    """Child occupancy logits ``[P, 8]`` of ``SparseClsHead`` (vae.py:270-271): GroupNorm
+    ``{name}.cls_head.fc.0``, swish and the 3x3x3 convolution ``{name}.cls_head.fc.2``."""
+    p = params
+    return conv_gn_swish(x, level, p[f"{name}.cls_head.fc.0.weights"], p[f"{name}.cls_head.fc.0.bias"],
+                         p[f"{name}.cls_head.fc.2.weight"], p[f"{name}.cls_head.fc.2.bias"], eps=eps)
+
+
+def upsample(x: torch.Tensor, level: Level, params: dict, name: str, out: torch.dtype | None = None,
+             mask: torch.Tensor | None = None, eps: float = 1e-6) -> tuple[torch.Tensor, Level, torch.Tensor]:
+    """One octree upsampling of the decoder (vae.py:316-327): occupancy logits, children
+    where a logit is positive (or the given ``[P, 8]`` ``mask``), their neighbour table
+    from the parent table, their projected features and coordinates
+    ``coords[parent] * 2 + (s >> 2 & 1, s >> 1 & 1, s & 1)``.
+    Returns ``(features [C, ch], Level of the children, mask [P, 8])``."""
+    if mask is None:
+        mask = occupancy(x, level, params, name, eps) > 0
+    table, parent, slot = child_neighbour_table(level.table, mask)
+    w = params[f"{name}.proj.weight"]
+    y = children(x, parent, slot, w, out=out if out is not None else x.dtype)
+    coords = level.coords.to(table.device, torch.int32)
+    sl = slot.to(torch.int32)
+    bits = torch.stack([(sl >> 2) & 1, (sl >> 1) & 1, sl & 1], 1)
+    child_coords = coords[parent.long()] * 2 + bits
+    return y, Level(child_coords, table), mask

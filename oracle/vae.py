@@ -1,10 +1,11 @@
-"""VAE convolution prologue oracle (NumPy): GroupNorm statistics, GroupNorm + swish,
-the gathered activation block, and the residual block built from them. Test
+"""VAE decoder oracle (NumPy): GroupNorm statistics, GroupNorm + swish, the gathered
+activation block, the residual block built from them, and one octree upsampling
+(occupancy logits, child map, child projection, child coordinates). Test
 infrastructure only.
 
-Follows SparconvVAEDecoderMLX.group_stats / conv_gn_swish / resnet
-(src/hi3d_mac/mlx_backend/vae.py:141-218) and gather_group_norm_swish
-(src/hi3d_mac/mlx_backend/kernels.py:240-296).
+Follows SparconvVAEDecoderMLX.group_stats / conv_gn_swish / resnet / children /
+occupancy and the upsampling step of __call__ (src/hi3d_mac/mlx_backend/vae.py:141-244,
+270-271,316-327) and gather_group_norm_swish (src/hi3d_mac/mlx_backend/kernels.py:240-296).
 """
 
 from __future__ import annotations
@@ -12,6 +13,7 @@ from __future__ import annotations
 import numpy as np
 
 from .conv import gather_conv_f64
+from .kmap import child_neighbour_table
 
 
 def groups_for(c: int) -> int:
@@ -84,3 +86,39 @@ def resnet_f64(x, table, p: dict, name: str, eps: float = 1e-6):
         shortcut = x64
     return conv_gn_swish_f64(h, table, f(f"{name}.block.3.weights"), f(f"{name}.block.3.bias"),
                              f(f"{name}.block.5.weight"), f(f"{name}.block.5.bias"), residual=shortcut, eps=eps)
+
+
+def children_f64(x, parent, slot, weight):
+    """Kept children's features in float64 the reference's way (vae.py:220-244): project
+    every parent to all eight children, ``(x @ weight.T).reshape(-1, C)`` with
+    ``weight [8C, C]``, and take rows ``parent * 8 + slot``."""
+    x = np.asarray(x, np.float64)
+    c = x.shape[1]
+    proj = (x @ np.asarray(weight, np.float64).T).reshape(-1, c)
+    flat = np.asarray(parent, np.int64) * 8 + np.asarray(slot, np.int64)
+    return proj[flat]
+
+
+def child_coords(coords, parent, slot):
+    """``coords[parent] * 2 + (s >> 2 & 1, s >> 1 & 1, s & 1)`` (vae.py:324-325)."""
+    s = np.asarray(slot, np.int64)
+    bits = np.stack([(s >> 2) & 1, (s >> 1) & 1, s & 1], 1)
+    return (np.asarray(coords, np.int64)[np.asarray(parent, np.int64)] * 2 + bits).astype(np.int32)
+
+
+def occupancy_f64(x, table, p: dict, name: str, eps: float = 1e-6):
+    """``SparseClsHead`` logits ``[P, 8]`` in float64 (vae.py:270-271)."""
+    f = lambda k: np.asarray(p[k], np.float64)
+    return conv_gn_swish_f64(x, table, f(f"{name}.cls_head.fc.0.weights"), f(f"{name}.cls_head.fc.0.bias"),
+                             f(f"{name}.cls_head.fc.2.weight"), f(f"{name}.cls_head.fc.2.bias"), eps=eps)
+
+
+def upsample_f64(x, coords, table, p: dict, name: str, mask=None, eps: float = 1e-6):
+    """One decoder upsampling (vae.py:316-327) in float64: ``mask = logits > 0`` unless
+    given, then the child table, parent and slot, the children's features and
+    coordinates. Returns ``(features, coords, table, parent, slot, mask)``."""
+    if mask is None:
+        mask = occupancy_f64(x, table, p, name, eps) > 0
+    ctable, parent, slot = child_neighbour_table(np.asarray(table), np.asarray(mask, bool))
+    feats = children_f64(x, parent, slot, p[f"{name}.proj.weight"])
+    return feats, child_coords(coords, parent, slot), ctable, parent, slot, mask

@@ -1,9 +1,12 @@
-"""VAE convolution prologue on the GPU: GroupNorm statistics, GroupNorm + swish (per row
-and gathered), and the conv_gn_swish / resnet compositions against the float64 oracle
-(src/hi3d_mac/mlx_backend/vae.py:141-218, kernels.py:240-296). Gates: statistics to
-fp32 rounding (rel 1e-5); activations 1e-5 (fp32) / 2e-3 (fp16), the reference test's
-tolerances (tests/test_mlx_kernels.py:63-76); convolutions max-abs / RMS <= 1e-5 (fp32),
-1e-2 (fp16); the residual block <= 1e-4 (fp32, two chained GroupNorms)."""
+"""VAE decoder pieces on the GPU: GroupNorm statistics, GroupNorm + swish (per row and
+gathered), the conv_gn_swish / resnet compositions, and octree upsampling (occupancy
+logits, child map, child projection) against the float64 oracle
+(src/hi3d_mac/mlx_backend/vae.py:141-244,316-327, kernels.py:240-296). Gates:
+statistics to fp32 rounding (rel 1e-5); activations 1e-5 (fp32) / 2e-3 (fp16), the
+reference test's tolerances (tests/test_mlx_kernels.py:63-76); convolutions and
+projections max-abs / RMS <= 1e-5 (fp32), 1e-2 (fp16), 3e-2 (bf16); the residual block
+<= 1e-4 (fp32, two chained GroupNorms); child tables, parents, slots and coordinates
+exact."""
 
 from __future__ import annotations
 
@@ -125,3 +128,120 @@ def test_resnet_matches_float64(cuda, with_res_conv):
     got = vae.resnet(torch.as_tensor(x).to(cuda), level, gp, "r").cpu().numpy()
     ref = ovae.resnet_f64(x, table, p, "r")
     assert oconv.rel_err(got, ref) <= 1e-4
+
+
+GATE = {torch.float32: 1e-5, torch.float16: 1e-2, torch.bfloat16: 3e-2}
+
+
+def _children_case(cuda, p, c, density, seed):
+    """Parents with random occupancy and the child map of a random parent table."""
+    from hi3d_amd import sparse
+
+    rng = np.random.default_rng(seed)
+    mask = rng.random((p, 8)) < density
+    table = rng.integers(0, p + 1, (p, 27)).astype(np.int32)
+    _, parent, slot = sparse.child_neighbour_table(torch.as_tensor(table).to(cuda), torch.as_tensor(mask).to(cuda))
+    return rng, mask, parent, slot
+
+
+@pytest.mark.parametrize("dtype,c", [(torch.float16, 64), (torch.float16, 256), (torch.float16, 512),
+                                     (torch.bfloat16, 128), (torch.float32, 512)])
+def test_children_slot_layout_exact(cuda, dtype, c):
+    """A weight stacking ``s * I`` per slot makes child ``(p, s)`` equal ``s * x[p]``
+    exactly (small integers): every child's row, slot block and order, bit for bit."""
+    from hi3d_amd import vae
+
+    rng, _, parent, slot = _children_case(cuda, 700, c, 0.5, c)
+    x = torch.as_tensor(rng.integers(-8, 9, (700, c)).astype(np.float32)).to(cuda).to(dtype)
+    w = torch.cat([s * torch.eye(c, device=cuda) for s in range(8)]).to(dtype)
+    got = vae.children(x, parent, slot, w)
+    want = slot.to(dtype)[:, None] * x[parent.long()]
+    assert got.dtype == dtype and torch.equal(got, want)
+
+
+@pytest.mark.parametrize("dtype,c,p,density", [(torch.float16, 128, 3000, 0.5), (torch.float16, 256, 2500, 0.3),
+                                               (torch.float16, 512, 1500, 0.6), (torch.bfloat16, 256, 2000, 0.5),
+                                               (torch.float32, 64, 3000, 0.5), (torch.float32, 256, 1200, 0.4),
+                                               (torch.float32, 512, 900, 0.5)])
+def test_children_matches_float64(cuda, dtype, c, p, density):
+    """Kept children's projected features against the reference's full projection and
+    take (vae.py:220-244), at the decoder's projection widths (512, 512, 256) and
+    narrower ones; output in the weight dtype and converted to fp32 on request."""
+    from hi3d_amd import vae
+
+    rng, mask, parent, slot = _children_case(cuda, p, c, density, p + c)
+    x = torch.as_tensor(rng.normal(0, 1, (p, c)).astype(np.float32)).to(cuda).to(dtype)
+    w = torch.as_tensor(rng.normal(0, c ** -0.5, (8 * c, c)).astype(np.float32)).to(cuda).to(dtype)
+    got = vae.children(x, parent, slot, w)
+    ref = ovae.children_f64(x.float().cpu().numpy(), parent.cpu().numpy(), slot.cpu().numpy(), w.float().cpu().numpy())
+    assert got.shape == (int(mask.sum()), c) and got.dtype == dtype
+    assert oconv.rel_err(got.float().cpu().numpy(), ref) <= GATE[dtype]
+    as_f32 = vae.children(x, parent, slot, w, out=torch.float32)
+    assert as_f32.dtype == torch.float32 and torch.equal(as_f32, got.float())
+
+
+def _upsample_params(rng, c, wdt):
+    p = {
+        "u.cls_head.fc.0.weights": rng.uniform(0.5, 1.5, (1, c)).astype(np.float32),
+        "u.cls_head.fc.0.bias": rng.normal(0, 0.1, (1, c)).astype(np.float32),
+        "u.cls_head.fc.2.weight": rng.normal(0, (27 * c) ** -0.5, (27 * c, 8)).astype(np.float32),
+        "u.cls_head.fc.2.bias": rng.normal(0, 0.3, (8,)).astype(np.float32),
+        "u.proj.weight": rng.normal(0, c ** -0.5, (8 * c, c)).astype(np.float32),
+    }
+    gemm = ("u.cls_head.fc.2.weight", "u.cls_head.fc.2.bias", "u.proj.weight")
+    gp = {k: torch.as_tensor(v).to(wdt if k in gemm else torch.float32) for k, v in p.items()}
+    return {k: v.float().numpy() for k, v in gp.items()}, gp
+
+
+@pytest.mark.parametrize("dtype,c", [(torch.float32, 64), (torch.float16, 128), (torch.float32, 256)])
+def test_upsample_matches_float64(cuda, dtype, c):
+    """One decoder upsampling (vae.py:316-327) on a 16^3 cube at density 0.5: occupancy
+    logits against float64 (the decision ``> 0`` agrees wherever the float64 logit is
+    clear of zero by the gate), then, on the GPU's own mask, child table, parents,
+    slots and coordinates exact and projected features within the gate."""
+    from hi3d_amd import vae
+
+    coords, level = _level(cuda)
+    table = level.table.cpu().numpy()
+    rng = np.random.default_rng(c)
+    p, gp = _upsample_params(rng, c, dtype)
+    gp = {k: v.to(cuda) for k, v in gp.items()}
+    x = torch.as_tensor(rng.normal(0, 1, (len(coords), c)).astype(np.float32)).to(cuda).to(dtype)
+    xr = x.float().cpu().numpy()
+    logits = vae.occupancy(x, level, gp, "u")
+    ref_logits = ovae.occupancy_f64(xr, table, p, "u")
+    assert oconv.rel_err(logits.float().cpu().numpy(), ref_logits) <= GATE[dtype]
+    y, child, mask = vae.upsample(x, level, gp, "u")
+    m = mask.cpu().numpy()
+    clear = np.abs(ref_logits) > 4 * GATE[dtype] * np.sqrt(np.mean(ref_logits ** 2))
+    assert np.array_equal(m[clear], ref_logits[clear] > 0)
+    assert 0.2 < m.mean() < 0.8
+    feats, ccoords, ctable, parent, slot, _ = ovae.upsample_f64(xr, coords, table, p, "u", mask=m)
+    assert np.array_equal(child.table.cpu().numpy(), ctable)
+    assert np.array_equal(child.coords.cpu().numpy(), ccoords)
+    assert y.dtype == dtype and oconv.rel_err(y.float().cpu().numpy(), feats) <= GATE[dtype]
+    # the children's own map is what a fresh hash of their coordinates gives
+    from hi3d_amd import sparse
+
+    assert torch.equal(sparse.neighbour_table(child.coords), child.table)
+
+
+def test_upsample_with_given_and_empty_masks(cuda):
+    """A caller's mask replaces the occupancy decision (the reference's force_masks,
+    vae.py:318-320); an all-empty mask yields no children."""
+    from hi3d_amd import vae
+
+    coords, level = _level(cuda, side=8)
+    rng = np.random.default_rng(9)
+    c = 64
+    p, gp = _upsample_params(rng, c, torch.float16)
+    gp = {k: v.to(cuda) for k, v in gp.items()}
+    x = torch.as_tensor(rng.normal(0, 1, (len(coords), c)).astype(np.float16)).to(cuda)
+    m = rng.random((len(coords), 8)) < 0.25
+    y, child, mask = vae.upsample(x, level, gp, "u", mask=torch.as_tensor(m).to(cuda))
+    feats, ccoords, ctable, _, _, _ = ovae.upsample_f64(x.float().cpu().numpy(), coords, level.table.cpu().numpy(),
+                                                       p, "u", mask=m)
+    assert np.array_equal(child.coords.cpu().numpy(), ccoords) and np.array_equal(child.table.cpu().numpy(), ctable)
+    assert oconv.rel_err(y.float().cpu().numpy(), feats) <= 1e-2
+    y, child, _ = vae.upsample(x, level, gp, "u", mask=torch.zeros((len(coords), 8), dtype=torch.bool, device=cuda))
+    assert y.shape == (0, c) and child.n == 0 and child.table.shape == (0, 27)

@@ -417,3 +417,43 @@ def test_vae_swish_form_and_gathered_block():
             r = table[o, k]
             want = np.zeros(c) if r == n else ovae.swish_reference_form(((x[r] - mean) * inv) * w + b)
             assert np.array_equal(blk[o, k * c:(k + 1) * c], want)
+
+
+def test_vae_children_oracle_slot_layout():
+    """The child projection oracle against three independent forms: a weight stacking
+    ``s * I`` per slot gives ``slot * x[parent]`` (a transposed or reordered block layout
+    fails this), a per-child product with that slot's ``[C, C]`` block, and
+    SerializedUnpooling's own masking of the full projection ``feat.view(8P, C)[mask]``
+    (src/sparc3d/models/autoencoders/blocks.py:535-543) with the mask flattened
+    parent-major."""
+    from oracle import vae as ovae
+
+    rng = np.random.default_rng(31)
+    p, c = 9, 6
+    x = rng.integers(-4, 5, size=(p, c)).astype(np.float64)
+    mask = rng.random((p, 8)) < 0.5
+    table = rng.integers(0, p + 1, (p, 27)).astype(np.int32)
+    _, parent, slot = okmap.child_neighbour_table(table, mask)
+    eye = np.concatenate([s * np.eye(c) for s in range(8)])
+    got = ovae.children_f64(x, parent, slot, eye)
+    assert np.array_equal(got, slot[:, None] * x[parent])
+    w = rng.normal(size=(8 * c, c))
+    got = ovae.children_f64(x, parent, slot, w)
+    for i in range(parent.size):
+        s = slot[i]
+        assert np.allclose(got[i], w[s * c:(s + 1) * c] @ x[parent[i]], rtol=1e-13, atol=1e-13)
+    feat = x @ w.T
+    assert np.array_equal(feat.reshape(p * 8, c)[mask.reshape(-1)], got)
+
+
+def test_vae_child_coords_match_unpooling_grid():
+    """Child coordinates against SerializedUnpooling's ``inv_grid_coord`` table
+    (src/sparc3d/models/autoencoders/blocks.py:526-533): ``coords * 2 + inv_grid[slot]``."""
+    from oracle import vae as ovae
+
+    inv_grid = np.array([[0, 0, 0], [0, 0, 1], [0, 1, 0], [0, 1, 1], [1, 0, 0], [1, 0, 1], [1, 1, 0], [1, 1, 1]])
+    rng = np.random.default_rng(32)
+    coords = rng.integers(0, 50, (20, 3)).astype(np.int32)
+    parent = rng.integers(0, 20, 40)
+    slot = rng.integers(0, 8, 40)
+    assert np.array_equal(ovae.child_coords(coords, parent, slot), coords[parent] * 2 + inv_grid[slot])
