@@ -1,0 +1,272 @@
+// Gather convolution with at most 16 output channels (octree occupancy heads, output
+// layers):
+//
+//   out[o] = act(bias + sum_k in[table[o, k]] . W[:, k, :]^T)  (+ residual[o] after act)
+//
+// The tile kernels of conv.hip compute 64..256 output channels per tile; with 8 output
+// channels most of their MFMA work and all of their weight staging would be padding.
+// Here one wave owns 64 output rows (half a plan tile; the plan groups rows by their
+// neighbour-presence mask, so the rows of a wave mostly share one mask) as four 16-row
+// groups and multiplies with 16x16 MFMAs: the weights are the first operand (output
+// channels as the 16 rows, zeros past cout), the gathered input rows the second, so
+// lane l's four accumulators of group g are output channels 4*(l/16)..+3 of row slot
+// 16*g + l%16. A K step is 64 bytes of every row: lane l reads the 16 bytes at byte
+// 16*(l/16) + 64*step of its row for both operands (the contraction only needs both
+// operands to split K the same way). Offsets that none of the wave's 64 rows has are
+// skipped (a wave-uniform mask); absent entries of a present offset read a 16-byte
+// zero vector. Loads go straight to registers, two stages deep; the wave's gather
+// indices sit in LDS ([offset][64 rows], 16 consecutive words per read).
+//
+// Replaces the occupancy head's dense gathered GEMM (SparseClsHead, Conv3d(C, 8):
+// src/hi3d_mac/mlx_backend/vae.py:270-271,166-192; src/sparc3d/models/autoencoders/
+// blocks.py:181-197).
+
+#include "common.h"
+#include "conv_tile.h"
+
+namespace hi3d {
+namespace {
+
+constexpr int kNarrowWaves = 4;
+constexpr int kNarrowRows = 64;        // output rows per wave
+constexpr int kNarrowMaxKvol = 32;
+constexpr int kNarrowMaxCout = 16;
+
+__device__ __attribute__((aligned(16))) const uint32_t g_narrow_zero[4] = {0u, 0u, 0u, 0u};
+
+// One 64-byte K step of a 16x16 block: 16 bytes per lane per operand.
+template <typename T>
+struct Mfma16;
+
+template <>
+struct Mfma16<_Float16> {
+  __device__ __forceinline__ static void run(u32x4 a, u32x4 b, f32x4& c) {
+    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+};
+
+template <>
+struct Mfma16<__bf16> {
+  __device__ __forceinline__ static void run(u32x4 a, u32x4 b, f32x4& c) {
+    c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0,
+                                                0);
+  }
+};
+
+// fp32: the 16 bytes are 4 consecutive K values, one 16x16x4 MFMA each.
+template <>
+struct Mfma16<float> {
+  __device__ __forceinline__ static void run(u32x4 a, u32x4 b, f32x4& c) {
+    const f32x4 af = __builtin_bit_cast(f32x4, a), bf = __builtin_bit_cast(f32x4, b);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(af[0], bf[0], c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(af[1], bf[1], c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(af[2], bf[2], c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(af[3], bf[3], c, 0, 0, 0);
+  }
+};
+
+// 16-byte load through a global-address-space pointer (the opaque select of a gathered
+// row and the zero vector would otherwise become a flat access, which also counts in
+// the LDS counter and makes every wait a full drain).
+__device__ __forceinline__ u32x4 gload16(const char* p) {
+  return *(const __attribute__((address_space(1))) u32x4*)(p);
+}
+
+struct NarrowArgs {
+  const char* in;
+  const char* w;
+  const void* bias;
+  const void* residual;
+  const int32_t* rows;
+  const int32_t* gidx;
+  void* out;
+  int64_t n_in;
+  int64_t n_out;
+  int64_t ntiles;
+  int32_t cin;
+  int32_t cout;
+  int32_t kvol;
+  int32_t act;
+};
+
+template <typename T>
+__device__ __forceinline__ float narrow_f32(T v) {
+  return static_cast<float>(v);
+}
+
+// A stage is CH K steps (64 bytes each) of one present offset: 4 gathered 16-byte
+// loads per step (one per 16-row group) and one weight load. Two stages are in flight:
+// the loads of stage s + 1 are issued before stage s is multiplied.
+template <typename T, int CH>
+__global__ __launch_bounds__(kNarrowWaves * 64) void conv_narrow_kernel(NarrowArgs a) {
+  __shared__ int32_t entries[kNarrowWaves][kNarrowRows * kNarrowMaxKvol];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  // consecutive wave tiles on one XCD, so that neighbouring rows share its L2
+  const int64_t wt = xcd_remap(blockIdx.x, static_cast<int64_t>(gridDim.x)) * kNarrowWaves + wave;
+  if (wt >= 2 * a.ntiles) return;  // wave-uniform
+  const int64_t slot0 = wt * kNarrowRows;  // first row slot of this wave in the plan
+  const int64_t tile = wt >> 1;
+  const int half = static_cast<int>(wt & 1);
+  const int kvol = a.kvol;
+  const uint64_t n_in = static_cast<uint64_t>(a.n_in);
+  int32_t* ent = entries[wave];
+
+  // the wave's gather indices into LDS ([offset][64 rows]) and the offsets any of its
+  // rows has
+  uint32_t present = 0;
+  const int32_t* gsrc = a.gidx + tile * kvol * kTileRows + half * kNarrowRows + lane;
+  for (int k = 0; k < kvol; ++k) {
+    const int32_t e = gsrc[k * kTileRows];
+    ent[k * kNarrowRows + lane] = e;
+    const bool ok = static_cast<uint64_t>(static_cast<uint32_t>(e)) < n_in;
+    present |= __builtin_amdgcn_ballot_w64(ok) != 0 ? (1u << k) : 0u;
+  }
+  present = __builtin_amdgcn_readfirstlane(present);
+  wait_lgkm0();  // the wave reads entries other lanes wrote; only this wave uses its region
+  __builtin_amdgcn_wave_barrier();
+
+  const int r = lane & 15, q = lane >> 4;
+  const int rb = a.cin * static_cast<int>(sizeof(T));
+  const int nch = rb / (64 * CH);
+  const char* const zero = reinterpret_cast<const char*>(g_narrow_zero);
+  const bool wrow = r < a.cout;
+  f32x4 acc[4];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) acc[g] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // stage loads; absent rows (and weight rows past cout) read the zero vector
+  auto load = [&](u32x4(&wv)[CH], u32x4(&xv)[CH][4], int k, int c) {
+    const int byte0 = c * CH * 64;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int32_t e = ent[k * kNarrowRows + 16 * g + r];
+      const bool ok = static_cast<uint64_t>(static_cast<uint32_t>(e)) < n_in;
+      uint64_t pin = reinterpret_cast<uint64_t>(a.in) +
+                     static_cast<uint64_t>(static_cast<int64_t>(e) * rb + 16 * q + byte0);
+      asm volatile("" : "+v"(pin));
+      const char* src = ok ? reinterpret_cast<const char*>(pin) : zero;
+      const int step = ok ? 64 : 0;
+#pragma unroll
+      for (int cc = 0; cc < CH; ++cc) xv[cc][g] = gload16(src + cc * step);
+    }
+    uint64_t wpin = reinterpret_cast<uint64_t>(a.w) +
+                    static_cast<uint64_t>((static_cast<int64_t>(r) * kvol + k) * rb + 16 * q + byte0);
+    asm volatile("" : "+v"(wpin));
+    const char* wsrc = wrow ? reinterpret_cast<const char*>(wpin) : zero;
+    const int wstep = wrow ? 64 : 0;
+#pragma unroll
+    for (int cc = 0; cc < CH; ++cc) wv[cc] = gload16(wsrc + cc * wstep);
+  };
+  auto compute = [&](const u32x4(&wv)[CH], const u32x4(&xv)[CH][4]) {
+#pragma unroll
+    for (int cc = 0; cc < CH; ++cc) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) Mfma16<T>::run(wv[cc], xv[cc][g], acc[g]);
+    }
+  };
+
+  const int S = __builtin_popcount(present) * nch;
+  if (S > 0) {
+    // load cursor; past the last stage it stays there (the extra loads are discarded)
+    int kl = __builtin_ctz(present), cl = 0;
+    uint32_t rest = present & (present - 1u);
+    auto advance = [&]() {
+      if (++cl == nch) {
+        if (rest) {
+          cl = 0;
+          kl = __builtin_ctz(rest);
+          rest &= rest - 1u;
+        } else {
+          cl = nch - 1;
+        }
+      }
+    };
+    u32x4 wA[CH], xA[CH][4], wB[CH], xB[CH][4];
+    load(wA, xA, kl, cl);
+    advance();
+    // two stages per trip with no exit in between, so the only loads in flight at the
+    // top of a trip are those of the stage in A (a mid-trip exit would merge a path
+    // with B's loads still in flight into the back edge and make every wait a drain)
+    int s = 0;
+    for (; s + 2 <= S; s += 2) {
+      load(wB, xB, kl, cl);
+      advance();
+      compute(wA, xA);
+      load(wA, xA, kl, cl);
+      advance();
+      compute(wB, xB);
+    }
+    if (s < S) compute(wA, xA);  // odd stage count: the last stage is in A
+  }
+
+  // epilogue: lane holds channels 4q..4q+3 of row slot 16g + r
+  const T* bias = static_cast<const T*>(a.bias);
+  const T* res = static_cast<const T*>(a.residual);
+  T* out = static_cast<T*>(a.out);
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int32_t o = a.rows[slot0 + 16 * g + r];
+    if (o < 0 || o >= a.n_out) continue;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int j = 4 * q + i;
+      if (j >= a.cout) continue;
+      float v = acc[g][i];
+      if (bias) v += narrow_f32(bias[j]);
+      if (a.act == HI3D_ACT_SILU) v = v / (1.0f + expf(-v));
+      T t = static_cast<T>(v);
+      const int64_t at = static_cast<int64_t>(o) * a.cout + j;
+      if (res) t = static_cast<T>(narrow_f32(t) + narrow_f32(res[at]));
+      out[at] = t;
+    }
+  }
+}
+
+template <typename T>
+int launch_narrow(const NarrowArgs& a, hipStream_t stream) {
+  const int64_t blocks = ceil_div(2 * a.ntiles, kNarrowWaves);
+  HI3D_REQUIRE(blocks < (int64_t(1) << 31), "too many tiles");
+  const int steps = a.cin * static_cast<int>(sizeof(T)) / 64;
+  const dim3 grid(static_cast<unsigned>(blocks)), block(kNarrowWaves * 64);
+  if (steps % 2 == 0) {
+    hipLaunchKernelGGL((conv_narrow_kernel<T, 2>), grid, block, 0, stream, a);
+  } else {
+    hipLaunchKernelGGL((conv_narrow_kernel<T, 1>), grid, block, 0, stream, a);
+  }
+  HI3D_LAUNCH_CHECK();
+  return HI3D_OK;
+}
+
+}  // namespace
+}  // namespace hi3d
+
+using namespace hi3d;
+
+extern "C" int hi3d_gather_conv_narrow(const void* in, int64_t n_in, int32_t cin, const void* weight,
+                                       const void* bias, int32_t cout, int32_t kvol, const int32_t* rows,
+                                       const int32_t* gidx, const uint32_t* tile_mask, int64_t n_out,
+                                       const void* residual, int32_t act, int32_t dtype, void* out, void* stream) {
+  (void)tile_mask;  // each wave derives the mask of its own 64 rows from gidx
+  HI3D_REQUIRE(dtype == HI3D_F16 || dtype == HI3D_BF16 || dtype == HI3D_F32, "narrow conv takes F16, BF16 or F32");
+  const int es = dtype == HI3D_F32 ? 4 : 2;
+  HI3D_REQUIRE(cout >= 1 && cout <= kNarrowMaxCout, "narrow conv takes 1..16 output channels, got %d", cout);
+  HI3D_REQUIRE(kvol >= 1 && kvol <= kNarrowMaxKvol, "narrow conv takes 1..32 kernel offsets, got %d", kvol);
+  HI3D_REQUIRE(cin > 0 && (static_cast<int64_t>(cin) * es) % 64 == 0,
+               "narrow conv needs input rows of a multiple of 64 bytes (cin %d)", cin);
+  HI3D_REQUIRE(n_in >= 0 && n_out >= 0 && n_in < (int64_t(1) << 31) - 1 && n_out < (int64_t(1) << 31) - 1,
+               "bad sizes");
+  HI3D_REQUIRE(act == HI3D_ACT_NONE || act == HI3D_ACT_SILU, "unknown activation %d", act);
+  if (n_out == 0) return HI3D_OK;
+  HI3D_REQUIRE(in && weight && rows && gidx && out, "null pointer argument");
+  HI3D_REQUIRE(reinterpret_cast<uintptr_t>(in) % 16 == 0 && reinterpret_cast<uintptr_t>(weight) % 16 == 0,
+               "input and weight must be 16-byte aligned");
+  NarrowArgs a{static_cast<const char*>(in), static_cast<const char*>(weight), bias, residual, rows, gidx, out,
+               n_in, n_out, ceil_div(n_out, kTileRows), cin, cout, kvol, act};
+  hipStream_t s = as_stream(stream);
+  switch (dtype) {
+    case HI3D_F16: return launch_narrow<_Float16>(a, s);
+    case HI3D_BF16: return launch_narrow<__bf16>(a, s);
+    default: return launch_narrow<float>(a, s);
+  }
+}

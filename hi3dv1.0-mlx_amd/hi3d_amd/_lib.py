@@ -46,6 +46,7 @@ _SIGNATURES = {
     "hi3d_conv_plan": [_p, _i64, _i32, _i64, _p, _i64, _p, _i64, _p, _p, _p, _p],
     "hi3d_gather_conv": [_p, _i64, _i32, _p, _p, _i32, _i32, _p, _p, _p, _i64, _p, _i32, _i32, _p, _p],
     "hi3d_gather_conv_simple": [_p, _i64, _i32, _p, _p, _i32, _i32, _p, _i64, _p, _i32, _i32, _p, _p],
+    "hi3d_gather_conv_narrow": [_p, _i64, _i32, _p, _p, _i32, _i32, _p, _p, _p, _i64, _p, _i32, _i32, _p, _p],
     "hi3d_gather_mean": [_p, _i64, _i32, _p, _i32, _i64, _i32, _i32, _p, _p],
     "hi3d_halo_tile_rows": [],
     "hi3d_halo_capacity": [],

@@ -100,6 +100,55 @@ def gather_conv(
     return out
 
 
+def narrow_supported(dtype: torch.dtype, cin: int, cout: int, kvol: int) -> bool:
+    """Whether the narrow-output kernel takes this convolution (at most 16 outputs)."""
+    if dtype not in (torch.float16, torch.bfloat16, torch.float32) or not 1 <= cout <= 16 or not 1 <= kvol <= 32:
+        return False
+    es = torch.empty((), dtype=dtype).element_size()
+    return (cin * es) % 64 == 0
+
+
+def gather_conv_narrow(
+    features: torch.Tensor,
+    plan: ConvPlan,
+    weight: torch.Tensor,
+    bias: torch.Tensor | None = None,
+    act: str | None = None,
+    residual: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """The convolution for at most 16 output channels over a plan (16x16 MFMAs over
+    64-row halves of its tiles); fp16 / bf16 / fp32, 64-byte input rows."""
+    device = _lib.require_gpu(features, weight, bias, residual, plan.gidx)
+    dtype = features.dtype
+    if weight.dtype != dtype or (bias is not None and bias.dtype != dtype) or (
+        residual is not None and residual.dtype != dtype
+    ):
+        raise ValueError("features, weight, bias and residual must share one dtype")
+    if features.ndim != 2 or features.shape[0] != plan.n_in:
+        raise ValueError(f"expected features [{plan.n_in}, Cin], got {tuple(features.shape)}")
+    x = features.contiguous()
+    w = _flat_weight(weight, plan.kvol)
+    cin, cout = int(x.shape[1]), int(w.shape[0])
+    if int(w.shape[2]) != cin:
+        raise ValueError(f"weight expects {int(w.shape[2])} input channels, features have {cin}")
+    if not narrow_supported(dtype, cin, cout, plan.kvol):
+        raise ValueError(f"narrow path needs fp16/bf16/fp32, 1..16 outputs and 64-byte rows ({dtype}, {cin}->{cout})")
+    if x.data_ptr() % 16:
+        x = x.clone()
+    b = None if bias is None else bias.contiguous()
+    r = None if residual is None else residual.contiguous()
+    if r is not None and tuple(r.shape) != (plan.n_out, cout):
+        raise ValueError("residual must have the output's shape")
+    out = torch.empty((plan.n_out, cout), dtype=dtype, device=device)
+    _lib.call(
+        "hi3d_gather_conv_narrow",
+        _lib.ptr(x), plan.n_in, cin, _lib.ptr(w), _lib.ptr(b), cout, plan.kvol, _lib.ptr(plan.rows),
+        _lib.ptr(plan.gidx), _lib.ptr(plan.tile_mask), plan.n_out, _lib.ptr(r), ACTIVATIONS[act],
+        _lib.DTYPES[dtype], _lib.ptr(out), _lib.stream(device),
+    )
+    return out
+
+
 def gather_conv_simple(
     features: torch.Tensor,
     table: torch.Tensor,
@@ -142,8 +191,11 @@ def conv(
     act: str | None = None,
     residual: torch.Tensor | None = None,
 ) -> torch.Tensor:
-    """Dispatch to the MFMA kernel when it takes the shape, else to the simple kernel."""
+    """Dispatch to the narrow kernel for at most 16 outputs, to the MFMA tile kernels
+    when they take the shape, else to the simple kernel."""
     cin, cout = int(features.shape[1]), int(weight.shape[0])
+    if narrow_supported(features.dtype, cin, cout, plan.kvol):
+        return gather_conv_narrow(features, plan, weight, bias, act, residual)
     if mfma_supported(features.dtype, cin, cout):
         return gather_conv(features, plan, weight, bias, act, residual)
     return gather_conv_simple(features, plan.table, weight, bias, act, residual, n_in=plan.n_in)

@@ -169,6 +169,18 @@ int hi3d_gather_conv_simple(const void* in_dev, int64_t n_in, int32_t cin,
                             const void* residual_dev, int32_t act, int32_t dtype, void* out_dev,
                             void* stream);
 
+/* The convolution of hi3d_gather_conv over the same plan for at most 16 output
+ * channels: 16x16 MFMAs over 64-row halves of the plan's tiles, offsets none of a half's
+ * rows has skipped (tile_mask_dev is not read). F32, F16 or BF16; cout 1..16, kvol <= 32,
+ * cin*elem % 64 == 0, 16-byte aligned input and weight. Replaces the occupancy head's
+ * gathered GEMM (SparseClsHead Conv3d(C, 8), src/hi3d_mac/mlx_backend/vae.py:270-271
+ * over conv_gn_swish :166-192; src/sparc3d/models/autoencoders/blocks.py:181-197). */
+int hi3d_gather_conv_narrow(const void* in_dev, int64_t n_in, int32_t cin, const void* weight_dev,
+                            const void* bias_dev, int32_t cout, int32_t kvol, const int32_t* rows_dev,
+                            const int32_t* gidx_dev, const uint32_t* tile_mask_dev, int64_t n_out,
+                            const void* residual_dev, int32_t act, int32_t dtype, void* out_dev,
+                            void* stream);
+
 /* Mean of the present rows per table row: out[o] = sum_k in[table[o,k]] / (count + extra)
  * over entries < n_in; fp32 (F64: fp64) accumulation. With the stride-2 down table and
  * extra = 1 this is SparseDownsample's scatter_reduce(mean) onto a zero-initialised

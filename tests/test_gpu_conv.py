@@ -69,6 +69,45 @@ def test_mfma_conv_matches_float64(cuda, dtype, cin, cout):
     assert oconv.rel_err(y.float().cpu().numpy(), ref) <= GATE[dtype]
 
 
+@pytest.mark.parametrize("dtype,cin,cout,kvol,density,act,res", [
+    (torch.float16, 256, 8, 27, 0.15, None, False), (torch.float32, 512, 8, 27, 0.1, None, False),
+    (torch.bfloat16, 128, 16, 27, 0.2, "silu", True), (torch.float16, 32, 1, 27, 0.3, None, True),
+    (torch.float32, 48, 5, 27, 0.004, "silu", False), (torch.float16, 96, 12, 8, 0.2, None, False),
+    (torch.float16, 512, 8, 27, 0.05, None, False),
+])
+def test_narrow_conv_matches_float64(cuda, dtype, cin, cout, kvol, density, act, res):
+    """The narrow-output kernel (cout <= 16, 16x16 MFMAs) against float64 and against
+    the tile kernels on the same inputs: occupancy-head shapes (C 256 / 512 -> 8),
+    odd output counts, K steps of one, two and four 64-byte blocks, sparse sets where
+    most offsets of a 64-row tile are absent, and a few-offset table."""
+    from hi3d_amd import conv, kmap
+
+    rng = np.random.default_rng(cin * 31 + cout + kvol)
+    idx = _rand_indices(rng, 24, density, batch=2)
+    n = len(idx)
+    if kvol == 27:
+        table = kmap.build_kernel_map(torch.as_tensor(idx).to(cuda), [24] * 3, 2).table
+    else:
+        t = rng.integers(0, n + 1, (n - 7, kvol)).astype(np.int32)
+        t[rng.random(t.shape) < 0.6] = n
+        table = torch.as_tensor(t).to(cuda)
+    x, w, b = _case(rng, n, cin, cout, dtype, kvol)
+    r = torch.as_tensor(rng.standard_normal((int(table.shape[0]), cout), dtype=np.float32)).to(dtype) if res else None
+    xd, wd, bd = x.to(cuda), w.to(cuda), b.to(cuda)
+    rd = None if r is None else r.to(cuda)
+    assert conv.narrow_supported(dtype, cin, cout, kvol)
+    plan = kmap.build_plan(table, n)
+    y = conv.gather_conv_narrow(xd, plan, wd, bd, act=act, residual=rd)
+    ref = oconv.gather_conv_f64(x.float().numpy(), table.cpu().numpy(), w.float().numpy(), b.float().numpy(),
+                                act=act, residual=None if r is None else r.float().numpy())
+    assert y.dtype == dtype and y.shape == (int(table.shape[0]), cout)
+    assert oconv.rel_err(y.float().cpu().numpy(), ref) <= GATE[dtype]
+    assert torch.equal(conv.conv(xd, plan, wd, bd, act=act, residual=rd), y)  # conv() takes this kernel
+    if conv.mfma_supported(dtype, cin, cout):
+        tile = conv.gather_conv(xd, plan, wd, bd, act=act, residual=rd)
+        assert oconv.rel_err(tile.float().cpu().numpy(), ref) <= GATE[dtype]
+
+
 def test_epilogue_silu_and_residual(cuda):
     from hi3d_amd import conv, kmap
 

@@ -72,8 +72,20 @@ def test_c_argument_validation_without_launch():
     assert rc == _lib.ERR_INVALID
     rc = lib.hi3d_layer_norm_modulate(null, 4, 8, 1e-6, ctypes.c_void_p(16), null, null, null, null, null)
     assert rc == _lib.ERR_INVALID
+    # the narrow kernel: at most 16 outputs, 64-byte input rows, no float64
+    rc = lib.hi3d_gather_conv_narrow(null, 10, 64, null, null, 17, 27, null, null, null, 10, null, 0, _lib.F16, null,
+                                     null)
+    assert rc == _lib.ERR_INVALID and "1..16 output" in _lib.last_error()
+    rc = lib.hi3d_gather_conv_narrow(null, 10, 24, null, null, 8, 27, null, null, null, 10, null, 0, _lib.F16, null,
+                                     null)
+    assert rc == _lib.ERR_INVALID and "64 bytes" in _lib.last_error()
+    rc = lib.hi3d_gather_conv_narrow(null, 10, 64, null, null, 8, 27, null, null, null, 10, null, 0, _lib.F64, null,
+                                     null)
+    assert rc == _lib.ERR_INVALID
     # zero-size calls succeed without touching memory
     assert lib.hi3d_gather_conv_simple(null, 0, 3, null, null, 5, 27, null, 0, null, 0, _lib.F64, null, null) == 0
+    assert lib.hi3d_gather_conv_narrow(null, 0, 64, null, null, 8, 27, null, null, null, 0, null, 0, _lib.F16, null,
+                                       null) == 0
     assert lib.hi3d_w8a8_quantize(null, 0, 64, null, null, null, null) == 0
 
 
