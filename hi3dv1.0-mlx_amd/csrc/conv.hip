@@ -1282,6 +1282,9 @@ int launch_mfma(const ConvArgs& base, hipStream_t stream) {
       if (rb % 128 == 0) return launch_wide<T, 128, 8>(a, stream);
       return launch_ring<T, 128, 8>(a, stream);
     }
+    // 64- and 128-channel rows into 64 or 128 outputs: the 128-row ring tiles
+    if (a.kvol <= kMaxPipelinedKvol && (rb == 128 || rb == 256) && (a.cout == 64 || a.cout == 128))
+      return a.cout == 64 ? launch_ring<T, 64, 4, 128>(a, stream) : launch_ring<T, 128, 4, 128>(a, stream);
   }
   if constexpr (sizeof(T) == 4) {
     // fp32 (four 32x32x2 MFMAs per fragment): 128-row tiles so that small sets still
