@@ -578,7 +578,7 @@ struct RingShape {
   static constexpr int IDXL = (NIDX + NW - 1) / NW;  // index loads per wave
 };
 constexpr int kRingDepth = 4;
-constexpr int kRingMaxRowBytes = 512;
+constexpr int kRingMaxRowBytes = 1024;  // the zero row absent neighbours read is this long
 
 __device__ __attribute__((aligned(16))) const uint32_t g_zero_row[kRingMaxRowBytes / 4] = {};
 

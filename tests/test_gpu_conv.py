@@ -131,13 +131,18 @@ def test_epilogue_silu_and_residual(cuda):
     (torch.float16, 256, 256, 0.2, "silu", True), (torch.bfloat16, 192, 512, 0.1, None, True),
     (torch.float16, 256, 256, 0.004, None, False),
     (torch.float32, 64, 128, 0.15, "silu", True), (torch.float32, 128, 64, 0.1, None, True),
+    (torch.float16, 512, 512, 0.1, "silu", True), (torch.bfloat16, 512, 256, 0.15, None, False),
+    (torch.float16, 448, 128, 0.1, None, True), (torch.float16, 512, 128, 0.05, "silu", False),
+    (torch.float16, 64, 64, 0.15, "silu", True), (torch.bfloat16, 64, 128, 0.1, None, False),
+    (torch.float16, 128, 64, 0.004, None, True),
 ])
 def test_ring_kernel_variants(cuda, dtype, cin, cout, density, act, res):
-    """The ring kernels (fp16/bf16, Cout a multiple of 128, 256..512-byte rows): 256 x 256
+    """The ring kernels (fp16/bf16, Cout a multiple of 128, 256..1024-byte rows): 256 x 256
     tiles of 64-byte K steps (Cout a multiple of 256), 256 x 128 tiles of 128-byte K steps
     (rows a multiple of 128 bytes) and 384 x 128 tiles of 64-byte steps (320-byte rows);
-    fp32 with Cout 64 / 128 on 128-row tiles (four 32x32x2 MFMAs per fragment);
-    several output-column tiles, two to eight K steps per offset, SiLU and residual in
+    fp16/bf16 64- and 128-channel rows into 64 or 128 outputs, and fp32 with Cout 64 / 128,
+    on 128-row tiles (fp32: four 32x32x2 MFMAs per fragment);
+    several output-column tiles, two to sixteen K steps per offset, SiLU and residual in
     the epilogue, and isolated voxels (tiles whose only offset is the centre)."""
     from hi3d_amd import conv, kmap
 
