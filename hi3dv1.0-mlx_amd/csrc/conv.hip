@@ -35,6 +35,7 @@ struct ConvArgs {
   const int32_t* gidx;
   const uint32_t* tile_mask;
   int64_t ntiles;
+  int64_t n_out;  // output rows (plan entries at or past it are not written)
   int32_t ny;  // column tiles
   const char* residual;
   int32_t act;
@@ -195,7 +196,7 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a) {
     const int i = q / CPR, cc = q - (q / CPR) * CPR;
     const int32_t orow = a.rows[tile * BM + i];
     const int ncol = n0 + cc * EPC;
-    if (orow < 0 || ncol >= a.cout) continue;
+    if (orow < 0 || orow >= a.n_out || ncol >= a.cout) continue;
     u32x4 v = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(C) + (i * BN + cc * EPC) * sizeof(T));
     const int64_t off = static_cast<int64_t>(orow) * out_row_bytes + static_cast<int64_t>(ncol) * sizeof(T);
     if (a.residual != nullptr) {
@@ -485,7 +486,7 @@ __global__ __launch_bounds__(kPipeThreads) void conv_pipe_kernel(ConvArgs a) {
     const int i = q / CPR, cc = q - (q / CPR) * CPR;
     const int32_t orow = orows[i];
     const int ncol = n0 + cc * EPC;
-    if (orow < 0 || ncol >= a.cout) continue;
+    if (orow < 0 || orow >= a.n_out || ncol >= a.cout) continue;
     u32x4 v = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(C) + (i * BN + cc * EPC) * sizeof(T));
     const int64_t off = static_cast<int64_t>(orow) * out_row_bytes + static_cast<int64_t>(ncol) * sizeof(T);
     if (a.residual != nullptr) {
@@ -578,7 +579,7 @@ struct RingShape {
   static constexpr int IDXL = (NIDX + NW - 1) / NW;  // index loads per wave
 };
 constexpr int kRingDepth = 4;
-constexpr int kRingMaxRowBytes = 1024;  // the zero row absent neighbours read is this long
+constexpr int kRingMaxRowBytes = 2048;  // the zero row absent neighbours read is this long
 
 __device__ __attribute__((aligned(16))) const uint32_t g_zero_row[kRingMaxRowBytes / 4] = {};
 
@@ -608,6 +609,9 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_ring_kernel(ConvArgs a) {
   constexpr int IDXL = Sh::IDXL, LX = L / 2;  // cursor X issues loads 0..LX-1, Y the rest
   constexpr int RING = NS * STAGE;
   static_assert(STAGE % 1024 == 0 && LA * 16 * NW == BM && Sh::LB * 16 * NW == BN, "stage shape");
+  // the epilogue stages the whole output tile over the ring; past it lie the tile's
+  // output rows, which the stores read
+  static_assert(BM * BN * static_cast<int>(sizeof(T)) <= RING, "output tile must fit the ring");
   __shared__ __attribute__((aligned(16))) char smem[RING + 3 * IDX + 256];
   char* const idx_ring = smem + RING;
   char* const rows_lds = idx_ring + 2 * IDX;  // the tile's output rows
@@ -924,7 +928,7 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_ring_kernel(ConvArgs a) {
     const int64_t pt = tile * SUB + tr / kTileRows;
     if (pt >= a.ntiles) continue;
     const int32_t orow = reinterpret_cast<const int32_t*>(rows_lds)[tr];
-    if (orow < 0) continue;
+    if (orow < 0 || orow >= a.n_out) continue;
     u32x4 v = *reinterpret_cast<const u32x4*>(stg + row * ROWB + ((chunk ^ (row & (CPR - 1))) << 4));
     const int64_t off = static_cast<int64_t>(orow) * out_row_bytes + static_cast<int64_t>(cb + chunk * EPC) * ES;
     if (a.residual != nullptr) {
@@ -994,6 +998,7 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_wide_kernel(ConvArgs a) {
   constexpr int MB = 2, NB = Sh::NB, NF = MB + NB, NM = MB * NB, KG = 4, LG = L / (KG - 1);
   static_assert(STAGE == 49152 && LG * (KG - 1) == L && LG <= NM && LA * 8 * NW == BM, "stage shape");
   static_assert(sizeof(T) == 2, "16-bit elements (the epilogue packs four channels into 8 bytes)");
+  static_assert(BM * BN * 2 <= NS * STAGE, "output tile must fit the ring");
   __shared__ __attribute__((aligned(16))) char smem[NS * STAGE + 3 * IDX + 256];
   char* const idx_ring = smem + NS * STAGE;
   char* const rows_lds = idx_ring + 2 * IDX;  // the tile's output rows
@@ -1226,7 +1231,7 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_wide_kernel(ConvArgs a) {
     const int64_t pt = tile * SUB + tr / kTileRows;
     if (pt >= a.ntiles) continue;
     const int32_t orow = reinterpret_cast<const int32_t*>(rows_lds)[tr];
-    if (orow < 0) continue;
+    if (orow < 0 || orow >= a.n_out) continue;
     u32x4 v = *reinterpret_cast<const u32x4*>(stg + row * ROWB + ((chunk ^ (row & (CPR - 1))) << 4));
     const int64_t off = static_cast<int64_t>(orow) * out_row_bytes + static_cast<int64_t>(cb + chunk * 8) * sizeof(T);
     if (a.residual != nullptr) {
@@ -1269,7 +1274,7 @@ int launch_mfma(const ConvArgs& base, hipStream_t stream) {
   ConvArgs a = base;
   if constexpr (sizeof(T) == 2) {
     const int rb = a.cin * static_cast<int>(sizeof(T));
-    const bool ring_rows = rb % 64 == 0 && rb >= 4 * 64 && rb <= kRingMaxRowBytes;
+    const bool ring_rows = rb % 64 == 0 && rb >= 4 * 64 && rb <= 1024;
     const bool few = a.kvol <= 8 && (rb == 128 || rb == 256) && (a.cout == 64 || a.cout == 128);
     // 8 waves for the large tiles; 128-byte K steps for 128-channel tiles, whose gathers
     // are the larger share of their loads (measured: C128 0.46 vs 0.49 ms, C256 8.8 vs
@@ -1290,8 +1295,13 @@ int launch_mfma(const ConvArgs& base, hipStream_t stream) {
     // fp32 (four 32x32x2 MFMAs per fragment): 128-row tiles so that small sets still
     // spread over every CU (the 45k-voxel C64 shell makes 353 of them)
     const int rb = a.cin * 4;
-    if (a.kvol <= kMaxPipelinedKvol && (rb == 256 || rb == 512) && (a.cout == 64 || a.cout == 128))
-      return a.cout == 64 ? launch_ring<T, 64, 4, 128>(a, stream) : launch_ring<T, 128, 4, 128>(a, stream);
+    if (a.kvol <= kMaxPipelinedKvol && rb % 64 == 0 && rb >= 256 && rb <= kRingMaxRowBytes) {
+      if (a.cout == 64) return launch_ring<T, 64, 4, 128>(a, stream);
+      // 128 x 128 tiles (several column tiles for wider outputs): the largest fp32 tile
+      // whose staged output fits the ring (C256: 7.06 -> 6.28 ms, C512: 26.3 -> 24.4 ms
+      // against the pipelined kernel on 327,581 voxels)
+      if (a.cout % 128 == 0) return launch_ring<T, 128, 4, 128>(a, stream);
+    }
   }
   if (a.kvol <= kMaxPipelinedKvol) {
     if (a.cout <= 64) return launch_pipe<T, 256, 64, 8>(a, stream);
@@ -1395,6 +1405,7 @@ int hi3d_gather_conv(const void* in, int64_t n_in, int32_t cin, const void* weig
   a.gidx = gidx;
   a.tile_mask = tile_mask;
   a.ntiles = ceil_div(n_out, kTileRows);
+  a.n_out = n_out;
   a.residual = static_cast<const char*>(residual);
   a.act = act;
   a.out = static_cast<char*>(out);

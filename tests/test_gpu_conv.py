@@ -135,13 +135,16 @@ def test_epilogue_silu_and_residual(cuda):
     (torch.float16, 448, 128, 0.1, None, True), (torch.float16, 512, 128, 0.05, "silu", False),
     (torch.float16, 64, 64, 0.15, "silu", True), (torch.bfloat16, 64, 128, 0.1, None, False),
     (torch.float16, 128, 64, 0.004, None, True),
+    (torch.float32, 256, 256, 0.1, "silu", True), (torch.float32, 512, 128, 0.1, None, False),
+    (torch.float32, 64, 256, 0.15, None, True), (torch.float32, 80, 128, 0.1, "silu", False),
 ])
 def test_ring_kernel_variants(cuda, dtype, cin, cout, density, act, res):
     """The ring kernels (fp16/bf16, Cout a multiple of 128, 256..1024-byte rows): 256 x 256
     tiles of 64-byte K steps (Cout a multiple of 256), 256 x 128 tiles of 128-byte K steps
     (rows a multiple of 128 bytes) and 384 x 128 tiles of 64-byte steps (320-byte rows);
-    fp16/bf16 64- and 128-channel rows into 64 or 128 outputs, and fp32 with Cout 64 / 128,
-    on 128-row tiles (fp32: four 32x32x2 MFMAs per fragment);
+    fp16/bf16 64- and 128-channel rows into 64 or 128 outputs, and fp32 (Cout 64 or a
+    multiple of 128, rows up to 2 KB), on 128-row tiles (fp32: four 32x32x2 MFMAs per
+    fragment);
     several output-column tiles, two to sixteen K steps per offset, SiLU and residual in
     the epilogue, and isolated voxels (tiles whose only offset is the centre)."""
     from hi3d_amd import conv, kmap
@@ -155,7 +158,10 @@ def test_ring_kernel_variants(cuda, dtype, cin, cout, density, act, res):
                          residual=None if r is None else r.to(cuda))
     ref = oconv.gather_conv_f64(x.float().numpy(), km.table.cpu().numpy(), w.float().numpy(), b.float().numpy(),
                                 act=act, residual=None if r is None else r.float().numpy())
-    assert oconv.rel_err(y.float().cpu().numpy(), ref) <= GATE[dtype]
+    # fp32 sums of up to 27 * Cin products: above 256 input channels the rounding of the
+    # accumulation alone reaches 1.2-1.5e-5 of the RMS (the pipelined kernel's as well)
+    gate = 2e-5 if dtype == torch.float32 and cin > 256 else GATE[dtype]
+    assert oconv.rel_err(y.float().cpu().numpy(), ref) <= gate
 
 
 def test_halo_plan_resolves_the_table(cuda):
