@@ -27,6 +27,16 @@ at 256 (a Morton tile computes every offset for every row, 33-47 % of them on ab
 neighbours, and its halo reads conflict in LDS banks)."""
 
 
+def _output(out: torch.Tensor | None, n: int, c: int, dtype: torch.dtype, device) -> torch.Tensor:
+    """The output buffer: a new ``[n, c]`` tensor, or the caller's (which may be the
+    residual itself: each output element is read and written by one thread)."""
+    if out is None:
+        return torch.empty((n, c), dtype=dtype, device=device)
+    if tuple(out.shape) != (n, c) or out.dtype != dtype or not out.is_contiguous() or out.device != device:
+        raise ValueError(f"out must be a contiguous [{n}, {c}] {dtype} tensor on {device}")
+    return out
+
+
 def halo_supported(dtype: torch.dtype, cin: int, cout: int, kvol: int) -> bool:
     """Whether the halo kernel takes this convolution."""
     if dtype not in (torch.float16, torch.bfloat16) or kvol != 27:
@@ -80,8 +90,7 @@ def gather_conv(
     r = None if residual is None else residual.contiguous()
     if r is not None and tuple(r.shape) != (plan.n_out, cout):
         raise ValueError("residual must have the output's shape")
-    if out is None:
-        out = torch.empty((plan.n_out, cout), dtype=dtype, device=device)
+    out = _output(out, plan.n_out, cout, dtype, device)
     hp = plan.halo() if HALO and halo_supported(dtype, cin, cout, plan.kvol) else None
     if hp is not None:
         _lib.call(
@@ -115,6 +124,7 @@ def gather_conv_narrow(
     bias: torch.Tensor | None = None,
     act: str | None = None,
     residual: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """The convolution for at most 16 output channels over a plan (16x16 MFMAs over
     64-row halves of its tiles); fp16 / bf16 / fp32, 64-byte input rows."""
@@ -139,7 +149,7 @@ def gather_conv_narrow(
     r = None if residual is None else residual.contiguous()
     if r is not None and tuple(r.shape) != (plan.n_out, cout):
         raise ValueError("residual must have the output's shape")
-    out = torch.empty((plan.n_out, cout), dtype=dtype, device=device)
+    out = _output(out, plan.n_out, cout, dtype, device)
     _lib.call(
         "hi3d_gather_conv_narrow",
         _lib.ptr(x), plan.n_in, cin, _lib.ptr(w), _lib.ptr(b), cout, plan.kvol, _lib.ptr(plan.rows),
@@ -157,6 +167,7 @@ def gather_conv_simple(
     act: str | None = None,
     residual: torch.Tensor | None = None,
     n_in: int | None = None,
+    out: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """The same convolution from a plain table, any channel count, float64 too."""
     device = _lib.require_gpu(features, table, weight, bias, residual)
@@ -172,7 +183,7 @@ def gather_conv_simple(
     cin, cout = int(x.shape[1]), int(w.shape[0])
     n_out = int(t.shape[0])
     n_in = int(x.shape[0]) if n_in is None else int(n_in)
-    out = torch.empty((n_out, cout), dtype=dtype, device=device)
+    out = _output(out, n_out, cout, dtype, device)
     b = None if bias is None else bias.contiguous()
     r = None if residual is None else residual.to(dtype).contiguous()
     _lib.call(
@@ -190,12 +201,16 @@ def conv(
     bias: torch.Tensor | None = None,
     act: str | None = None,
     residual: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Dispatch to the narrow kernel for at most 16 outputs, to the MFMA tile kernels
-    when they take the shape, else to the simple kernel."""
+    when they take the shape, else to the simple kernel. ``out`` may be ``residual``
+    (the sum is then accumulated in place)."""
     cin, cout = int(features.shape[1]), int(weight.shape[0])
+    if out is not None and out.data_ptr() == features.data_ptr():
+        raise ValueError("out must not alias the gathered features")
     if narrow_supported(features.dtype, cin, cout, plan.kvol):
-        return gather_conv_narrow(features, plan, weight, bias, act, residual)
+        return gather_conv_narrow(features, plan, weight, bias, act, residual, out)
     if mfma_supported(features.dtype, cin, cout):
-        return gather_conv(features, plan, weight, bias, act, residual)
-    return gather_conv_simple(features, plan.table, weight, bias, act, residual, n_in=plan.n_in)
+        return gather_conv(features, plan, weight, bias, act, residual, out)
+    return gather_conv_simple(features, plan.table, weight, bias, act, residual, n_in=plan.n_in, out=out)

@@ -60,11 +60,16 @@ def group_stats(x: torch.Tensor, eps: float = 1e-6) -> tuple[torch.Tensor, torch
 
 def conv_gn_swish(x: torch.Tensor, level: Level, norm_weight: torch.Tensor, norm_bias: torch.Tensor,
                   weight_t: torch.Tensor, bias: torch.Tensor | None, out: torch.dtype | None = None,
-                  residual: torch.Tensor | None = None, eps: float = 1e-6) -> torch.Tensor:
+                  residual: torch.Tensor | list | None = None, eps: float = 1e-6) -> torch.Tensor:
     """``conv(swish(GroupNorm(x))) + bias`` (+ ``residual``) over ``level``'s map
     (vae.py:166-192). ``weight_t [27 * Cin, Cout]``; the activation is rounded to the
     weight dtype, the convolution accumulates in fp32 and adds ``bias`` in fp32; the
-    result is in ``out`` (default: fp32 for fp32 weights, else the weight dtype)."""
+    result is in ``out`` (default: fp32 for fp32 weights, else the weight dtype).
+
+    ``residual`` as a one-element list holding ``r`` (the reference's donation idiom)
+    returns ``r + conv(...)`` written into ``r``'s own buffer: the convolution's rounded
+    output is added in ``r``'s dtype by the epilogue, which reads and writes each
+    element once, so no second ``[n, Cout]`` tensor exists."""
     mean, inv = group_stats(x, eps)
     wdt = weight_t.dtype
     a = group_norm_swish(x, mean, inv, norm_weight, norm_bias, wdt)
@@ -72,27 +77,52 @@ def conv_gn_swish(x: torch.Tensor, level: Level, norm_weight: torch.Tensor, norm
     w = weight_t.T.reshape(cout, 27, cin).contiguous()
     if out is None:
         out = torch.float32 if wdt == torch.float32 else wdt
+    donated = None
+    if isinstance(residual, list):
+        if len(residual) != 1:
+            raise ValueError("residual holder must hold exactly one tensor")
+        donated = residual.pop()
+        residual = donated
     if out != wdt:
         y = _conv.conv(a, level.plan, w, None)
         y = y.float() + (0 if bias is None else bias.float())
         y = y.to(out)
-        return y if residual is None else (residual.float() + y.float()).to(residual.dtype)
+        if residual is None:
+            return y
+        if donated is not None:
+            return donated.add_(y.to(donated.dtype))
+        return (residual.float() + y.float()).to(residual.dtype)
     b = None if bias is None else bias.to(wdt)
+    if donated is not None and donated.dtype == wdt and donated.is_contiguous() and donated.data_ptr() != a.data_ptr():
+        return _conv.conv(a, level.plan, w, b, residual=donated, out=donated)
     r = None if residual is None else residual.to(wdt)
-    return _conv.conv(a, level.plan, w, b, residual=r)
+    y = _conv.conv(a, level.plan, w, b, residual=r)
+    return y if donated is None else donated.copy_(y)
 
 
-def resnet(x: torch.Tensor, level: Level, params: dict, name: str, eps: float = 1e-6) -> torch.Tensor:
+def resnet(x: torch.Tensor | list, level: Level, params: dict, name: str, eps: float = 1e-6) -> torch.Tensor:
     """``shortcut + conv(swish(GN(conv(swish(GN(x))))))`` (vae.py:200-218) with the
     reference's parameter names: ``{name}.block.0`` / ``.block.3`` GroupNorm
     (``.weights``, ``.bias``), ``.block.2`` / ``.block.5`` convolutions (``.weight``
-    ``[27 Cin, Cout]``, ``.bias``) and an optional ``{name}.res_conv`` linear."""
+    ``[27 Cin, Cout]``, ``.bias``) and an optional ``{name}.res_conv`` linear.
+
+    ``x`` may be a one-element list holding the input (the reference's holder): with an
+    identity shortcut the second convolution then accumulates into the input's buffer,
+    so two full-size activations are alive instead of three."""
     p = params
+    holder = x if isinstance(x, list) else None
+    if holder is not None:
+        if len(holder) != 1:
+            raise ValueError("input holder must hold exactly one tensor")
+        x = holder.pop()
     h = conv_gn_swish(x, level, p[f"{name}.block.0.weights"], p[f"{name}.block.0.bias"],
                       p[f"{name}.block.2.weight"], p[f"{name}.block.2.bias"], eps=eps)
     if f"{name}.res_conv.weight" in p:
         w = p[f"{name}.res_conv.weight"]
         shortcut = (x.to(w.dtype) @ w.T + p[f"{name}.res_conv.bias"]).to(h.dtype)
+    elif holder is not None and x.dtype == h.dtype:
+        shortcut = [x]
+        del x
     else:
         shortcut = x.to(h.dtype)
     return conv_gn_swish(h, level, p[f"{name}.block.3.weights"], p[f"{name}.block.3.bias"],

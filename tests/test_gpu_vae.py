@@ -245,3 +245,52 @@ def test_upsample_with_given_and_empty_masks(cuda):
     assert oconv.rel_err(y.float().cpu().numpy(), feats) <= 1e-2
     y, child, _ = vae.upsample(x, level, gp, "u", mask=torch.zeros((len(coords), 8), dtype=torch.bool, device=cuda))
     assert y.shape == (0, c) and child.n == 0 and child.table.shape == (0, 27)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_resnet_in_place_matches_composed(cuda, dtype):
+    """The reference's in-place residual test (tests/test_mlx_kernels.py:124-150): the
+    block on a donated input (a one-element holder) accumulates its second convolution
+    into the input's buffer and equals the composed block bit for bit."""
+    from hi3d_amd import vae
+
+    coords, level = _level(cuda)
+    rng = np.random.default_rng(3)
+    c = 32 if dtype == torch.float32 else 64
+    p = {}
+    for name in ("r.block.0", "r.block.3"):
+        p[f"{name}.weights"] = torch.as_tensor(rng.uniform(0.5, 1.5, (1, c)).astype(np.float32)).to(cuda)
+        p[f"{name}.bias"] = torch.as_tensor(rng.normal(0, 0.1, (1, c)).astype(np.float32)).to(cuda)
+    for name in ("r.block.2", "r.block.5"):
+        p[f"{name}.weight"] = torch.as_tensor(rng.normal(0, 0.05, (27 * c, c)).astype(np.float32)).to(cuda).to(dtype)
+        p[f"{name}.bias"] = torch.as_tensor(rng.normal(0, 0.1, (c,)).astype(np.float32)).to(cuda).to(dtype)
+    x = torch.as_tensor(rng.normal(0, 1, (len(coords), c)).astype(np.float32)).to(cuda).to(dtype)
+    composed = vae.resnet(x.clone(), level, p, "r")
+    donated = x.clone()
+    ptr = donated.data_ptr()
+    holder = [donated]
+    del donated
+    in_place = vae.resnet(holder, level, p, "r")
+    assert not holder and in_place.data_ptr() == ptr
+    assert torch.equal(composed, in_place)
+
+
+def test_conv_gn_swish_residual_holder(cuda):
+    """``residual`` as a holder: the result lives in the residual's buffer and equals
+    the out-of-place sum; the narrow kernel (8 outputs) accumulates in place too."""
+    from hi3d_amd import vae
+
+    coords, level = _level(cuda, seed=4)
+    rng = np.random.default_rng(8)
+    for c, cout in ((64, 64), (64, 8)):
+        t = lambda a: torch.as_tensor(a).to(cuda)
+        x = t(rng.normal(0, 1, (len(coords), c)).astype(np.float16))
+        gw, gb = t(rng.uniform(0.5, 1.5, (1, c)).astype(np.float32)), t(rng.normal(0, 0.1, (1, c)).astype(np.float32))
+        wt = t(rng.normal(0, 0.05, (27 * c, cout)).astype(np.float16))
+        bias = t(rng.normal(0, 0.1, cout).astype(np.float16))
+        r = t(rng.normal(0, 1, (len(coords), cout)).astype(np.float16))
+        ref = vae.conv_gn_swish(x, level, gw, gb, wt, bias, residual=r)
+        donated = r.clone()
+        ptr = donated.data_ptr()
+        got = vae.conv_gn_swish(x, level, gw, gb, wt, bias, residual=[donated])
+        assert got.data_ptr() == ptr and torch.equal(got, ref)
