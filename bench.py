@@ -10,8 +10,8 @@ runs on): achieved = 2 * P * Cin * Cout / average kernel time against the fp16 d
 peak. ``cpu_baseline`` times the reference's CPU fallback (oracle port: sort +
 searchsorted map, per-offset gather / matmul / index_add_) on the host cores.
 ``extra`` reports the other workloads: the fp32 sphere shell, the strided pair, W8A8
-int8 TOPS (GEMM alone and quantise + GEMM), the residual blocks, octree upsampling, and
-kernel-map builds.
+int8 TOPS (GEMM alone and quantise + GEMM), the residual blocks, octree upsampling,
+unique cube corners, and kernel-map builds.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
 """
@@ -324,6 +324,35 @@ def bench_upsample(steps: int, warmup: int):
     }
 
 
+def bench_unique(steps: int, warmup: int):
+    """Unique cube corners of the 1024^3 residual-block shells (mesh extraction's
+    ``torch.unique(dim=0)``): 8 corner rows of 3 int32 per voxel, with inverse and
+    counts; torch's own GPU ``unique(dim=0)`` timed on the same rows."""
+    import torch
+
+    from hi3d_amd import fast_unique, workloads
+
+    dev = torch.device("cuda:0")
+    idx = torch.as_tensor(workloads.coords_for("resblock_c256_fp16", device=dev)).to(dev)
+    xyz = idx[:, 1:].to(torch.int32)
+    off = torch.tensor([[i >> 2 & 1, i >> 1 & 1, i & 1] for i in range(8)], dtype=torch.int32, device=dev)
+    corners = (xyz[:, None, :] + off[None]).reshape(-1, 3).contiguous()
+    n = int(corners.shape[0])
+    _, ours = timed(lambda: fast_unique.unique_rows(corners, return_inverse=True, return_counts=True),
+                    steps, warmup)
+    u = int(fast_unique.unique_rows(corners).shape[0])
+    _, theirs = timed(lambda: torch.unique(corners, dim=0, return_inverse=True, return_counts=True),
+                      max(2, steps // 5), 1)
+    return {
+        "workload": "unique_corners_1024",
+        "rows": n,
+        "unique_rows": u,
+        "unique_ms": ours,
+        "rows_per_s": n / (ours * 1e-3),
+        "torch_unique_dim0_ms": theirs,
+    }
+
+
 def cpu_baseline(name: str, grid: int, cin: int, cout: int, max_rows: int | None):
     import torch
 
@@ -391,6 +420,8 @@ def main() -> int:
         extra["vae_resnet_c64_fp16"] = bench_vae(max(10, args.steps // 2), max(2, args.warmup // 2))
         log("VAE decoder octree upsampling C256 fp16, 512^3 fine shells' parents")
         extra["vae_upsample_c256_fp16"] = bench_upsample(max(10, args.steps // 2), max(2, args.warmup // 2))
+        log("unique cube corners of the 1024^3 shells")
+        extra["unique_corners_1024"] = bench_unique(max(5, args.steps // 10), 2)
     cpu = None
     if not args.no_cpu:
         log("CPU baseline (reference CPU fallback, oracle port)")

@@ -18,7 +18,7 @@ LIB_PATH = Path(os.environ.get("HI3D_AMD_LIB", Path(__file__).with_name("libhi3d
 
 OK, ERR_INVALID, ERR_HIP, ERR_UNSUPPORTED = 0, 1, 2, 3
 MAP_DUPLICATE, MAP_OVERFLOW, MAP_RANGE = 1, 2, 4
-F32, F16, BF16, F64 = 0, 1, 2, 3
+F32, F16, BF16, F64, I32, I64 = 0, 1, 2, 3, 4, 5
 ACT_NONE, ACT_SILU = 0, 1
 
 DTYPES = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16, torch.float64: F64}
@@ -46,6 +46,11 @@ _SIGNATURES = {
     "hi3d_conv_plan": [_p, _i64, _i32, _i64, _p, _i64, _p, _i64, _p, _p, _p, _p],
     "hi3d_gather_conv": [_p, _i64, _i32, _p, _p, _i32, _i32, _p, _p, _p, _i64, _p, _i32, _i32, _p, _p],
     "hi3d_gather_conv_simple": [_p, _i64, _i32, _p, _p, _i32, _i32, _p, _i64, _p, _i32, _i32, _p, _p],
+    "hi3d_unique_keys_workspace": [_i64, _p],
+    "hi3d_unique_keys": [_p, _i64, _i32, _p, _i64, _p, _p, _p, _p, _p],
+    "hi3d_pack_rows": [_p, _i32, _i64, _i32, _p, _p, _p, _p],
+    "hi3d_row_bounds": [_p, _i32, _i64, _i32, _p, _p, _p],
+    "hi3d_unpack_rows": [_p, _i64, _p, _i32, _p, _p, _p, _i32, _p],
     "hi3d_gather_conv_narrow": [_p, _i64, _i32, _p, _p, _i32, _i32, _p, _p, _p, _i64, _p, _i32, _i32, _p, _p],
     "hi3d_gather_mean": [_p, _i64, _i32, _p, _i32, _i64, _i32, _i32, _p, _p],
     "hi3d_halo_tile_rows": [],

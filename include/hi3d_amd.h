@@ -44,7 +44,7 @@ enum hi3d_map_flags {
   HI3D_MAP_RANGE = 4      /* a coordinate lies outside [0, spatial_shape) or the batch */
 };
 
-enum hi3d_dtype { HI3D_F32 = 0, HI3D_F16 = 1, HI3D_BF16 = 2, HI3D_F64 = 3 };
+enum hi3d_dtype { HI3D_F32 = 0, HI3D_F16 = 1, HI3D_BF16 = 2, HI3D_F64 = 3, HI3D_I32 = 4, HI3D_I64 = 5 };
 
 enum hi3d_act { HI3D_ACT_NONE = 0, HI3D_ACT_SILU = 1 };
 
@@ -180,6 +180,39 @@ int hi3d_gather_conv_narrow(const void* in_dev, int64_t n_in, int32_t cin, const
                             const int32_t* gidx_dev, const uint32_t* tile_mask_dev, int64_t n_out,
                             const void* residual_dev, int32_t act, int32_t dtype, void* out_dev,
                             void* stream);
+
+/* Workspace bytes of hi3d_unique_keys. */
+int hi3d_unique_keys_workspace(int64_t n, int64_t* bytes_host);
+
+/* Sorted unique values of keys_dev [n] int64, the inverse map and run lengths, equal to
+ * np.unique(keys, return_inverse=True, return_counts=True): uniq_dev [n] (first
+ * *n_unique_dev entries valid), inverse_dev [n] (int64 run of each key), counts_dev [n]
+ * or NULL. key_bits = 0 takes any int64; 1..63 promises keys in [0, 2^key_bits) and sorts
+ * only those bits. n < 2^31 - 1.
+ * Replaces unique_keys (src/hi3d_mac/fast_unique.py:25-56). */
+int hi3d_unique_keys(const int64_t* keys_dev, int64_t n, int32_t key_bits, void* workspace_dev,
+                     int64_t workspace_bytes, int64_t* uniq_dev, int64_t* inverse_dev, int64_t* counts_dev,
+                     int64_t* n_unique_dev, void* stream);
+
+/* Column minima lo_dev [d] and maxima hi_dev [d] (int64) of rows_dev [n, d] (I32 or
+ * I64, d <= 8, n >= 1): the value ranges that hi3d_pack_rows packs. Replaces the
+ * a.min / a.max of _packed_keys (src/hi3d_mac/fast_unique.py:61-62). */
+int hi3d_row_bounds(const void* rows_dev, int32_t dtype, int64_t n, int32_t d, int64_t* lo_dev,
+                    int64_t* hi_dev, void* stream);
+
+/* One int64 key per row of rows_dev [n, d] (I32 or I64, d <= 8) that keeps the rows'
+ * lexicographic order: key = sum_j (row[j] - lo[j]) * prod_{l > j} extent[l], with lo_dev
+ * and extent_dev [d] int64 on the device (the caller checks prod(extent) < 2^62).
+ * Replaces _packed_keys (src/hi3d_mac/fast_unique.py:59-71). */
+int hi3d_pack_rows(const void* rows_dev, int32_t dtype, int64_t n, int32_t d, const int64_t* lo_dev,
+                   const int64_t* extent_dev, int64_t* keys_dev, void* stream);
+
+/* Inverse of hi3d_pack_rows for the first *n_dev keys (at most n_max) into rows_dev
+ * [*n_dev, d]. Replaces the unpacking loop of unique_rows
+ * (src/hi3d_mac/fast_unique.py:74-91). */
+int hi3d_unpack_rows(const int64_t* keys_dev, int64_t n_max, const int64_t* n_dev, int32_t d,
+                     const int64_t* lo_dev, const int64_t* extent_dev, void* rows_dev, int32_t dtype,
+                     void* stream);
 
 /* Mean of the present rows per table row: out[o] = sum_k in[table[o,k]] / (count + extra)
  * over entries < n_in; fp32 (F64: fp64) accumulation. With the stride-2 down table and

@@ -82,6 +82,13 @@ def test_c_argument_validation_without_launch():
     rc = lib.hi3d_gather_conv_narrow(null, 10, 64, null, null, 8, 27, null, null, null, 10, null, 0, _lib.F64, null,
                                      null)
     assert rc == _lib.ERR_INVALID
+    # unique: key_bits range, row dtypes and widths
+    rc = lib.hi3d_unique_keys(null, 10, 64, null, 1 << 20, null, null, null, null, null)
+    assert rc == _lib.ERR_INVALID and "key_bits" in _lib.last_error()
+    rc = lib.hi3d_pack_rows(null, _lib.F32, 10, 3, null, null, null, null)
+    assert rc == _lib.ERR_INVALID and "I32 or I64" in _lib.last_error()
+    rc = lib.hi3d_pack_rows(null, _lib.I64, 10, 9, null, null, null, null)
+    assert rc == _lib.ERR_INVALID and "1..8" in _lib.last_error()
     # zero-size calls succeed without touching memory
     assert lib.hi3d_gather_conv_simple(null, 0, 3, null, null, 5, 27, null, 0, null, 0, _lib.F64, null, null) == 0
     assert lib.hi3d_gather_conv_narrow(null, 0, 64, null, null, 8, 27, null, null, null, 0, null, 0, _lib.F16, null,

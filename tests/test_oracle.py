@@ -457,3 +457,30 @@ def test_vae_child_coords_match_unpooling_grid():
     parent = rng.integers(0, 20, 40)
     slot = rng.integers(0, 8, 40)
     assert np.array_equal(ovae.child_coords(coords, parent, slot), coords[parent] * 2 + inv_grid[slot])
+
+
+def test_unique_oracle_against_numpy_and_torch():
+    """The unique oracle against ``np.unique`` (keys: negatives, duplicates, the int64
+    extremes, empty) and against ``torch.unique(dim=0)`` on the reference test's rows
+    (tests/test_backends.py:182-190: 20000 x 3 in [-5, 40), generator seed 0)."""
+    from oracle import unique as ounique
+
+    rng = np.random.default_rng(41)
+    keys = np.concatenate([rng.integers(-1000, 1000, 5000), [np.iinfo(np.int64).min, np.iinfo(np.int64).max, 0]])
+    for counts in (False, True):
+        got = ounique.unique_keys(keys, return_counts=counts)
+        ref = np.unique(keys, return_inverse=True, return_counts=counts)
+        assert np.array_equal(got[0], ref[0]) and np.array_equal(got[1], ref[1])
+        if counts:
+            assert np.array_equal(got[2], ref[2])
+        empty = ounique.unique_keys(np.empty(0, np.int64), return_counts=counts)
+        ref = np.unique(np.empty(0, np.int64), return_inverse=True, return_counts=counts)
+        assert np.array_equal(empty[0], ref[0]) and np.array_equal(empty[1], ref[1])
+        assert (empty[2] is None) == (not counts)
+    g = torch.Generator().manual_seed(0)
+    rows = torch.randint(-5, 40, (20000, 3), generator=g)
+    ref = torch.unique(rows, dim=0, return_inverse=True, return_counts=True)
+    got = ounique.unique_rows(rows.numpy(), return_inverse=True, return_counts=True)
+    for a, b in zip(ref, got):
+        assert np.array_equal(a.numpy(), b)
+    assert ounique.packed_keys(np.array([[0, 0], [2**40, 2**30]])) is None
