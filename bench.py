@@ -11,7 +11,7 @@ peak. ``cpu_baseline`` times the reference's CPU fallback (oracle port: sort +
 searchsorted map, per-offset gather / matmul / index_add_) on the host cores.
 ``extra`` reports the other workloads: the fp32 sphere shell, the strided pair, W8A8
 int8 TOPS (GEMM alone and quantise + GEMM), the residual blocks, octree upsampling,
-unique cube corners, and kernel-map builds.
+transformer I/O resampling, unique cube corners, and kernel-map builds.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
 """
@@ -324,6 +324,50 @@ def bench_upsample(steps: int, warmup: int):
     }
 
 
+def bench_geometry(steps: int, warmup: int):
+    """Refiner transformer I/O resampling on the 1024^3 residual-block shells at C256
+    fp16: mean pool down, parent copy up, and the up block's first convolution from the
+    coarse rows (against the same convolution of materialised upsampled features)."""
+    import numpy as np
+    import torch
+
+    from hi3d_amd import conv, workloads
+    from hi3d_amd.geometry import Geometry
+
+    dev = torch.device("cuda:0")
+    idx = torch.as_tensor(workloads.coords_for("resblock_c256_fp16", device=dev)).to(dev)
+    coords = idx[:, 1:].contiguous()
+    build_wall, _ = timed(lambda: Geometry(coords), 2, 1)
+    geo = Geometry(coords)
+    c = 256
+    x = torch.as_tensor(workloads.normal((geo.full.n, c), 1.0, 81, np.float16)).to(dev)
+    h = torch.as_tensor(workloads.normal((geo.low.n, c), 1.0, 82, np.float16)).to(dev)
+    w = torch.as_tensor(workloads.normal((c, 27 * c), 1.0 / np.sqrt(27 * c), 83, np.float16)).to(dev)
+    b = torch.as_tensor(workloads.normal((c,), 0.02, 84, np.float16)).to(dev)
+    geo.up_conv_plan  # built once per pass, like the reference's up_conv_index
+    geo.full.plan
+    _, down = timed(lambda: geo.downsample(x), steps, warmup)
+    _, up = timed(lambda: geo.upsample(h), steps, warmup)
+    _, upc = timed(lambda: geo.up_conv(h, w, b), max(3, steps // 5), max(1, warmup // 2))
+    w3 = w.reshape(c, 27, c).contiguous()
+    _, composed = timed(lambda: conv.conv(geo.upsample(h), geo.full.plan, w3, b), max(3, steps // 5),
+                        max(1, warmup // 2))
+    pairs = int((geo.full.table < geo.full.n).sum())
+    return {
+        "workload": "transformer_io_c256_fp16",
+        "voxels": geo.full.n,
+        "coarse_voxels": geo.low.n,
+        "geometry_build_ms": build_wall,
+        "downsample_ms": down,
+        "downsample_gbs": (geo.full.n + geo.low.n) * c * 2 / (down * 1e-3) / 1e9,
+        "upsample_ms": up,
+        "upsample_gbs": (geo.full.n + geo.low.n) * c * 2 / (up * 1e-3) / 1e9,
+        "up_conv_ms": upc,
+        "up_conv_tflops": 2.0 * pairs * c * c / (upc * 1e-3) / 1e12,
+        "upsample_then_conv_ms": composed,
+    }
+
+
 def bench_unique(steps: int, warmup: int):
     """Unique cube corners of the 1024^3 residual-block shells (mesh extraction's
     ``torch.unique(dim=0)``): 8 corner rows of 3 int32 per voxel, with inverse and
@@ -420,6 +464,8 @@ def main() -> int:
         extra["vae_resnet_c64_fp16"] = bench_vae(max(10, args.steps // 2), max(2, args.warmup // 2))
         log("VAE decoder octree upsampling C256 fp16, 512^3 fine shells' parents")
         extra["vae_upsample_c256_fp16"] = bench_upsample(max(10, args.steps // 2), max(2, args.warmup // 2))
+        log("transformer I/O resampling C256 fp16, 1024^3 shells")
+        extra["transformer_io_c256_fp16"] = bench_geometry(max(10, args.steps // 2), max(2, args.warmup // 2))
         log("unique cube corners of the 1024^3 shells")
         extra["unique_corners_1024"] = bench_unique(max(5, args.steps // 10), 2)
     cpu = None

@@ -1360,11 +1360,53 @@ __global__ void gather_mean_kernel(const T* __restrict__ in, int64_t n_in, int c
   out[idx] = static_cast<T>(acc / static_cast<Acc>(cnt + extra));
 }
 
+// The same mean with 16 bytes of a row per thread (rows a multiple of 16 bytes, 16-byte
+// aligned): the table entries are read once per chunk instead of once per element, and
+// each present row moves in one 16-byte load. Same summation order (present entries in
+// table order), so the results equal gather_mean_kernel's.
+template <typename T, typename Acc>
+__global__ void gather_mean_vec_kernel(const T* __restrict__ in, int64_t n_in, int c, const int32_t* __restrict__ table,
+                                       int kvol, int64_t n_out, int extra, T* __restrict__ out) {
+  constexpr int E = 16 / static_cast<int>(sizeof(T));
+  const int cpr = c / E;
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= n_out * cpr) return;
+  const int64_t o = idx / cpr;
+  const int j = static_cast<int>(idx - o * cpr) * E;
+  Acc acc[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) acc[e] = 0;
+  int cnt = 0;
+  for (int k = 0; k < kvol; ++k) {
+    const int32_t src = table[o * kvol + k];
+    if (static_cast<uint64_t>(static_cast<uint32_t>(src)) >= static_cast<uint64_t>(n_in)) continue;
+    const uint4 raw = *reinterpret_cast<const uint4*>(in + static_cast<int64_t>(src) * c + j);
+    const T* v = reinterpret_cast<const T*>(&raw);
+#pragma unroll
+    for (int e = 0; e < E; ++e) acc[e] += static_cast<Acc>(v[e]);
+    ++cnt;
+  }
+  uint4 res;
+  T* r = reinterpret_cast<T*>(&res);
+  const Acc div = static_cast<Acc>(cnt + extra);
+#pragma unroll
+  for (int e = 0; e < E; ++e) r[e] = static_cast<T>(acc[e] / div);
+  *reinterpret_cast<uint4*>(out + o * c + j) = res;
+}
+
 template <typename T, typename Acc>
 int launch_mean(const void* in, int64_t n_in, int c, const int32_t* table, int kvol, int64_t n_out, int extra, void* out,
                 hipStream_t stream) {
   const int64_t total = n_out * c;
   if (total == 0) return HI3D_OK;
+  constexpr int E = 16 / static_cast<int>(sizeof(T));
+  if (c % E == 0 && ((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(out)) & 15) == 0) {
+    const int64_t chunks = total / E;
+    hipLaunchKernelGGL((gather_mean_vec_kernel<T, Acc>), dim3(static_cast<unsigned>(ceil_div(chunks, 256))), dim3(256),
+                       0, stream, static_cast<const T*>(in), n_in, c, table, kvol, n_out, extra, static_cast<T*>(out));
+    HI3D_LAUNCH_CHECK();
+    return HI3D_OK;
+  }
   hipLaunchKernelGGL((gather_mean_kernel<T, Acc>), dim3(static_cast<unsigned>(ceil_div(total, 256))), dim3(256), 0,
                      stream, static_cast<const T*>(in), n_in, c, table, kvol, n_out, extra, static_cast<T*>(out));
   HI3D_LAUNCH_CHECK();

@@ -358,6 +358,32 @@ __global__ void coarse_counts_kernel(const int32_t* __restrict__ ids, int64_t n,
   }
 }
 
+// parent_table[o, k] = inverse[table[o, k]] for present entries, n_low for absent ones
+__global__ void parent_table_kernel(const int32_t* __restrict__ table, int64_t total, int64_t n,
+                                    const int32_t* __restrict__ inverse, int64_t n_low, int32_t* __restrict__ out) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int32_t t = table[i];
+  out[i] = static_cast<uint64_t>(static_cast<uint32_t>(t)) < static_cast<uint64_t>(n) ? inverse[t]
+                                                                                       : static_cast<int32_t>(n_low);
+}
+
+// out[i] = in[index[i]] for rows of rb bytes (a multiple of 16): one 16-byte chunk per
+// thread
+__global__ void gather_rows_kernel(const char* __restrict__ in, int64_t n_in, int rb, const int32_t* __restrict__ index,
+                                   int64_t n, char* __restrict__ out) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int cpr = rb >> 4;
+  const int64_t row = t / cpr;
+  if (row >= n) return;
+  const int c = static_cast<int>(t - row * cpr);
+  const int32_t src = index[row];
+  uint4 v = make_uint4(0u, 0u, 0u, 0u);
+  if (static_cast<uint64_t>(static_cast<uint32_t>(src)) < static_cast<uint64_t>(n_in))
+    v = *reinterpret_cast<const uint4*>(in + static_cast<int64_t>(src) * rb + c * 16);
+  *reinterpret_cast<uint4*>(out + row * rb + c * 16) = v;
+}
+
 __global__ void stride2_tables_kernel(const int32_t* __restrict__ inverse,
                                       const uint8_t* __restrict__ slot, int64_t n, int64_t n_low,
                                       int32_t* __restrict__ down, int32_t* __restrict__ up) {
@@ -624,6 +650,35 @@ int hi3d_stride2_tables(const int32_t* inverse, const uint8_t* slot, int64_t n, 
   if (down) launch_fill<int32_t>(down, n_low * 8, static_cast<int32_t>(n), stream);
   hipLaunchKernelGGL(stride2_tables_kernel, dim3(static_cast<unsigned>(ceil_div(n, 256))), dim3(256), 0, stream,
                      inverse, slot, n, n_low, down, up);
+  HI3D_LAUNCH_CHECK();
+  return HI3D_OK;
+}
+
+int hi3d_parent_table(const int32_t* table, int64_t n, int32_t kvol, const int32_t* inverse, int64_t n_low,
+                      int32_t* out, void* stream_) {
+  hipStream_t stream = as_stream(stream_);
+  HI3D_REQUIRE(n >= 0 && n_low >= 0 && n_low < (int64_t(1) << 31) - 1 && kvol >= 1 && kvol <= 1024, "bad sizes");
+  if (n == 0) return HI3D_OK;
+  HI3D_REQUIRE(table && inverse && out, "null pointer argument");
+  const int64_t total = n * kvol;
+  hipLaunchKernelGGL(parent_table_kernel, dim3(static_cast<unsigned>(ceil_div(total, 256))), dim3(256), 0, stream,
+                     table, total, n, inverse, n_low, out);
+  HI3D_LAUNCH_CHECK();
+  return HI3D_OK;
+}
+
+int hi3d_gather_rows(const void* in, int64_t n_in, int32_t row_bytes, const int32_t* index, int64_t n, void* out,
+                     void* stream_) {
+  hipStream_t stream = as_stream(stream_);
+  HI3D_REQUIRE(row_bytes > 0 && row_bytes % 16 == 0, "row bytes must be a positive multiple of 16, got %d", row_bytes);
+  HI3D_REQUIRE(n >= 0 && n_in >= 0, "bad sizes");
+  if (n == 0) return HI3D_OK;
+  HI3D_REQUIRE(in && index && out, "null pointer argument");
+  HI3D_REQUIRE(((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(out)) & 15) == 0,
+               "rows must be 16-byte aligned");
+  const int64_t total = n * (row_bytes / 16);
+  hipLaunchKernelGGL(gather_rows_kernel, dim3(static_cast<unsigned>(ceil_div(total, 256))), dim3(256), 0, stream,
+                     static_cast<const char*>(in), n_in, row_bytes, index, n, static_cast<char*>(out));
   HI3D_LAUNCH_CHECK();
   return HI3D_OK;
 }

@@ -18,6 +18,11 @@ from . import _lib
 
 ROTATIONS = ("h64", "none")
 
+FORMAT = "hi3d-w8a8-h64"
+"""safetensors metadata ``format`` of released W8A8 checkpoints (models/w8a8/manifest.json:11)."""
+REQUIRED_SCALE = "blocks.0.self_attn.to_qkv.w8_scale"
+"""The scale whose absence makes the reference refuse a file in W8A8 mode (transformer.py:299-300)."""
+
 
 @lru_cache(None)
 def _signs_np(width: int) -> np.ndarray:
@@ -113,3 +118,54 @@ def quantize_weight(weight: torch.Tensor, rotation: str = "h64", multiplier: tor
     the activations when ``rotation == "h64"`` (format ``hi3d-w8a8-h64``,
     models/w8a8/manifest.json:10-17). Uses the activation quantiser on the rows."""
     return quantize_activation(weight.to(torch.float16), multiplier, rotation)
+
+
+def load_checkpoint(path, device: torch.device | str = "cuda", require_blocks: bool = True) -> dict[str, torch.Tensor]:
+    """Tensors of a released ``hi3d-w8a8-h64`` safetensors file on ``device``:
+    ``<name>.weight`` int8 ``[N, K]`` (rows rotated like the activations),
+    ``<name>.w8_scale`` float32 ``[N]`` and every other tensor as stored
+    (transformer.py:289-301; models/w8a8/manifest.json:10-17). Read with the safetensors
+    loader, which executes nothing from the file. Raises the reference's ValueError when
+    the metadata format is not ``hi3d-w8a8-h64`` or (``require_blocks``) the first block's
+    QKV scale is missing, and a ValueError for a scale whose weight is not a matching
+    int8 matrix."""
+    from safetensors import safe_open
+
+    with safe_open(str(path), framework="pt", device="cpu") as f:
+        meta = f.metadata() or {}
+        if meta.get("format") != FORMAT:
+            raise ValueError("W8A8 requires the released Hi3Dv1.0-mlx-w8a8 checkpoints")
+        tensors = {k: f.get_tensor(k) for k in f.keys()}
+    if require_blocks and REQUIRED_SCALE not in tensors:
+        raise ValueError("W8A8 requires the released Hi3Dv1.0-mlx-w8a8 checkpoints")
+    for key, scale in tensors.items():
+        if not key.endswith(".w8_scale"):
+            continue
+        w = tensors.get(key[: -len(".w8_scale")] + ".weight")
+        if w is None or w.dtype != torch.int8 or w.ndim != 2 or scale.dtype != torch.float32 or tuple(scale.shape) != (w.shape[0],):
+            raise ValueError(f"{key}: expected an int8 [N, K] weight and a float32 [N] scale")
+    return {k: v.to(device) for k, v in tensors.items()}
+
+
+def quantize_checkpoint(tensors: dict[str, torch.Tensor], names, rotation: str = "h64") -> dict[str, torch.Tensor]:
+    """``{name}.weight`` of every projection in ``names`` converted to the released layout
+    (int8 rows + float32 ``{name}.w8_scale``, :func:`quantize_weight`); other tensors kept."""
+    out = dict(tensors)
+    for name in names:
+        w, sw = quantize_weight(tensors[f"{name}.weight"], rotation)
+        out[f"{name}.weight"] = w
+        out[f"{name}.w8_scale"] = sw
+    return out
+
+
+def save_checkpoint(path, tensors: dict[str, torch.Tensor]) -> None:
+    """Write ``tensors`` as a ``hi3d-w8a8-h64`` safetensors file (host copies)."""
+    from safetensors.torch import save_file
+
+    save_file({k: v.detach().cpu().contiguous() for k, v in tensors.items()}, str(path), metadata={"format": FORMAT})
+
+
+def linear_named(x: torch.Tensor, tensors: dict[str, torch.Tensor], name: str) -> torch.Tensor:
+    """``linear`` with ``{name}.weight`` / ``.w8_scale`` / ``.bias`` from a loaded
+    checkpoint, as the reference's block linears call it (transformer.py:503-507)."""
+    return linear(x, tensors[f"{name}.weight"], tensors[f"{name}.w8_scale"], tensors[f"{name}.bias"])

@@ -181,6 +181,20 @@ int hi3d_gather_conv_narrow(const void* in_dev, int64_t n_in, int32_t cin, const
                             const void* residual_dev, int32_t act, int32_t dtype, void* out_dev,
                             void* stream);
 
+/* out_dev [n, kvol] = inverse_dev[table_dev[o, k]] where the entry is present (< n), n_low
+ * where it is absent: the map of a convolution over a fine set whose inputs are the
+ * coarse parents of the fine neighbours. Replaces Geometry.up_conv_index
+ * (src/hi3d_mac/mlx_backend/transformer.py:253-259), which flattens it with the offset
+ * for a per-tap projection. */
+int hi3d_parent_table(const int32_t* table_dev, int64_t n, int32_t kvol, const int32_t* inverse_dev,
+                      int64_t n_low, int32_t* out_dev, void* stream);
+
+/* out_dev[i] = in_dev[index_dev[i]] for rows of row_bytes (a multiple of 16; 16-byte
+ * aligned pointers), zero rows for indices outside [0, n_in). Replaces
+ * Geometry.upsample's take (src/hi3d_mac/mlx_backend/transformer.py:265-266). */
+int hi3d_gather_rows(const void* in_dev, int64_t n_in, int32_t row_bytes, const int32_t* index_dev, int64_t n,
+                     void* out_dev, void* stream);
+
 /* Workspace bytes of hi3d_unique_keys. */
 int hi3d_unique_keys_workspace(int64_t n, int64_t* bytes_host);
 

@@ -185,3 +185,45 @@ def test_gemm_full_output_bit_exact(cuda, m, n, k, with_bias):
     assert np.array_equal(got, ref), int((got != ref).sum())
     out2, _ = w8a8.gemm(dev[0], dev[1], dev[2], dev[3], bias_t, return_acc=True)
     assert torch.equal(out, out2)
+
+
+def test_checkpoint_round_trip(cuda, tmp_path):
+    """A ``hi3d-w8a8-h64`` safetensors file (written here: no released checkpoint is
+    available offline) loads with its int8 rows and float32 scales and drives the same
+    projection bits as the in-memory weights; files of another format, or without the
+    first block's QKV scale, are refused with the reference's message
+    (src/hi3d_mac/mlx_backend/transformer.py:289-301)."""
+    from hi3d_amd import w8a8
+
+    rng = np.random.default_rng(17)
+    k, n = 1024, 3072
+    dense = {
+        "blocks.0.self_attn.to_qkv.weight": torch.as_tensor((rng.standard_normal((n, k)) / 32).astype(np.float16)).to(cuda),
+        "blocks.0.self_attn.to_qkv.bias": torch.as_tensor((rng.standard_normal(n) * 0.02).astype(np.float16)).to(cuda),
+        "blocks.0.norm1.weight": torch.as_tensor(rng.standard_normal(k).astype(np.float32)).to(cuda),
+    }
+    q = w8a8.quantize_checkpoint(dense, ["blocks.0.self_attn.to_qkv"])
+    path = tmp_path / "w8a8.safetensors"
+    w8a8.save_checkpoint(path, q)
+    loaded = w8a8.load_checkpoint(path, cuda)
+    assert set(loaded) == set(q)
+    for key in q:
+        assert loaded[key].dtype == q[key].dtype and torch.equal(loaded[key], q[key])
+    wq, sw = loaded["blocks.0.self_attn.to_qkv.weight"], loaded["blocks.0.self_attn.to_qkv.w8_scale"]
+    rq, rs = ow8a8.quantize_activation(dense["blocks.0.self_attn.to_qkv.weight"].cpu().numpy())
+    assert np.array_equal(wq.cpu().numpy(), rq) and np.array_equal(sw.cpu().numpy(), rs)
+    x = torch.as_tensor(rng.standard_normal((300, k)).astype(np.float16)).to(cuda)
+    got = w8a8.linear_named(x, loaded, "blocks.0.self_attn.to_qkv")
+    want = w8a8.linear(x, wq, sw, dense["blocks.0.self_attn.to_qkv.bias"])
+    assert torch.equal(got, want)
+    from safetensors.torch import save_file
+
+    other = tmp_path / "fp16.safetensors"
+    save_file({k: v.cpu() for k, v in dense.items()}, str(other), metadata={"format": "pt"})
+    with pytest.raises(ValueError, match="released Hi3Dv1.0-mlx-w8a8"):
+        w8a8.load_checkpoint(other, cuda)
+    partial = tmp_path / "partial.safetensors"
+    w8a8.save_checkpoint(partial, {"blocks.0.norm1.weight": dense["blocks.0.norm1.weight"]})
+    with pytest.raises(ValueError, match="released Hi3Dv1.0-mlx-w8a8"):
+        w8a8.load_checkpoint(partial, cuda)
+    assert set(w8a8.load_checkpoint(partial, cuda, require_blocks=False)) == {"blocks.0.norm1.weight"}

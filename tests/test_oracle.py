@@ -484,3 +484,34 @@ def test_unique_oracle_against_numpy_and_torch():
     for a, b in zip(ref, got):
         assert np.array_equal(a.numpy(), b)
     assert ounique.packed_keys(np.array([[0, 0], [2**40, 2**30]])) is None
+
+
+def test_geometry_oracle_up_conv_is_conv_of_upsampled():
+    """The reference's projection form of the up block's first convolution equals a
+    dense ``F.conv3d(padding=1)`` of the upsampled volume (float64, 12^3 grid), and the
+    mean pool equals ``scatter_reduce(mean, include_self)`` onto zeros."""
+    from oracle import geometry as ogeo
+
+    rng = np.random.default_rng(51)
+    side = 12
+    idx = np.argwhere(rng.random((side,) * 3) < 0.3).astype(np.int32)
+    n = len(idx)
+    table = okmap.neighbour_table_dense(idx)
+    low, inverse = np.unique(idx // 2, axis=0, return_inverse=True)
+    inverse = inverse.reshape(-1)
+    n_low = len(low)
+    cin, cout = 5, 3
+    h = rng.normal(size=(n_low, cin))
+    w = rng.normal(size=(cout, 27 * cin))
+    b = rng.normal(size=cout)
+    got = ogeo.up_conv_f64(h, table, inverse, w, b)
+    up = ogeo.upsample(h, inverse)
+    dense = torch.zeros((1, cin, side, side, side), dtype=torch.float64)
+    dense[0, :, idx[:, 0], idx[:, 1], idx[:, 2]] = torch.as_tensor(up.T)
+    wt = torch.as_tensor(w.reshape(cout, 3, 3, 3, cin)).permute(0, 4, 1, 2, 3)
+    ref = F.conv3d(dense, wt, torch.as_tensor(b), padding=1)[0][:, idx[:, 0], idx[:, 1], idx[:, 2]].T.numpy()
+    assert np.allclose(got, ref, rtol=1e-12, atol=1e-12)
+    x = rng.normal(size=(n, 4))
+    pooled = torch.zeros((n_low, 4), dtype=torch.float64).scatter_reduce(
+        0, torch.as_tensor(inverse)[:, None].expand(-1, 4), torch.as_tensor(x), reduce="mean", include_self=True)
+    assert np.allclose(ogeo.downsample_f64(x, inverse, n_low), pooled.numpy(), rtol=1e-12, atol=1e-12)
