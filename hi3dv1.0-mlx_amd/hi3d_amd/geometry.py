@@ -34,7 +34,7 @@ class Geometry:
         self.full = Level.from_coords(coords)
         n = self.full.n
         indices = torch.cat([torch.zeros((n, 1), dtype=torch.int32, device=device), coords], 1)
-        extent = (coords.max(dim=0).values + 1).tolist() if n else [1, 1, 1]
+        extent = [v + 1 for v in _kmap.column_bounds(coords)[1]] if n else [1, 1, 1]
         s = _kmap.stride2_structure(indices, extent, 1)
         self._structure = s
         self.low = Level.from_coords(s.low[:, 1:].contiguous())

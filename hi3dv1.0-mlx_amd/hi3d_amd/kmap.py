@@ -30,6 +30,21 @@ PLAN_SMALL_WINDOW = 1 << 18
 PLAN_LARGE_WINDOW = 1 << 18
 
 
+def column_bounds(a: torch.Tensor) -> tuple[list[int], list[int]]:
+    """Per-column minima and maxima of non-empty integer rows ``a [N, d]`` (d <= 8), from
+    one GPU pass (``hi3d_row_bounds``) and one host read."""
+    device = _lib.require_gpu(a)
+    if a.dim() != 2 or a.shape[0] == 0 or a.dtype not in (torch.int32, torch.int64):
+        raise ValueError("column_bounds needs non-empty int32 / int64 rows [N, d]")
+    a = a.contiguous()
+    d = int(a.shape[1])
+    bounds = torch.empty((2, d), dtype=torch.int64, device=device)
+    _lib.call("hi3d_row_bounds", _lib.ptr(a), _lib.I64 if a.dtype == torch.int64 else _lib.I32, int(a.shape[0]), d,
+              _lib.ptr(bounds[0]), _lib.ptr(bounds[1]), _lib.stream(device))
+    lo, hi = bounds.tolist()
+    return lo, hi
+
+
 def _as_coords(indices: torch.Tensor) -> torch.Tensor:
     if indices.ndim != 2 or indices.shape[1] != 4:
         raise ValueError(f"expected coords [N, 4], got {tuple(indices.shape)}")
@@ -256,9 +271,10 @@ def neighbour_table(coords: torch.Tensor) -> torch.Tensor:
     n = int(xyz.shape[0])
     if n == 0:
         return torch.empty((0, 27), dtype=torch.int32, device=coords.device)
-    if int(xyz.min()) < 0:
+    lo, hi = column_bounds(xyz)
+    if min(lo) < 0:
         raise ValueError("grid coordinates must be non-negative")
-    extent = (xyz.max(dim=0).values + 1).tolist()
+    extent = [v + 1 for v in hi]
     indices = torch.cat([torch.zeros((n, 1), dtype=torch.int32, device=coords.device), xyz], 1)
     return build_kernel_map(indices, extent, 1, 3).table
 
@@ -334,7 +350,7 @@ def downsample_structure(coords: torch.Tensor) -> tuple[torch.Tensor, torch.Tens
     _lib.require_gpu(coords)
     xyz = coords.to(torch.int32)
     n = int(xyz.shape[0])
-    extent = (xyz.max(dim=0).values + 1).tolist() if n else [1, 1, 1]
+    extent = [v + 1 for v in column_bounds(xyz)[1]] if n else [1, 1, 1]
     indices = torch.cat([torch.zeros((n, 1), dtype=torch.int32, device=coords.device), xyz], 1)
     s = stride2_structure(indices, extent, 1)
     return s.low[:, 1:].contiguous(), s.inverse, s.counts

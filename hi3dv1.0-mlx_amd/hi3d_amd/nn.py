@@ -199,7 +199,7 @@ class SparseDownsample(nn.Module):
         if factor != (2, 2, 2):
             raise NotImplementedError("the GPU downsample implements factor 2")
         coords = input.coords
-        extent = (coords[:, 1:].max(dim=0).values + 1).tolist()
+        extent = [v + 1 for v in _kmap.column_bounds(coords.to(torch.int32))[1][1:]]
         s = _kmap.stride2_structure(coords, extent)
         feats = input.feats.contiguous()
         device = _lib.require_gpu(feats)

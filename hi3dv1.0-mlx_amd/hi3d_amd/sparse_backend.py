@@ -15,6 +15,7 @@ from typing import Any, Optional, Tuple
 import torch
 from torch import nn
 
+from . import kmap as _kmap
 from . import spconv
 
 _SPARSE_CONV_FLAG = "_sparc3d_sparse_conv"
@@ -74,10 +75,15 @@ def sparse_tensor(
     if coords.ndim != 2 or coords.shape[1] != 4:
         raise ValueError(f"expected coords [N, 4], got {tuple(coords.shape)}")
     coords = coords.int().contiguous()
-    grid = coords[:, 1:]
-    if int(grid.min()) < 0:
+    if coords.shape[0] == 0:
+        lo, hi = [0] * 4, [0] * 4
+    elif coords.is_cuda:
+        lo, hi = _kmap.column_bounds(coords)
+    else:  # a host-side container (validation only; the convolutions need the GPU)
+        lo, hi = coords.min(dim=0).values.tolist(), coords.max(dim=0).values.tolist()
+    if min(lo[1:]) < 0:
         raise ValueError("grid coordinates must be non-negative")
-    extent = (grid.max(dim=0).values + 1).tolist()
+    extent = [v + 1 for v in hi[1:]]
     if spatial_shape is None:
         spatial_shape = tuple(extent)
     elif any(bound < size for bound, size in zip(spatial_shape, extent)):
@@ -86,7 +92,7 @@ def sparse_tensor(
         features=feats,
         indices=coords,
         spatial_shape=list(spatial_shape),
-        batch_size=int(coords[:, 0].max()) + 1,
+        batch_size=hi[0] + 1,
     )
 
 
