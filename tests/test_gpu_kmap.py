@@ -203,3 +203,57 @@ def test_plan_covers_every_row_once(cuda):
         present = (gidx != km.n)
         exp = (present.any(axis=2).astype(np.uint64) << np.arange(27, dtype=np.uint64)).sum(1).astype(np.uint32)
         assert np.array_equal(masks, exp)
+
+
+def test_blocked_assembly_matches_single_block(cuda):
+    """The reference's blocked-assembly test (tests/test_mlx_kernels.py:92-102): row
+    blocks concatenated, and assembled in place past the size threshold, equal one block."""
+    from hi3d_amd import sparse
+
+    x = torch.randn((1000, 16), device=cuda)
+    fn = lambda s, e: x[s:e] * 2 + 1
+    whole = fn(0, 1000)
+    assert torch.equal(sparse.blocked(1000, 64, fn, 16, torch.float32), whole)
+    old = sparse.ASSEMBLE_IN_PLACE_BYTES
+    try:
+        sparse.ASSEMBLE_IN_PLACE_BYTES = 0  # force the in-place path
+        assert torch.equal(sparse.blocked(1000, 64, fn, 16, torch.float32, device=cuda), whole)
+    finally:
+        sparse.ASSEMBLE_IN_PLACE_BYTES = old
+
+
+def test_blocked_accumulate_adds_in_place(cuda):
+    """tests/test_mlx_kernels.py:105-121: the accumulated result lives in the donated
+    buffer and the peak stays within one block of the inputs."""
+    from hi3d_amd import sparse
+
+    n, c = 200_000, 128
+    base = torch.randn((n, c), device=cuda)
+    h = torch.randn((n, c), device=cuda)
+    expected = base + h * 2
+    ptr = base.data_ptr()
+    fn = lambda s, e: h[s:e] * 2
+    holder = [base]
+    del base
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats(cuda)
+    before = torch.cuda.memory_allocated(cuda)
+    out = sparse.blocked(n, 20_000, fn, c, torch.float32, accumulate=holder)
+    torch.cuda.synchronize()
+    assert out.data_ptr() == ptr and torch.equal(out, expected)
+    assert torch.cuda.max_memory_allocated(cuda) - before < n * c * 4 // 2
+
+
+@pytest.mark.parametrize("dtype,c", [(torch.float16, 64), (torch.float32, 3)])
+def test_gather_neighbours_matches_take(cuda, dtype, c):
+    """``gather_neighbours(pad_rows(x), level, s, e)`` equals taking the padded rows by
+    the table (sparse.py:175-182), absent neighbours reading the zero row."""
+    from hi3d_amd import sparse
+
+    data = np.load(GOLDEN / "child_10cube.npz")
+    level = sparse.Level.from_coords(torch.as_tensor(data["coords"]).to(cuda))
+    x = torch.randn((level.n, c), device=cuda).to(dtype)
+    padded = sparse.pad_rows(x)
+    assert padded.shape == (level.n + 1, c) and not padded[-1].any()
+    got = sparse.gather_neighbours(padded, level, 5, 77)
+    assert torch.equal(got, padded[level.table[5:77].long()])
