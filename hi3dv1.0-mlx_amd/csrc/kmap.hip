@@ -200,6 +200,64 @@ __global__ __launch_bounds__(256) void probe_kernel(const int4* __restrict__ coo
     if (cnt[k]) atomicAdd(&counts[k], cnt[k]);
 }
 
+// Dense-grid variant for grids of at most kDenseMaxCells cells: one int32 cell per grid
+// position holds its row (-1 empty). Row ids land by CAS (a second claim is a duplicate,
+// as in the hash), and the lookups of a block's rows read neighbouring cells, nine short
+// z-runs per row, instead of random hash slots.
+constexpr int64_t kDenseMaxCells = int64_t(1) << 31;
+
+__global__ void dense_scatter_kernel(const int4* __restrict__ coords, int64_t n, Grid g, int32_t* __restrict__ cells,
+                                     int32_t* __restrict__ status) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int4 c = coords[i];
+  if (!g.inside(c.x, c.y, c.z, c.w)) {
+    atomicOr(status, HI3D_MAP_RANGE);
+    return;
+  }
+  const int32_t prev = atomicCAS(&cells[g.key(c.x, c.y, c.z, c.w)], -1, static_cast<int32_t>(i));
+  if (prev != -1) atomicOr(status, HI3D_MAP_DUPLICATE);
+}
+
+__global__ __launch_bounds__(256) void dense_lookup_kernel(const int4* __restrict__ coords, int64_t n, Grid g,
+                                                           int ksize, const int32_t* __restrict__ cells,
+                                                           int32_t* __restrict__ nbr, int32_t* __restrict__ counts) {
+  __shared__ int32_t cnt[kMaxKvol];
+  const int kvol = ksize * ksize * ksize;
+  const int half = ksize / 2;
+  const int center = kvol / 2;
+  for (int k = threadIdx.x; k < kvol; k += blockDim.x) cnt[k] = 0;
+  __syncthreads();
+  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * kProbeRows;
+  const int rows = static_cast<int>(n - row0 < kProbeRows ? n - row0 : kProbeRows);
+  const int cells_n = rows * kvol;
+  const int32_t absent = static_cast<int32_t>(n);
+  for (int j = threadIdx.x; j < cells_n; j += blockDim.x) {
+    const int r = j / kvol;
+    const int k = j - r * kvol;
+    const int64_t o = row0 + r;
+    int32_t found;
+    if (k == center) {
+      found = static_cast<int32_t>(o);
+    } else {
+      const int4 c = coords[o];
+      const int x = c.y + k / (ksize * ksize) - half;
+      const int y = c.z + (k / ksize) % ksize - half;
+      const int z = c.w + k % ksize - half;
+      found = absent;
+      if (g.inside(c.x, x, y, z)) {
+        const int32_t v = cells[g.key(c.x, x, y, z)];
+        if (v >= 0) found = v;
+      }
+    }
+    nbr[o * kvol + k] = found;
+    if (found != absent) atomicAdd(&cnt[k], 1);
+  }
+  __syncthreads();
+  for (int k = threadIdx.x; k < kvol; k += blockDim.x)
+    if (cnt[k]) atomicAdd(&counts[k], cnt[k]);
+}
+
 int64_t default_capacity(int64_t n) {
   int64_t cap = 64;
   while (cap < 2 * n) cap <<= 1;
@@ -537,6 +595,51 @@ int hi3d_kmap_subm(const int32_t* coords, int64_t n, int32_t sx, int32_t sy, int
     hipLaunchKernelGGL(probe_kernel<false>, dim3(static_cast<unsigned>(ceil_div(n, kProbeRows))), dim3(256), 0,
                        stream, c4, n, g, ksize, slots, nullptr, mask, nbr, counts);
   }
+  HI3D_LAUNCH_CHECK();
+  return HI3D_OK;
+}
+
+int hi3d_kmap_dense_workspace(int32_t batch_size, int32_t sx, int32_t sy, int32_t sz, int64_t* bytes) {
+  HI3D_REQUIRE(bytes != nullptr, "bytes_host is NULL");
+  HI3D_REQUIRE(sx > 0 && sy > 0 && sz > 0 && batch_size > 0, "spatial_shape and batch_size must be positive");
+  const int64_t cells = static_cast<int64_t>(batch_size) * sx * sy * sz;
+  HI3D_REQUIRE(cells <= kDenseMaxCells, "dense map grid of %lld cells exceeds 2^31", static_cast<long long>(cells));
+  *bytes = align_up(cells * 4, 256);
+  return HI3D_OK;
+}
+
+int hi3d_kmap_subm_dense(const int32_t* coords, int64_t n, int32_t sx, int32_t sy, int32_t sz, int32_t batch_size,
+                         int32_t ksize, void* workspace, int64_t workspace_bytes, int32_t* nbr, int32_t* counts,
+                         int32_t* status, void* stream_) {
+  hipStream_t stream = as_stream(stream_);
+  HI3D_REQUIRE(n >= 0, "n must be non-negative");
+  HI3D_REQUIRE(ksize >= 1 && ksize % 2 == 1 && ksize * ksize * ksize <= kMaxKvol,
+               "ksize must be odd and at most 7, got %d", ksize);
+  HI3D_REQUIRE(n < (int64_t(1) << 31) - 1, "at most 2^31-2 voxels");
+  int64_t need = 0;
+  int rc = hi3d_kmap_dense_workspace(batch_size, sx, sy, sz, &need);
+  if (rc != HI3D_OK) return rc;
+  HI3D_REQUIRE(counts && status && (n == 0 || (coords && nbr && workspace)), "null pointer argument");
+  const int kvol = ksize * ksize * ksize;
+  launch_fill<int32_t>(counts, kvol, 0, stream);
+  launch_fill<int32_t>(status, 1, 0, stream);
+  if (n == 0) {
+    HI3D_LAUNCH_CHECK();
+    return HI3D_OK;
+  }
+  HI3D_REQUIRE(workspace_bytes >= need, "workspace too small: %lld < %lld bytes",
+               static_cast<long long>(workspace_bytes), static_cast<long long>(need));
+  Grid g{sx, sy, sz, batch_size};
+  auto* cells = static_cast<int32_t*>(workspace);
+  // clear the grid with 16-byte stores (the workspace is 256-byte aligned)
+  const int64_t ncells = static_cast<int64_t>(batch_size) * sx * sy * sz;
+  launch_fill<int4>(reinterpret_cast<int4*>(cells), ncells / 4, make_int4(-1, -1, -1, -1), stream);
+  launch_fill<int32_t>(cells + (ncells & ~int64_t(3)), ncells & 3, -1, stream);
+  const int4* c4 = reinterpret_cast<const int4*>(coords);
+  hipLaunchKernelGGL(dense_scatter_kernel, dim3(static_cast<unsigned>(ceil_div(n, 256))), dim3(256), 0, stream, c4, n,
+                     g, cells, status);
+  hipLaunchKernelGGL(dense_lookup_kernel, dim3(static_cast<unsigned>(ceil_div(n, kProbeRows))), dim3(256), 0, stream,
+                     c4, n, g, ksize, cells, nbr, counts);
   HI3D_LAUNCH_CHECK();
   return HI3D_OK;
 }

@@ -25,6 +25,10 @@ Measured with the 8-wave kernels: on the 543k-voxel C128 shells 2^18..2^20-row w
 0.444-0.454 ms against 0.455-0.462 ms at 2^16 (smaller windows keep gathers in L2 but
 group fewer rows of equal offset masks); on the 4.4M-voxel C256 shells 2^18 is best
 (7.99 ms, 8.10-8.17 ms at 2^19..2^20, 8.18-8.22 ms at 2^17)."""
+KMAP_DENSE_MAX_CELLS: int = 1 << 31
+"""Grids of at most this many cells (batch * sx * sy * sz) build their map through a
+dense grid of rows (``hi3d_kmap_subm_dense``) instead of the hash; ``0`` always hashes."""
+
 PLAN_GLOBAL_ROWS = 1 << 21
 PLAN_SMALL_WINDOW = 1 << 18
 PLAN_LARGE_WINDOW = 1 << 18
@@ -205,7 +209,9 @@ def build_kernel_map(
     capacity: int | None = None,
     check: bool = True,
 ) -> KernelMap:
-    """Hash-built submanifold kernel map of ``indices [N, 4]`` ``(batch, x, y, z)``.
+    """Submanifold kernel map of ``indices [N, 4]`` ``(batch, x, y, z)``: through a dense
+    grid of rows when the grid has at most ``KMAP_DENSE_MAX_CELLS`` cells and no hash
+    ``capacity`` is asked for, else through the voxel hash (same table either way).
 
     With ``check`` the device status word is read (one sync): duplicate or out-of-range
     coordinates raise ``ValueError``, a full hash table raises ``RuntimeError``.
@@ -219,17 +225,26 @@ def build_kernel_map(
     if ksize % 2 == 0 or ksize < 1:
         raise ValueError(f"only odd kernel sizes have a submanifold map, got {ksize}")
     kvol = ksize**3
-    key64 = int(batch_size) * sx * sy * sz >= 0xFFFFFFFF
-    cap = int(capacity or 0)
-    ws = _lib.workspace(_lib.query("hi3d_kmap_workspace", n, cap, int(key64)), device)
+    cells = int(batch_size) * sx * sy * sz
     table = torch.empty((n, kvol), dtype=torch.int32, device=device)
     counts = torch.empty(kvol, dtype=torch.int32, device=device)
     status = torch.empty(1, dtype=torch.int32, device=device)
-    _lib.call(
-        "hi3d_kmap_subm",
-        _lib.ptr(coords), n, sx, sy, sz, int(batch_size), int(ksize), cap, _lib.ptr(ws), ws.numel(),
-        _lib.ptr(table), _lib.ptr(counts), _lib.ptr(status), _lib.stream(device),
-    )
+    if capacity is None and cells <= KMAP_DENSE_MAX_CELLS:
+        ws = _lib.workspace(_lib.query("hi3d_kmap_dense_workspace", int(batch_size), sx, sy, sz), device)
+        _lib.call(
+            "hi3d_kmap_subm_dense",
+            _lib.ptr(coords), n, sx, sy, sz, int(batch_size), int(ksize), _lib.ptr(ws), ws.numel(),
+            _lib.ptr(table), _lib.ptr(counts), _lib.ptr(status), _lib.stream(device),
+        )
+    else:
+        key64 = cells >= 0xFFFFFFFF
+        cap = int(capacity or 0)
+        ws = _lib.workspace(_lib.query("hi3d_kmap_workspace", n, cap, int(key64)), device)
+        _lib.call(
+            "hi3d_kmap_subm",
+            _lib.ptr(coords), n, sx, sy, sz, int(batch_size), int(ksize), cap, _lib.ptr(ws), ws.numel(),
+            _lib.ptr(table), _lib.ptr(counts), _lib.ptr(status), _lib.stream(device),
+        )
     if check:
         flags = int(status.item())
         if flags & _lib.MAP_DUPLICATE:

@@ -72,6 +72,19 @@ int hi3d_kmap_subm(const int32_t* coords_dev, int64_t n, int32_t sx, int32_t sy,
                    int64_t workspace_bytes, int32_t* nbr_dev, int32_t* counts_dev,
                    int32_t* status_dev, void* stream);
 
+/* Workspace bytes of hi3d_kmap_subm_dense: one int32 cell per grid position
+ * (batch_size*sx*sy*sz <= 2^31). */
+int hi3d_kmap_dense_workspace(int32_t batch_size, int32_t sx, int32_t sy, int32_t sz, int64_t* bytes_host);
+
+/* The submanifold kernel map of hi3d_kmap_subm (same table, counts and status flags;
+ * HI3D_MAP_OVERFLOW never set) through a dense grid of rows instead of the hash: for
+ * grids small enough to clear, the lookups of neighbouring rows read neighbouring
+ * cells. Replaces the dense-grid lookup of neighbour_table
+ * (src/hi3d_mac/mlx_backend/sparse.py:29-43). */
+int hi3d_kmap_subm_dense(const int32_t* coords_dev, int64_t n, int32_t sx, int32_t sy, int32_t sz,
+                         int32_t batch_size, int32_t ksize, void* workspace_dev, int64_t workspace_bytes,
+                         int32_t* nbr_dev, int32_t* counts_dev, int32_t* status_dev, void* stream);
+
 /* Workspace bytes of hi3d_kmap_pairs. */
 int hi3d_kmap_pairs_workspace(int64_t n, int32_t kvol, int64_t* bytes_host);
 

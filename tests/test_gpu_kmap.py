@@ -257,3 +257,34 @@ def test_gather_neighbours_matches_take(cuda, dtype, c):
     assert padded.shape == (level.n + 1, c) and not padded[-1].any()
     got = sparse.gather_neighbours(padded, level, 5, 77)
     assert torch.equal(got, padded[level.table[5:77].long()])
+
+
+@pytest.mark.parametrize("ksize,batch,n_side,density", [(3, 1, 20, 0.2), (3, 3, 16, 0.5), (5, 2, 12, 0.3),
+                                                        (3, 1, 64, 0.01)])
+def test_dense_and_hash_maps_agree(cuda, ksize, batch, n_side, density):
+    """The dense-grid map and the hash map give the same table and counts bit for bit,
+    and both equal the oracle; both flag duplicates and out-of-range coordinates."""
+    from hi3d_amd import kmap
+
+    rng = np.random.default_rng(n_side * 10 + batch)
+    idx = _rand_indices(rng, n_side, density, batch=batch)
+    t = torch.as_tensor(idx).to(cuda)
+    dense = kmap.build_kernel_map(t, [n_side] * 3, batch, ksize)
+    hashed = kmap.build_kernel_map(t, [n_side] * 3, batch, ksize, capacity=1 << 16)
+    assert torch.equal(dense.table, hashed.table) and torch.equal(dense.counts, hashed.counts)
+    ref = okmap.neighbour_table(idx, [n_side] * 3, ksize)
+    assert np.array_equal(dense.table.cpu().numpy(), ref)
+    dup = torch.cat([t, t[3:4]])
+    for cap in (None, 1 << 16):
+        with pytest.raises(ValueError, match="duplicate"):
+            kmap.build_kernel_map(dup, [n_side] * 3, batch, ksize, capacity=cap)
+        bad = t.clone()
+        bad[5, 2] = n_side
+        with pytest.raises(ValueError, match="outside"):
+            kmap.build_kernel_map(bad, [n_side] * 3, batch, ksize, capacity=cap)
+    old = kmap.KMAP_DENSE_MAX_CELLS
+    try:
+        kmap.KMAP_DENSE_MAX_CELLS = 0  # the hash without a capacity
+        assert torch.equal(kmap.build_kernel_map(t, [n_side] * 3, batch, ksize).table, dense.table)
+    finally:
+        kmap.KMAP_DENSE_MAX_CELLS = old
