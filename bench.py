@@ -237,8 +237,9 @@ def bench_block(steps: int, warmup: int):
 
 
 def bench_vae(steps: int, warmup: int):
-    """VAE decoder residual block (GroupNorm + swish -> conv, twice, + shortcut) at C64
-    fp16 on the 512^3 fine shells, with its kernels timed apart."""
+    """VAE decoder residual block (GroupNorm + swish -> conv, twice, + shortcut) at the
+    finest decoder stage's width, C128 fp16, on the 512^3 fine shells, with its kernels
+    timed apart; the block on a donated input (in-place accumulate) beside it."""
     import numpy as np
     import torch
 
@@ -247,7 +248,7 @@ def bench_vae(steps: int, warmup: int):
     dev = torch.device("cuda:0")
     idx = workloads.coords_for("down2_up2_c64_c128_fp16", device=dev)
     level = sparse.Level.from_coords(torch.as_tensor(idx[:, 1:]).to(dev))
-    n, c = level.n, 64
+    n, c = level.n, 128
     x = torch.as_tensor(workloads.normal((n, c), 1.0, 61, np.float16)).to(dev)
     p = {}
     for i, name in enumerate(("v.block.0", "v.block.3")):
@@ -261,66 +262,20 @@ def bench_vae(steps: int, warmup: int):
     _, sw = timed(lambda: kernels.group_norm_swish(x, mean, inv, p["v.block.0.weights"], p["v.block.0.bias"],
                                                    torch.float16), steps, warmup)
     b_wall, b_ev = timed(lambda: vae.resnet(x, level, p, "v"), max(3, steps // 5), max(1, warmup // 2))
+    pool = [x.clone() for _ in range(6)]  # each in-place call consumes its input
+    ip_wall, _ = timed(lambda: vae.resnet([pool.pop()], level, p, "v"), 5, 1)
+    pairs = int((level.table < n).sum())
     return {
-        "workload": "vae_resnet_c64_fp16",
+        "workload": "vae_resnet_c128_fp16",
         "voxels": n,
         "block_ms": b_wall,
+        "block_in_place_ms": ip_wall,
+        "block_conv_tflops": 2 * 2.0 * pairs * c * c / (b_wall * 1e-3) / 1e12,
         "group_stats_ms": st,
         "group_stats_gbs": n * c * 2 / (st * 1e-3) / 1e9,
         "gn_swish_ms": sw,
         "gn_swish_gbs": 2 * n * c * 2 / (sw * 1e-3) / 1e9,
         "voxels_per_s": n / (b_wall * 1e-3),
-    }
-
-
-def bench_upsample(steps: int, warmup: int):
-    """One decoder octree upsampling at C256 fp16: the 512^3 fine shells' parents (their
-    2x2x2 coarse set) with the fine shells' own occupancy as the child mask, so the kept
-    children are exactly the fine set. Occupancy logits, child map and child projection
-    timed apart."""
-    import numpy as np
-    import torch
-
-    from hi3d_amd import kmap as _kmap
-    from hi3d_amd import sparse, vae, workloads
-
-    dev = torch.device("cuda:0")
-    idx = torch.as_tensor(workloads.coords_for("down2_up2_c64_c128_fp16", device=dev)).to(dev)
-    s2 = _kmap.stride2_structure(idx, [int(v) + 1 for v in idx[:, 1:].max(0).values.tolist()], 1)
-    level = sparse.Level.from_coords(s2.low[:, 1:].contiguous())
-    p_n, c = level.n, 256
-    mask = torch.zeros((p_n, 8), dtype=torch.bool, device=dev)
-    mask[s2.inverse.long(), s2.slot.long()] = True
-    x = torch.as_tensor(workloads.normal((p_n, c), 1.0, 71, np.float16)).to(dev)
-    params = {
-        "u.cls_head.fc.0.weights": torch.as_tensor(1.0 + workloads.normal((1, c), 0.1, 72)).to(dev),
-        "u.cls_head.fc.0.bias": torch.as_tensor(workloads.normal((1, c), 0.1, 73)).to(dev),
-        "u.cls_head.fc.2.weight": torch.as_tensor(workloads.normal((27 * c, 8), 1.0 / np.sqrt(27 * c), 74, np.float16)).to(dev),
-        "u.cls_head.fc.2.bias": torch.as_tensor(workloads.normal((8,), 0.02, 75, np.float16)).to(dev),
-        "u.proj.weight": torch.as_tensor(workloads.normal((8 * c, c), 1.0 / np.sqrt(c), 76, np.float16)).to(dev),
-    }
-    _, occ = timed(lambda: vae.occupancy(x, level, params, "u"), steps, warmup)
-    _, cmap = timed(lambda: sparse.child_neighbour_table(level.table, mask), steps, warmup)
-    _, parent, slot = sparse.child_neighbour_table(level.table, mask)
-    n_child = int(parent.shape[0])
-    w = params["u.proj.weight"]
-    _, plan_ms = timed(lambda: vae.child_plan(parent, slot, p_n), steps, warmup)
-    plan = vae.child_plan(parent, slot, p_n)
-    _, proj = timed(lambda: vae.children(x, parent, slot, w, plan=plan), steps, warmup)
-    up_wall, _ = timed(lambda: vae.upsample(x, level, params, "u", mask=mask), max(3, steps // 5), max(1, warmup // 2))
-    flops = 2.0 * n_child * c * c
-    return {
-        "workload": "vae_upsample_c256_fp16",
-        "parents": p_n,
-        "children": n_child,
-        "occupancy_ms": occ,
-        "child_map_ms": cmap,
-        "child_plan_ms": plan_ms,
-        "projection_ms": proj,
-        "projection_tflops": flops / (proj * 1e-3) / 1e12,
-        "projection_gbs": (n_child + p_n) * c * 2 / (proj * 1e-3) / 1e9,
-        "upsample_given_mask_ms": up_wall,
-        "children_per_s": n_child / (up_wall * 1e-3),
     }
 
 
@@ -460,8 +415,8 @@ def main() -> int:
         extra["w8a8_linear"] = bench_w8a8(max(10, args.steps // 2), max(3, args.warmup // 2))
         log("workload 5: residual block C256 fp16, 1024^3 shells")
         extra["resblock_c256_fp16"] = bench_block(max(10, args.steps // 2), max(2, args.warmup // 2))
-        log("VAE decoder residual block C64 fp16, 512^3 fine shells")
-        extra["vae_resnet_c64_fp16"] = bench_vae(max(10, args.steps // 2), max(2, args.warmup // 2))
+        log("VAE decoder residual block C128 fp16, 512^3 fine shells")
+        extra["vae_resnet_c128_fp16"] = bench_vae(max(10, args.steps // 2), max(2, args.warmup // 2))
         log("VAE decoder octree upsampling C256 fp16, 512^3 fine shells' parents")
         extra["vae_upsample_c256_fp16"] = bench_upsample(max(10, args.steps // 2), max(2, args.warmup // 2))
         log("transformer I/O resampling C256 fp16, 1024^3 shells")
