@@ -50,22 +50,43 @@ __global__ void iota_kernel(int32_t* __restrict__ rows, int64_t n) {
   if (i < n) rows[i] = static_cast<int32_t>(i);
 }
 
+// The table rows order[p0 .. p0 + nrows) into LDS as [row][kvol] (absent past n_out):
+// consecutive threads read consecutive entries of a row, so a wave's loads touch a few
+// rows' contiguous entries instead of one entry of 64 scattered rows.
+__device__ __forceinline__ void stage_rows(const int32_t* __restrict__ table, const int32_t* __restrict__ order,
+                                           int64_t p0, int64_t n_out, int kvol, int nrows, int32_t absent,
+                                           int32_t* __restrict__ lds) {
+  const int total = nrows * kvol;
+  for (int e = threadIdx.x; e < total; e += blockDim.x) {
+    const int row = e / kvol;
+    const int k = e - row * kvol;
+    const int64_t p = p0 + row;
+    lds[e] = p < n_out ? table[static_cast<int64_t>(order[p]) * kvol + k] : absent;
+  }
+}
+
 // key = (window << 32) | presence mask, for rows taken in Morton order.
-__global__ void mask_keys_kernel(const int32_t* __restrict__ table, int64_t n_out, int kvol, int64_t n_in,
-                                 const int32_t* __restrict__ order, int64_t window,
-                                 unsigned long long* __restrict__ keys, int32_t* __restrict__ rows) {
-  int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (p >= n_out) return;
-  const int32_t r = order[p];
+constexpr int kMaskRows = 256;
+__global__ __launch_bounds__(kMaskRows) void mask_keys_kernel(const int32_t* __restrict__ table, int64_t n_out,
+                                                              int kvol, int64_t n_in,
+                                                              const int32_t* __restrict__ order, int64_t window,
+                                                              unsigned long long* __restrict__ keys,
+                                                              int32_t* __restrict__ rows) {
+  __shared__ int32_t staged[kMaskRows * 32];
+  const int64_t p0 = static_cast<int64_t>(blockIdx.x) * kMaskRows;
+  const int64_t p = p0 + threadIdx.x;
   uint32_t mask = 0;
   if (kvol <= 32) {
-    const int32_t* t = table + static_cast<int64_t>(r) * kvol;
+    stage_rows(table, order, p0, n_out, kvol, kMaskRows, static_cast<int32_t>(n_in), staged);
+    __syncthreads();
+    const int32_t* t = staged + threadIdx.x * kvol;
     for (int k = 0; k < kvol; ++k)
-      if (static_cast<uint32_t>(t[k]) < static_cast<uint64_t>(n_in)) mask |= 1u << k;
+      if (static_cast<uint64_t>(static_cast<uint32_t>(t[k])) < static_cast<uint64_t>(n_in)) mask |= 1u << k;
   }
+  if (p >= n_out) return;
   const uint64_t w = window > 0 ? static_cast<uint64_t>(p / window) : 0;
   keys[p] = (w << 32) | mask;
-  rows[p] = r;
+  rows[p] = order[p];
 }
 
 // One block of kTileRows threads per tile: output rows, transposed gather indices and
@@ -77,6 +98,7 @@ __global__ __launch_bounds__(kTileRows) void tile_kernel(const int32_t* __restri
                                                          int32_t* __restrict__ gidx,
                                                          uint32_t* __restrict__ tile_mask) {
   __shared__ uint32_t wave_mask[kTileRows / 64];
+  __shared__ int32_t staged[kTileRows * 32];
   const int64_t tile = blockIdx.x;
   const int r = threadIdx.x;
   const int64_t p = tile * kTileRows + r;
@@ -85,14 +107,25 @@ __global__ __launch_bounds__(kTileRows) void tile_kernel(const int32_t* __restri
   uint32_t mask = 0;
   int32_t* g = gidx + tile * kvol * kTileRows + r;
   const int32_t absent = static_cast<int32_t>(n_in);
-  for (int k = 0; k < kvol; ++k) {
-    int32_t v = absent;
-    if (row >= 0) {
-      v = table[static_cast<int64_t>(row) * kvol + k];
-      if (static_cast<uint32_t>(v) >= static_cast<uint64_t>(n_in)) v = absent;
+  if (kvol <= 32) {
+    stage_rows(table, order, tile * kTileRows, n_out, kvol, kTileRows, absent, staged);
+    __syncthreads();
+    const int32_t* t = staged + r * kvol;
+    for (int k = 0; k < kvol; ++k) {
+      int32_t v = t[k];
+      if (static_cast<uint64_t>(static_cast<uint32_t>(v)) >= static_cast<uint64_t>(n_in)) v = absent;
+      g[k * kTileRows] = v;
+      if (v != absent) mask |= 1u << k;
     }
-    g[k * kTileRows] = v;
-    if (v != absent && k < 32) mask |= 1u << k;
+  } else {
+    for (int k = 0; k < kvol; ++k) {
+      int32_t v = absent;
+      if (row >= 0) {
+        v = table[static_cast<int64_t>(row) * kvol + k];
+        if (static_cast<uint64_t>(static_cast<uint32_t>(v)) >= static_cast<uint64_t>(n_in)) v = absent;
+      }
+      g[k * kTileRows] = v;
+    }
   }
   // OR-reduce over the wave, then over the block
   for (int d = 32; d >= 1; d >>= 1) mask |= __shfl_xor(mask, d, 64);
@@ -247,7 +280,8 @@ int hi3d_conv_plan(const int32_t* table, int64_t n_out, int32_t kvol, int64_t n_
   // second key: (window, mask); the sort is stable, so Morton order survives inside
   int32_t* ord_in = const_cast<int32_t*>(order);
   int32_t* ord_alt = (ord_in == r0) ? r1 : r0;
-  hipLaunchKernelGGL(mask_keys_kernel, dim3(blocks), dim3(256), 0, stream, table, n_out, kvol, n_in, ord_in,
+  hipLaunchKernelGGL(mask_keys_kernel, dim3(static_cast<unsigned>(ceil_div(n_out, kMaskRows))), dim3(kMaskRows), 0,
+                     stream, table, n_out, kvol, n_in, ord_in,
                      window_rows, k0, ord_alt);
   int64_t windows = window_rows > 0 ? ceil_div(n_out, window_rows) : 1;
   int end_bit = 32;
