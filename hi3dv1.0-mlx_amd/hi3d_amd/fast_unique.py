@@ -64,7 +64,8 @@ def _packed_keys(a: torch.Tensor):
 def unique_rows(x: torch.Tensor, return_inverse: bool = False, return_counts: bool = False):
     """``torch.unique(x, dim=0, return_inverse=..., return_counts=...)`` for integer rows:
     sorted unique rows in ``x``'s dtype, int64 inverse and counts. Rows whose value
-    ranges multiply past 2^62 go to ``torch.unique`` itself, as in the reference."""
+    ranges multiply past 2^62 go to ``torch.unique`` itself, as in the reference; so do
+    empty inputs and rows of more than 8 columns (the packing kernels take up to 8)."""
     device = _lib.require_gpu(x)
     if x.dim() != 2 or x.dtype not in _INT_DTYPES:
         raise ValueError("x must be a 2-D integer tensor")
