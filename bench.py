@@ -279,6 +279,57 @@ def bench_vae(steps: int, warmup: int):
     }
 
 
+def bench_upsample(steps: int, warmup: int):
+    """One decoder octree upsampling at C256 fp16: the 512^3 fine shells' parents (their
+    2x2x2 coarse set) with the fine shells' own occupancy as the child mask, so the kept
+    children are exactly the fine set. Occupancy logits, child map and child projection
+    timed apart."""
+    import numpy as np
+    import torch
+
+    from hi3d_amd import kmap as _kmap
+    from hi3d_amd import sparse, vae, workloads
+
+    dev = torch.device("cuda:0")
+    idx = torch.as_tensor(workloads.coords_for("down2_up2_c64_c128_fp16", device=dev)).to(dev)
+    s2 = _kmap.stride2_structure(idx, [int(v) + 1 for v in idx[:, 1:].max(0).values.tolist()], 1)
+    level = sparse.Level.from_coords(s2.low[:, 1:].contiguous())
+    p_n, c = level.n, 256
+    mask = torch.zeros((p_n, 8), dtype=torch.bool, device=dev)
+    mask[s2.inverse.long(), s2.slot.long()] = True
+    x = torch.as_tensor(workloads.normal((p_n, c), 1.0, 71, np.float16)).to(dev)
+    params = {
+        "u.cls_head.fc.0.weights": torch.as_tensor(1.0 + workloads.normal((1, c), 0.1, 72)).to(dev),
+        "u.cls_head.fc.0.bias": torch.as_tensor(workloads.normal((1, c), 0.1, 73)).to(dev),
+        "u.cls_head.fc.2.weight": torch.as_tensor(workloads.normal((27 * c, 8), 1.0 / np.sqrt(27 * c), 74, np.float16)).to(dev),
+        "u.cls_head.fc.2.bias": torch.as_tensor(workloads.normal((8,), 0.02, 75, np.float16)).to(dev),
+        "u.proj.weight": torch.as_tensor(workloads.normal((8 * c, c), 1.0 / np.sqrt(c), 76, np.float16)).to(dev),
+    }
+    _, occ = timed(lambda: vae.occupancy(x, level, params, "u"), steps, warmup)
+    _, cmap = timed(lambda: sparse.child_neighbour_table(level.table, mask), steps, warmup)
+    _, parent, slot = sparse.child_neighbour_table(level.table, mask)
+    n_child = int(parent.shape[0])
+    w = params["u.proj.weight"]
+    _, plan_ms = timed(lambda: vae.child_plan(parent, slot, p_n), steps, warmup)
+    plan = vae.child_plan(parent, slot, p_n)
+    _, proj = timed(lambda: vae.children(x, parent, slot, w, plan=plan), steps, warmup)
+    up_wall, _ = timed(lambda: vae.upsample(x, level, params, "u", mask=mask), max(3, steps // 5), max(1, warmup // 2))
+    flops = 2.0 * n_child * c * c
+    return {
+        "workload": "vae_upsample_c256_fp16",
+        "parents": p_n,
+        "children": n_child,
+        "occupancy_ms": occ,
+        "child_map_ms": cmap,
+        "child_plan_ms": plan_ms,
+        "projection_ms": proj,
+        "projection_tflops": flops / (proj * 1e-3) / 1e12,
+        "projection_gbs": (n_child + p_n) * c * 2 / (proj * 1e-3) / 1e9,
+        "upsample_given_mask_ms": up_wall,
+        "children_per_s": n_child / (up_wall * 1e-3),
+    }
+
+
 def bench_geometry(steps: int, warmup: int):
     """Refiner transformer I/O resampling on the 1024^3 residual-block shells at C256
     fp16: mean pool down, parent copy up, and the up block's first convolution from the

@@ -205,3 +205,16 @@ def test_workload_generators_match_stated_sizes():
     c2 = workloads.coords_for("subm3_c128_fp16")
     assert 400_000 <= len(c2) <= 600_000
     assert c2[:, 1:].min() >= 0 and c2[:, 1:].max() < 256
+
+
+def test_bench_main_calls_defined_functions():
+    """Every workload function bench.py's main() calls is defined in bench.py (a CPU check
+    of the driver contract's entry point; the workloads themselves need the GPU)."""
+    import ast
+
+    tree = ast.parse((ROOT / "bench.py").read_text())
+    defined = {node.name for node in tree.body if isinstance(node, ast.FunctionDef)}
+    main = next(node for node in tree.body if isinstance(node, ast.FunctionDef) and node.name == "main")
+    called = {node.func.id for node in ast.walk(main) if isinstance(node, ast.Call) and isinstance(node.func, ast.Name)}
+    wanted = {name for name in called if name.startswith(("bench_", "cpu_baseline", "measured_traffic"))}
+    assert wanted and wanted <= defined, sorted(wanted - defined)
