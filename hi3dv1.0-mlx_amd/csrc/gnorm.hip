@@ -282,9 +282,9 @@ int hi3d_group_stats(const void* x, int32_t dtype, int64_t n, int32_t c, int32_t
                      int64_t workspace_bytes, float* mean, float* inv, void* stream_) {
   hipStream_t s = as_stream(stream_);
   if (const int rc = check_rows(x, dtype, c); rc != HI3D_OK) return rc;
-  HI3D_REQUIRE(n > 0, "no rows");
+  HI3D_REQUIRE(n >= 0, "negative row count");
   HI3D_REQUIRE(groups > 0 && c % groups == 0, "channels (%d) must split into %d groups", c, groups);
-  HI3D_REQUIRE(workspace && mean && inv, "null pointer argument");
+  HI3D_REQUIRE((x || n == 0) && workspace && mean && inv, "null pointer argument");
   const int blocks = stats_blocks(n, c);
   HI3D_REQUIRE(workspace_bytes >= stats_workspace(n, c), "workspace too small");
   float* partial = static_cast<float*>(workspace);

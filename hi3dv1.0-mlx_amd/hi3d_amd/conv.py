@@ -207,7 +207,7 @@ def conv(
     when they take the shape, else to the simple kernel. ``out`` may be ``residual``
     (the sum is then accumulated in place)."""
     cin, cout = int(features.shape[1]), int(weight.shape[0])
-    if out is not None and out.data_ptr() == features.data_ptr():
+    if out is not None and features.numel() and out.data_ptr() == features.data_ptr():
         raise ValueError("out must not alias the gathered features")
     if narrow_supported(features.dtype, cin, cout, plan.kvol):
         return gather_conv_narrow(features, plan, weight, bias, act, residual, out)

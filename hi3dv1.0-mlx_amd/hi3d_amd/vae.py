@@ -38,10 +38,11 @@ def group_stats(x: torch.Tensor, eps: float = 1e-6) -> tuple[torch.Tensor, torch
     """Per-channel ``(mean, 1 / sqrt(var + eps))`` in fp32 of ``x [n, C]`` over
     ``groups_for(C)`` groups (vae.py:141-164). Column sums are fp32 per block and fp64
     across blocks; the reference sums in fp32, so the statistics agree to fp32
-    rounding, not bit for bit."""
+    rounding, not bit for bit. With no rows the divisor ``n * width + eps`` gives mean 0
+    and ``1 / sqrt(eps)``, as in the reference."""
     device = _lib.require_gpu(x)
-    if x.dim() != 2 or x.shape[0] == 0:
-        raise ValueError("x must be a non-empty [n, C]")
+    if x.dim() != 2:
+        raise ValueError("x must be [n, C]")
     n, c = int(x.shape[0]), int(x.shape[1])
     if x.dtype not in (torch.float16, torch.bfloat16, torch.float32):
         raise ValueError(f"unsupported dtype {x.dtype}")

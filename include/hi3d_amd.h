@@ -314,7 +314,8 @@ int hi3d_group_stats_workspace(int64_t n, int32_t c, int64_t* bytes_host);
  * 16-byte aligned) over `groups` groups of c / groups consecutive channels: per
  * channel fp32 sums of x and x^2, then per group mean = S1 / (n w + eps),
  * var = S2 / (n w + eps) - mean^2, inv = 1 / sqrt(var + eps), written per channel to
- * mean_dev / inv_dev [c] fp32. Replaces SparconvVAEDecoderMLX.group_stats
+ * mean_dev / inv_dev [c] fp32 (n = 0 gives mean 0, inv 1 / sqrt(eps), as the divisor
+ * n w + eps does; x_dev may then be NULL). Replaces SparconvVAEDecoderMLX.group_stats
  * (src/hi3d_mac/mlx_backend/vae.py:141-164). */
 int hi3d_group_stats(const void* x_dev, int32_t dtype, int64_t n, int32_t c, int32_t groups, float eps,
                      void* workspace_dev, int64_t workspace_bytes, float* mean_dev, float* inv_dev,
