@@ -19,19 +19,21 @@ import torch
 from . import _lib
 
 PLAN_WINDOW_ROWS: int | None = None
-"""Rows per mask-sorting window of a convolution plan; ``None`` picks by size
-(``PLAN_SMALL_WINDOW`` rows up to ``PLAN_GLOBAL_ROWS`` rows, else ``PLAN_LARGE_WINDOW``).
-Measured with the 8-wave kernels: on the 543k-voxel C128 shells 2^18..2^20-row windows
-0.444-0.454 ms against 0.455-0.462 ms at 2^16 (smaller windows keep gathers in L2 but
-group fewer rows of equal offset masks); on the 4.4M-voxel C256 shells 2^18 is best
-(7.99 ms, 8.10-8.17 ms at 2^19..2^20, 8.18-8.22 ms at 2^17)."""
+"""Rows per mask-sorting window of a convolution plan (``0``: one window over all
+rows); ``None`` picks by size (``PLAN_SMALL_WINDOW`` up to ``PLAN_GLOBAL_ROWS`` rows,
+else ``PLAN_LARGE_WINDOW``). Smaller windows keep the gathers of neighbouring tiles in
+L2; larger ones group more rows of equal offset masks, so tiles run fewer absent
+(row, offset) pairs. Measured with the corner-major mask keys: on the 543k-voxel C128
+shells one window 0.3775 ms against 0.3804 ms at 2^18; on the 1.1M-voxel shells one
+window C64 0.243 / C128 0.554 ms against 0.257 / 0.575 ms at 2^18; on the 4.4M-voxel
+C256 shells 2^19 is best (7.09 ms; 7.28 at 2^18, 7.22-7.25 at 2^20 .. one window)."""
 KMAP_DENSE_MAX_CELLS: int = 1 << 31
 """Grids of at most this many cells (batch * sx * sy * sz) build their map through a
 dense grid of rows (``hi3d_kmap_subm_dense``) instead of the hash; ``0`` always hashes."""
 
 PLAN_GLOBAL_ROWS = 1 << 21
-PLAN_SMALL_WINDOW = 1 << 18
-PLAN_LARGE_WINDOW = 1 << 18
+PLAN_SMALL_WINDOW = 0
+PLAN_LARGE_WINDOW = 1 << 19
 
 
 def column_bounds(a: torch.Tensor) -> tuple[list[int], list[int]]:

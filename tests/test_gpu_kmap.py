@@ -205,6 +205,22 @@ def test_plan_covers_every_row_once(cuda):
         assert np.array_equal(masks, exp)
 
 
+def test_plan_work_on_shell_set(cuda):
+    """The default plan of the 543k-voxel shell set (one mask-sorting window) runs at
+    most 1.052 (row, offset) products per present pair in 128-row tiles: rows sorted by
+    their presence mask with the corner offsets as the most significant key bits give
+    1.0453; sorting the plain mask value gives 1.0592."""
+    from hi3d_amd import kmap, workloads
+
+    idx = workloads.coords_for("subm3_c128_fp16")
+    km = kmap.build_kernel_map(torch.as_tensor(idx).to(cuda), [256] * 3, 1)
+    plan = km.plan()
+    masks = plan.tile_mask.cpu().numpy().astype(np.uint32)
+    computed = sum(bin(int(m)).count("1") for m in masks) * 128
+    present = int((km.table != km.n).sum())
+    assert computed <= 1.052 * present, computed / present
+
+
 def test_blocked_assembly_matches_single_block(cuda):
     """The reference's blocked-assembly test (tests/test_mlx_kernels.py:92-102): row
     blocks concatenated, and assembled in place past the size threshold, equal one block."""
