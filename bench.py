@@ -142,7 +142,8 @@ def bench_stride2(steps: int, warmup: int):
     y = torch.empty((nc, 128), dtype=torch.float16, device=dev)
     z = torch.empty((nf, 64), dtype=torch.float16, device=dev)
     d_wall, d_ev = timed(lambda: conv.gather_conv(x, dp, wd, None, out=y), steps, warmup)
-    u_wall, u_ev = timed(lambda: conv.gather_conv(y, up, wu, None, out=z), steps, warmup)
+    u_wall, u_ev = timed(lambda: conv.stride2_up(y, s, wu, None, out=z), steps, warmup)
+    ug_wall, ug_ev = timed(lambda: conv.gather_conv(y, up, wu, None, out=z), steps, warmup)
     flops = 2.0 * nf * 64 * 128
     bytes_conv = 2 * (nf * 64 + nc * 128 + 8 * 64 * 128) + 5 * nf
     return {
@@ -152,6 +153,7 @@ def bench_stride2(steps: int, warmup: int):
         "structure_ms": map_wall,
         "down_ms": d_wall,
         "up_ms": u_wall,
+        "up_gather_ms": ug_wall,
         "down_tflops": flops / (d_ev * 1e-3) / 1e12,
         "up_tflops": flops / (u_ev * 1e-3) / 1e12,
         "down_gbs_alg": bytes_conv / (d_ev * 1e-3) / 1e9,

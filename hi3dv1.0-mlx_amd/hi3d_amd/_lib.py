@@ -50,6 +50,8 @@ _SIGNATURES = {
     "hi3d_kmap_subm_dense": [_p, _i64, _i32, _i32, _i32, _i32, _i32, _p, _i64, _p, _p, _p, _p],
     "hi3d_parent_table": [_p, _i64, _i32, _p, _i64, _p, _p],
     "hi3d_gather_rows": [_p, _i64, _i32, _p, _i64, _p, _p],
+    "hi3d_stride2_up_supported": [_i32, _i32, _i32],
+    "hi3d_stride2_up_conv": [_p, _i64, _i32, _p, _p, _i32, _p, _i64, _i32, _p, _p],
     "hi3d_unique_keys_workspace": [_i64, _p],
     "hi3d_unique_keys": [_p, _i64, _i32, _p, _i64, _p, _p, _p, _p, _p],
     "hi3d_pack_rows": [_p, _i32, _i64, _i32, _p, _p, _p, _p],

@@ -8,6 +8,8 @@ channel counts and dtypes (float64) the MFMA kernel does not take. Both compute
 
 with ``W`` in spconv's ``[Cout, K, Cin]`` layout (reference:
 src/hi3d_mac/torch_backend/sparse_conv.py:152-195; src/hi3d_mac/mlx_backend/sparse.py:191-214).
+``stride2_up`` runs the transpose of the 2x2x2 / stride-2 convolution parent-major, each
+coarse row read once, for the shapes its kernel takes.
 """
 
 from __future__ import annotations
@@ -214,3 +216,40 @@ def conv(
     if mfma_supported(features.dtype, cin, cout):
         return gather_conv(features, plan, weight, bias, act, residual, out)
     return gather_conv_simple(features, plan.table, weight, bias, act, residual, n_in=plan.n_in, out=out)
+
+
+def stride2_up_supported(dtype: torch.dtype, cin: int, cout: int) -> bool:
+    """Whether the parent-major transposed kernel takes this shape."""
+    if dtype not in (torch.float16, torch.bfloat16):
+        return False
+    return bool(_lib.lib().hi3d_stride2_up_supported(int(cin), int(cout), _lib.DTYPES[dtype]))
+
+
+def stride2_up(features: torch.Tensor, structure, weight: torch.Tensor, bias: torch.Tensor | None = None,
+               out: torch.Tensor | None = None) -> torch.Tensor:
+    """Transpose of the 2x2x2 / stride-2 convolution onto the fine set of ``structure``
+    (a :class:`~hi3d_amd.kmap.Stride2Structure`): ``out[i] = b + W[:, slot(i), :] @
+    features[parent(i)]`` with ``W [Cout, 8, Cin]`` (or spconv's ``[Cout, 2, 2, 2, Cin]``).
+    Shapes the parent-major kernel takes (fp16 / bf16, Cin 64 or 128, Cout 64) read each
+    coarse row once and write each fine row once; the others run the gather convolution
+    over the structure's up table."""
+    device = _lib.require_gpu(features, weight, bias, out)
+    n_c, n_f = structure.n_coarse, structure.n_fine
+    cin, cout = int(features.shape[1]), int(weight.shape[0])
+    if features.dim() != 2 or int(features.shape[0]) != n_c:
+        raise ValueError(f"expected features [{n_c}, C], got {tuple(features.shape)}")
+    w = _flat_weight(weight, 8)
+    if int(w.shape[2]) != cin:
+        raise ValueError(f"weight takes {int(w.shape[2])} input channels, features have {cin}")
+    if not stride2_up_supported(features.dtype, cin, cout):
+        return conv(features, structure.up_plan(), w, bias, out=out)
+    if w.dtype != features.dtype:
+        raise ValueError(f"weight dtype {w.dtype} differs from the features' {features.dtype}")
+    x = features.contiguous()
+    if x.data_ptr() % 16:
+        x = x.clone()
+    b = None if bias is None else bias.to(features.dtype).contiguous()
+    y = _output(out, n_f, cout, features.dtype, device)
+    _lib.call("hi3d_stride2_up_conv", _lib.ptr(x), n_c, cin, _lib.ptr(w), _lib.ptr(b), cout,
+              _lib.ptr(structure.down), n_f, _lib.DTYPES[features.dtype], _lib.ptr(y), _lib.stream(device))
+    return y

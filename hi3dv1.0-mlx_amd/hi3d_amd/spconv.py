@@ -369,7 +369,7 @@ class SparseInverseConv3d(nn.Module):
         _check_weight_dtype(input.features, self.weight)
         w = self.weight.reshape(self.out_channels, 8, self.in_channels)
         b = None if self.bias is None else self.bias.to(input.features.dtype)
-        out = _conv.conv(input.features, s.up_plan(), w, b)
+        out = _conv.stride2_up(input.features, s, w, b)
         return SparseConvTensor(out, data.indices, data.spatial_shape, input.batch_size, input.indice_dict)
 
 

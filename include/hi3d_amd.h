@@ -123,6 +123,24 @@ int hi3d_downsample_structure(const int32_t* coords_dev, int64_t n, int32_t sx, 
 int hi3d_stride2_tables(const int32_t* inverse_dev, const uint8_t* slot_dev, int64_t n,
                         int64_t n_low, int32_t* down_dev, int32_t* up_dev, void* stream);
 
+/* Whether hi3d_stride2_up_conv takes this shape (1) or not (0): F16 / BF16, cin 64 or
+ * 128, cout 64. */
+int hi3d_stride2_up_supported(int32_t cin, int32_t cout, int32_t dtype);
+
+/* Transpose of the strided convolution onto the fine set, parent-major:
+ * out[down[c, s]] = bias + W[:, s, :] in[c] for every coarse row c and slot s with
+ * down[c, s] < n_f. in_dev [n_c, cin], weight_dev [cout, 8, cin] (spconv's
+ * [cout, 2, 2, 2, cin]), bias_dev [cout] or NULL, down_dev the [n_c, 8] table of
+ * hi3d_stride2_tables, out_dev [n_f, cout]; every fine row has exactly one (parent,
+ * slot), so every output row is written once. fp32 accumulation, bias added in fp32,
+ * one rounding. 16-byte aligned in, weight and out; n_f * cout * 2 < 2^31.
+ * (No reference function, as for hi3d_stride2_tables: the strided pair's up half,
+ * SparseInverseConv3d over the spconv weight layout of
+ * src/sparc3d/nn/sparse/conv.py:27-35.) */
+int hi3d_stride2_up_conv(const void* in_dev, int64_t n_c, int32_t cin, const void* weight_dev,
+                         const void* bias_dev, int32_t cout, const int32_t* down_dev, int64_t n_f,
+                         int32_t dtype, void* out_dev, void* stream);
+
 /* Workspace bytes of hi3d_child_neighbour_table. */
 int hi3d_child_table_workspace(int64_t n_parents, int64_t* bytes_host);
 

@@ -359,3 +359,49 @@ def test_gather_mean_pooling(cuda):
     back = snn.SparseUpsample(2)(pooled)
     assert torch.equal(back.coords, t.coords)
     assert np.allclose(back.feats.cpu().numpy(), pooled.feats.cpu().numpy()[inverse])
+
+
+@pytest.mark.parametrize("dtype,cin,n_side,density,with_bias", [
+    (torch.float16, 128, 20, 0.3, True), (torch.bfloat16, 128, 16, 0.5, False), (torch.float16, 64, 24, 0.2, True),
+    (torch.bfloat16, 64, 9, 0.9, True),
+])
+def test_stride2_up_parent_major(cuda, dtype, cin, n_side, density, with_bias):
+    """The parent-major transposed kernel against float64 and bit for bit against the
+    gather convolution over the up table (both sum each output's 8-slot products in the
+    same K order and add the bias in fp32 once); coarse sets that are not a multiple of
+    the 32-row tile, parents with one to eight children."""
+    from hi3d_amd import conv, kmap
+
+    rng = np.random.default_rng(cin + n_side)
+    idx = _rand_indices(rng, n_side, density)
+    s = kmap.stride2_structure(torch.as_tensor(idx).to(cuda), [n_side] * 3, 1)
+    y = torch.as_tensor(rng.standard_normal((s.n_coarse, cin), dtype=np.float32)).to(dtype).to(cuda)
+    w = torch.as_tensor(rng.standard_normal((64, 2, 2, 2, cin), dtype=np.float32) / np.sqrt(8 * cin)).to(dtype).to(cuda)
+    b = torch.as_tensor(rng.standard_normal(64, dtype=np.float32) * 0.1).to(dtype).to(cuda) if with_bias else None
+    assert conv.stride2_up_supported(dtype, cin, 64)
+    z = conv.stride2_up(y, s, w, b)
+    assert z.shape == (s.n_fine, 64) and z.dtype == dtype
+    gathered = conv.gather_conv(y, s.up_plan(), w.reshape(64, 8, cin), b)
+    assert torch.equal(z, gathered)
+    ref = oconv.gather_conv_f64(y.float().cpu().numpy(), s.up.cpu().numpy(), w.reshape(64, 8, cin).float().cpu().numpy(),
+                                None if b is None else b.float().cpu().numpy())
+    assert oconv.rel_err(z.float().cpu().numpy(), ref) <= GATE[dtype]
+    out = torch.full_like(z, float("nan"))
+    assert conv.stride2_up(y, s, w, b, out=out) is out and torch.equal(out, z)
+
+
+def test_stride2_up_workload_fp16(cuda):
+    """512^3 shells, C128 -> 64 fp16: every fine row written, bit-equal to the gather
+    convolution, and within the fp16 gate of float64 on sampled rows."""
+    from hi3d_amd import conv, kmap, workloads
+
+    idx = workloads.coords_for("down2_up2_c64_c128_fp16")
+    s = kmap.stride2_structure(torch.as_tensor(idx).to(cuda), [512] * 3, 1)
+    y = torch.as_tensor(workloads.normal((s.n_coarse, 128), 1.0, 41, np.float16)).to(cuda)
+    w = torch.as_tensor(workloads.normal((64, 8, 128), 1.0 / np.sqrt(8 * 128), 42, np.float16)).to(cuda)
+    z = conv.stride2_up(y, s, w, None, out=torch.full((s.n_fine, 64), float("nan"), dtype=torch.float16, device=cuda))
+    assert bool(torch.isfinite(z).all())
+    assert torch.equal(z, conv.gather_conv(y, s.up_plan(), w))
+    rows = np.random.default_rng(3).choice(s.n_fine, 4096, replace=False)
+    ref = oconv.gather_conv_f64(y.float().cpu().numpy(), s.up.cpu().numpy(), w.float().cpu().numpy(), rows=rows)
+    assert oconv.rel_err(z.float().cpu().numpy()[rows], ref) <= 1e-2
