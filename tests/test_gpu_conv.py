@@ -137,6 +137,7 @@ def test_epilogue_silu_and_residual(cuda):
     (torch.float16, 128, 64, 0.004, None, True),
     (torch.float32, 256, 256, 0.1, "silu", True), (torch.float32, 512, 128, 0.1, None, False),
     (torch.float32, 64, 256, 0.15, None, True), (torch.float32, 80, 128, 0.1, "silu", False),
+    (torch.bfloat16, 256, 128, 0.15, "silu", True), (torch.float16, 128, 384, 0.1, None, True),
 ])
 def test_ring_kernel_variants(cuda, dtype, cin, cout, density, act, res):
     """The ring kernels (fp16/bf16, Cout a multiple of 128, 256..1024-byte rows): 256 x 256
