@@ -89,7 +89,16 @@ def test_c_argument_validation_without_launch():
     assert rc == _lib.ERR_INVALID and "I32 or I64" in _lib.last_error()
     rc = lib.hi3d_pack_rows(null, _lib.I64, 10, 9, null, null, null, null)
     assert rc == _lib.ERR_INVALID and "1..8" in _lib.last_error()
+    # the parent-major transposed conv: fp16 / bf16, cin 64 or 128, cout 64; outputs under 2 GiB
+    assert lib.hi3d_stride2_up_supported(128, 64, _lib.F16) == 1 and lib.hi3d_stride2_up_supported(64, 64, _lib.BF16) == 1
+    assert lib.hi3d_stride2_up_supported(256, 64, _lib.F16) == 0 and lib.hi3d_stride2_up_supported(128, 128, _lib.F16) == 0
+    assert lib.hi3d_stride2_up_supported(128, 64, _lib.F32) == 0
+    rc = lib.hi3d_stride2_up_conv(null, 10, 256, null, null, 64, null, 30, _lib.F16, null, null)
+    assert rc == _lib.ERR_INVALID and "cin 64 or 128" in _lib.last_error()
+    rc = lib.hi3d_stride2_up_conv(null, 10, 128, null, null, 64, null, 1 << 24, _lib.F16, null, null)
+    assert rc == _lib.ERR_INVALID and "2 GiB" in _lib.last_error()
     # zero-size calls succeed without touching memory
+    assert lib.hi3d_stride2_up_conv(null, 0, 128, null, null, 64, null, 0, _lib.F16, null, null) == 0
     assert lib.hi3d_gather_conv_simple(null, 0, 3, null, null, 5, 27, null, 0, null, 0, _lib.F64, null, null) == 0
     assert lib.hi3d_gather_conv_narrow(null, 0, 64, null, null, 8, 27, null, null, null, 0, null, 0, _lib.F16, null,
                                        null) == 0
