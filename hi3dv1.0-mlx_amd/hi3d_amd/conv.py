@@ -14,6 +14,8 @@ coarse row read once, for the shapes its kernel takes.
 
 from __future__ import annotations
 
+import functools
+
 import torch
 
 from . import _lib
@@ -218,6 +220,7 @@ def conv(
     return gather_conv_simple(features, plan.table, weight, bias, act, residual, n_in=plan.n_in, out=out)
 
 
+@functools.lru_cache(maxsize=None)
 def stride2_up_supported(dtype: torch.dtype, cin: int, cout: int) -> bool:
     """Whether the parent-major transposed kernel takes this shape."""
     if dtype not in (torch.float16, torch.bfloat16):
