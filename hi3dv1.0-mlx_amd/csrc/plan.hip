@@ -57,12 +57,24 @@ __device__ __forceinline__ void stage_rows(const int32_t* __restrict__ table, co
                                            int64_t p0, int64_t n_out, int kvol, int nrows, int32_t absent,
                                            int32_t* __restrict__ lds) {
   const int total = nrows * kvol;
-  for (int e = threadIdx.x; e < total; e += blockDim.x) {
+  const int bd = blockDim.x;
+  auto fetch = [&](int e) -> int32_t {
     const int row = e / kvol;
     const int k = e - row * kvol;
     const int64_t p = p0 + row;
-    lds[e] = p < n_out ? table[static_cast<int64_t>(order[p]) * kvol + k] : absent;
+    return p < n_out ? table[static_cast<int64_t>(order[p]) * kvol + k] : absent;
+  };
+  // eight independent loads in flight per thread before their LDS stores
+  constexpr int U = 8;
+  int e = threadIdx.x;
+  for (; e + (U - 1) * bd < total; e += U * bd) {
+    int32_t v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = fetch(e + u * bd);
+#pragma unroll
+    for (int u = 0; u < U; ++u) lds[e + u * bd] = v[u];
   }
+  for (; e < total; e += bd) lds[e] = fetch(e);
 }
 
 // key = (window << 32) | presence mask, for rows taken in Morton order.
