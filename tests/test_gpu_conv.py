@@ -73,11 +73,13 @@ def test_mfma_conv_matches_float64(cuda, dtype, cin, cout):
     (torch.float16, 256, 8, 27, 0.15, None, False), (torch.float32, 512, 8, 27, 0.1, None, False),
     (torch.bfloat16, 128, 16, 27, 0.2, "silu", True), (torch.float16, 32, 1, 27, 0.3, None, True),
     (torch.float32, 48, 5, 27, 0.004, "silu", False), (torch.float16, 96, 12, 8, 0.2, None, False),
-    (torch.float16, 512, 8, 27, 0.05, None, False),
+    (torch.float16, 512, 8, 27, 0.05, None, False), (torch.bfloat16, 64, 8, 8, 0.2, "silu", True),
+    (torch.float16, 128, 3, 27, 0.02, None, True),
 ])
 def test_narrow_conv_matches_float64(cuda, dtype, cin, cout, kvol, density, act, res):
-    """The narrow-output kernel (cout <= 16, 16x16 MFMAs) against float64 and against
-    the tile kernels on the same inputs: occupancy-head shapes (C 256 / 512 -> 8),
+    """The narrow-output kernels (cout <= 16, 16x16 MFMAs; 16-bit rows of 128-byte
+    multiples staged through LDS, the others loaded to registers) against float64 and
+    against the tile kernels on the same inputs: occupancy-head shapes (C 256 / 512 -> 8),
     odd output counts, K steps of one, two and four 64-byte blocks, sparse sets where
     most offsets of a 64-row tile are absent, and a few-offset table."""
     from hi3d_amd import conv, kmap
