@@ -226,46 +226,51 @@ __global__ __launch_bounds__(kNarrowWaves * 64) void conv_narrow_kernel(NarrowAr
 // The same convolution for 16-bit rows of a multiple of 128 bytes, with the gathers
 // staged through LDS: a wave-wide direct-to-LDS load then covers 8 rows x 128 bytes (8
 // full lines) instead of 16 rows x 64 bytes, half the addresser work per byte. Each
-// wave owns its LDS (gather indices, a 3-slot ring of stages) and synchronises with no
-// other wave. A stage is one 128-byte K chunk of one present offset: 64 gathered rows
-// and the 16 weight rows (zeros past cout), 10 loads per wave, so the vmcnt waits are
-// constants. Rows use the XOR swizzle of the tile kernels (chunk c of row r at
-// c ^ ((r >> 1) & 7)), so the 16-row fragment reads are free of bank conflicts.
-constexpr int kNarrowStage = (kNarrowRows + 16) * 128;            // 10 KB
-constexpr int kNarrowLdsWave = 3 * kNarrowStage + kNarrowMaxKvol * kNarrowRows * 4;
+// wave (one per workgroup) owns its LDS (gather indices, a 3-slot ring of stages) and
+// synchronises with no other wave. A stage is one 128-byte K chunk of one present
+// offset: the wave's ROWS gathered rows and the 16 weight rows (zeros past cout),
+// ROWS / 8 + 2 loads, so the vmcnt waits are constants. Rows use the XOR swizzle of the
+// tile kernels (chunk c of row r at c ^ ((r >> 1) & 7)), so the 16-row fragment reads
+// are free of bank conflicts.
+// output rows per wave: more waves per CU outweigh the weight rows each stage reloads
+// (occupancy head: 64 rows 0.465 ms, 32 rows 0.423 ms, 16 rows 0.408 ms)
+constexpr int kNarrowLdsRows = 16;
 
 __device__ __attribute__((aligned(16))) const uint32_t g_narrow_zero_row[32] = {};
 
-template <typename T>
+template <typename T, int ROWS>
 __global__ __launch_bounds__(64) void conv_narrow_lds_kernel(NarrowArgs a) {
-  __shared__ __attribute__((aligned(16))) char smem[kNarrowLdsWave];
+  constexpr int STAGE = (ROWS + 16) * 128, PARTS = kTileRows / ROWS, G = ROWS / 16;
+  constexpr int OPL = 1024 / (ROWS * 4);  // offsets per 16-byte-per-lane index load
+  __shared__ __attribute__((aligned(16))) char smem[3 * STAGE + kNarrowMaxKvol * ROWS * 4];
   char* const ring = smem;
-  int32_t* const ent = reinterpret_cast<int32_t*>(smem + 3 * kNarrowStage);
+  int32_t* const ent = reinterpret_cast<int32_t*>(smem + 3 * STAGE);
   const int lane = threadIdx.x;
   const int64_t wt = xcd_remap(blockIdx.x, static_cast<int64_t>(gridDim.x));
-  if (wt >= 2 * a.ntiles) return;  // wave-uniform
-  const int64_t slot0 = wt * kNarrowRows;
-  const int64_t tile = wt >> 1;
-  const int half = static_cast<int>(wt & 1);
+  if (wt >= PARTS * a.ntiles) return;  // wave-uniform
+  const int64_t slot0 = wt * ROWS;
+  const int64_t tile = wt / PARTS;
+  const int half = static_cast<int>(wt % PARTS);
   const int kvol = a.kvol;
   const uint64_t n_in = static_cast<uint64_t>(a.n_in);
   const int rb = a.cin * static_cast<int>(sizeof(T));
   const int nch = rb >> 7;
 
-  // gather indices [offset][64 rows]: four offsets per 16-byte-per-lane load
+  // gather indices [offset][ROWS rows]: OPL offsets per 16-byte-per-lane load
   {
-    const int groups = (kvol + 3) >> 2;
+    const int groups = (kvol + OPL - 1) / OPL;
     for (int i = 0; i < groups; ++i) {
-      int k = 4 * i + (lane >> 4);
+      int k = OPL * i + lane / (ROWS / 4);
       if (k >= kvol) k = kvol - 1;
-      lds_dma16(a.gidx + (tile * kvol + k) * kTileRows + half * kNarrowRows + (lane & 15) * 4,
-                smem + 3 * kNarrowStage + i * 1024);
+      lds_dma16(a.gidx + (tile * kvol + k) * kTileRows + half * ROWS + (lane % (ROWS / 4)) * 4,
+                smem + 3 * STAGE + i * 1024);
     }
     wait_vmcnt<0>();
   }
   uint32_t present = 0;
   for (int k = 0; k < kvol; ++k) {
-    const bool ok = static_cast<uint64_t>(static_cast<uint32_t>(ent[k * kNarrowRows + lane])) < n_in;
+    const bool ok =
+        lane < ROWS && static_cast<uint64_t>(static_cast<uint32_t>(ent[k * ROWS + (lane % ROWS)])) < n_in;
     present |= __builtin_amdgcn_ballot_w64(ok) != 0 ? (1u << k) : 0u;
   }
   present = __builtin_amdgcn_readfirstlane(present);
@@ -274,12 +279,12 @@ __global__ __launch_bounds__(64) void conv_narrow_lds_kernel(NarrowArgs a) {
   const int lr = lane >> 3, pc = lane & 7;
   const char* const zrow = reinterpret_cast<const char*>(g_narrow_zero_row);
   auto issue = [&](int slot, int k, int c) {
-    char* st = ring + slot * kNarrowStage;
+    char* st = ring + slot * STAGE;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < ROWS / 8; ++j) {
       const int row = 8 * j + lr;
       const int lc = pc ^ ((row >> 1) & 7);
-      const int32_t e = ent[k * kNarrowRows + row];
+      const int32_t e = ent[k * ROWS + row];
       const bool ok = static_cast<uint64_t>(static_cast<uint32_t>(e)) < n_in;
       uint64_t pin = reinterpret_cast<uint64_t>(a.in) + static_cast<uint64_t>(static_cast<int64_t>(e) * rb + c * 128 + lc * 16);
       asm volatile("" : "+v"(pin));
@@ -292,21 +297,21 @@ __global__ __launch_bounds__(64) void conv_narrow_lds_kernel(NarrowArgs a) {
       uint64_t wpin = reinterpret_cast<uint64_t>(a.w) +
                       static_cast<uint64_t>((static_cast<int64_t>(o) * kvol + k) * rb + c * 128 + lc * 16);
       asm volatile("" : "+v"(wpin));
-      lds_dma16(o < a.cout ? reinterpret_cast<const char*>(wpin) : zrow + lc * 16, st + kNarrowRows * 128 + j * 1024);
+      lds_dma16(o < a.cout ? reinterpret_cast<const char*>(wpin) : zrow + lc * 16, st + ROWS * 128 + j * 1024);
     }
   };
-  f32x4 acc[4];
+  f32x4 acc[G];
 #pragma unroll
-  for (int g = 0; g < 4; ++g) acc[g] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int g = 0; g < G; ++g) acc[g] = f32x4{0.f, 0.f, 0.f, 0.f};
   const int fr = lane & 15, fq = lane >> 4;
   auto compute = [&](int slot) {
-    const char* st = ring + slot * kNarrowStage;
+    const char* st = ring + slot * STAGE;
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
       const int lc = 4 * kk + fq;
-      const u32x4 w = *reinterpret_cast<const u32x4*>(st + kNarrowRows * 128 + fr * 128 + ((lc ^ ((fr >> 1) & 7)) << 4));
+      const u32x4 w = *reinterpret_cast<const u32x4*>(st + ROWS * 128 + fr * 128 + ((lc ^ ((fr >> 1) & 7)) << 4));
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
+      for (int g = 0; g < G; ++g) {
         const int row = 16 * g + fr;
         const u32x4 x = *reinterpret_cast<const u32x4*>(st + row * 128 + ((lc ^ ((row >> 1) & 7)) << 4));
         Mfma16<T>::run(w, x, acc[g]);
@@ -336,7 +341,7 @@ __global__ __launch_bounds__(64) void conv_narrow_lds_kernel(NarrowArgs a) {
     }
     int slot = 0;
     for (int s = 0; s + 1 < S; ++s) {
-      wait_vmcnt<10>();  // stage s is in LDS; stage s + 1 may still be in flight
+      wait_vmcnt<ROWS / 8 + 2>();  // stage s is in LDS; stage s + 1 may still be in flight
       compute(slot);
       if (s + 2 < S) {
         issue(slot == 0 ? 2 : slot - 1, kl, cl);  // the slot of stage s - 1, consumed
@@ -353,7 +358,7 @@ __global__ __launch_bounds__(64) void conv_narrow_lds_kernel(NarrowArgs a) {
   const T* res = static_cast<const T*>(a.residual);
   T* out = static_cast<T*>(a.out);
 #pragma unroll
-  for (int g = 0; g < 4; ++g) {
+  for (int g = 0; g < G; ++g) {
     const int32_t o = a.rows[slot0 + 16 * g + fr];
     if (o < 0 || o >= a.n_out) continue;
 #pragma unroll
@@ -378,9 +383,10 @@ int launch_narrow(const NarrowArgs& a, hipStream_t stream) {
   const int steps = a.cin * static_cast<int>(sizeof(T)) / 64;
   if constexpr (sizeof(T) == 2) {
     if (steps % 2 == 0) {  // 128-byte rows: one wave per workgroup, gathers staged in LDS
-      const int64_t waves = 2 * a.ntiles;
+      const int64_t waves = (kTileRows / kNarrowLdsRows) * a.ntiles;
       HI3D_REQUIRE(waves < (int64_t(1) << 31), "too many tiles");
-      hipLaunchKernelGGL((conv_narrow_lds_kernel<T>), dim3(static_cast<unsigned>(waves)), dim3(64), 0, stream, a);
+      hipLaunchKernelGGL((conv_narrow_lds_kernel<T, kNarrowLdsRows>), dim3(static_cast<unsigned>(waves)), dim3(64), 0,
+                         stream, a);
       HI3D_LAUNCH_CHECK();
       return HI3D_OK;
     }
