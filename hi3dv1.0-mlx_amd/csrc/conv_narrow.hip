@@ -15,7 +15,9 @@
 // operands to split K the same way). Offsets that none of the wave's 64 rows has are
 // skipped (a wave-uniform mask); absent entries of a present offset read a 16-byte
 // zero vector. Loads go straight to registers, two stages deep; the wave's gather
-// indices sit in LDS ([offset][64 rows], 16 consecutive words per read).
+// indices sit in LDS ([offset][64 rows], 16 consecutive words per read). 16-bit rows of
+// a multiple of 128 bytes take conv_narrow_lds_kernel below instead (16-row waves,
+// gathers staged through LDS).
 //
 // Replaces the occupancy head's dense gathered GEMM (SparseClsHead, Conv3d(C, 8):
 // src/hi3d_mac/mlx_backend/vae.py:270-271,166-192; src/sparc3d/models/autoencoders/

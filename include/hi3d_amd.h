@@ -201,8 +201,9 @@ int hi3d_gather_conv_simple(const void* in_dev, int64_t n_in, int32_t cin,
                             void* stream);
 
 /* The convolution of hi3d_gather_conv over the same plan for at most 16 output
- * channels: 16x16 MFMAs over 64-row halves of the plan's tiles, offsets none of a half's
- * rows has skipped (tile_mask_dev is not read). F32, F16 or BF16; cout 1..16, kvol <= 32,
+ * channels: 16x16 MFMAs over 16-row parts of the plan's tiles (F16 / BF16 rows of a
+ * multiple of 128 bytes, gathered through LDS) or 64-row halves (the other rows, loaded
+ * to registers), offsets none of a part's rows has skipped (tile_mask_dev is not read). F32, F16 or BF16; cout 1..16, kvol <= 32,
  * cin*elem % 64 == 0, 16-byte aligned input and weight. Replaces the occupancy head's
  * gathered GEMM (SparseClsHead Conv3d(C, 8), src/hi3d_mac/mlx_backend/vae.py:270-271
  * over conv_gn_swish :166-192; src/sparc3d/models/autoencoders/blocks.py:181-197). */
