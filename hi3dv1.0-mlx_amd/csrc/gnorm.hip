@@ -151,20 +151,33 @@ __global__ __launch_bounds__(256) void group_finish_kernel(const double* __restr
 // reference's form e = 1 / (1 + exp(|u|)), sigmoid = u < 0 ? e : 1 - e. exp and the
 // reciprocal use the hardware's exp2 and rcp (about 2 ulp; the reference computes this
 // activation under Metal's fast math, and its tests gate it at 1e-5 / 2e-3).
-__device__ __forceinline__ void gn_swish8(float (&v)[8], const float* __restrict__ mean, const float* __restrict__ inv,
-                                          const float* __restrict__ weight, const float* __restrict__ bias, int ch) {
-#pragma clang fp contract(off)
+struct GnParams8 {
   float m[8], iv[8], w[8], b[8];
-  load8(mean + ch, m);
-  load8(inv + ch, iv);
-  load8(weight + ch, w);
-  load8(bias + ch, b);
+};
+
+__device__ __forceinline__ void gn_load8(GnParams8& p, const float* __restrict__ mean, const float* __restrict__ inv,
+                                         const float* __restrict__ weight, const float* __restrict__ bias, int ch) {
+  load8(mean + ch, p.m);
+  load8(inv + ch, p.iv);
+  load8(weight + ch, p.w);
+  load8(bias + ch, p.b);
+}
+
+__device__ __forceinline__ void gn_swish8(float (&v)[8], const GnParams8& p) {
+#pragma clang fp contract(off)
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const float u = ((v[e] - m[e]) * iv[e]) * w[e] + b[e];
+    const float u = ((v[e] - p.m[e]) * p.iv[e]) * p.w[e] + p.b[e];
     const float s = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(fabsf(u) * 1.44269504088896341f));
     v[e] = u * (u < 0.0f ? s : 1.0f - s);
   }
+}
+
+__device__ __forceinline__ void gn_swish8(float (&v)[8], const float* __restrict__ mean, const float* __restrict__ inv,
+                                          const float* __restrict__ weight, const float* __restrict__ bias, int ch) {
+  GnParams8 p;
+  gn_load8(p, mean, inv, weight, bias, ch);
+  gn_swish8(v, p);
 }
 
 // out [n, c] = swish(GN(x)) in Tout; 8 channels per thread, grid-stride.
@@ -175,8 +188,23 @@ __global__ __launch_bounds__(256) void gn_swish_kernel(const Tin* __restrict__ x
                                                        const float* __restrict__ bias, Tout* __restrict__ out) {
   const int tc = c >> 3;
   const int64_t total = n * tc;
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < total;
-       i += static_cast<int64_t>(gridDim.x) * 256) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+  const int64_t first = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (stride % tc == 0) {
+    // the thread's channel group is the same in every step: its parameters load once
+    const int ch = static_cast<int>(first % tc) * 8;
+    GnParams8 p;
+    gn_load8(p, mean, inv, weight, bias, ch);
+    for (int64_t i = first; i < total; i += stride) {
+      const int64_t row = i / tc;
+      float v[8];
+      load8(x + row * c + ch, v);
+      gn_swish8(v, p);
+      store8(out + row * c + ch, v);
+    }
+    return;
+  }
+  for (int64_t i = first; i < total; i += stride) {
     const int64_t row = i / tc;
     const int ch = static_cast<int>(i - row * tc) * 8;
     float v[8];
