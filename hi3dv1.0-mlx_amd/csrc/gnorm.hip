@@ -65,7 +65,21 @@ __global__ __launch_bounds__(256) void colsum_kernel(const T* __restrict__ x, in
   float s1[8] = {}, s2[8] = {};
   if (r0 < rpi) {
     const int64_t step = static_cast<int64_t>(gridDim.x) * rpi;
-    for (int64_t row = static_cast<int64_t>(blockIdx.x) * rpi + r0; row < n; row += step) {
+    int64_t row = static_cast<int64_t>(blockIdx.x) * rpi + r0;
+    // four rows' loads in flight, then their sums in row order
+    for (; row + 3 * step < n; row += 4 * step) {
+      float v[4][8];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) load8(x + (row + u * step) * c + cc * 8, v[u]);
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          s1[e] += v[u][e];
+          s2[e] += v[u][e] * v[u][e];
+        }
+    }
+    for (; row < n; row += step) {
       float v[8];
       load8(x + row * c + cc * 8, v);
 #pragma unroll
