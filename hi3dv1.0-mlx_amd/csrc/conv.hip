@@ -1376,15 +1376,25 @@ __global__ void gather_mean_vec_kernel(const T* __restrict__ in, int64_t n_in, i
   Acc acc[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) acc[e] = 0;
+  // every entry's load is issued (absent ones read zeros, which leave the sums
+  // unchanged: they start at +0 and never become -0), so the loads overlap
   int cnt = 0;
-  for (int k = 0; k < kvol; ++k) {
-    const int32_t src = table[o * kvol + k];
-    if (static_cast<uint64_t>(static_cast<uint32_t>(src)) >= static_cast<uint64_t>(n_in)) continue;
-    const uint4 raw = *reinterpret_cast<const uint4*>(in + static_cast<int64_t>(src) * c + j);
-    const T* v = reinterpret_cast<const T*>(&raw);
+  for (int k0 = 0; k0 < kvol; k0 += 8) {
+    uint4 raw[8];
 #pragma unroll
-    for (int e = 0; e < E; ++e) acc[e] += static_cast<Acc>(v[e]);
-    ++cnt;
+    for (int u = 0; u < 8; ++u) {
+      const int k = k0 + u;
+      const int32_t src = k < kvol ? table[o * kvol + k] : -1;
+      const bool ok = static_cast<uint64_t>(static_cast<uint32_t>(src)) < static_cast<uint64_t>(n_in);
+      cnt += ok ? 1 : 0;
+      raw[u] = ok ? *reinterpret_cast<const uint4*>(in + static_cast<int64_t>(src) * c + j) : make_uint4(0u, 0u, 0u, 0u);
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const T* v = reinterpret_cast<const T*>(&raw[u]);
+#pragma unroll
+      for (int e = 0; e < E; ++e) acc[e] += static_cast<Acc>(v[e]);
+    }
   }
   uint4 res;
   T* r = reinterpret_cast<T*>(&res);

@@ -428,18 +428,26 @@ __global__ void parent_table_kernel(const int32_t* __restrict__ table, int64_t t
 
 // out[i] = in[index[i]] for rows of rb bytes (a multiple of 16): one 16-byte chunk per
 // thread
+// Thread t copies chunks c, c + q, .. (G of them, q = cpr / G) of one row: one index
+// load and G independent 16-byte loads in flight; consecutive threads still cover
+// consecutive chunks in each of the G store steps.
+template <int G>
 __global__ void gather_rows_kernel(const char* __restrict__ in, int64_t n_in, int rb, const int32_t* __restrict__ index,
                                    int64_t n, char* __restrict__ out) {
   const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const int cpr = rb >> 4;
-  const int64_t row = t / cpr;
+  const int q = (rb >> 4) / G;
+  const int64_t row = t / q;
   if (row >= n) return;
-  const int c = static_cast<int>(t - row * cpr);
+  const int c = static_cast<int>(t - row * q);
   const int32_t src = index[row];
-  uint4 v = make_uint4(0u, 0u, 0u, 0u);
-  if (static_cast<uint64_t>(static_cast<uint32_t>(src)) < static_cast<uint64_t>(n_in))
-    v = *reinterpret_cast<const uint4*>(in + static_cast<int64_t>(src) * rb + c * 16);
-  *reinterpret_cast<uint4*>(out + row * rb + c * 16) = v;
+  const bool ok = static_cast<uint64_t>(static_cast<uint32_t>(src)) < static_cast<uint64_t>(n_in);
+  uint4 v[G];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+    v[g] = ok ? *reinterpret_cast<const uint4*>(in + static_cast<int64_t>(src) * rb + (c + g * q) * 16)
+              : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+  for (int g = 0; g < G; ++g) *reinterpret_cast<uint4*>(out + row * rb + (c + g * q) * 16) = v[g];
 }
 
 __global__ void stride2_tables_kernel(const int32_t* __restrict__ inverse,
@@ -779,9 +787,16 @@ int hi3d_gather_rows(const void* in, int64_t n_in, int32_t row_bytes, const int3
   HI3D_REQUIRE(in && index && out, "null pointer argument");
   HI3D_REQUIRE(((reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(out)) & 15) == 0,
                "rows must be 16-byte aligned");
-  const int64_t total = n * (row_bytes / 16);
-  hipLaunchKernelGGL(gather_rows_kernel, dim3(static_cast<unsigned>(ceil_div(total, 256))), dim3(256), 0, stream,
-                     static_cast<const char*>(in), n_in, row_bytes, index, n, static_cast<char*>(out));
+  const int cpr = row_bytes / 16;
+  if (cpr % 4 == 0) {
+    const int64_t total = n * (cpr / 4);
+    hipLaunchKernelGGL(gather_rows_kernel<4>, dim3(static_cast<unsigned>(ceil_div(total, 256))), dim3(256), 0, stream,
+                       static_cast<const char*>(in), n_in, row_bytes, index, n, static_cast<char*>(out));
+  } else {
+    const int64_t total = n * cpr;
+    hipLaunchKernelGGL(gather_rows_kernel<1>, dim3(static_cast<unsigned>(ceil_div(total, 256))), dim3(256), 0, stream,
+                       static_cast<const char*>(in), n_in, row_bytes, index, n, static_cast<char*>(out));
+  }
   HI3D_LAUNCH_CHECK();
   return HI3D_OK;
 }
