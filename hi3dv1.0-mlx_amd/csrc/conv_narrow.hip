@@ -231,7 +231,8 @@ __global__ __launch_bounds__(kNarrowWaves * 64) void conv_narrow_kernel(NarrowAr
 // wave (one per workgroup) owns its LDS (gather indices, a 3-slot ring of stages) and
 // synchronises with no other wave. A stage is one 128-byte K chunk of one present
 // offset: the wave's ROWS gathered rows and the 16 weight rows (zeros past cout),
-// ROWS / 8 + 2 loads, so the vmcnt waits are constants. Rows use the XOR swizzle of the
+// ROWS / 8 + WL loads (WL = 1 when cout <= 8: weight rows 8..15 are zeroed once), so
+// the vmcnt waits are constants. Rows use the XOR swizzle of the
 // tile kernels (chunk c of row r at c ^ ((r >> 1) & 7)), so the 16-row fragment reads
 // are free of bank conflicts.
 // output rows per wave: more waves per CU outweigh the weight rows each stage reloads
@@ -240,7 +241,7 @@ constexpr int kNarrowLdsRows = 16;
 
 __device__ __attribute__((aligned(16))) const uint32_t g_narrow_zero_row[32] = {};
 
-template <typename T, int ROWS>
+template <typename T, int ROWS, int WL>
 __global__ __launch_bounds__(64) void conv_narrow_lds_kernel(NarrowArgs a) {
   constexpr int STAGE = (ROWS + 16) * 128, PARTS = kTileRows / ROWS, G = ROWS / 16;
   constexpr int OPL = 1024 / (ROWS * 4);  // offsets per 16-byte-per-lane index load
@@ -257,6 +258,13 @@ __global__ __launch_bounds__(64) void conv_narrow_lds_kernel(NarrowArgs a) {
   const uint64_t n_in = static_cast<uint64_t>(a.n_in);
   const int rb = a.cin * static_cast<int>(sizeof(T));
   const int nch = rb >> 7;
+  if constexpr (WL == 1) {
+    // at most 8 outputs: weight rows 8..15 of every ring slot stay zero, and a stage
+    // loads rows 0..7 only
+#pragma unroll
+    for (int sl = 0; sl < 3; ++sl)
+      *reinterpret_cast<u32x4*>(smem + sl * STAGE + ROWS * 128 + 1024 + lane * 16) = u32x4{0u, 0u, 0u, 0u};
+  }
 
   // gather indices [offset][ROWS rows]: OPL offsets per 16-byte-per-lane load
   {
@@ -293,7 +301,7 @@ __global__ __launch_bounds__(64) void conv_narrow_lds_kernel(NarrowArgs a) {
       lds_dma16(ok ? reinterpret_cast<const char*>(pin) : zrow + lc * 16, st + j * 1024);
     }
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
+    for (int j = 0; j < WL; ++j) {
       const int o = 8 * j + lr;
       const int lc = pc ^ ((o >> 1) & 7);
       uint64_t wpin = reinterpret_cast<uint64_t>(a.w) +
@@ -343,7 +351,7 @@ __global__ __launch_bounds__(64) void conv_narrow_lds_kernel(NarrowArgs a) {
     }
     int slot = 0;
     for (int s = 0; s + 1 < S; ++s) {
-      wait_vmcnt<ROWS / 8 + 2>();  // stage s is in LDS; stage s + 1 may still be in flight
+      wait_vmcnt<ROWS / 8 + WL>();  // stage s is in LDS; stage s + 1 may still be in flight
       compute(slot);
       if (s + 2 < S) {
         issue(slot == 0 ? 2 : slot - 1, kl, cl);  // the slot of stage s - 1, consumed
@@ -387,8 +395,12 @@ int launch_narrow(const NarrowArgs& a, hipStream_t stream) {
     if (steps % 2 == 0) {  // 128-byte rows: one wave per workgroup, gathers staged in LDS
       const int64_t waves = (kTileRows / kNarrowLdsRows) * a.ntiles;
       HI3D_REQUIRE(waves < (int64_t(1) << 31), "too many tiles");
-      hipLaunchKernelGGL((conv_narrow_lds_kernel<T, kNarrowLdsRows>), dim3(static_cast<unsigned>(waves)), dim3(64), 0,
-                         stream, a);
+      if (a.cout <= 8)
+        hipLaunchKernelGGL((conv_narrow_lds_kernel<T, kNarrowLdsRows, 1>), dim3(static_cast<unsigned>(waves)), dim3(64),
+                           0, stream, a);
+      else
+        hipLaunchKernelGGL((conv_narrow_lds_kernel<T, kNarrowLdsRows, 2>), dim3(static_cast<unsigned>(waves)), dim3(64),
+                           0, stream, a);
       HI3D_LAUNCH_CHECK();
       return HI3D_OK;
     }
