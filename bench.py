@@ -1,19 +1,23 @@
 """Benchmark of the Hi3D sparse hot path on one MI355X.
 
-Headline (``value``): voxels/s of the submanifold 3x3x3 convolution, C 128->128, fp16
-with fp32 accumulation, on the 256^3 union of 8 seeded ellipsoid 2-voxel shells
-(~543k voxels, kernel map cached as in the reference's usage). One step = one
-convolution pass over the whole active set with inputs resident in HBM.
+Headline (``value``): voxels/s of the sparse residual block, C256 fp16 with fp32
+accumulation, on the 1024^3 union of 8 seeded ellipsoid 1-voxel shells (~4.43M voxels,
+kernel map cached as in the reference's usage). One step = one pass of the block over
+the whole active set with inputs resident in HBM: adaLN projection of the conditioning
+vector, LayerNorm + modulate, submanifold 3x3x3 conv + SiLU, conv + residual add.
 
-``roofline`` is measured live for that convolution kernel (HIP events on the stream it
-runs on): achieved = 2 * P * Cin * Cout / average kernel time against the fp16 dense MFMA
-peak. ``cpu_baseline`` times the reference's CPU fallback (oracle port: sort +
-searchsorted map, per-offset gather / matmul / index_add_) on the host cores.
-``extra`` reports the other workloads: the fp32 sphere shell, the strided pair, W8A8
-int8 TOPS (GEMM alone and quantise + GEMM), the residual blocks, octree upsampling,
-transformer I/O resampling, unique cube corners, and kernel-map builds.
+``roofline`` is measured live for the block's convolution kernel (HIP events around
+each convolution inside the timed steps, on the stream they run on): achieved =
+2 * P * Cin * Cout / average launch time against the fp16 dense MFMA peak.
+``cpu_baseline`` times the reference's CPU fallback of the block (oracle port: sort +
+searchsorted map, per-offset gather / matmul / index_add_, LayerNorm) on the host cores
+for a sample of output rows. ``extra`` reports the other workloads: the fp32 sphere
+shell and the C128 shells (with kernel-map builds through the dense grid and the
+hash), the strided pair, W8A8 int8 TOPS (GEMM alone and quantise + GEMM), the VAE
+blocks, octree upsampling, transformer I/O resampling and unique cube corners, with
+CPU baselines of the fp32 shell (in full) and of W8A8 (sampled tokens).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only a,b] [--quick] [--no-cpu]
 """
 
 from __future__ import annotations
@@ -35,12 +39,12 @@ PEAK_FP32_TFLOPS = 157.3
 PEAK_INT8_TOPS = 5000.0
 PEAK_HBM_GBS = 8000.0
 
-# Headline kernel (fp16, Cout 128: the 384-row ring kernel) and the counter summary that
-# holds its measured HBM traffic per launch: FETCH_SIZE and WRITE_SIZE per dispatch from
+# Headline kernel (the block's C256 convolution: 256 x 256 ring tiles) and the counter
+# summary that holds its measured HBM traffic per launch: FETCH_SIZE and WRITE_SIZE per dispatch from
 # two rocprofv3 --pmc runs of this script, each scaled by the factor the same counter
 # reads for a plain device copy of known size (`--copy-probe`).
-HEADLINE_KERNEL = "conv_wide_kernel<_Float16, 128, 8>"
-TRAFFIC_SUMMARY = ROOT / "profiles" / "conv_wide_subm3_c128_fp16_traffic.txt"
+HEADLINE_KERNEL = "conv_ring_kernel<_Float16, 256, 8, 256>"
+TRAFFIC_SUMMARY = ROOT / "profiles" / "conv_ring_resblock_c256_fp16_traffic.txt"
 
 
 def measured_traffic():
@@ -52,6 +56,19 @@ def measured_traffic():
     except (OSError, ValueError):
         pass
     return None
+
+
+_COORDS: dict = {}
+
+
+def coords_of(name: str, device=None):
+    """Seeded voxel coordinates of a workload, generated once per run (on the GPU when a
+    device is given) and shared by its GPU and host measurements."""
+    if name not in _COORDS:
+        from hi3d_amd import workloads
+
+        _COORDS[name] = workloads.coords_for(name, device=device) if device is not None else workloads.coords_for(name)
+    return _COORDS[name]
 
 
 def log(msg: str) -> None:
@@ -85,7 +102,7 @@ def bench_subm(name: str, grid: int, cin: int, cout: int, dtype, steps: int, war
     from hi3d_amd import conv, kmap, workloads
 
     dev = torch.device("cuda:0")
-    idx = workloads.coords_for(name, device=dev)
+    idx = coords_of(name, dev)
     n = len(idx)
     coords = torch.as_tensor(idx).to(dev)
     np_dtype = np.float16 if dtype == torch.float16 else np.float32
@@ -93,6 +110,7 @@ def bench_subm(name: str, grid: int, cin: int, cout: int, dtype, steps: int, war
     w = torch.as_tensor(workloads.normal((cout, 27, cin), 1.0 / np.sqrt(27 * cin), seed + 2, np_dtype)).to(dev)
     # kernel map build (hash insert + probe) and plan, timed separately
     map_wall, map_ev = timed(lambda: kmap.build_kernel_map(coords, [grid] * 3, 1, check=False), 5, 2)
+    hash_wall, hash_ev = timed(lambda: kmap.build_kernel_map(coords, [grid] * 3, 1, capacity=0, check=False), 5, 2)
     km = kmap.build_kernel_map(coords, [grid] * 3, 1)
     plan_wall, plan_ev = timed(lambda: kmap.build_plan(km.table, km.n, km.indices), 3, 1)
     plan = km.plan()
@@ -116,7 +134,9 @@ def bench_subm(name: str, grid: int, cin: int, cout: int, dtype, steps: int, war
         "eff_tflops": flops / (ev * 1e-3) / 1e12,
         "conv_alg_bytes": conv_bytes,
         "map_ms": map_wall,
-        "map_alg_gbs": map_bytes / (map_wall * 1e-3) / 1e9,
+        "map_dense_ms": map_ev,
+        "map_hash_ms": hash_ev,
+        "map_alg_gbs_hash": map_bytes / (hash_ev * 1e-3) / 1e9,
         "plan_ms": plan_wall,
         "flops": flops,
         "tile_rows": int(plan.rows.shape[0]) // max(plan.ntiles, 1),
@@ -130,7 +150,7 @@ def bench_stride2(steps: int, warmup: int):
     from hi3d_amd import conv, kmap, workloads
 
     dev = torch.device("cuda:0")
-    idx = workloads.coords_for("down2_up2_c64_c128_fp16", device=dev)
+    idx = coords_of("down2_up2_c64_c128_fp16", dev)
     coords = torch.as_tensor(idx).to(dev)
     map_wall, _ = timed(lambda: kmap.stride2_structure(coords, [512] * 3, 1), 3, 1)
     s = kmap.stride2_structure(coords, [512] * 3, 1)
@@ -196,7 +216,11 @@ def bench_w8a8(steps: int, warmup: int):
     return res
 
 
-def bench_block(steps: int, warmup: int):
+def bench_block(steps: int, warmup: int, settle_s: float = 0.0):
+    """The residual block on the 1024^3 shells, C256 fp16: one step = adaLN projection,
+    LayerNorm + modulate, conv + SiLU, conv + residual over every voxel. HIP events
+    around each convolution inside the timed steps give the convolution kernel's average
+    launch time (both run on the current stream)."""
     import numpy as np
     import torch
 
@@ -204,12 +228,14 @@ def bench_block(steps: int, warmup: int):
     from hi3d_amd.block import ResBlockWeights
 
     dev = torch.device("cuda:0")
-    idx = workloads.coords_for("resblock_c256_fp16", device=dev)
+    idx = coords_of("resblock_c256_fp16", dev)
     n = len(idx)
     c, d = 256, 1024
     coords = torch.as_tensor(idx).to(dev)
-    map_wall, _ = timed(lambda: kmap.build_kernel_map(coords, [1024] * 3, 1, check=False), 3, 1)
+    map_wall, map_ev = timed(lambda: kmap.build_kernel_map(coords, [1024] * 3, 1, check=False), 3, 1)
+    hash_wall, hash_ev = timed(lambda: kmap.build_kernel_map(coords, [1024] * 3, 1, capacity=0, check=False), 3, 1)
     km = kmap.build_kernel_map(coords, [1024] * 3, 1)
+    plan_wall, plan_ev = timed(lambda: kmap.build_plan(km.table, km.n, km.indices), 3, 1)
     plan = km.plan()
     pairs = int(km.counts.sum())
     x = torch.as_tensor(workloads.normal((n, c), 1.0, 52, np.float16)).to(dev)
@@ -220,21 +246,45 @@ def bench_block(steps: int, warmup: int):
         torch.as_tensor(workloads.normal((c, 27, c), 1.0 / np.sqrt(27 * c), 56, np.float16)).to(dev), None,
         torch.as_tensor(workloads.normal((c, 27, c), 1.0 / np.sqrt(27 * c), 57, np.float16)).to(dev), None,
     )
-    s_steps = max(3, steps // 5)
-    b_wall, b_ev = timed(lambda: block.residual_block(x, plan, cond, weights), s_steps, max(1, warmup // 2))
+    # clocks settle on untimed passes first (the shader clock ramps under sustained load)
+    t_end = time.perf_counter() + settle_s
+    while time.perf_counter() < t_end:
+        block.residual_block(x, plan, cond, weights)
+        torch.cuda.synchronize()
+    for _ in range(warmup):
+        block.residual_block(x, plan, cond, weights)
+    torch.cuda.synchronize()
+    conv_ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    t0 = time.perf_counter()
+    for i in range(steps):
+        block.residual_block(x, plan, cond, weights, conv_events=conv_ev[i])
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    conv_ms = [e[0].elapsed_time(e[1]) for e in conv_ev] + [e[1].elapsed_time(e[2]) for e in conv_ev]
+    conv_avg = sum(conv_ms) / len(conv_ms)
     s1p, sh = kernels.adaln_projection(weights.proj_weight, weights.proj_bias, cond)
     ln_wall, ln_ev = timed(lambda: kernels.layer_norm_modulate(x, 1e-6, scale=s1p, shift=sh), steps, warmup)
-    flops = 2 * 2.0 * pairs * c * c
+    conv_flops = 2.0 * pairs * c * c
+    conv_bytes = 2 * (n * c + n * c + 27 * c * c) + 4 * 27 * n
     return {
         "workload": "resblock_c256_fp16",
         "voxels": n,
         "pairs": pairs,
-        "map_ms": map_wall,
-        "block_ms": b_wall,
-        "block_eff_tflops": flops / (b_ev * 1e-3) / 1e12,
+        "channels": c,
+        "block_ms": wall,
+        "voxels_per_s": n / (wall * 1e-3),
+        "block_eff_tflops": 2 * conv_flops / (wall * 1e-3) / 1e12,
+        "conv_kernel_ms": conv_avg,
+        "conv_kernel_ms_min": min(conv_ms),
+        "conv_flops": conv_flops,
+        "conv_alg_bytes": conv_bytes,
+        "conv_eff_tflops": conv_flops / (conv_avg * 1e-3) / 1e12,
         "ln_ms": ln_ev,
         "ln_gbs": 4.0 * n * c / (ln_ev * 1e-3) / 1e9,
-        "voxels_per_s": n / (b_wall * 1e-3),
+        "map_dense_ms": map_ev,
+        "map_hash_ms": hash_ev,
+        "map_alg_gbs_hash": n * 356 / (hash_ev * 1e-3) / 1e9,
+        "plan_ms": plan_ev,
     }
 
 
@@ -248,7 +298,7 @@ def bench_vae(steps: int, warmup: int):
     from hi3d_amd import kernels, sparse, vae, workloads
 
     dev = torch.device("cuda:0")
-    idx = workloads.coords_for("down2_up2_c64_c128_fp16", device=dev)
+    idx = coords_of("down2_up2_c64_c128_fp16", dev)
     level = sparse.Level.from_coords(torch.as_tensor(idx[:, 1:]).to(dev))
     n, c = level.n, 128
     x = torch.as_tensor(workloads.normal((n, c), 1.0, 61, np.float16)).to(dev)
@@ -293,7 +343,7 @@ def bench_upsample(steps: int, warmup: int):
     from hi3d_amd import sparse, vae, workloads
 
     dev = torch.device("cuda:0")
-    idx = torch.as_tensor(workloads.coords_for("down2_up2_c64_c128_fp16", device=dev)).to(dev)
+    idx = torch.as_tensor(coords_of("down2_up2_c64_c128_fp16", dev)).to(dev)
     s2 = _kmap.stride2_structure(idx, [int(v) + 1 for v in idx[:, 1:].max(0).values.tolist()], 1)
     level = sparse.Level.from_coords(s2.low[:, 1:].contiguous())
     p_n, c = level.n, 256
@@ -343,7 +393,7 @@ def bench_geometry(steps: int, warmup: int):
     from hi3d_amd.geometry import Geometry
 
     dev = torch.device("cuda:0")
-    idx = torch.as_tensor(workloads.coords_for("resblock_c256_fp16", device=dev)).to(dev)
+    idx = torch.as_tensor(coords_of("resblock_c256_fp16", dev)).to(dev)
     coords = idx[:, 1:].contiguous()
     build_wall, _ = timed(lambda: Geometry(coords), 2, 1)
     geo = Geometry(coords)
@@ -385,7 +435,7 @@ def bench_unique(steps: int, warmup: int):
     from hi3d_amd import fast_unique, workloads
 
     dev = torch.device("cuda:0")
-    idx = torch.as_tensor(workloads.coords_for("resblock_c256_fp16", device=dev)).to(dev)
+    idx = torch.as_tensor(coords_of("resblock_c256_fp16", dev)).to(dev)
     xyz = idx[:, 1:].to(torch.int32)
     off = torch.tensor([[i >> 2 & 1, i >> 1 & 1, i & 1] for i in range(8)], dtype=torch.int32, device=dev)
     corners = (xyz[:, None, :] + off[None]).reshape(-1, 3).contiguous()
@@ -405,27 +455,69 @@ def bench_unique(steps: int, warmup: int):
     }
 
 
-def cpu_baseline(name: str, grid: int, cin: int, cout: int, max_rows: int | None):
-    import torch
+def cpu_threads() -> int:
+    """Host threads for the CPU baselines: the process's CPU share (``OMP_NUM_THREADS``
+    when the launcher sets it, as GPU hosts that split their cores per GPU do), else
+    every core ``os.cpu_count()`` reports."""
+    try:
+        share = int(os.environ.get("OMP_NUM_THREADS", "0"))
+    except ValueError:
+        share = 0
+    return share if share > 0 else (os.cpu_count() or 1)
 
+
+def cpu_baseline_block(sample_rows: int):
+    """The residual block on the host (reference CPU fallback per stage, oracle port),
+    on a random sample of output rows over the full map of the 1024^3 shells."""
     from hi3d_amd import workloads
     from oracle import baseline
 
-    idx = workloads.coords_for(name)
-    threads = min(os.cpu_count() or 1, 16)
-    torch.set_num_threads(threads)
-    r = baseline.time_subm_conv(idx, [grid] * 3, cin, cout, repeats=3, max_rows=max_rows, threads=threads)
+    idx = coords_of("resblock_c256_fp16")
+    threads = cpu_threads()
+    r = baseline.time_resblock(idx, [1024] * 3, 256, 1024, sample_rows=sample_rows, threads=threads)
     return r
+
+
+def cpu_baseline_conv(name: str, grid: int, cin: int, cout: int):
+    """One submanifold convolution on the host over the whole set (map cached)."""
+    from hi3d_amd import workloads
+    from oracle import baseline
+
+    idx = coords_of(name)
+    return baseline.time_subm_conv(idx, [grid] * 3, cin, cout, repeats=3, threads=cpu_threads())
+
+
+def cpu_baseline_w8a8(rows: int):
+    """Host quantiser + integer GEMM of both W8A8 shapes on ``rows`` sampled tokens."""
+    import torch
+
+    from oracle import baseline
+
+    torch.set_num_threads(cpu_threads())
+    out = {}
+    for tag, (m, k, n) in {"A": (65536, 1024, 4096), "B": (65536, 4096, 1024)}.items():
+        r = baseline.time_w8a8(rows, k, n)
+        ops = 2.0 * rows * n * k
+        out[tag] = {**r, "full_m": m, "tops_gemm": ops / r["gemm_s"] / 1e12,
+                    "tops_quant_gemm": ops / (r["quant_s"] + r["gemm_s"]) / 1e12}
+    return out
+
+
+WORKLOADS = ("resblock", "subm3_c128_fp16", "subm3_c64_fp32", "stride2", "w8a8", "vae_resnet", "vae_upsample",
+             "transformer_io", "unique")
 
 
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=100, help="untimed steps first (100 let the clocks settle)")
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--settle", type=float, default=2.0,
+                    help="seconds of untimed headline passes before its warm-up (clock ramp)")
+    ap.add_argument("--only", default="", help=f"comma-separated workloads to run, of {', '.join(WORKLOADS)}")
     ap.add_argument("--quick", action="store_true", help="headline workload only")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--cpu-rows", type=int, default=None, help="row sample of the CPU baseline")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    ap.add_argument("--cpu-rows", type=int, default=400_000, help="output-row sample of the block's CPU baseline")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (calibrates HBM byte counters) and exit")
     args = ap.parse_args()
@@ -444,6 +536,12 @@ def main() -> int:
         print("bench.py measures one GPU: the sparse hot path runs on a single MI355X here "
               "(multi-GPU sharding is a design note, not a measured path). Use --gpus 1.", file=sys.stderr)
         return 2
+    only = [w for w in args.only.split(",") if w]
+    unknown = sorted(set(only) - set(WORKLOADS))
+    if unknown:
+        print(f"unknown workloads {unknown}; choose from {WORKLOADS}", file=sys.stderr)
+        return 2
+    selected = only or (["resblock"] if args.quick else list(WORKLOADS))
 
     import torch
 
@@ -455,40 +553,69 @@ def main() -> int:
     _lib.lib()
     torch.backends.cuda.matmul.allow_tf32 = False
 
-    log("headline: subm3 C128 fp16 on the 256^3 ellipsoid shells")
-    head = bench_subm("subm3_c128_fp16", 256, 128, 128, torch.float16, args.steps, args.warmup)
-    log(f"  {head['voxels']} voxels, {head['conv_ms']:.3f} ms/step, {head['eff_tflops']:.1f} eff TFLOP/s")
+    head = None
     extra = {}
-    if not args.quick:
-        log("workload 1: subm3 C64 fp32, 128^3 sphere shell")
-        extra["subm3_c64_fp32"] = bench_subm("subm3_c64_fp32", 128, 64, 64, torch.float32, args.steps, args.warmup)
-        log("workload 3: stride-2 down/up fp16, 512^3 shells")
-        extra["down2_up2_c64_c128_fp16"] = bench_stride2(args.steps, args.warmup)
-        log("workload 4: W8A8 int8 linear")
-        extra["w8a8_linear"] = bench_w8a8(max(10, args.steps // 2), max(3, args.warmup // 2))
-        log("workload 5: residual block C256 fp16, 1024^3 shells")
-        extra["resblock_c256_fp16"] = bench_block(max(10, args.steps // 2), max(2, args.warmup // 2))
-        log("VAE decoder residual block C128 fp16, 512^3 fine shells")
-        extra["vae_resnet_c128_fp16"] = bench_vae(max(10, args.steps // 2), max(2, args.warmup // 2))
-        log("VAE decoder octree upsampling C256 fp16, 512^3 fine shells' parents")
-        extra["vae_upsample_c256_fp16"] = bench_upsample(max(10, args.steps // 2), max(2, args.warmup // 2))
-        log("transformer I/O resampling C256 fp16, 1024^3 shells")
-        extra["transformer_io_c256_fp16"] = bench_geometry(max(10, args.steps // 2), max(2, args.warmup // 2))
-        log("unique cube corners of the 1024^3 shells")
-        extra["unique_corners_1024"] = bench_unique(max(5, args.steps // 10), 2)
+    half_steps, half_warm = max(10, args.steps // 2), max(2, args.warmup // 2)
+    for name in selected:
+        if name == "resblock":
+            log("headline: residual block C256 fp16 on the 1024^3 ellipsoid shells")
+            head = bench_block(args.steps, args.warmup, args.settle)
+            log(f"  {head['voxels']} voxels, {head['block_ms']:.3f} ms/step, conv {head['conv_kernel_ms']:.3f} ms "
+                f"({head['conv_eff_tflops']:.1f} TFLOP/s)")
+        elif name == "subm3_c128_fp16":
+            log("subm3 C128 fp16 on the 256^3 ellipsoid shells")
+            extra[name] = bench_subm(name, 256, 128, 128, torch.float16, args.steps, args.warmup)
+        elif name == "subm3_c64_fp32":
+            log("subm3 C64 fp32, 128^3 sphere shell")
+            extra[name] = bench_subm(name, 128, 64, 64, torch.float32, args.steps, args.warmup)
+        elif name == "stride2":
+            log("stride-2 down/up fp16, 512^3 shells")
+            extra["down2_up2_c64_c128_fp16"] = bench_stride2(args.steps, args.warmup)
+        elif name == "w8a8":
+            log("W8A8 int8 linear")
+            extra["w8a8_linear"] = bench_w8a8(half_steps, max(3, half_warm))
+        elif name == "vae_resnet":
+            log("VAE decoder residual block C128 fp16, 512^3 fine shells")
+            extra["vae_resnet_c128_fp16"] = bench_vae(half_steps, half_warm)
+        elif name == "vae_upsample":
+            log("VAE decoder octree upsampling C256 fp16, 512^3 fine shells' parents")
+            extra["vae_upsample_c256_fp16"] = bench_upsample(half_steps, half_warm)
+        elif name == "transformer_io":
+            log("transformer I/O resampling C256 fp16, 1024^3 shells")
+            extra["transformer_io_c256_fp16"] = bench_geometry(half_steps, half_warm)
+        elif name == "unique":
+            log("unique cube corners of the 1024^3 shells")
+            extra["unique_corners_1024"] = bench_unique(max(5, args.steps // 10), 2)
+    if head is None:  # a partial run (profiling): the workloads' own figures only
+        print(json.dumps({"partial": selected, "extra": extra}), flush=True)
+        return 0
+
     cpu = None
     if not args.no_cpu:
-        log("CPU baseline (reference CPU fallback, oracle port)")
-        r = cpu_baseline("subm3_c128_fp16", 256, 128, 128, args.cpu_rows)
+        log(f"CPU baseline: residual block on {args.cpu_rows} sampled voxels (reference CPU fallback, oracle port)")
+        r = cpu_baseline_block(args.cpu_rows)
         cpu = {
-            "value": r["rows"] / r["conv_s"],
+            "value": r["sample_rows"] / r["block_s"],
             "unit": "voxels/s",
             "cores": r["torch_threads"],
             "kind": "port",
-            "sample": (f"subm3 C128 conv (map cached) on {r['rows']} voxels of the 256^3 shells, fp32 on host, "
-                       f"median of 3 after 1 warm-up; map build {r['map_s']:.2f} s; {r['model']}"),
+            "sample": (f"C256 residual block (adaLN projection, LayerNorm + modulate, conv + SiLU, conv + residual; "
+                       f"fp32 on host) for {r['sample_rows']} randomly sampled output voxels of the {r['rows']}-voxel "
+                       f"1024^3 shells over the full kernel map (built once on host in {r['map_s']:.2f} s, cached); "
+                       f"median of 2 after 1 warm-up; {r['torch_threads']} threads of the {r['cpu_count']} "
+                       f"cores os.cpu_count() reports; {r['model']}"),
+            "host_cpu_count": r["cpu_count"],
         }
-    achieved = head["eff_tflops"]
+        if "subm3_c64_fp32" in extra:
+            log("CPU baseline: subm3 C64 fp32 sphere shell in full")
+            c1 = cpu_baseline_conv("subm3_c64_fp32", 128, 64, 64)
+            extra["subm3_c64_fp32"]["cpu_baseline"] = {
+                "voxels_per_s": c1["rows"] / c1["conv_s"], "conv_s": c1["conv_s"], "map_s": c1["map_s"],
+                "rows": c1["rows"], "threads": c1["torch_threads"], "sample": "all voxels, map cached"}
+        if "w8a8_linear" in extra:
+            log("CPU baseline: W8A8 quantiser + integer GEMM on 4096 sampled tokens")
+            extra["w8a8_linear"]["cpu_baseline"] = cpu_baseline_w8a8(4096)
+    conv_tflops = head["conv_eff_tflops"]
     line = {
         "metric": "sparse-conv voxels/s + eff. TFLOP/s; W8A8 GEMM int8 TOPS (1 MI355X)",
         "value": head["voxels_per_s"],
@@ -496,30 +623,32 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": head["conv_ms"],
+        "ms_per_step": head["block_ms"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp16",
         "data": "synthetic",
         "config": {
-            "workload": "subm3_c128_fp16",
-            "grid": 256,
+            "workload": "resblock_c256_fp16",
+            "grid": 1024,
             "voxels": head["voxels"],
             "pairs": head["pairs"],
-            "cin": 128,
-            "cout": 128,
-            "kernel": "3x3x3 submanifold, map cached",
+            "channels": 256,
+            "step": "adaLN projection + LayerNorm/modulate + 3x3x3 submanifold conv + SiLU + conv + residual, "
+                    "kernel map cached",
+            "clock_settle_s": args.settle,
         },
-        "eff_tflops": head["eff_tflops"],
+        "eff_tflops": head["block_eff_tflops"],
         "roofline": {
             "bound": "mfma",
-            "achieved": achieved,
+            "achieved": conv_tflops,
             "peak": PEAK_FP16_TFLOPS,
             "unit": "TFLOP/s",
-            "frac": achieved / PEAK_FP16_TFLOPS,
+            "frac": conv_tflops / PEAK_FP16_TFLOPS,
             "traffic": measured_traffic(),
             "traffic_source": TRAFFIC_SUMMARY.name,
+            "alg_flops": head["conv_flops"],
             "alg_bytes": head["conv_alg_bytes"],
             "kernel": HEADLINE_KERNEL,
             "kernel_ms": head["conv_kernel_ms"],

@@ -37,9 +37,21 @@ def residual_block(
     w: ResBlockWeights,
     eps: float = 1e-6,
     apply_silu_to_cond: bool = False,
+    conv_events=None,
 ) -> torch.Tensor:
-    """``x + conv2(silu(conv1(LN(x) * (1 + scale) + shift)))`` over one kernel map."""
+    """``x + conv2(silu(conv1(LN(x) * (1 + scale) + shift)))`` over one kernel map.
+
+    ``conv_events``: optional three ``torch.cuda.Event``s recorded on the current stream
+    before the first convolution, between the two and after the second (the convolutions
+    run on that stream), for timing them inside a pass of the block."""
     scale1p, shift = adaln_projection(w.proj_weight, w.proj_bias, cond, apply_silu_to_cond)
     h = layer_norm_modulate(x, eps, scale=scale1p, shift=shift)
+    if conv_events is not None:
+        conv_events[0].record()
     h = _conv.conv(h, plan, w.conv1_weight, w.conv1_bias, act="silu")
-    return _conv.conv(h, plan, w.conv2_weight, w.conv2_bias, residual=x)
+    if conv_events is not None:
+        conv_events[1].record()
+    out = _conv.conv(h, plan, w.conv2_weight, w.conv2_bias, residual=x)
+    if conv_events is not None:
+        conv_events[2].record()
+    return out

@@ -21,7 +21,9 @@ Pinning map (oracle function -> checks here):
   w8a8.int_gemm / epilogue            -> float64 matmul of small integers, the reference
                                          test's tolerance (tests/test_w8a8_inference.py:20)
   norm.layer_norm_modulate            -> float64 LayerNorm (torch.nn.functional)
-  norm.adaln_projection / residual_block_f64 -> explicit float64 composition
+  norm.adaln_projection              -> closed forms (zero weight, identity halves, SiLU
+                                         from math.exp), torch linear + chunk(2)
+  norm.residual_block_f64            -> explicit float64 composition
 """
 
 from __future__ import annotations
@@ -334,6 +336,46 @@ def test_layer_norm_golden():
     assert hashlib.sha256(got.tobytes()).hexdigest() == str(data["mod"])
 
 
+def test_adaln_projection_closed_forms():
+    """adaln_projection pinned by closed forms that a swapped (scale, shift) split, a
+    dropped ``1 +`` or a missing bias would fail (chunk order (scale, shift):
+    src/hi3d_mac/mlx_backend/transformer.py:413-416, sparc3d_transformer.py:134):
+      * W = 0, b = [s; t]        -> (fp16(1 + fp16(s)), fp16(t));
+      * W = [I; 0], b = 0         -> (fp16(1 + fp16(cond)), 0);
+      * W = [0; I], b = 0         -> (1, fp16(cond));
+      * W = [I; 0] with SiLU      -> (fp16(1 + fp16(c / (1 + e^-c))), 0), per element from
+        math.exp, with silu(0) = 0;
+      * a dense W against torch's linear + chunk(2) in float64."""
+    import math
+
+    c, d = 6, 6
+    s = np.array([0.5, -0.25, 0.0, 2.0, -1.0, 0.125])
+    t = np.array([0.75, -3.0, 0.0625, 1.0, -0.5, 4.0])
+    scale1p, shift = onorm.adaln_projection(np.zeros((2 * c, d)), np.concatenate([s, t]), np.ones(d))
+    assert scale1p.dtype == np.float16 and shift.dtype == np.float16
+    assert np.array_equal(scale1p, (1.0 + s).astype(np.float16))
+    assert np.array_equal(shift, t.astype(np.float16))
+    cond = np.array([0.1, -0.2, 0.3, 0.0, 5.0, -7.0])
+    eye, zero = np.eye(c), np.zeros((c, d))
+    scale1p, shift = onorm.adaln_projection(np.vstack([eye, zero]), None, cond)
+    want = (np.float32(1.0) + cond.astype(np.float16).astype(np.float32)).astype(np.float16)
+    assert np.array_equal(scale1p, want) and np.array_equal(shift, np.zeros(c, np.float16))
+    scale1p, shift = onorm.adaln_projection(np.vstack([zero, eye]), np.zeros(2 * c), cond)
+    assert np.array_equal(scale1p, np.ones(c, np.float16)) and np.array_equal(shift, cond.astype(np.float16))
+    scale1p, shift = onorm.adaln_projection(np.vstack([eye, zero]), None, cond, apply_silu=True)
+    silu = np.array([v / (1.0 + math.exp(-v)) for v in cond])
+    assert silu[3] == 0.0
+    want = (np.float32(1.0) + silu.astype(np.float16).astype(np.float32)).astype(np.float16)
+    assert np.array_equal(scale1p, want) and np.array_equal(shift, np.zeros(c, np.float16))
+    rng = np.random.default_rng(13)
+    w, b, x = rng.standard_normal((2 * c, d)), rng.standard_normal(2 * c), rng.standard_normal(d)
+    y = F.linear(torch.as_tensor(x)[None], torch.as_tensor(w), torch.as_tensor(b))
+    scale, sh = (v[0].numpy() for v in y.chunk(2, dim=1))
+    scale1p, shift = onorm.adaln_projection(w, b, x)
+    assert np.array_equal(scale1p, (1.0 + scale.astype(np.float16).astype(np.float32)).astype(np.float16))
+    assert np.array_equal(shift, sh.astype(np.float16))
+
+
 def test_residual_block_composition():
     rng = np.random.default_rng(9)
     idx = _rand_indices(rng, 8, 0.3)
@@ -374,6 +416,19 @@ def test_cpu_baseline_runs_on_a_sample():
     table = okmap.neighbour_table(idx, [10] * 3)
     ref = oconv.gather_conv_f64(feats, table, weight.reshape(6, 27, 8))
     assert oconv.rel_err(got, ref) <= 1e-5
+    # the sampled-row form: the sample's part of the full map, queried from the output
+    # side, gives the same pair sets, and the conv of those rows equals the full conv's
+    n = len(idx)
+    sample = torch.as_tensor(rng.permutation(n)[:150])
+    full = baseline.restrict_to_rows(pairs[0], pairs[1], n, sample)
+    part = baseline.kernel_map_rows(torch.as_tensor(idx), [10] * 3, sample)
+    for k in range(27):
+        assert sorted(zip(full[0][k].tolist(), full[1][k].tolist())) == sorted(
+            zip(part[0][k].tolist(), part[1][k].tolist()))
+    rows = baseline.subm_conv_rows(torch.as_tensor(feats), *part, torch.as_tensor(weight), None, sample).numpy()
+    assert oconv.rel_err(rows, ref[sample.numpy()]) <= 1e-5
+    r = baseline.time_resblock(idx, [10] * 3, 8, 12, sample_rows=100, repeats=1, threads=1)
+    assert r["sample_rows"] == 100 and r["rows"] == n and r["block_s"] > 0
 
 
 def test_vae_group_stats_oracle_against_numpy_moments():
