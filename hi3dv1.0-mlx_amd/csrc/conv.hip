@@ -598,7 +598,7 @@ __device__ __forceinline__ const char* gather_src(const char* in, int32_t g, uin
 }
 
 __device__ __forceinline__ int ring_off(int row, int chunk) {
-  return row * 64 + ((chunk ^ (((row >> 1) ^ (row >> 3)) & 3)) << 4);
+  return row * 64 + ((chunk ^ ((row >> 2) & 3)) << 4);
 }
 
 template <typename T, int BN, int NW, int BMv>
@@ -639,9 +639,9 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_ring_kernel(ConvArgs a) {
 
   // load u of this wave covers stage rows (wave + NW u) * 16 + lane / 4 (gathered rows for
   // u < LA, weight rows for u - LA after), at physical chunk lane % 4, i.e. logical chunk
-  // `coff` / 16 (the swizzle repeats every 64 rows)
+  // `coff` / 16 (the swizzle repeats every 16 rows)
   const int r0 = wave * 16 + (lane >> 2);
-  const int coff = ((lane & 3) ^ (((r0 >> 1) ^ (r0 >> 3)) & 3)) * 16;
+  const int coff = ((lane & 3) ^ ((r0 >> 2) & 3)) * 16;
   const char* wrow[Sh::LB];
 #pragma unroll
   for (int j = 0; j < Sh::LB; ++j)

@@ -63,7 +63,7 @@ struct HaloArgs {
 __device__ __attribute__((aligned(16))) const uint32_t g_halo_zero[kHMaxRowBytes / 4] = {};
 
 __device__ __forceinline__ int hoff(int row, int chunk) {
-  return row * 64 + ((chunk ^ (((row >> 1) ^ (row >> 3)) & 3)) << 4);
+  return row * 64 + ((chunk ^ ((row >> 2) & 3)) << 4);
 }
 
 __device__ __forceinline__ float hsilu(float x) { return x / (1.0f + expf(-x)); }
@@ -90,14 +90,14 @@ __global__ __launch_bounds__(kHThreads, 1) void conv_halo_kernel(HaloArgs a) {
 #pragma unroll
   for (int j = 0; j < 6; ++j) {
     const int hr = (wave + 8 * j) * 16 + (lane >> 2);
-    const int c = (lane & 3) ^ (((hr >> 1) ^ (hr >> 3)) & 3);
+    const int c = (lane & 3) ^ ((hr >> 2) & 3);
     const int32_t g = a.halo[tile * kHMax + hr];
     hsrc[j] = static_cast<uint64_t>(static_cast<uint32_t>(g)) < n_in ? a.in + static_cast<int64_t>(g) * rb + c * 16
                                                                        : zero + c * 16;
   }
   // weight loads: load u (offset u of the pair) covers weight rows 16 wave .. +15
   const int br = wave * 16 + (lane >> 2);
-  const int bc = (lane & 3) ^ (((br >> 1) ^ (br >> 3)) & 3);
+  const int bc = (lane & 3) ^ ((br >> 2) & 3);
   const char* const wsrc = a.weight + static_cast<int64_t>(n0 + br) * kHKvol * rb + bc * 16;
   const char* const wzero = zero + bc * 16;
   // A-fragment LDS offsets of this wave's offsets k = 2 p + th (K-group 0; K-group 1 is

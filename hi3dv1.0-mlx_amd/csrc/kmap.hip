@@ -350,21 +350,37 @@ __global__ __launch_bounds__(256) void pair_write_kernel(const int32_t* __restri
 }
 
 // ------------------------------------------------------------ stride-2 structure --
-__global__ void half_keys_kernel(const int4* __restrict__ coords, int64_t n, int32_t hx, int32_t hy,
-                                 int32_t hz, unsigned long long* __restrict__ keys,
-                                 int32_t* __restrict__ rows) {
+// Sort key of fine row i: its coarse cell's packed code times 8 plus its slot, so the
+// rows of one coarse cell sort together and two rows with the same coordinate sort next
+// to each other. Coordinates outside [0, batch) x [0, sx) x [0, sy) x [0, sz) raise the
+// range flag and take key 0 (the result is then discarded by the caller).
+__global__ void half_keys_kernel(const int4* __restrict__ coords, int64_t n, int32_t batch, int32_t sx, int32_t sy,
+                                 int32_t sz, int32_t hx, int32_t hy, int32_t hz, unsigned long long* __restrict__ keys,
+                                 int32_t* __restrict__ rows, int32_t* __restrict__ status) {
   int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= n) return;
   int4 c = coords[i];
-  keys[i] = ((static_cast<unsigned long long>(c.x) * hx + (c.y >> 1)) * hy + (c.z >> 1)) * hz + (c.w >> 1);
+  const bool inside = c.x >= 0 && c.x < batch && c.y >= 0 && c.y < sx && c.z >= 0 && c.z < sy && c.w >= 0 && c.w < sz;
+  if (!inside) {
+    if (status) atomicOr(status, HI3D_MAP_RANGE);
+    c = make_int4(0, 0, 0, 0);
+  }
+  const unsigned long long cell =
+      ((static_cast<unsigned long long>(c.x) * hx + (c.y >> 1)) * hy + (c.z >> 1)) * hz + (c.w >> 1);
+  keys[i] = cell * 8 + static_cast<unsigned long long>(((c.y & 1) << 2) | ((c.z & 1) << 1) | (c.w & 1));
   rows[i] = static_cast<int32_t>(i);
 }
 
+// heads[i] = 1 where sorted position i starts a coarse cell; equal neighbouring keys
+// (same cell and slot) are a repeated coordinate
 __global__ void run_heads_kernel(const unsigned long long* __restrict__ keys, int64_t n,
-                                 int32_t* __restrict__ heads) {
+                                 int32_t* __restrict__ heads, int32_t* __restrict__ status) {
   int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= n) return;
-  heads[i] = (i == 0 || keys[i] != keys[i - 1]) ? 1 : 0;
+  const unsigned long long k = keys[i];
+  const unsigned long long prev = i > 0 ? keys[i - 1] : ~k;
+  heads[i] = (i == 0 || (k >> 3) != (prev >> 3)) ? 1 : 0;
+  if (i > 0 && k == prev && status) atomicOr(status, HI3D_MAP_DUPLICATE);
 }
 
 // After the inclusive scan, ids[i] - 1 is the coarse row of sorted position i.
@@ -382,10 +398,10 @@ __global__ void coarse_emit_kernel(const unsigned long long* __restrict__ keys,
   inverse[r] = c;
   int4 f = coords[r];
   slot[r] = static_cast<uint8_t>(((f.y & 1) << 2) | ((f.z & 1) << 1) | (f.w & 1));
-  const bool head = (i == 0) || keys[i] != keys[i - 1];
-  const bool tail = (i == n - 1) || keys[i] != keys[i + 1];
+  const bool head = (i == 0) || (keys[i] >> 3) != (keys[i - 1] >> 3);
+  const bool tail = (i == n - 1) || (keys[i] >> 3) != (keys[i + 1] >> 3);
   if (head) {
-    unsigned long long k = keys[i];
+    unsigned long long k = keys[i] >> 3;
     int4 l;
     l.w = static_cast<int>(k % hz);
     k /= hz;
@@ -409,7 +425,7 @@ __global__ void coarse_counts_kernel(const int32_t* __restrict__ ids, int64_t n,
                                      int32_t* __restrict__ counts) {
   int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= n) return;
-  const bool head = (i == 0) || keys[i] != keys[i - 1];
+  const bool head = (i == 0) || (keys[i] >> 3) != (keys[i - 1] >> 3);
   if (head) {
     const int32_t c = ids[i] - 1;
     counts[c] = counts[c] - static_cast<int32_t>(i) + 1;  // tail - head + 1
@@ -561,36 +577,29 @@ int hi3d_kmap_workspace(int64_t n, int64_t capacity, int32_t key64, int64_t* byt
   return HI3D_OK;
 }
 
-int hi3d_kmap_subm(const int32_t* coords, int64_t n, int32_t sx, int32_t sy, int32_t sz,
-                   int32_t batch_size, int32_t ksize, int64_t capacity, void* workspace,
-                   int64_t workspace_bytes, int32_t* nbr, int32_t* counts, int32_t* status,
-                   void* stream_) {
-  hipStream_t stream = as_stream(stream_);
+// Argument checks shared by the hash-map entry points (clears counts and status).
+static int kmap_subm_begin(const int32_t* coords, int64_t n, int32_t sx, int32_t sy, int32_t sz, int32_t batch_size,
+                           int32_t ksize, int32_t* nbr, int32_t* counts, int32_t* status, hipStream_t stream) {
   HI3D_REQUIRE(n >= 0, "n must be non-negative");
   HI3D_REQUIRE(ksize >= 1 && ksize % 2 == 1 && ksize * ksize * ksize <= kMaxKvol,
                "ksize must be odd and at most 7, got %d", ksize);
   HI3D_REQUIRE(sx > 0 && sy > 0 && sz > 0 && batch_size > 0, "spatial_shape and batch_size must be positive");
   HI3D_REQUIRE(n < (int64_t(1) << 31) - 1, "at most 2^31-2 voxels");
-  HI3D_REQUIRE(counts && status && (n == 0 || (coords && nbr && workspace)), "null pointer argument");
+  HI3D_REQUIRE(counts && status && (n == 0 || (coords && nbr)), "null pointer argument");
   const int kvol = ksize * ksize * ksize;
   launch_fill<int32_t>(counts, kvol, 0, stream);
   launch_fill<int32_t>(status, 1, 0, stream);
-  if (n == 0) {
-    HI3D_LAUNCH_CHECK();
-    return HI3D_OK;
-  }
-  const uint64_t space = static_cast<uint64_t>(batch_size) * sx * sy * sz;
-  const bool key64 = space >= 0xFFFFFFFFull;
-  int64_t cap = capacity > 0 ? capacity : default_capacity(n);
-  int64_t need = 0;
-  int rc = hi3d_kmap_workspace(n, cap, key64, &need);
-  if (rc != HI3D_OK) return rc;
-  HI3D_REQUIRE(workspace_bytes >= need, "workspace too small: %lld < %lld bytes",
-               static_cast<long long>(workspace_bytes), static_cast<long long>(need));
-  Grid g{sx, sy, sz, batch_size};
+  HI3D_LAUNCH_CHECK();
+  return HI3D_OK;
+}
+
+// Hash build + probe over a table of `cap` slots at `table` (cap * 8 bytes of slots, then
+// for 64-bit keys cap * 4 bytes of rows at the next 256-byte boundary).
+static int kmap_subm_hash(const int32_t* coords, int64_t n, Grid g, int32_t ksize, bool key64, int64_t cap,
+                          char* table, int32_t* nbr, int32_t* counts, int32_t* status, hipStream_t stream) {
   const uint64_t mask = static_cast<uint64_t>(cap - 1);
-  auto* slots = static_cast<unsigned long long*>(workspace);
-  int32_t* vals = key64 ? reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + align_up(cap * 8, 256)) : nullptr;
+  auto* slots = reinterpret_cast<unsigned long long*>(table);
+  int32_t* vals = key64 ? reinterpret_cast<int32_t*>(table + align_up(cap * 8, 256)) : nullptr;
   launch_fill<unsigned long long>(slots, cap, kEmpty, stream);
   const unsigned blocks = static_cast<unsigned>(ceil_div(n, 256));
   const int4* c4 = reinterpret_cast<const int4*>(coords);
@@ -605,6 +614,26 @@ int hi3d_kmap_subm(const int32_t* coords, int64_t n, int32_t sx, int32_t sy, int
   }
   HI3D_LAUNCH_CHECK();
   return HI3D_OK;
+}
+
+int hi3d_kmap_subm(const int32_t* coords, int64_t n, int32_t sx, int32_t sy, int32_t sz,
+                   int32_t batch_size, int32_t ksize, int64_t capacity, void* workspace,
+                   int64_t workspace_bytes, int32_t* nbr, int32_t* counts, int32_t* status,
+                   void* stream_) {
+  hipStream_t stream = as_stream(stream_);
+  int rc = kmap_subm_begin(coords, n, sx, sy, sz, batch_size, ksize, nbr, counts, status, stream);
+  if (rc != HI3D_OK || n == 0) return rc;
+  HI3D_REQUIRE(workspace != nullptr, "null pointer argument");
+  const uint64_t space = static_cast<uint64_t>(batch_size) * sx * sy * sz;
+  const bool key64 = space >= 0xFFFFFFFFull;
+  int64_t cap = capacity > 0 ? capacity : default_capacity(n);
+  int64_t need = 0;
+  rc = hi3d_kmap_workspace(n, cap, key64, &need);
+  if (rc != HI3D_OK) return rc;
+  HI3D_REQUIRE(workspace_bytes >= need, "workspace too small: %lld < %lld bytes",
+               static_cast<long long>(workspace_bytes), static_cast<long long>(need));
+  return kmap_subm_hash(coords, n, Grid{sx, sy, sz, batch_size}, ksize, key64, cap, static_cast<char*>(workspace), nbr,
+                        counts, status, stream);
 }
 
 int hi3d_kmap_dense_workspace(int32_t batch_size, int32_t sx, int32_t sy, int32_t sz, int64_t* bytes) {
@@ -708,12 +737,14 @@ int hi3d_downsample_workspace(int64_t n, int64_t* bytes) {
 
 int hi3d_downsample_structure(const int32_t* coords, int64_t n, int32_t sx, int32_t sy, int32_t sz,
                               int32_t batch_size, void* workspace, int64_t workspace_bytes, int32_t* low,
-                              int32_t* inverse, int32_t* counts, uint8_t* slot, int64_t* n_low, void* stream_) {
+                              int32_t* inverse, int32_t* counts, uint8_t* slot, int64_t* n_low, int32_t* status,
+                              void* stream_) {
   hipStream_t stream = as_stream(stream_);
   int64_t need = 0;
   int rc = hi3d_downsample_workspace(n, &need);
   if (rc != HI3D_OK) return rc;
   HI3D_REQUIRE(n_low != nullptr, "n_low_dev is NULL");
+  if (status) launch_fill<int32_t>(status, 1, 0, stream);
   if (n == 0) {
     launch_fill<int64_t>(n_low, 1, 0, stream);
     HI3D_LAUNCH_CHECK();
@@ -733,16 +764,18 @@ int hi3d_downsample_structure(const int32_t* coords, int64_t n, int32_t sx, int3
   void* temp = ws.take<char>(static_cast<int64_t>(temp_bytes));
   const unsigned blocks = static_cast<unsigned>(ceil_div(n, 256));
   const int4* c4 = reinterpret_cast<const int4*>(coords);
-  hipLaunchKernelGGL(half_keys_kernel, dim3(blocks), dim3(256), 0, stream, c4, n, hx, hy, hz, k0, r0);
+  const uint64_t space = static_cast<uint64_t>(batch_size) * hx * hy * hz * 8;  // cells x slots
+  HI3D_REQUIRE(space < (uint64_t(1) << 62), "grid too large for 64-bit keys");
+  hipLaunchKernelGGL(half_keys_kernel, dim3(blocks), dim3(256), 0, stream, c4, n, batch_size, sx, sy, sz, hx, hy, hz,
+                     k0, r0, status);
   hipcub::DoubleBuffer<unsigned long long> kb(k0, k1);
   hipcub::DoubleBuffer<int32_t> vb(r0, r1);
-  const uint64_t space = static_cast<uint64_t>(batch_size) * hx * hy * hz;
   int end_bit = 1;
   while (end_bit < 64 && (1ull << end_bit) < space) ++end_bit;
   HI3D_HIP_CHECK(hipcub::DeviceRadixSort::SortPairs(temp, temp_bytes, kb, vb, static_cast<int>(n), 0, end_bit, stream));
   const unsigned long long* sk = kb.Current();
   const int32_t* sr = vb.Current();
-  hipLaunchKernelGGL(run_heads_kernel, dim3(blocks), dim3(256), 0, stream, sk, n, ids);
+  hipLaunchKernelGGL(run_heads_kernel, dim3(blocks), dim3(256), 0, stream, sk, n, ids, status);
   size_t scan_bytes = temp_bytes;
   HI3D_HIP_CHECK(hipcub::DeviceScan::InclusiveSum(temp, scan_bytes, ids, ids, static_cast<int>(n), stream));
   hipLaunchKernelGGL(coarse_emit_kernel, dim3(blocks), dim3(256), 0, stream, sk, sr, ids, n, hx, hy, hz, c4,

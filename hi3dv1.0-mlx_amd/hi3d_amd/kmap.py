@@ -331,7 +331,10 @@ class Stride2Structure:
 
 
 def stride2_structure(indices: torch.Tensor, spatial_shape: Sequence[int], batch_size: int | None = None) -> Stride2Structure:
-    """Coarse set, parent/slot maps and gather tables of a 2x2x2 stride-2 convolution."""
+    """Coarse set, parent/slot maps and gather tables of a 2x2x2 stride-2 convolution.
+    Raises ``ValueError`` for coordinates outside ``spatial_shape`` / ``batch_size`` and
+    for repeated coordinates (one host read of the device status word, taken with the
+    coarse row count)."""
     coords = _as_coords(indices)
     device = _lib.require_gpu(coords)
     n = int(coords.shape[0])
@@ -342,15 +345,20 @@ def stride2_structure(indices: torch.Tensor, spatial_shape: Sequence[int], batch
     inverse = torch.empty(n, dtype=torch.int32, device=device)
     counts = torch.empty(max(n, 1), dtype=torch.int32, device=device)
     slot = torch.empty(n, dtype=torch.uint8, device=device)
-    n_low_t = torch.empty(1, dtype=torch.int64, device=device)
+    n_low_t = torch.empty(2, dtype=torch.int64, device=device)  # coarse row count, then the status word
     ws = _lib.workspace(_lib.query("hi3d_downsample_workspace", n), device)
     stream = _lib.stream(device)
     _lib.call(
         "hi3d_downsample_structure",
         _lib.ptr(coords), n, sx, sy, sz, int(batch_size), _lib.ptr(ws), ws.numel(), _lib.ptr(low),
-        _lib.ptr(inverse), _lib.ptr(counts), _lib.ptr(slot), _lib.ptr(n_low_t), stream,
+        _lib.ptr(inverse), _lib.ptr(counts), _lib.ptr(slot), _lib.ptr(n_low_t), _lib.ptr(n_low_t[1:]), stream,
     )
-    n_low = int(n_low_t.item())
+    n_low, flags = (int(v) for v in n_low_t.tolist())
+    flags &= 0xFFFFFFFF
+    if flags & _lib.MAP_RANGE:
+        raise ValueError(f"coordinates outside spatial_shape {[sx, sy, sz]} or batch {batch_size}")
+    if flags & _lib.MAP_DUPLICATE:
+        raise ValueError("duplicate coordinates: every active voxel must appear once")
     low, counts = low[:n_low], counts[:n_low]
     down = torch.empty((n_low, 8), dtype=torch.int32, device=device)
     up = torch.empty((n, 8), dtype=torch.int32, device=device)

@@ -25,6 +25,10 @@ from . import kmap as _kmap
 from .kernels import gather_group_norm_swish, group_norm_swish
 from .sparse import Level, child_neighbour_table
 
+SKIP_POINTS = 12_000_000
+"""Residual blocks over more rows than this return their input unchanged: upstream's
+``_RESNET_SKIP_POINTS``, kept by the reference (vae.py:29-30,209-210)."""
+
 __all__ = ["groups_for", "group_stats", "group_norm_swish", "gather_group_norm_swish", "conv_gn_swish", "resnet",
            "child_plan", "children", "occupancy", "upsample"]
 
@@ -64,8 +68,16 @@ def conv_gn_swish(x: torch.Tensor, level: Level, norm_weight: torch.Tensor, norm
                   residual: torch.Tensor | list | None = None, eps: float = 1e-6) -> torch.Tensor:
     """``conv(swish(GroupNorm(x))) + bias`` (+ ``residual``) over ``level``'s map
     (vae.py:166-192). ``weight_t [27 * Cin, Cout]``; the activation is rounded to the
-    weight dtype, the convolution accumulates in fp32 and adds ``bias`` in fp32; the
-    result is in ``out`` (default: fp32 for fp32 weights, else the weight dtype).
+    weight dtype and the convolution accumulates in fp32; the result is in ``out``
+    (default: fp32 for fp32 weights, else the weight dtype).
+
+    Bias rounding: when ``out`` differs from the weight dtype the accumulator is rounded
+    to the weight dtype, the fp32 bias added in fp32 and the sum rounded to ``out``, as
+    the reference computes ``((g @ w).astype(F32) + bias).astype(out)``. When ``out`` is
+    the weight dtype the epilogue adds the bias (rounded to that dtype) to the fp32
+    accumulator and rounds once, which skips the reference's intermediate rounding: the
+    two differ by at most about one unit in the last place of ``out``, inside the
+    1e-2-of-RMS gate the parity tests apply.
 
     ``residual`` as a one-element list holding ``r`` (the reference's donation idiom)
     returns ``r + conv(...)`` written into ``r``'s own buffer: the convolution's rounded
@@ -101,11 +113,13 @@ def conv_gn_swish(x: torch.Tensor, level: Level, norm_weight: torch.Tensor, norm
     return y if donated is None else donated.copy_(y)
 
 
-def resnet(x: torch.Tensor | list, level: Level, params: dict, name: str, eps: float = 1e-6) -> torch.Tensor:
+def resnet(x: torch.Tensor | list, level: Level, params: dict, name: str, eps: float = 1e-6,
+           skip_points: int = SKIP_POINTS) -> torch.Tensor:
     """``shortcut + conv(swish(GN(conv(swish(GN(x))))))`` (vae.py:200-218) with the
     reference's parameter names: ``{name}.block.0`` / ``.block.3`` GroupNorm
     (``.weights``, ``.bias``), ``.block.2`` / ``.block.5`` convolutions (``.weight``
-    ``[27 Cin, Cout]``, ``.bias``) and an optional ``{name}.res_conv`` linear.
+    ``[27 Cin, Cout]``, ``.bias``) and an optional ``{name}.res_conv`` linear. Levels of
+    more than ``skip_points`` rows return the input unchanged, as upstream does.
 
     ``x`` may be a one-element list holding the input (the reference's holder): with an
     identity shortcut the second convolution then accumulates into the input's buffer,
@@ -116,6 +130,8 @@ def resnet(x: torch.Tensor | list, level: Level, params: dict, name: str, eps: f
         if len(holder) != 1:
             raise ValueError("input holder must hold exactly one tensor")
         x = holder.pop()
+    if int(x.shape[0]) > skip_points:
+        return x
     h = conv_gn_swish(x, level, p[f"{name}.block.0.weights"], p[f"{name}.block.0.bias"],
                       p[f"{name}.block.2.weight"], p[f"{name}.block.2.bias"], eps=eps)
     if f"{name}.res_conv.weight" in p:

@@ -80,19 +80,28 @@ def gemm(
     return_acc: bool = False,
 ):
     """Int8 GEMM with fused dequant: ``fp16(((float)acc * sa) * sw + bias)``; with
-    ``return_acc`` also the int32 accumulators."""
+    ``return_acc`` also the int32 accumulators. ``q [M, K]`` and ``w [N, K]`` int8,
+    ``sa [M]`` and ``sw [N]`` float32, ``bias [N]`` (cast to fp16) or None."""
     device = _lib.require_gpu(q, sa, w, sw, bias)
+    if q.dtype != torch.int8 or w.dtype != torch.int8 or q.ndim != 2 or w.ndim != 2 or int(w.shape[1]) != int(q.shape[1]):
+        raise ValueError("q [M, K] and w [N, K] must be int8 with matching K")
     m, k = int(q.shape[0]), int(q.shape[1])
     n = int(w.shape[0])
-    if q.dtype != torch.int8 or w.dtype != torch.int8 or int(w.shape[1]) != k:
-        raise ValueError("q [M, K] and w [N, K] must be int8 with matching K")
+    if sa.dtype != torch.float32 or sw.dtype != torch.float32:
+        raise ValueError("W8A8 requires float32 scales")
+    if tuple(sa.shape) != (m,) or tuple(sw.shape) != (n,):
+        raise ValueError(f"scales must be sa [{m}] and sw [{n}], got {tuple(sa.shape)} and {tuple(sw.shape)}")
+    if bias is not None and tuple(bias.shape) != (n,):
+        raise ValueError(f"bias must be [{n}], got {tuple(bias.shape)}")
+    # contiguous operands bound to locals, so every buffer outlives the launch
+    qc, sac, wc, swc = q.contiguous(), sa.contiguous(), w.contiguous(), sw.contiguous()
+    b = None if bias is None else bias.to(torch.float16).contiguous()
     out = torch.empty((m, n), dtype=torch.float16, device=device)
     acc = torch.empty((m, n), dtype=torch.int32, device=device) if return_acc else None
-    b = None if bias is None else bias.to(torch.float16).contiguous()
     _lib.call(
         "hi3d_w8a8_gemm",
-        _lib.ptr(q.contiguous()), _lib.ptr(sa.contiguous()), _lib.ptr(w.contiguous()), _lib.ptr(sw.contiguous()),
-        _lib.ptr(b), m, n, k, _lib.ptr(out), _lib.ptr(acc), _lib.stream(device),
+        _lib.ptr(qc), _lib.ptr(sac), _lib.ptr(wc), _lib.ptr(swc), _lib.ptr(b), m, n, k, _lib.ptr(out), _lib.ptr(acc),
+        _lib.stream(device),
     )
     return (out, acc) if return_acc else out
 

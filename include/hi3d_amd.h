@@ -106,13 +106,16 @@ int hi3d_downsample_workspace(int64_t n, int64_t* bytes_host);
  * (lexicographic), inverse[i] = coarse row of fine row i, counts[c] = children of c,
  * slot[i] = (x&1)*4 + (y&1)*2 + (z&1). n_low_dev receives the coarse row count (int64).
  * low_dev must hold n rows of 4 int32 (only the first n_low are written); counts_dev n.
+ * status_dev (one int32, may be NULL) is cleared, then receives HI3D_MAP_RANGE for a
+ * coordinate outside [0, batch_size) x [0, sx) x [0, sy) x [0, sz) and
+ * HI3D_MAP_DUPLICATE for a repeated coordinate; the outputs are then meaningless.
  * Replaces: downsample_structure (src/hi3d_mac/mlx_backend/sparse.py:217-233) and the
  * coordinate part of SparseDownsample (src/sparc3d/nn/sparse/spatial.py:34-63). */
 int hi3d_downsample_structure(const int32_t* coords_dev, int64_t n, int32_t sx, int32_t sy,
                               int32_t sz, int32_t batch_size, void* workspace_dev,
                               int64_t workspace_bytes, int32_t* low_dev, int32_t* inverse_dev,
                               int32_t* counts_dev, uint8_t* slot_dev, int64_t* n_low_dev,
-                              void* stream);
+                              int32_t* status_dev, void* stream);
 
 /* Gather tables of the strided pair: down_dev [n_low, 8] = fine row of child slot s of
  * each coarse voxel (sentinel n), up_dev [n, 8] = coarse parent in column slot[i] and

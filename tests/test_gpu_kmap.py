@@ -86,6 +86,31 @@ def test_errors_duplicate_range_overflow(cuda):
         kmap.build_kernel_map(torch.as_tensor(idx).to(cuda), [8, 8, 8], capacity=64)
 
 
+def test_stride2_structure_errors(cuda):
+    """The stride-2 structure raises the submanifold map's errors: a coordinate outside
+    spatial_shape (also negative, or a batch index past batch_size) and a repeated
+    coordinate, including through get_indice_pairs with a caller's spatial_shape; a
+    valid set after a failing call is unaffected (the status word is cleared)."""
+    from hi3d_amd import kmap, spconv
+
+    dup = np.array([[0, 1, 1, 1], [0, 2, 2, 2], [0, 1, 1, 1], [0, 3, 3, 3]], np.int32)
+    with pytest.raises(ValueError, match="duplicate"):
+        kmap.stride2_structure(torch.as_tensor(dup).to(cuda), [4, 4, 4])
+    for bad in ([0, 4, 2, 2], [0, 1, -1, 2], [0, 1, 2, 5], [1, 1, 1, 1]):
+        idx = np.array([[0, 1, 1, 1], bad], np.int32)
+        with pytest.raises(ValueError, match="outside"):
+            kmap.stride2_structure(torch.as_tensor(idx).to(cuda), [4, 4, 5], 1)
+    idx = np.array([[0, 1, 1, 1], [0, 7, 2, 2]], np.int32)
+    with pytest.raises(ValueError, match="outside"):
+        spconv.get_indice_pairs(torch.as_tensor(idx).to(cuda), 1, [4, 4, 4], spconv.ConvAlgo.Native, (2, 2, 2),
+                                (2, 2, 2), (0, 0, 0), (1, 1, 1), (0, 0, 0), False, False)
+    ok = np.array([[0, 1, 1, 1], [0, 0, 1, 1], [0, 3, 2, 2]], np.int32)
+    s = kmap.stride2_structure(torch.as_tensor(ok).to(cuda), [4, 4, 4])
+    assert s.low.cpu().tolist() == [[0, 0, 0, 0], [0, 1, 1, 1]]
+    assert s.inverse.cpu().tolist() == [0, 0, 1] and s.counts.cpu().tolist() == [2, 1]
+    assert s.slot.cpu().tolist() == [7, 3, 4]
+
+
 def test_empty_and_single(cuda):
     from hi3d_amd import kmap
 

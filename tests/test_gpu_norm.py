@@ -70,6 +70,19 @@ def test_adaln_projection(cuda):
         rs, rh = onorm.adaln_projection(w, b, cond, silu)
         np.testing.assert_allclose(s1p.float().cpu().numpy(), rs.astype(np.float32), atol=2e-3, rtol=1e-3)
         np.testing.assert_allclose(sh.float().cpu().numpy(), rh.astype(np.float32), atol=2e-3, rtol=1e-3)
+    # closed forms: W = 0, b = [s; t] gives exactly (fp16(1 + s), fp16(t)); W = [0; I]
+    # gives (1, fp16(cond)) whatever the summation order
+    s = np.linspace(-2, 2, 256).astype(np.float32)
+    t = np.linspace(3, -1, 256).astype(np.float32)
+    s1p, sh = kernels.adaln_projection(torch.zeros((512, 1024), device=cuda), torch.as_tensor(np.concatenate([s, t])).to(cuda),
+                                       torch.as_tensor(cond).to(cuda))
+    assert np.array_equal(s1p.cpu().numpy(), (1 + s.astype(np.float16).astype(np.float32)).astype(np.float16))
+    assert np.array_equal(sh.cpu().numpy(), t.astype(np.float16))
+    eye = np.zeros((512, 256), np.float32)
+    eye[256:] = np.eye(256)
+    s1p, sh = kernels.adaln_projection(torch.as_tensor(eye).to(cuda), None, torch.as_tensor(cond[:256]).to(cuda))
+    assert np.array_equal(s1p.cpu().numpy(), np.ones(256, np.float16))
+    assert np.array_equal(sh.cpu().numpy(), cond[:256].astype(np.float16))
 
 
 def _block_weights(rng, c, d, cuda):

@@ -128,6 +128,13 @@ def test_resnet_matches_float64(cuda, with_res_conv):
     got = vae.resnet(torch.as_tensor(x).to(cuda), level, gp, "r").cpu().numpy()
     ref = ovae.resnet_f64(x, table, p, "r")
     assert oconv.rel_err(got, ref) <= 1e-4
+    # above skip_points rows the block returns its input itself (upstream's skip), also
+    # from a holder, which it empties
+    xt = torch.as_tensor(x).to(cuda)
+    assert vae.resnet(xt, level, gp, "r", skip_points=len(coords) - 1) is xt
+    holder = [xt]
+    assert vae.resnet(holder, level, gp, "r", skip_points=len(coords) - 1) is xt and holder == []
+    assert vae.SKIP_POINTS == 12_000_000
 
 
 GATE = {torch.float32: 1e-5, torch.float16: 1e-2, torch.bfloat16: 3e-2}

@@ -159,6 +159,69 @@ def test_workload4_shapes_sampled(cuda):
             assert err < 0.15
 
 
+def test_workload4_every_row_accumulators_bit_exact(cuda):
+    """Both workload shapes, [65536, 1024] x [4096, 1024]^T and [65536, 4096] x
+    [1024, 4096]^T, on the codes of the outlier-laden activations and the quantised
+    weights: every int32 accumulator equals the float64 product of the codes (exact:
+    |acc| <= 127^2 * 4096 < 2^53), and every fp16 output equals the unfused float32
+    epilogue of those accumulators. Shape A runs the persistent kernel (K = 1024), shape
+    B the one-tile kernel (K = 4096); the accumulator dump comes from the same kernel
+    as the fp16 output, whose bits must not change with it."""
+    from hi3d_amd import w8a8
+
+    for m, k, n in ((65536, 1024, 4096), (65536, 4096, 1024)):
+        g = torch.Generator(device=cuda).manual_seed(k)
+        x = torch.randn((m, k), device=cuda, generator=g)
+        x = torch.where(torch.rand((m, k), device=cuda, generator=g) < 0.01, x * 20, x).half()
+        wf = (torch.randn((n, k), device=cuda, generator=g) / 32).half()
+        bias = (torch.randn(n, device=cuda, generator=g) * 0.02).half()
+        wq, sw = w8a8.quantize_weight(wf)
+        q, sa = w8a8.quantize_activation(x)
+        del x, wf
+        plain = w8a8.gemm(q, sa, wq, sw, bias)
+        out, acc = w8a8.gemm(q, sa, wq, sw, bias, return_acc=True)
+        assert torch.equal(plain, out)
+        del plain
+        wd = torch.as_tensor(wq.cpu().numpy().astype(np.float64))
+        swn, bn = sw.cpu().numpy(), bias.cpu().numpy()
+        for r0 in range(0, m, 8192):
+            qd = torch.as_tensor(q[r0:r0 + 8192].cpu().numpy().astype(np.float64))
+            ref = (qd @ wd.T).numpy().astype(np.int64)
+            got = acc[r0:r0 + 8192].cpu().numpy()
+            assert np.array_equal(got.astype(np.int64), ref), (m, k, n, r0)
+            want = ow8a8.epilogue(ref.astype(np.int32), sa[r0:r0 + 8192].cpu().numpy(), swn, bn)
+            assert np.array_equal(out[r0:r0 + 8192].cpu().numpy(), want), (m, k, n, r0)
+        del out, acc
+
+
+def test_gemm_non_contiguous_operands_and_scale_checks(cuda):
+    """A transposed weight and a column-sliced activation give the bits of their
+    contiguous copies; float16 or short scale vectors and a short bias are refused
+    before any launch."""
+    from hi3d_amd import w8a8
+
+    rng = np.random.default_rng(31)
+    m, n, k = 1000, 520, 320
+    q_wide = torch.as_tensor(rng.integers(-127, 128, size=(m, k + 64), dtype=np.int8)).to(cuda)
+    w_t = torch.as_tensor(rng.integers(-127, 128, size=(k, n), dtype=np.int8)).to(cuda)
+    sa = torch.as_tensor(rng.uniform(1e-3, 1e-2, m).astype(np.float32)).to(cuda)
+    sw = torch.as_tensor(rng.uniform(1e-4, 1e-3, n).astype(np.float32)).to(cuda)
+    bias = torch.as_tensor(rng.normal(0, 0.02, n).astype(np.float16)).to(cuda)
+    q, w = q_wide[:, 32:32 + k], w_t.T
+    assert not q.is_contiguous() and not w.is_contiguous()
+    got, acc = w8a8.gemm(q, sa, w, sw, bias, return_acc=True)
+    want, acc_want = w8a8.gemm(q.contiguous(), sa, w.contiguous(), sw, bias, return_acc=True)
+    assert torch.equal(got, want) and torch.equal(acc, acc_want)
+    ref = q.cpu().numpy().astype(np.float64) @ w.cpu().numpy().astype(np.float64).T
+    assert np.array_equal(acc.cpu().numpy().astype(np.int64), ref.astype(np.int64))
+    with pytest.raises(ValueError, match="float32 scales"):
+        w8a8.gemm(q, sa.half(), w, sw, bias)
+    with pytest.raises(ValueError, match="scales must be"):
+        w8a8.gemm(q, sa, w, sw[:-1], bias)
+    with pytest.raises(ValueError, match="bias must be"):
+        w8a8.gemm(q, sa, w, sw, bias[:-1])
+
+
 @pytest.mark.parametrize("m,n,k,with_bias", [(1000, 520, 320, True), (4096, 4096, 1024, True), (300, 264, 1984, False),
                                              (256, 256, 256, True), (2600, 1032, 1536, True), (1000, 520, 4096, True),
                                              (600, 300, 2112, False)])
