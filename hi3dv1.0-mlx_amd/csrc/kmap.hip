@@ -19,6 +19,7 @@
 #include <algorithm>
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 
 #include "common.h"
 
@@ -557,6 +558,37 @@ __global__ void child_table_kernel(const int32_t* __restrict__ parent_table, con
   table[j] = lookup[static_cast<int64_t>(np) * 8 + t.ss[s][k]];
 }
 
+// Hash table of hi3d_kmap_subm_noalloc: a device array of this library, one copy per GPU,
+// held until the process ends. Host code never passes its name to a kernel (that is a
+// host-side stand-in); it passes the address hipGetSymbolAddress returns for the
+// current device.
+static __device__ __align__(256) unsigned long long scratch[HI3D_KMAP_NOALLOC_BYTES / 8];
+
+// Largest sets it takes: capacity (a power of two >= 2N) times 8 bytes (32-bit keys)
+// or 8 + 4 bytes (64-bit keys) within the array.
+constexpr int64_t kNoAllocMax32 = HI3D_KMAP_NOALLOC_BYTES / 8 / 2;
+constexpr int64_t kNoAllocMax64 = HI3D_KMAP_NOALLOC_BYTES / 16 / 2;
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+char* g_scratch[kMaxDevices] = {};
+
+// Address of the current device's copy of `scratch` (looked up once per device).
+int scratch_address(char** out) {
+  int dev = -1;
+  HI3D_HIP_CHECK(hipGetDevice(&dev));
+  HI3D_REQUIRE(dev >= 0 && dev < kMaxDevices, "device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch[dev] == nullptr) {
+    void* p = nullptr;
+    HI3D_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    HI3D_REQUIRE(p != nullptr && (reinterpret_cast<uintptr_t>(p) & 255) == 0, "scratch symbol has no usable address");
+    g_scratch[dev] = static_cast<char*>(p);
+  }
+  *out = g_scratch[dev];
+  return HI3D_OK;
+}
+
 }  // namespace
 }  // namespace hi3d
 
@@ -634,6 +666,30 @@ int hi3d_kmap_subm(const int32_t* coords, int64_t n, int32_t sx, int32_t sy, int
                static_cast<long long>(workspace_bytes), static_cast<long long>(need));
   return kmap_subm_hash(coords, n, Grid{sx, sy, sz, batch_size}, ksize, key64, cap, static_cast<char*>(workspace), nbr,
                         counts, status, stream);
+}
+
+// The same map with the hash table in `scratch`, a device array of this library (no
+// allocation, no workspace). Every call on a GPU reuses that GPU's copy: calls that
+// overlap on one GPU (two streams, two host threads) race on it.
+int hi3d_kmap_subm_noalloc(const int32_t* coords, int64_t n, int32_t sx, int32_t sy, int32_t sz, int32_t batch_size,
+                           int32_t ksize, int32_t* nbr, int32_t* counts, int32_t* status, void* stream_) {
+  hipStream_t stream = as_stream(stream_);
+  int rc = kmap_subm_begin(coords, n, sx, sy, sz, batch_size, ksize, nbr, counts, status, stream);
+  if (rc != HI3D_OK || n == 0) return rc;
+  const uint64_t space = static_cast<uint64_t>(batch_size) * sx * sy * sz;
+  const bool key64 = space >= 0xFFFFFFFFull;
+  const int64_t cap = default_capacity(n);
+  const int64_t need = key64 ? align_up(cap * 8, 256) + cap * 4 : cap * 8;  // slots (+ rows)
+  HI3D_REQUIRE(need <= HI3D_KMAP_NOALLOC_BYTES,
+               "%lld voxels need a %lld-byte hash table; the allocation-free map holds at most %lld bytes (%s keys: up "
+               "to %lld voxels)",
+               static_cast<long long>(n), static_cast<long long>(need), static_cast<long long>(HI3D_KMAP_NOALLOC_BYTES),
+               key64 ? "64-bit" : "32-bit", static_cast<long long>(key64 ? kNoAllocMax64 : kNoAllocMax32));
+  char* table = nullptr;
+  rc = scratch_address(&table);
+  if (rc != HI3D_OK) return rc;
+  return kmap_subm_hash(coords, n, Grid{sx, sy, sz, batch_size}, ksize, key64, cap, table, nbr, counts, status,
+                        stream);
 }
 
 int hi3d_kmap_dense_workspace(int32_t batch_size, int32_t sx, int32_t sy, int32_t sz, int64_t* bytes) {

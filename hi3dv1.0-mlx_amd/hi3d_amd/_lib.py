@@ -34,6 +34,7 @@ _SIGNATURES = {
     "hi3d_version": [],
     "hi3d_kmap_workspace": [_i64, _i64, _i32, _p],
     "hi3d_kmap_subm": [_p, _i64, _i32, _i32, _i32, _i32, _i32, _i64, _p, _i64, _p, _p, _p, _p],
+    "hi3d_kmap_subm_noalloc": [_p, _i64, _i32, _i32, _i32, _i32, _i32, _p, _p, _p, _p],
     "hi3d_kmap_pairs_workspace": [_i64, _i32, _p],
     "hi3d_kmap_pairs": [_p, _i64, _i32, _p, _i64, _p, _p, _p, _p],
     "hi3d_downsample_workspace": [_i64, _p],

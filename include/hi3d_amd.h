@@ -72,6 +72,22 @@ int hi3d_kmap_subm(const int32_t* coords_dev, int64_t n, int32_t sx, int32_t sy,
                    int64_t workspace_bytes, int32_t* nbr_dev, int32_t* counts_dev,
                    int32_t* status_dev, void* stream);
 
+/* Bytes of the device array that holds hi3d_kmap_subm_noalloc's hash table (one copy
+ * per GPU the library runs on, held until the process ends). */
+#define HI3D_KMAP_NOALLOC_BYTES (128ll << 20)
+
+/* hi3d_kmap_subm without allocation or workspace: the same table, counts and status
+ * (identical for every coordinate set), with the hash table in a fixed device array of
+ * HI3D_KMAP_NOALLOC_BYTES. No counterpart in the reference: for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc). Takes up to 2^23 voxels with 32-bit keys and 2^22 with 64-bit
+ * keys (batch*sx*sy*sz >= 2^32 - 1); larger sets return HI3D_ERR_INVALID before any
+ * launch. Every call on a GPU reuses that GPU's array, so calls that overlap on one GPU
+ * (two streams or two host threads) race. */
+int hi3d_kmap_subm_noalloc(const int32_t* coords_dev, int64_t n, int32_t sx, int32_t sy, int32_t sz,
+                           int32_t batch_size, int32_t ksize, int32_t* nbr_dev, int32_t* counts_dev,
+                           int32_t* status_dev, void* stream);
+
 /* Workspace bytes of hi3d_kmap_subm_dense: one int32 cell per grid position
  * (batch_size*sx*sy*sz <= 2^31). */
 int hi3d_kmap_dense_workspace(int32_t batch_size, int32_t sx, int32_t sy, int32_t sz, int64_t* bytes_host);
