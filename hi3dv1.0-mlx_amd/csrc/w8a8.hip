@@ -783,6 +783,297 @@ __global__ __launch_bounds__(256, 1) void w8a8_gemm_persistent_kernel(
   stage(G - 1, M4{});
 }
 
+// ---------------------------------------------------------- ping-pong GEMM --
+// 256 x 256 tiles, 8 waves in two groups of four. Group g holds tokens 128 g .. +127;
+// wave q of a group holds channels 64 q .. +63 (2 x 4 blocks of v_mfma_i32_32x32x32_i8,
+// 128 accumulator registers), so two waves share each SIMD. The groups alternate: in
+// phase A of stage s group 0 multiplies stage s while group 1 issues its share of the
+// loads of stage s + 3 and reads its fragments of stage s; in phase B group 1 multiplies
+// while group 0 issues its loads and reads its fragments of stage s + 1. One barrier
+// ends each phase, so each SIMD always has one wave with a full phase of MFMAs (16, 512
+// cycles) queued while the other one feeds LDS: loads and matrix work overlap by
+// construction instead of by the interleaving of one wave's instruction stream.
+//  * Ring: 4 stages of 64 bytes of K (256 token rows + 256 channel rows, 32 KB), rows in
+//    the 64-byte rotated layout (chunk c of row r at c ^ ((r >> 2) & 3)). Each wave loads
+//    16 rows of tokens and 16 rows of channels per 8 KB half (4 direct-to-LDS loads per
+//    stage); a stage's loads are issued three stages ahead (group 1 in phase A, group 0
+//    in phase B of stage s - 3) into the slot of stage s - 1, which both groups finished
+//    reading before the barrier that opens phase A(s).
+//  * Waits: before the barrier that ends phase A(s), each wave waits for its loads of
+//    stage s + 1 (group 1 has the loads of s + 2 and s + 3 behind them, group 0 those of
+//    s + 2), so stage s + 1 is complete when group 0 reads it in phase B(s).
+//  * Epilogue: each wave converts its accumulators in registers (the reference's
+//    fp16(((float)acc * sa) * sw + bias), no contraction) into an fp16 tile in LDS, then
+//    every thread stores whole 16-byte row chunks (512-byte rows, coalesced).
+//  * Tile order: the chip deals workgroups round-robin over its 8 XCDs; XCD x takes
+//    channel-tile group x % G and token part x / G, channel tiles innermost, so the
+//    channel rows of its group stay in its L2 and the tiles sharing a token block run
+//    together (G chosen on the host from the operand sizes).
+constexpr int kPPStage = 32768, kPPHalf = 16384, kPPRing = 4;
+constexpr int kRawBufferFlags = 0x00020000;  // buffer descriptor word 3 for raw byte loads
+
+__device__ __forceinline__ __attribute__((address_space(3))) void* lds_ptr(char* p) {
+  return (__attribute__((address_space(3))) void*)(p);
+}
+
+template <bool kDump>
+__global__ __launch_bounds__(512, 1) void w8a8_gemm_pp_kernel(const int8_t* __restrict__ qa, const float* __restrict__ sa,
+                                                              const int8_t* __restrict__ w, const float* __restrict__ sw,
+                                                              const _Float16* __restrict__ bias, int64_t m, int n, int k,
+                                                              _Float16* __restrict__ out, int32_t* __restrict__ acc_out,
+                                                              int64_t mt_count, int nt_count, int groups) {
+#pragma clang fp contract(off)
+  __shared__ __attribute__((aligned(16))) char smem[kPPRing * kPPStage + 256 * 4 * 2 + 256 * 2];
+  float* const s_sa = reinterpret_cast<float*>(smem + kPPRing * kPPStage);
+  float* const s_sw = s_sa + 256;
+  _Float16* const s_bias = reinterpret_cast<_Float16*>(s_sw + 256);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = wave >> 2, q = wave & 3;
+
+  // this block's tile
+  const int xcd = static_cast<int>(blockIdx.x & 7);
+  const int64_t local = blockIdx.x >> 3;
+  const int parts = 8 / groups;
+  const int cg = xcd % groups, part = xcd / groups;
+  const int cpg = (nt_count + groups - 1) / groups;
+  const int64_t mpp = (mt_count + parts - 1) / parts;
+  const int nt_lo = cg * cpg, nt_hi = nt_count < nt_lo + cpg ? nt_count : nt_lo + cpg;
+  const int ntg = nt_hi - nt_lo;
+  const int64_t mt_lo = part * mpp, mt_hi = mt_count < mt_lo + mpp ? mt_count : mt_lo + mpp;
+  if (ntg <= 0) return;
+  const int64_t mt = mt_lo + local / ntg;
+  if (mt >= mt_hi) return;
+  const int64_t m0 = mt * 256;
+  const int n0 = (nt_lo + static_cast<int>(local % ntg)) * 256;
+
+  // scales and bias of the tile (older than every ring load, so complete at the first wait)
+  {
+    const int64_t ra = m0 + (wave & 3) * 64 + lane;
+    const int cb = n0 + (wave & 3) * 64 + lane;
+    if (wave < 4) lds_dma4(sa + (ra < m ? ra : m - 1), reinterpret_cast<char*>(s_sa) + (wave & 3) * 256);
+    else lds_dma4(sw + (cb < n ? cb : n - 1), reinterpret_cast<char*>(s_sw) + (wave & 3) * 256);
+    if (wave < 2) {
+      const int d = n0 / 2 + wave * 64 + lane;  // bias dword: channels 2 d, 2 d + 1 (n is even)
+      const uint32_t* b32 = bias != nullptr ? reinterpret_cast<const uint32_t*>(bias) + (d < n / 2 ? d : n / 2 - 1)
+                                            : g_zero_bias + ((wave * 64 + lane) & 127);
+      lds_dma4(b32, reinterpret_cast<char*>(s_bias) + wave * 256);
+    }
+  }
+
+  // This wave's 4 loads per stage: token rows and channel rows 128 g + (2 q + j) * 16 +
+  // lane / 4, through buffer descriptors of the tile's rows (rows past the matrix read
+  // zeros), with the stage's K offset as the scalar offset: no vector arithmetic per load.
+  const int rows_a = m - m0 < 256 ? static_cast<int>(m - m0) : 256;
+  const int rows_b = n - n0 < 256 ? n - n0 : 256;
+  const __amdgpu_buffer_rsrc_t ra = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(qa + m0 * k), 0, rows_a * k,
+                                                                      kRawBufferFlags);
+  const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<int8_t*>(w + static_cast<int64_t>(n0) * k), 0, rows_b * k, kRawBufferFlags);
+  const int c16 = ((lane & 3) ^ ((lane >> 4) & 3)) * 16;
+  int vo[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) vo[j] = (128 * g + (2 * q + j) * 16 + (lane >> 2)) * k + c16;
+  auto issue = [&](int s, auto slc) {
+    constexpr int SL = decltype(slc)::value;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, lds_ptr(smem + SL * kPPStage + (8 * g + 2 * q + j) * 1024), 16,
+                                               vo[j], s * 64, 0, 0);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, lds_ptr(smem + SL * kPPStage + kPPHalf + (8 * g + 2 * q + j) * 1024),
+                                               16, vo[j], s * 64, 0, 0);
+  };
+
+  // fragment reads: per-lane bases for each K-group (slots 0-1 and 2-3, so that the
+  // slot and block parts of every address are immediate offsets)
+  u32x4 fw[2][2], fq[2][4];  // [K-group][channel block] / [K-group][token block]
+  const char* bw[2][2];
+  const char* bq[2][2];
+#pragma unroll
+  for (int G = 0; G < 2; ++G) {
+    const int c = 2 * G + (lane >> 5);
+    bw[G][0] = smem + kPPHalf + lds_off64(64 * q + (lane & 31), c);
+    bq[G][0] = smem + lds_off64(128 * g + (lane & 31), c);
+    bw[G][1] = bw[G][0] + 2 * kPPStage;
+    bq[G][1] = bq[G][0] + 2 * kPPStage;
+  }
+  auto read_frags = [&](auto slc) {
+    constexpr int SL = decltype(slc)::value;
+#pragma unroll
+    for (int G = 0; G < 2; ++G) {
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb)
+        fw[G][nb] = *reinterpret_cast<const u32x4*>(bw[G][SL >> 1] + (SL & 1) * kPPStage + nb * 2048);
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb)
+        fq[G][mb] = *reinterpret_cast<const u32x4*>(bq[G][SL >> 1] + (SL & 1) * kPPStage + mb * 2048);
+    }
+  };
+  i32x16 acc[2][4];
+#pragma unroll
+  for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[nb][mb][v] = 0;
+  auto compute = [&]() {
+    wait_lgkm0();
+    __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int G = 0; G < 2; ++G)
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb)
+          acc[nb][mb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, fw[G][nb]),
+                                                            __builtin_bit_cast(i32x4, fq[G][mb]), acc[nb][mb], 0, 0, 0);
+    __builtin_amdgcn_s_setprio(0);
+  };
+  auto wait_after = [&](int after) {
+    if (after == 8) wait_vmcnt<8>();
+    else if (after == 4) wait_vmcnt<4>();
+    else wait_vmcnt<0>();
+  };
+  using SL0 = std::integral_constant<int, 0>;
+  using SL1 = std::integral_constant<int, 1>;
+  using SL2 = std::integral_constant<int, 2>;
+  using SL3 = std::integral_constant<int, 3>;
+
+  // Prologue: stages 0 and 1 from both groups, stage 2 from group 1 (group 0 issues its
+  // share in phase -1, where it also reads the fragments of stage 0); stage 0 complete.
+  const int S = k >> 6;  // a multiple of 4
+  issue(0, SL0{});
+  issue(1, SL1{});
+  if (g == 1) {
+    issue(2, SL2{});
+    wait_vmcnt<8>();
+  } else {
+    wait_vmcnt<4>();
+  }
+  raw_barrier();
+  if (g == 0) {
+    issue(2, SL2{});
+    read_frags(SL0{});
+  }
+  raw_barrier();
+
+  // Stage s is two phases: A(s), group 0 multiplies while group 1 prepares (its loads of
+  // stage s + 3, its fragments of stage s), and B(s), group 1 multiplies while group 0
+  // prepares (loads of s + 3, fragments of s + 1). Each group runs its own straight-line
+  // loop, four stages (one per ring slot) per iteration; both pass the same two barriers
+  // per stage. Past the last stage the fragment reads read a stale slot nothing multiplies.
+  auto g0_stage = [&](int s, auto slc) {
+    constexpr int SL = decltype(slc)::value;
+    __builtin_amdgcn_sched_barrier(0);
+    compute();  // A(s)
+    __builtin_amdgcn_sched_barrier(0);
+    if (s + 1 < S) wait_after(s + 2 < S ? 4 : 0);  // own loads of stage s + 1 landed
+    raw_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    if (s + 3 < S) issue(s + 3, std::integral_constant<int, (SL + 3) & 3>{});  // B(s)
+    read_frags(std::integral_constant<int, (SL + 1) & 3>{});
+    __builtin_amdgcn_sched_barrier(0);
+    raw_barrier();
+  };
+  auto g1_stage = [&](int s, auto slc) {
+    constexpr int SL = decltype(slc)::value;
+    __builtin_amdgcn_sched_barrier(0);
+    if (s + 3 < S) issue(s + 3, std::integral_constant<int, (SL + 3) & 3>{});  // A(s)
+    read_frags(slc);
+    __builtin_amdgcn_sched_barrier(0);
+    if (s + 1 < S) wait_after((s + 2 < S ? 4 : 0) + (s + 3 < S ? 4 : 0));
+    raw_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    compute();  // B(s)
+    __builtin_amdgcn_sched_barrier(0);
+    raw_barrier();
+  };
+  if (g == 0) {
+    for (int s = 0; s < S; s += 4) {
+      g0_stage(s, SL0{});
+      g0_stage(s + 1, SL1{});
+      g0_stage(s + 2, SL2{});
+      g0_stage(s + 3, SL3{});
+    }
+  } else {
+    for (int s = 0; s < S; s += 4) {
+      g1_stage(s, SL0{});
+      g1_stage(s + 1, SL1{});
+      g1_stage(s + 2, SL2{});
+      g1_stage(s + 3, SL3{});
+    }
+  }
+
+  // epilogue: the ring becomes a 256 x 256 fp16 tile (512-byte rows, 16-byte chunks
+  // rotated by the row) written from the accumulators, then stored row-contiguously
+  char* const C = smem;
+#pragma unroll
+  for (int mb = 0; mb < 4; ++mb) {
+    const int row = 128 * g + mb * 32 + (lane & 31);
+    const float sar = s_sa[row];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int col = 64 * q + nb * 32 + 8 * q4 + 4 * (lane >> 5);
+        const f32x4 swv = *reinterpret_cast<const f32x4*>(s_sw + col);
+        _Float16 bv[4];
+        __builtin_memcpy(bv, s_bias + col, sizeof(bv));
+        _Float16 h[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          h[e] = static_cast<_Float16>((static_cast<float>(acc[nb][mb][4 * q4 + e]) * sar) * swv[e] +
+                                       static_cast<float>(bv[e]));
+        *reinterpret_cast<uint2*>(C + row * 512 + (((col >> 3) ^ (row & 31)) << 4) + (col & 7) * 2) =
+            __builtin_bit_cast(uint2, h);
+        if constexpr (kDump) {
+          if (m0 + row < m && n0 + col < n) {  // n % 8 == 0: the 4 channels are all inside
+            const i32x4 v = {acc[nb][mb][4 * q4], acc[nb][mb][4 * q4 + 1], acc[nb][mb][4 * q4 + 2],
+                             acc[nb][mb][4 * q4 + 3]};
+            *reinterpret_cast<i32x4*>(acc_out + (m0 + row) * n + n0 + col) = v;
+          }
+        }
+      }
+    }
+  }
+  wait_lgkm0();
+  raw_barrier();
+#pragma unroll 4
+  for (int i = 0; i < 16; ++i) {
+    const int idx = i * 512 + tid;
+    const int row = idx >> 5, ch = idx & 31;
+    if (m0 + row < m && n0 + ch * 8 < n)
+      *reinterpret_cast<u32x4*>(out + (m0 + row) * n + n0 + ch * 8) =
+          *reinterpret_cast<const u32x4*>(C + row * 512 + ((ch ^ (row & 31)) << 4));
+  }
+}
+
+// Channel-tile groups of the ping-pong GEMM's tile order: the G (1, 2, 4 or 8, at most
+// the channel-tile count) that minimises the operand bytes the XCDs fetch past their L2:
+// token rows are fetched once per group, and channel rows once per XCD when the group's
+// slice fits in half the 4 MB L2, else once per round of the token blocks an XCD holds
+// in flight.
+int pp_groups(int64_t mt, int nt, int k) {
+  int best = 1;
+  double best_cost = -1.0;
+  for (int gr = 1; gr <= 8 && gr <= nt; gr *= 2) {
+    const int parts = 8 / gr;
+    const int64_t cpg = (nt + gr - 1) / gr;
+    const int64_t mpp = (mt + parts - 1) / parts;
+    const double b_xcd = static_cast<double>(cpg) * 256.0 * k;
+    const int64_t in_flight = cpg >= 32 ? 1 : 32 / cpg;
+    const int64_t rounds = (mpp + in_flight - 1) / in_flight;
+    const double cost = static_cast<double>(mt) * 256.0 * k * gr + 8.0 * b_xcd * (b_xcd > (2 << 20) ? rounds : 1);
+    if (best_cost < 0 || cost < best_cost) {
+      best_cost = cost;
+      best = gr;
+    }
+  }
+  return best;
+}
+
 template <int NP>
 void launch_quant(const _Float16* x, int64_t m, int k, const float* signs, int8_t* q, float* s, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(std::min<int64_t>(ceil_div(m, 4), int64_t(compute_units()) * 8)));
@@ -845,6 +1136,25 @@ int hi3d_w8a8_gemm(const int8_t* q, const float* sa, const int8_t* w, const floa
   // The persistent kernel removes the per-tile load latency and overlaps tiles; its stage
   // loop is slower than the one-tile kernel's, so it pays off for short K loops only
   // (measured: K = 1024 faster, K = 4096 slower).
+  // The ping-pong kernel takes K a multiple of 256 with n % 8 == 0 (with
+  // acc_out it also stores the int32 accumulators, 16-byte aligned).
+  if (k % 256 == 0 && n % 8 == 0 && static_cast<int64_t>(k) * 256 < (int64_t(1) << 31) &&
+      (reinterpret_cast<uintptr_t>(sa) & 3) == 0 && (reinterpret_cast<uintptr_t>(sw) & 3) == 0 &&
+      (reinterpret_cast<uintptr_t>(bias) & 3) == 0 && (reinterpret_cast<uintptr_t>(acc_out) & 15) == 0) {
+    const int gr = pp_groups(mtiles, ntiles, k);
+    const int parts = 8 / gr;
+    const int64_t per_xcd = static_cast<int64_t>((ntiles + gr - 1) / gr) * ((mtiles + parts - 1) / parts);
+    HI3D_REQUIRE(per_xcd * 8 < (int64_t(1) << 31), "problem too large");
+    const dim3 grid(static_cast<unsigned>(per_xcd * 8));
+    if (acc_out)
+      hipLaunchKernelGGL(w8a8_gemm_pp_kernel<true>, grid, dim3(512), 0, stream, q, sa, w, sw, b, m, n, k, o, acc_out,
+                         mtiles, ntiles, gr);
+    else
+      hipLaunchKernelGGL(w8a8_gemm_pp_kernel<false>, grid, dim3(512), 0, stream, q, sa, w, sw, b, m, n, k, o, acc_out,
+                         mtiles, ntiles, gr);
+    HI3D_LAUNCH_CHECK();
+    return HI3D_OK;
+  }
   // With acc_out the same kernel also stores the int32 accumulators (16-byte aligned).
   if (k % 64 == 0 && k >= 4 * 64 && k < 32 * 64 && m >= kGemmBM && n >= kGemmBN && n % 8 == 0 &&
       static_cast<int64_t>(kGemmBM) * k < (int64_t(1) << 32) && (reinterpret_cast<uintptr_t>(sa) & 3) == 0 &&
