@@ -816,6 +816,11 @@ __device__ __forceinline__ __attribute__((address_space(3))) void* lds_ptr(char*
   return (__attribute__((address_space(3))) void*)(p);
 }
 
+// 32-bit LDS address of a pointer into shared memory (for LDS instructions in asm)
+__device__ __forceinline__ uint32_t lds_addr(char* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds_ptr(p)));
+}
+
 template <bool kDump>
 __global__ __launch_bounds__(512, 1) void w8a8_gemm_pp_kernel(const int8_t* __restrict__ qa, const float* __restrict__ sa,
                                                               const int8_t* __restrict__ w, const float* __restrict__ sw,
@@ -1050,6 +1055,377 @@ __global__ __launch_bounds__(512, 1) void w8a8_gemm_pp_kernel(const int8_t* __re
   }
 }
 
+// ------------------------------------------------ persistent ping-pong GEMM --
+// The ping-pong kernel's stage loop, run persistently over a list of tiles per
+// workgroup (the same XCD-aware order). The stage sequence continues across tiles: the
+// loads of a tile's stages 0-2 are issued during the previous tile's last three stages,
+// so no tile waits for its first loads.
+//  * Epilogue, after a tile's last stage: its ring slot (3) is the only free one (the
+//    next tile's stages 0-2 are in flight into slots 0-2). The tile leaves in four rounds
+//    of 64 rows: each wave converts one 32-row block of its accumulators (the reference's
+//    fp16(((float)acc * sa) * sw + bias), no contraction), writes it to slot 3 as fp16
+//    (512-byte rows, 16-byte chunks rotated by the row), and after a barrier every thread
+//    stores four 16-byte row chunks. These stores queue behind the next tile's first
+//    loads and drain while it runs.
+//  * Stores go through a buffer descriptor over the tile's valid rows, and a chunk past
+//    the last channel gets an offset past the descriptor: no store is predicated, every
+//    wave issues the same operations and the vmcnt waits are exact. At stages 0 and 1 of
+//    a tile the operations younger than the awaited loads include the epilogue's 16
+//    stores and the next tile's 2 scale loads.
+//  * Scales: sa, sw and bias of the next tile are loaded (2 direct-to-LDS loads per wave,
+//    sa and sw in one, bias halves in the other) right after the epilogue that last read
+//    them; group 0 widens the bias to fp32 in phase B of stage 3, after every wave's scale
+//    loads have passed a wait.
+//  * A tile's first MFMAs take a zero accumulator operand (no clearing). After its last
+//    tile a workgroup still issues the loads of a tile past its list through empty
+//    descriptors (zeros into slots nobody reads), so the stage code has no tail form; it
+//    waits for all of them before it exits.
+constexpr int kPQScale = kPPRing * kPPStage;  // s_sa (1 KB), s_sw (1 KB), bias fp16 (512 B), bias fp32 (1 KB)
+constexpr int kPQEpiOps = 16 + 2;              // epilogue stores + scale loads per wave
+constexpr int kPQPastRecords = 0x7FFFFFF0;      // store offset that every descriptor drops
+
+// Position in a workgroup's tile list: list index j, token tile mi and channel tile ni
+// of the XCD's range.
+struct PQTile {
+  int64_t j;
+  int mi, ni;
+};
+
+// Load descriptors of one tile's token rows (a) and channel rows (b).
+struct PQSrc {
+  __amdgpu_buffer_rsrc_t a, b;
+};
+
+template <bool kDump>
+__global__ __launch_bounds__(512, 1) void w8a8_gemm_pq_kernel(const int8_t* __restrict__ qa, const float* __restrict__ sa,
+                                                              const int8_t* __restrict__ w, const float* __restrict__ sw,
+                                                              const _Float16* __restrict__ bias, int64_t m, int n, int k,
+                                                              _Float16* __restrict__ out, int32_t* __restrict__ acc_out,
+                                                              int64_t mt_count, int nt_count, int groups) {
+#pragma clang fp contract(off)
+  __shared__ __attribute__((aligned(16))) char smem[kPQScale + 256 * 4 * 3 + 256 * 2];
+  float* const s_sa = reinterpret_cast<float*>(smem + kPQScale);
+  float* const s_sw = s_sa + 256;
+  float* const s_b32 = s_sw + 256;
+  _Float16* const s_b16 = reinterpret_cast<_Float16*>(s_b32 + 256);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = wave >> 2, q = wave & 3;
+
+  // this workgroup's tiles: items local, local + wpx, ... of its XCD's list
+  const int xcd = static_cast<int>(blockIdx.x & 7);
+  const int64_t local = blockIdx.x >> 3, wpx = gridDim.x >> 3;
+  const int parts = 8 / groups;
+  const int cg = xcd % groups, part = xcd / groups;
+  const int cpg = (nt_count + groups - 1) / groups;
+  const int64_t mpp = (mt_count + parts - 1) / parts;
+  const int nt_lo = cg * cpg, nt_hi = nt_count < nt_lo + cpg ? nt_count : nt_lo + cpg;
+  const int ntg = nt_hi - nt_lo;
+  const int64_t mt_lo = part * mpp, mt_hi = mt_count < mt_lo + mpp ? mt_count : mt_lo + mpp;
+  if (ntg <= 0 || mt_hi <= mt_lo) return;
+  const int64_t items = ntg * (mt_hi - mt_lo);
+  if (local >= items) return;
+  const int64_t count = (items - local + wpx - 1) / wpx;
+  // Tile j of the list is item local + j wpx = (token tile mi, channel tile ni) of the
+  // XCD's range; the walk steps (mi, ni) with scalar additions (no division in the loop).
+  const int step_m = static_cast<int>(wpx / ntg), step_n = static_cast<int>(wpx % ntg);
+  auto advance = [&](PQTile t) {
+    t.j += 1;
+    t.mi += step_m;
+    t.ni += step_n;
+    if (t.ni >= ntg) {
+      t.ni -= ntg;
+      t.mi += 1;
+    }
+    return t;
+  };
+  auto tile_m0 = [&](const PQTile& t) { return (mt_lo + t.mi) * 256; };
+  auto tile_n0 = [&](const PQTile& t) { return (nt_lo + t.ni) * 256; };
+
+  // load descriptors of a tile's token and channel rows (rows past the matrix read
+  // zeros; a tile past the list gets empty descriptors)
+  auto src_of = [&](const PQTile& t) {
+    PQSrc r;
+    if (t.j < count) {
+      const int64_t m0 = tile_m0(t);
+      const int n0 = tile_n0(t);
+      const int rows_a = m - m0 < 256 ? static_cast<int>(m - m0) : 256;
+      const int rows_b = n - n0 < 256 ? n - n0 : 256;
+      r.a = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(qa + m0 * k), 0, rows_a * k, kRawBufferFlags);
+      r.b = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(w + static_cast<int64_t>(n0) * k), 0, rows_b * k,
+                                              kRawBufferFlags);
+    } else {
+      r.a = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(qa), 0, 0, kRawBufferFlags);
+      r.b = __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(w), 0, 0, kRawBufferFlags);
+    }
+    return r;
+  };
+  // scales and bias of a tile (the caller passes the last tile again in place of one
+  // past the list): every wave issues exactly two loads; a missing bias reads zeros
+  const __amdgpu_buffer_rsrc_t rs_a =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(sa), 0, static_cast<int>(m * 4), kRawBufferFlags);
+  const __amdgpu_buffer_rsrc_t rs_w = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(sw), 0, n * 4, kRawBufferFlags);
+  const __amdgpu_buffer_rsrc_t rs_b = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<_Float16*>(bias != nullptr ? bias : reinterpret_cast<const _Float16*>(g_zero_bias)), 0,
+      bias != nullptr ? n * 2 : 0, kRawBufferFlags);
+  // Per-lane values of the epilogue and the scale loads are rebuilt from the lane index
+  // recomputed in place (volatile, so not hoisted), so that the compiler keeps nothing
+  // of them live across the stage loop (where it would be spilled: a scratch reload is
+  // a vector memory operation, and its wait would also wait for the ring loads).
+  auto lane_now = []() {
+    int l;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+    return l;
+  };
+  auto load_scales = [&](const PQTile& t) {
+    const int lane = lane_now();
+    const int64_t m0 = tile_m0(t);
+    const int n0 = tile_n0(t);
+    if (wave < 4) {
+      const int64_t r = m0 + wave * 64 + lane;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_a, lds_ptr(reinterpret_cast<char*>(s_sa) + wave * 256), 4,
+                                               static_cast<int>(r < m ? r : m - 1) * 4, 0, 0, 0);
+    } else {
+      const int c = n0 + (wave - 4) * 64 + lane;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_w, lds_ptr(reinterpret_cast<char*>(s_sw) + (wave - 4) * 256), 4,
+                                               (c < n ? c : n - 1) * 4, 0, 0, 0);
+    }
+    const int d = n0 / 2 + (wave & 1) * 64 + lane;  // bias dword: channels 2 d, 2 d + 1 (n is even)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_b, lds_ptr(reinterpret_cast<char*>(s_b16) + (wave & 1) * 256), 4,
+                                             (d < n / 2 ? d : n / 2 - 1) * 4, 0, 0, 0);
+  };
+
+  const int c16 = ((lane & 3) ^ ((lane >> 4) & 3)) * 16;
+  int vo[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) vo[j] = (128 * g + (2 * q + j) * 16 + (lane >> 2)) * k + c16;
+  auto issue = [&](const PQSrc& r, int s, auto slc) {
+    constexpr int SL = decltype(slc)::value;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r.a, lds_ptr(smem + SL * kPPStage + (8 * g + 2 * q + j) * 1024), 16,
+                                               vo[j], s * 64, 0, 0);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r.b, lds_ptr(smem + SL * kPPStage + kPPHalf + (8 * g + 2 * q + j) * 1024),
+                                               16, vo[j], s * 64, 0, 0);
+  };
+
+  u32x4 fw[2][2], fq[2][4];
+  const char* bw[2][2];
+  const char* bq[2][2];
+#pragma unroll
+  for (int G = 0; G < 2; ++G) {
+    const int c = 2 * G + (lane >> 5);
+    bw[G][0] = smem + kPPHalf + lds_off64(64 * q + (lane & 31), c);
+    bq[G][0] = smem + lds_off64(128 * g + (lane & 31), c);
+    bw[G][1] = bw[G][0] + 2 * kPPStage;
+    bq[G][1] = bq[G][0] + 2 * kPPStage;
+  }
+  auto read_frags = [&](auto slc) {
+    constexpr int SL = decltype(slc)::value;
+#pragma unroll
+    for (int G = 0; G < 2; ++G) {
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb)
+        fw[G][nb] = *reinterpret_cast<const u32x4*>(bw[G][SL >> 1] + (SL & 1) * kPPStage + nb * 2048);
+#pragma unroll
+      for (int mb = 0; mb < 4; ++mb)
+        fq[G][mb] = *reinterpret_cast<const u32x4*>(bq[G][SL >> 1] + (SL & 1) * kPPStage + mb * 2048);
+    }
+  };
+  i32x16 acc[2][4];
+  auto compute = [&](auto first) {
+    constexpr bool kFirst = decltype(first)::value;
+    wait_lgkm0();
+    __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int G = 0; G < 2; ++G)
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb)
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb) {
+          if (kFirst && G == 0)
+            acc[nb][mb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, fw[G][nb]),
+                                                              __builtin_bit_cast(i32x4, fq[G][mb]), i32x16{}, 0, 0, 0);
+          else
+            acc[nb][mb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(__builtin_bit_cast(i32x4, fw[G][nb]),
+                                                              __builtin_bit_cast(i32x4, fq[G][mb]), acc[nb][mb], 0, 0, 0);
+        }
+    __builtin_amdgcn_s_setprio(0);
+  };
+  auto wait_n = [&](auto nn) {
+    constexpr int N = decltype(nn)::value;
+    wait_vmcnt<N>();
+  };
+
+  // Epilogue of the tile at (m0, n0): four rounds of 64 rows through ring slot 3.
+  char* const C = smem + 3 * kPPStage;
+  auto epilogue = [&](int64_t m0, int n0) {
+    const int lane = lane_now(), tid = wave * 64 + lane;
+    const int rows_a = m - m0 < 256 ? static_cast<int>(m - m0) : 256;
+    const __amdgpu_buffer_rsrc_t ro =
+        __builtin_amdgcn_make_buffer_rsrc(out + m0 * n, 0, rows_a * n * 2, kRawBufferFlags);
+    const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc(
+        kDump ? acc_out + m0 * n : acc_out, 0, kDump ? rows_a * n * 4 : 0, kRawBufferFlags);
+    const int srow = 32 * g + (lane & 31);  // staging row of this lane
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = 128 * g + 32 * r + (lane & 31);
+      const float sar = s_sa[row];
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) {
+          const int col = 64 * q + nb * 32 + 8 * q4 + 4 * (lane >> 5);
+          const f32x4 swv = *reinterpret_cast<const f32x4*>(s_sw + col);
+          const f32x4 bv = *reinterpret_cast<const f32x4*>(s_b32 + col);
+          _Float16 h[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            h[e] = static_cast<_Float16>((static_cast<float>(acc[nb][r][4 * q4 + e]) * sar) * swv[e] + bv[e]);
+          // written through asm: the compiler cannot tell slot 3 from the slots that the
+          // next tile's loads are filling and would wait for all of them first
+          const uint32_t dst = lds_addr(C + srow * 512 + (((col >> 3) ^ (srow & 31)) << 4) + (col & 7) * 2);
+          typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+          const u32x2 hv = __builtin_bit_cast(u32x2, h);
+          asm volatile("ds_write_b64 %0, %1" ::"v"(dst), "v"(hv) : "memory");
+          if constexpr (kDump) {
+            const i32x4 v = {acc[nb][r][4 * q4], acc[nb][r][4 * q4 + 1], acc[nb][r][4 * q4 + 2], acc[nb][r][4 * q4 + 3]};
+            const int off = n0 + col < n ? (row * n + n0 + col) * 4 : kPQPastRecords;
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rd, off, 0, 0);
+          }
+        }
+      }
+      if (r == 3 && g == 0) read_frags(std::integral_constant<int, 0>{});  // the next tile's stage 0
+      wait_lgkm0();
+      raw_barrier();
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int idx = i * 512 + tid;
+        const int sr = idx >> 5, ch = idx & 31;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(C + sr * 512 + ((ch ^ (sr & 31)) << 4));
+        const int trow = (sr < 32 ? 0 : 96) + 32 * r + sr;
+        const int off = n0 + ch * 8 < n ? (trow * n + n0 + ch * 8) * 2 : kPQPastRecords;
+        __builtin_amdgcn_raw_buffer_store_b128(v, ro, off, 0, 0);
+      }
+      wait_lgkm0();
+      raw_barrier();
+    }
+    if constexpr (kDump) wait_vmcnt<0>();
+  };
+
+  using SL0 = std::integral_constant<int, 0>;
+  using SL1 = std::integral_constant<int, 1>;
+  using SL2 = std::integral_constant<int, 2>;
+  using SL3 = std::integral_constant<int, 3>;
+  using Yes = std::true_type;
+  using No = std::false_type;
+  using W4 = std::integral_constant<int, 4>;
+  using W8 = std::integral_constant<int, 8>;
+  using WE0 = std::integral_constant<int, 4 + kPQEpiOps>;      // group 0, stages 0-1
+  using WE1 = std::integral_constant<int, 8 + kPQEpiOps>;      // group 1, stages 0-1
+
+  // Prologue: scales of tile 0, stages 0-2 of tile 0 from every wave, all complete.
+  const int S = k >> 6;  // a multiple of 4, at least 8
+  PQTile t0 = {0, static_cast<int>(local / ntg), static_cast<int>(local % ntg)};
+  PQTile t1 = advance(t0);
+  PQSrc cur = src_of(t0), nxt = src_of(t1);
+  load_scales(t0);
+  issue(cur, 0, SL0{});
+  issue(cur, 1, SL1{});
+  issue(cur, 2, SL2{});
+  wait_vmcnt<0>();
+  raw_barrier();
+  if (g == 0) read_frags(SL0{});
+
+  // Stage s of a tile: phase A(s), group 0 multiplies while group 1 issues its loads of
+  // stage s + 3 and reads its fragments of s; phase B(s), group 1 multiplies while group
+  // 0 issues its loads of s + 3 and reads its fragments of s + 1. Stage s + 3 belongs to
+  // the next tile for s >= S - 3 (descriptor `nxt`, K offset s + 3 - S). Group 0 reads
+  // the next tile's first fragments inside the epilogue, once its accumulators are
+  // converted, so that both never hold registers at the same time.
+  auto g0_stage = [&](const PQSrc& r, int s3, auto slc, auto wn, auto first, auto widen, auto readf) {
+    constexpr int SL = decltype(slc)::value;
+    __builtin_amdgcn_sched_barrier(0);
+    compute(first);  // A(s)
+    __builtin_amdgcn_sched_barrier(0);
+    wait_n(wn);  // own loads of stage s + 1 landed
+    raw_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    issue(r, s3, std::integral_constant<int, (SL + 3) & 3>{});  // B(s)
+    if constexpr (decltype(readf)::value) read_frags(std::integral_constant<int, (SL + 1) & 3>{});
+    if constexpr (decltype(widen)::value) {
+      const int t = wave * 64 + lane_now();
+      s_b32[t] = static_cast<float>(s_b16[t]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    raw_barrier();
+  };
+  auto g1_stage = [&](const PQSrc& r, int s3, auto slc, auto wn, auto first) {
+    constexpr int SL = decltype(slc)::value;
+    __builtin_amdgcn_sched_barrier(0);
+    issue(r, s3, std::integral_constant<int, (SL + 3) & 3>{});  // A(s)
+    read_frags(slc);
+    __builtin_amdgcn_sched_barrier(0);
+    wait_n(wn);
+    raw_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    compute(first);  // B(s)
+    __builtin_amdgcn_sched_barrier(0);
+    raw_barrier();
+  };
+
+  // Each group runs its own copy of the tile loop (the branch on the group stays out of
+  // the loop).
+  auto tile_end = [&]() {
+    epilogue(tile_m0(t0), tile_n0(t0));
+    load_scales(t1.j < count ? t1 : t0);
+    t0 = t1;
+    t1 = advance(t1);
+    cur = nxt;
+    nxt = src_of(t1);
+  };
+  if (g == 0) {
+    for (int64_t j = 0; j < count; ++j) {
+      g0_stage(cur, 3, SL0{}, WE0{}, Yes{}, No{}, Yes{});
+      g0_stage(cur, 4, SL1{}, WE0{}, No{}, No{}, Yes{});
+      g0_stage(cur, 5, SL2{}, W4{}, No{}, No{}, Yes{});
+      g0_stage(cur, 6, SL3{}, W4{}, No{}, Yes{}, Yes{});
+      for (int s = 4; s < S - 4; s += 4) {
+        g0_stage(cur, s + 3, SL0{}, W4{}, No{}, No{}, Yes{});
+        g0_stage(cur, s + 4, SL1{}, W4{}, No{}, No{}, Yes{});
+        g0_stage(cur, s + 5, SL2{}, W4{}, No{}, No{}, Yes{});
+        g0_stage(cur, s + 6, SL3{}, W4{}, No{}, No{}, Yes{});
+      }
+      g0_stage(cur, S - 1, SL0{}, W4{}, No{}, No{}, Yes{});
+      g0_stage(nxt, 0, SL1{}, W4{}, No{}, No{}, Yes{});
+      g0_stage(nxt, 1, SL2{}, W4{}, No{}, No{}, Yes{});
+      g0_stage(nxt, 2, SL3{}, W4{}, No{}, No{}, No{});
+      tile_end();
+    }
+  } else {
+    for (int64_t j = 0; j < count; ++j) {
+      g1_stage(cur, 3, SL0{}, WE1{}, Yes{});
+      g1_stage(cur, 4, SL1{}, WE1{}, No{});
+      g1_stage(cur, 5, SL2{}, W8{}, No{});
+      g1_stage(cur, 6, SL3{}, W8{}, No{});
+      for (int s = 4; s < S - 4; s += 4) {
+        g1_stage(cur, s + 3, SL0{}, W8{}, No{});
+        g1_stage(cur, s + 4, SL1{}, W8{}, No{});
+        g1_stage(cur, s + 5, SL2{}, W8{}, No{});
+        g1_stage(cur, s + 6, SL3{}, W8{}, No{});
+      }
+      g1_stage(cur, S - 1, SL0{}, W8{}, No{});
+      g1_stage(nxt, 0, SL1{}, W8{}, No{});
+      g1_stage(nxt, 1, SL2{}, W8{}, No{});
+      g1_stage(nxt, 2, SL3{}, W8{}, No{});
+      tile_end();
+    }
+  }
+  wait_vmcnt<0>();  // the loads past the list land before the workgroup's LDS is released
+}
+
 // Channel-tile groups of the ping-pong GEMM's tile order: the G (1, 2, 4 or 8, at most
 // the channel-tile count) that minimises the operand bytes the XCDs fetch past their L2:
 // token rows are fetched once per group, and channel rows once per XCD when the group's
@@ -1136,6 +1512,31 @@ int hi3d_w8a8_gemm(const int8_t* q, const float* sa, const int8_t* w, const floa
   // The persistent kernel removes the per-tile load latency and overlaps tiles; its stage
   // loop is slower than the one-tile kernel's, so it pays off for short K loops only
   // (measured: K = 1024 faster, K = 4096 slower).
+  // The persistent ping-pong kernel takes K a multiple of 256 from 512 on with n % 8 == 0
+  // and 32-bit byte offsets within a tile of the output (and of acc_out, 16-byte aligned,
+  // whose int32 accumulators it also stores).
+  const bool aligned4 = ((reinterpret_cast<uintptr_t>(sa) | reinterpret_cast<uintptr_t>(sw) |
+                          reinterpret_cast<uintptr_t>(bias)) & 3) == 0 &&
+                        (reinterpret_cast<uintptr_t>(acc_out) & 15) == 0;
+  if (k % 256 == 0 && k >= 512 && n % 8 == 0 && static_cast<int64_t>(k) * 256 < (int64_t(1) << 31) &&
+      m < (int64_t(1) << 29) &&
+      static_cast<int64_t>(n) * (acc_out ? 1024 : 512) < (int64_t(1) << 31) - 4096 && aligned4) {
+    const int gr = pp_groups(mtiles, ntiles, k);
+    const int parts = 8 / gr;
+    const int64_t per_xcd = static_cast<int64_t>((ntiles + gr - 1) / gr) * ((mtiles + parts - 1) / parts);
+    const int cus = compute_units();
+    HI3D_REQUIRE(cus > 0, "cannot query the compute unit count");
+    const int64_t wpx = std::min<int64_t>(per_xcd, std::max(1, cus / 8));
+    const dim3 grid(static_cast<unsigned>(wpx * 8));
+    if (acc_out)
+      hipLaunchKernelGGL(w8a8_gemm_pq_kernel<true>, grid, dim3(512), 0, stream, q, sa, w, sw, b, m, n, k, o, acc_out,
+                         mtiles, ntiles, gr);
+    else
+      hipLaunchKernelGGL(w8a8_gemm_pq_kernel<false>, grid, dim3(512), 0, stream, q, sa, w, sw, b, m, n, k, o, acc_out,
+                         mtiles, ntiles, gr);
+    HI3D_LAUNCH_CHECK();
+    return HI3D_OK;
+  }
   // The ping-pong kernel takes K a multiple of 256 with n % 8 == 0 (with
   // acc_out it also stores the int32 accumulators, 16-byte aligned).
   if (k % 256 == 0 && n % 8 == 0 && static_cast<int64_t>(k) * 256 < (int64_t(1) << 31) &&

@@ -164,9 +164,10 @@ def test_workload4_every_row_accumulators_bit_exact(cuda):
     [1024, 4096]^T, on the codes of the outlier-laden activations and the quantised
     weights: every int32 accumulator equals the float64 product of the codes (exact:
     |acc| <= 127^2 * 4096 < 2^53), and every fp16 output equals the unfused float32
-    epilogue of those accumulators. Shape A runs the persistent kernel (K = 1024), shape
-    B the one-tile kernel (K = 4096); the accumulator dump comes from the same kernel
-    as the fp16 output, whose bits must not change with it."""
+    epilogue of those accumulators. Both shapes run the persistent ping-pong kernel (K =
+    1024: 16 stages per tile, 16 tiles per workgroup; K = 4096: 64 stages, 4 tiles); the
+    accumulator dump comes from the same kernel as the fp16 output, whose bits must not
+    change with it."""
     from hi3d_amd import w8a8
 
     for m, k, n in ((65536, 1024, 4096), (65536, 4096, 1024)):
@@ -224,13 +225,16 @@ def test_gemm_non_contiguous_operands_and_scale_checks(cuda):
 
 @pytest.mark.parametrize("m,n,k,with_bias", [(1000, 520, 320, True), (4096, 4096, 1024, True), (300, 264, 1984, False),
                                              (256, 256, 256, True), (2600, 1032, 1536, True), (1000, 520, 4096, True),
-                                             (600, 300, 2112, False)])
+                                             (600, 300, 2112, False), (200, 264, 512, True), (513, 8, 768, False),
+                                             (777, 1800, 2560, True)])
 def test_gemm_full_output_bit_exact(cuda, m, n, k, with_bias):
-    """Every output bit-equal to the oracle on both fused-output paths: the persistent
-    full-tile kernel (m, n >= 256, n % 8 == 0, k % 64 == 0, 256 <= k < 2048) and the
-    one-tile kernel (here k >= 2048), including ragged edges (the persistent kernel moves
-    the last tile of each dimension back so it overlaps its neighbour) and a missing
-    bias; both also equal the accumulator-dump variant's output."""
+    """Every output bit-equal to the oracle on every fused-output path: the persistent
+    ping-pong kernel (k % 256 == 0, k >= 512, n % 8 == 0: ragged rows and channel tiles
+    through its store descriptors, one tile per workgroup or several, k = 512 and 768
+    with no middle stage loop), the ping-pong kernel (k = 256), the persistent four-wave
+    kernel (k % 64 == 0, k < 2048, m, n >= 256: its edge tiles move back to overlap their
+    neighbours) and the one-tile kernel (the rest), with and without bias; each also
+    equals its accumulator-dump variant's output."""
     from hi3d_amd import w8a8
 
     rng = np.random.default_rng(m * 7 + n * 3 + k)
