@@ -95,6 +95,21 @@ def timed(fn, steps: int, warmup: int):
     return wall, ev
 
 
+def dense_fresh(fn):
+    """Run a kernel-map build with a dense grid cleared inside the call (not kept)."""
+    from hi3d_amd import kmap
+
+    def run():
+        old = kmap.KMAP_DENSE_KEEP
+        kmap.KMAP_DENSE_KEEP = False
+        try:
+            return fn()
+        finally:
+            kmap.KMAP_DENSE_KEEP = old
+
+    return run
+
+
 def bench_subm(name: str, grid: int, cin: int, cout: int, dtype, steps: int, warmup: int, seed: int = 0):
     import numpy as np
     import torch
@@ -111,6 +126,7 @@ def bench_subm(name: str, grid: int, cin: int, cout: int, dtype, steps: int, war
     # kernel map build (hash insert + probe) and plan, timed separately
     map_wall, map_ev = timed(lambda: kmap.build_kernel_map(coords, [grid] * 3, 1, check=False), 5, 2)
     hash_wall, hash_ev = timed(lambda: kmap.build_kernel_map(coords, [grid] * 3, 1, capacity=0, check=False), 5, 2)
+    _, fresh_ev = timed(dense_fresh(lambda: kmap.build_kernel_map(coords, [grid] * 3, 1, check=False)), 5, 2)
     km = kmap.build_kernel_map(coords, [grid] * 3, 1)
     plan_wall, plan_ev = timed(lambda: kmap.build_plan(km.table, km.n, km.indices), 3, 1)
     plan = km.plan()
@@ -135,6 +151,7 @@ def bench_subm(name: str, grid: int, cin: int, cout: int, dtype, steps: int, war
         "conv_alg_bytes": conv_bytes,
         "map_ms": map_wall,
         "map_dense_ms": map_ev,
+        "map_dense_fresh_ms": fresh_ev,
         "map_hash_ms": hash_ev,
         "map_alg_gbs_hash": map_bytes / (hash_ev * 1e-3) / 1e9,
         "plan_ms": plan_wall,
@@ -234,6 +251,7 @@ def bench_block(steps: int, warmup: int, settle_s: float = 0.0):
     coords = torch.as_tensor(idx).to(dev)
     map_wall, map_ev = timed(lambda: kmap.build_kernel_map(coords, [1024] * 3, 1, check=False), 3, 1)
     hash_wall, hash_ev = timed(lambda: kmap.build_kernel_map(coords, [1024] * 3, 1, capacity=0, check=False), 3, 1)
+    _, fresh_ev = timed(dense_fresh(lambda: kmap.build_kernel_map(coords, [1024] * 3, 1, check=False)), 3, 1)
     km = kmap.build_kernel_map(coords, [1024] * 3, 1)
     plan_wall, plan_ev = timed(lambda: kmap.build_plan(km.table, km.n, km.indices), 3, 1)
     plan = km.plan()
@@ -282,6 +300,7 @@ def bench_block(steps: int, warmup: int, settle_s: float = 0.0):
         "ln_ms": ln_ev,
         "ln_gbs": 4.0 * n * c / (ln_ev * 1e-3) / 1e9,
         "map_dense_ms": map_ev,
+        "map_dense_fresh_ms": fresh_ev,
         "map_hash_ms": hash_ev,
         "map_alg_gbs_hash": n * 356 / (hash_ev * 1e-3) / 1e9,
         "plan_ms": plan_ev,

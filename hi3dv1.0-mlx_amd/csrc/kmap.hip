@@ -220,6 +220,15 @@ __global__ void dense_scatter_kernel(const int4* __restrict__ coords, int64_t n,
   if (prev != -1) atomicOr(status, HI3D_MAP_DUPLICATE);
 }
 
+// Puts back the -1 of every cell the scatter may have claimed (out-of-range rows claim
+// none; a duplicate's cell is its first row's).
+__global__ void dense_restore_kernel(const int4* __restrict__ coords, int64_t n, Grid g, int32_t* __restrict__ cells) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int4 c = coords[i];
+  if (g.inside(c.x, c.y, c.z, c.w)) cells[g.key(c.x, c.y, c.z, c.w)] = -1;
+}
+
 __global__ __launch_bounds__(256) void dense_lookup_kernel(const int4* __restrict__ coords, int64_t n, Grid g,
                                                            int ksize, const int32_t* __restrict__ cells,
                                                            int32_t* __restrict__ nbr, int32_t* __restrict__ counts) {
@@ -701,9 +710,15 @@ int hi3d_kmap_dense_workspace(int32_t batch_size, int32_t sx, int32_t sy, int32_
   return HI3D_OK;
 }
 
-int hi3d_kmap_subm_dense(const int32_t* coords, int64_t n, int32_t sx, int32_t sy, int32_t sz, int32_t batch_size,
-                         int32_t ksize, void* workspace, int64_t workspace_bytes, int32_t* nbr, int32_t* counts,
-                         int32_t* status, void* stream_) {
+}  // extern "C"
+
+namespace {
+
+// kept: the grid arrives with every cell -1 and is left that way (the scatter's cells
+// are put back after the lookup), instead of being cleared whole on entry.
+int kmap_subm_dense(const int32_t* coords, int64_t n, int32_t sx, int32_t sy, int32_t sz, int32_t batch_size,
+                    int32_t ksize, void* workspace, int64_t workspace_bytes, int32_t* nbr, int32_t* counts,
+                    int32_t* status, void* stream_, bool kept) {
   hipStream_t stream = as_stream(stream_);
   HI3D_REQUIRE(n >= 0, "n must be non-negative");
   HI3D_REQUIRE(ksize >= 1 && ksize % 2 == 1 && ksize * ksize * ksize <= kMaxKvol,
@@ -724,17 +739,40 @@ int hi3d_kmap_subm_dense(const int32_t* coords, int64_t n, int32_t sx, int32_t s
                static_cast<long long>(workspace_bytes), static_cast<long long>(need));
   Grid g{sx, sy, sz, batch_size};
   auto* cells = static_cast<int32_t*>(workspace);
-  // clear the grid with 16-byte stores (the workspace is 256-byte aligned)
-  const int64_t ncells = static_cast<int64_t>(batch_size) * sx * sy * sz;
-  launch_fill<int4>(reinterpret_cast<int4*>(cells), ncells / 4, make_int4(-1, -1, -1, -1), stream);
-  launch_fill<int32_t>(cells + (ncells & ~int64_t(3)), ncells & 3, -1, stream);
+  if (!kept) {
+    // clear the grid with 16-byte stores (the workspace is 256-byte aligned)
+    const int64_t ncells = static_cast<int64_t>(batch_size) * sx * sy * sz;
+    launch_fill<int4>(reinterpret_cast<int4*>(cells), ncells / 4, make_int4(-1, -1, -1, -1), stream);
+    launch_fill<int32_t>(cells + (ncells & ~int64_t(3)), ncells & 3, -1, stream);
+  }
   const int4* c4 = reinterpret_cast<const int4*>(coords);
   hipLaunchKernelGGL(dense_scatter_kernel, dim3(static_cast<unsigned>(ceil_div(n, 256))), dim3(256), 0, stream, c4, n,
                      g, cells, status);
   hipLaunchKernelGGL(dense_lookup_kernel, dim3(static_cast<unsigned>(ceil_div(n, kProbeRows))), dim3(256), 0, stream,
                      c4, n, g, ksize, cells, nbr, counts);
+  if (kept)
+    hipLaunchKernelGGL(dense_restore_kernel, dim3(static_cast<unsigned>(ceil_div(n, 256))), dim3(256), 0, stream, c4,
+                       n, g, cells);
   HI3D_LAUNCH_CHECK();
   return HI3D_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int hi3d_kmap_subm_dense(const int32_t* coords, int64_t n, int32_t sx, int32_t sy, int32_t sz, int32_t batch_size,
+                         int32_t ksize, void* workspace, int64_t workspace_bytes, int32_t* nbr, int32_t* counts,
+                         int32_t* status, void* stream) {
+  return kmap_subm_dense(coords, n, sx, sy, sz, batch_size, ksize, workspace, workspace_bytes, nbr, counts, status,
+                         stream, false);
+}
+
+int hi3d_kmap_subm_dense_kept(const int32_t* coords, int64_t n, int32_t sx, int32_t sy, int32_t sz,
+                              int32_t batch_size, int32_t ksize, void* grid, int64_t grid_bytes, int32_t* nbr,
+                              int32_t* counts, int32_t* status, void* stream) {
+  return kmap_subm_dense(coords, n, sx, sy, sz, batch_size, ksize, grid, grid_bytes, nbr, counts, status, stream,
+                         true);
 }
 
 int hi3d_kmap_pairs_workspace(int64_t n, int32_t kvol, int64_t* bytes) {

@@ -101,6 +101,16 @@ int hi3d_kmap_subm_dense(const int32_t* coords_dev, int64_t n, int32_t sx, int32
                          int32_t batch_size, int32_t ksize, void* workspace_dev, int64_t workspace_bytes,
                          int32_t* nbr_dev, int32_t* counts_dev, int32_t* status_dev, void* stream);
 
+/* hi3d_kmap_subm_dense over a grid that persists between calls: grid_dev (its size
+ * from hi3d_kmap_dense_workspace) holds -1 in every cell on entry and is left so on
+ * return (the cells the rows claim are put back after the lookup), so a call costs
+ * O(n) instead of clearing 4 bytes per grid cell (4 GiB at 1024^3). The caller fills a
+ * new grid with -1 once; calls sharing a grid must not overlap. Same reference
+ * interface as hi3d_kmap_subm_dense. */
+int hi3d_kmap_subm_dense_kept(const int32_t* coords_dev, int64_t n, int32_t sx, int32_t sy, int32_t sz,
+                              int32_t batch_size, int32_t ksize, void* grid_dev, int64_t grid_bytes, int32_t* nbr_dev,
+                              int32_t* counts_dev, int32_t* status_dev, void* stream);
+
 /* Workspace bytes of hi3d_kmap_pairs. */
 int hi3d_kmap_pairs_workspace(int64_t n, int32_t kvol, int64_t* bytes_host);
 

@@ -329,3 +329,39 @@ def test_dense_and_hash_maps_agree(cuda, ksize, batch, n_side, density):
         assert torch.equal(kmap.build_kernel_map(t, [n_side] * 3, batch, ksize).table, dense.table)
     finally:
         kmap.KMAP_DENSE_MAX_CELLS = old
+
+
+def test_kept_dense_grid_stays_clear(cuda):
+    """The dense map over a grid kept between calls: each build equals the oracle and the
+    per-call grid's map, and leaves every cell of the kept grid at -1 again, also after a
+    build that reports duplicate or out-of-range coordinates; two different sets in a row
+    on the same grid both come out exact (no cell of the first survives into the second)."""
+    from hi3d_amd import kmap
+
+    rng = np.random.default_rng(42)
+    side = 24
+    kmap.release_dense_grids()
+    sets = [_rand_indices(rng, side, 0.2, batch=2), _rand_indices(rng, side, 0.05, batch=2)]
+    for idx in sets:
+        t = torch.as_tensor(idx).to(cuda)
+        kept = kmap.build_kernel_map(t, [side] * 3, 2)
+        assert np.array_equal(kept.table.cpu().numpy(), okmap.neighbour_table(idx, [side] * 3))
+        old = kmap.KMAP_DENSE_KEEP
+        try:
+            kmap.KMAP_DENSE_KEEP = False
+            fresh = kmap.build_kernel_map(t, [side] * 3, 2)
+        finally:
+            kmap.KMAP_DENSE_KEEP = old
+        assert torch.equal(kept.table, fresh.table) and torch.equal(kept.counts, fresh.counts)
+        (grid,) = kmap._DENSE_GRIDS.values()
+        assert int(grid.numel()) >= 2 * side**3 and bool((grid == -1).all())
+        dup = torch.cat([t, t[7:9]])
+        with pytest.raises(ValueError, match="duplicate"):
+            kmap.build_kernel_map(dup, [side] * 3, 2)
+        bad = t.clone()
+        bad[3, 1] = side
+        with pytest.raises(ValueError, match="outside"):
+            kmap.build_kernel_map(bad, [side] * 3, 2)
+        assert bool((grid == -1).all())
+    kmap.release_dense_grids()
+    assert not kmap._DENSE_GRIDS
