@@ -35,7 +35,8 @@ from . import kmap as _kmap
 
 
 class ConvAlgo(enum.Enum):
-    """spconv algorithm selector; every value maps to the same gather-MFMA path."""
+    """Accepted for spconv compatibility; the value is ignored: every member runs the
+    one output-stationary gather-MFMA kernel."""
 
     Native = 0
     MaskImplicitGemm = 1
@@ -43,7 +44,9 @@ class ConvAlgo(enum.Enum):
 
 
 class _PairTable:
-    """``[2, K, N]``-indexable view over per-offset pair lists stored back to back."""
+    """Answers ``pairs[side, k, rows]`` from the GPU's compacted lists: side 0 = input
+    rows, side 1 = output rows, offset k occupying ``[offsets[k], offsets[k+1])`` of one
+    flat buffer per side (so no ``[2, K, N]`` padding is ever materialised)."""
 
     def __init__(self, src: torch.Tensor, dst: torch.Tensor, offsets: torch.Tensor):
         self._sides = (src, dst)
@@ -103,7 +106,9 @@ class IndiceData:
 
 
 class SparseConvTensor:
-    """Features, ``[N, 4]`` int32 ``(batch, x, y, z)`` indices and a shared pair cache."""
+    """A feature matrix over its voxel coordinates (rows of ``(batch, x, y, z)``), the
+    grid extent, and the ``indice_dict`` that every tensor derived from it shares, so a
+    kernel map built for one layer is found by the next layer with the same key."""
 
     def __init__(
         self,
@@ -124,7 +129,8 @@ class SparseConvTensor:
         return self._features
 
     def replace_feature(self, feature: torch.Tensor) -> "SparseConvTensor":
-        """Return a tensor over the same coordinates that shares the pair cache."""
+        """New features on the same voxels; the coordinate rows and the cache are shared,
+    not copied."""
         return SparseConvTensor(feature, self.indices, self.spatial_shape, self.batch_size, self.indice_dict)
 
     def find_indice_pair(self, key: str | None) -> IndiceData | None:
@@ -141,11 +147,9 @@ def _voxel_keys(indices: torch.Tensor, spatial_shape: Sequence[int]) -> torch.Te
 def subm_pairs(
     indices: torch.Tensor, spatial_shape: Sequence[int], kernel_size: int = 3
 ) -> tuple[list[torch.Tensor], list[torch.Tensor], torch.Tensor]:
-    """Per-offset ``(input row, output row)`` pairs of a submanifold convolution.
-
-    Returns ``(sources, targets, counts)`` with one int64 tensor per flat kernel offset,
-    built on the GPU from the hashed kernel map.
-    """
+    """The kernel map as lists: for each of the ``kernel_size**3`` offsets, the input
+    rows and the output rows they feed (int64, ascending input row), and the list
+    lengths. Built on the GPU (dense grid or hash, then a compaction of the table)."""
     km = _kmap.build_kernel_map(indices, spatial_shape, None, kernel_size)
     src, dst, offsets = km.pairs()
     off = offsets.tolist()
@@ -224,7 +228,10 @@ def _check_weight_dtype(features: torch.Tensor, weight: torch.Tensor) -> None:
 
 
 class SubMConv3d(nn.Module):
-    """Submanifold 3D convolution with spconv's parameter names and layout."""
+    """3x3x3 (any odd k) convolution evaluated only at the input's own voxels. Takes
+    spconv's constructor arguments and keeps its weight as ``[Cout, k, k, k, Cin]``, so
+    checkpoints load unchanged; the forward pass is one gather-MFMA launch over the
+    kernel map cached under ``indice_key``."""
 
     def __init__(
         self,
