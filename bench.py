@@ -43,8 +43,8 @@ PEAK_HBM_GBS = 8000.0
 # summary that holds its measured HBM traffic per launch: FETCH_SIZE and WRITE_SIZE per dispatch from
 # two rocprofv3 --pmc runs of this script, each scaled by the factor the same counter
 # reads for a plain device copy of known size (`--copy-probe`).
-HEADLINE_KERNEL = "conv_ring_kernel<_Float16, 256, 8, 256>"
-TRAFFIC_SUMMARY = ROOT / "profiles" / "conv_ring_resblock_c256_fp16_traffic.txt"
+HEADLINE_KERNEL = "conv_wide2_kernel<_Float16>"
+TRAFFIC_SUMMARY = ROOT / "profiles" / "conv_wide2_resblock_c256_fp16_traffic.txt"
 
 
 def measured_traffic():

@@ -1257,6 +1257,286 @@ int launch_wide(const ConvArgs& base, hipStream_t stream) {
   return HI3D_OK;
 }
 
+// ------------------------------------------- 256 x 256 two-slot wide kernel --
+// The wide kernel's 128-byte K steps at the 256 x 256 tile of the ring kernel: each
+// gathered and weight row moves as one 128-byte request per stage (L2-resident gathers
+// of 128-byte rows run ~1.6x the rate of 64-byte ones), at the ring kernel's gathered
+// bytes per flop. A stage is (256 + 256) x 128 bytes = 64 KB, so the ring holds two.
+//  * Tile: 256 output rows (two plan tiles, masks ORed) x 256 channels; 8 waves in a
+//    4 x 2 grid, each 64 rows x 128 channels as 4 x 2 blocks of 32x32x16 MFMAs (weights
+//    first), four K-groups of 16 elements per stage.
+//  * Stage s: K-groups 0..2 (fragment reads of K-groups 1..3 of s, from its slot); a
+//    wait for every outstanding load (those of stage s + 1, issued in K-group 3 of stage
+//    s - 1) and the barrier; K-group 3, whose fragment reads are stage s + 1's K-group
+//    0 and during which the wave issues its 8 loads of stage s + 2 (one after each
+//    MFMA) into the slot of stage s, free after the barrier. A stage's loads thus have
+//    K-group 3 of one stage and K-groups 0..2 of the next (~1,500 MFMA cycles per SIMD)
+//    to land.
+//  * Gather indices as in the other kernels: a two-slot ring, the next offset's 256
+//    indices issued when the load cursor enters an offset (one index DMA per stage,
+//    a dummy otherwise, so the waits stay exact: before each barrier nothing is in
+//    flight but stage s + 1's loads and that DMA).
+//  * Rows use the 128-byte XOR swizzle; the epilogue stages the fp16 tile over both
+//    slots and writes 16-byte row chunks (bias, SiLU, residual as in the ring kernel).
+constexpr int kW2Stage = 65536, kW2StageA = 32768, kW2Idx = 1024;
+
+template <typename T>
+__global__ __launch_bounds__(512, 1) void conv_wide2_kernel(ConvArgs a) {
+  constexpr int BM = 256, BN = 256, NW = 8, WM = 4, NS = 2, SUB = BM / kTileRows;
+  constexpr int MB = 2, NB = 4, NF = MB + NB, NM = MB * NB, LA = 4, LB = 4, L = LA + LB;
+  static_assert(sizeof(T) == 2, "16-bit elements");
+  static_assert(BM * BN * 2 <= NS * kW2Stage && LA * 8 * NW == BM && LB * 8 * NW == BN && L == NM, "shape");
+  __shared__ __attribute__((aligned(16))) char smem[NS * kW2Stage + 3 * kW2Idx + 256];
+  char* const idx_ring = smem + NS * kW2Stage;
+  char* const rows_lds = idx_ring + 2 * kW2Idx;  // the tile's output rows
+  char* const idx_dummy = rows_lds + kW2Idx;     // target of the index DMA of stages entering no offset
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave % WM, wn = wave / WM;
+  const int64_t item = xcd_remap(blockIdx.x, static_cast<int64_t>(gridDim.x));
+  const int64_t tile = item / a.ny;
+  const int n0 = static_cast<int>(item - tile * a.ny) * BN;
+  const int kvol = a.kvol;
+  uint32_t mask = 0;
+#pragma unroll
+  for (int h = 0; h < SUB; ++h) {
+    const int64_t pt = tile * SUB + h;
+    if (pt < a.ntiles) mask |= a.tile_mask[pt];
+  }
+  mask &= (1u << kvol) - 1u;
+  const int rb = a.cin * static_cast<int>(sizeof(T));
+  const int KB = rb >> 7;
+  const int taps = __popc(mask);
+  const int S = taps * KB;
+  const uint64_t n_in = static_cast<uint64_t>(a.n_in);
+
+  // load j of this wave covers rows (wave + NW j) * 8 + lane / 8 at physical chunk
+  // lane % 8, i.e. logical chunk coff / 16 (the swizzle repeats every 16 rows)
+  const int r0 = wave * 8 + (lane >> 3);
+  const int coff = ((lane & 7) ^ ((r0 >> 1) & 7)) * 16;
+  const char* wrow[LB];
+#pragma unroll
+  for (int j = 0; j < LB; ++j)
+    wrow[j] = a.weight + static_cast<int64_t>(n0 + r0 + 8 * NW * j) * kvol * rb + coff;
+  const char* const zrow = reinterpret_cast<const char*>(g_zero_row) + coff;
+
+  // gather indices of offset k into slot `slot`: wave w < 4 covers rows 64 w .. +63
+  // (waves 4..7 repeat wave 3's load)
+  auto issue_idx = [&](int k, int slot) {
+    const int i = wave < BM / 64 ? wave : BM / 64 - 1;
+    int64_t pt = tile * SUB + (i >> 1);
+    if (pt >= a.ntiles) pt = a.ntiles - 1;
+    lds_dma4(a.gidx + (pt * kvol + k) * kTileRows + (i & 1) * 64 + lane, idx_ring + slot * kW2Idx + i * 256);
+  };
+  {  // the tile's output rows reach LDS at the start (complete by the first wait)
+    const int i = wave < BM / 64 ? wave : BM / 64 - 1;
+    int64_t pt = tile * SUB + (i >> 1);
+    if (pt >= a.ntiles) pt = a.ntiles - 1;
+    lds_dma4(a.rows + pt * kTileRows + (i & 1) * 64 + lane, rows_lds + i * 256);
+  }
+
+  uint32_t rest;  // offsets after the current one of the load cursor
+  int ck, ckb, cord;
+  const char* src[LA];
+  auto enter_offset = [&]() {
+    const int32_t* gi = reinterpret_cast<const int32_t*>(idx_ring + (cord & 1) * kW2Idx);
+    int32_t g[LA];
+#pragma unroll
+    for (int j = 0; j < LA; ++j) g[j] = gi[r0 + 8 * NW * j];
+#pragma unroll
+    for (int j = 0; j < LA; ++j) src[j] = gather_src(a.in, g[j], n_in, rb, coff, zrow);
+  };
+  auto advance = [&]() {
+    if (++ckb == KB) {
+      ckb = 0;
+      ck = rest ? __builtin_ctz(rest) : ck;
+      rest &= rest - 1u;
+      ++cord;
+    }
+  };
+  auto issue_load = [&](int slot, int u) {  // u = 0..L-1: LA gathered, then LB weight loads
+    char* st = smem + slot * kW2Stage;
+    if (u < LA)
+      lds_dma16(src[u] + ckb * 128, st + (wave + NW * u) * 1024);
+    else
+      lds_dma16(wrow[u - LA] + ck * rb + ckb * 128, st + kW2StageA + (wave + NW * (u - LA)) * 1024);
+  };
+  // the cursor's stage: enter its offset when it starts one (and fetch the next
+  // offset's indices), else one dummy index DMA
+  auto cursor_indices = [&]() {
+    if (ckb == 0) {
+      wait_lgkm0();
+      enter_offset();
+      issue_idx(rest ? __builtin_ctz(rest) : ck, (cord + 1) & 1);
+    } else {
+      lds_dma4(a.gidx + lane, idx_dummy);
+    }
+  };
+
+  f32x16 acc[NB][MB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[nb][mb][v] = 0.0f;
+  u32x4 fa[2][MB], fb[2][NB];
+  auto frag_one = [&](int slot, auto gc, int i) {  // K-group G of the stage in `slot`
+    constexpr int G = decltype(gc)::value;
+    const char* st = smem + slot * kW2Stage;
+    const int c = 2 * G + (lane >> 5);
+    if (i < NB)
+      fb[G & 1][i] = *reinterpret_cast<const u32x4*>(st + kW2StageA + wide_off(wn * NB * 32 + i * 32 + (lane & 31), c));
+    else
+      fa[G & 1][i - NB] = *reinterpret_cast<const u32x4*>(st + wide_off(wm * 64 + (i - NB) * 32 + (lane & 31), c));
+  };
+  auto mma_one = [&](auto gc, int i) {  // i = nb * MB + mb
+    constexpr int G = decltype(gc)::value;
+    Mfma<T>::run(fb[G & 1][i / MB], fa[G & 1][i % MB], acc[i / MB][i % MB]);
+  };
+  using G0 = std::integral_constant<int, 0>;
+  using G1 = std::integral_constant<int, 1>;
+  using G2 = std::integral_constant<int, 2>;
+  using G3 = std::integral_constant<int, 3>;
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+
+  // Stage s in slot SL. MODE 0: loads of stage s + 2 in K-group 3; 1: s = S - 2 (no
+  // loads); 2: s = S - 1 (no loads, nothing follows).
+  auto stage = [&](int SL, auto modec) {
+    constexpr int MODE = decltype(modec)::value;
+    const int NSL = SL ^ 1;
+    auto group = [&](auto gc) {
+      constexpr int G = decltype(gc)::value;
+      wait_lgkm0();
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < NM; ++i) {
+        mma_one(gc, i);
+        __builtin_amdgcn_sched_barrier(0);
+        if (i < NF) {
+          if constexpr (G < 3)
+            frag_one(SL, std::integral_constant<int, G + 1>{}, i);
+          else if constexpr (MODE != 2)
+            frag_one(NSL, G0{}, i);
+        }
+        if constexpr (G == 3 && MODE == 0) issue_load(SL, i);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
+    group(G0{});
+    group(G1{});
+    group(G2{});
+    if constexpr (MODE != 2) {
+      wait_vmcnt<0>();  // stage s + 1 (and the index DMA issued with it) landed
+      raw_barrier();
+    }
+    if constexpr (MODE == 0) cursor_indices();
+    group(G3{});
+    if constexpr (MODE == 0) advance();
+  };
+
+  if (S > 0) {  // S = taps * KB >= 2
+    ck = mask ? __builtin_ctz(mask) : 0;
+    rest = mask & (mask - 1u);
+    ckb = 0;
+    cord = 0;
+    issue_idx(ck, 0);
+    wait_vmcnt<0>();
+    raw_barrier();
+    // prologue: stages 0 and 1 (the cursor enters offset 0 at stage 0, and offset 1 at
+    // stage 1 when KB = 1... KB >= 2 here, so stage 1 is offset 0's second step)
+    cursor_indices();
+    for (int u = 0; u < L; ++u) issue_load(0, u);
+    advance();
+    if (S > 1) {
+      cursor_indices();
+      for (int u = 0; u < L; ++u) issue_load(1, u);
+      advance();
+    }
+    wait_vmcnt<0>();
+    raw_barrier();
+#pragma unroll
+    for (int i = 0; i < NF; ++i) frag_one(0, G0{}, i);
+
+    int slot = 0;
+    for (int s = 0; s + 2 < S; ++s) {
+      stage(slot, I0{});
+      slot ^= 1;
+    }
+    stage(slot, I1{});
+    stage(slot ^ 1, I2{});
+  }
+
+  // epilogue: each wave stages its 64 x 128 block
+  wait_vmcnt<0>();
+  __syncthreads();
+  const T* bias = static_cast<const T*>(a.bias);
+  constexpr int ROWB = NB * 64, CPR = NB * 4;
+  char* stg = smem + wave * (64 * ROWB);
+  const int cb = n0 + wn * NB * 32;
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int j0 = nb * 32 + 8 * q + 4 * (lane >> 5);
+      float b[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) b[e] = bias != nullptr ? to_f32(bias[cb + j0 + e]) : 0.0f;
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        const int row = mb * 32 + (lane & 31);
+        T h[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float x = acc[nb][mb][4 * q + e] + b[e];
+          if (a.act == HI3D_ACT_SILU) x = silu(x);
+          h[e] = static_cast<T>(x);
+        }
+        uint2 packed;
+        __builtin_memcpy(&packed, h, 8);
+        *reinterpret_cast<uint2*>(stg + row * ROWB + (((j0 >> 3) ^ (row & (CPR - 1))) << 4) + (j0 & 4) * 2) = packed;
+      }
+    }
+  }
+  wait_lgkm0();
+  const int64_t out_row_bytes = static_cast<int64_t>(a.cout) * sizeof(T);
+#pragma unroll 4
+  for (int i = 0; i < CPR; ++i) {
+    const int row = lane / CPR + (64 / CPR) * i;  // 0..63 within this wave's rows
+    const int chunk = lane % CPR;
+    const int tr = wm * 64 + row;
+    const int64_t pt = tile * SUB + tr / kTileRows;
+    if (pt >= a.ntiles) continue;
+    const int32_t orow = reinterpret_cast<const int32_t*>(rows_lds)[tr];
+    if (orow < 0 || orow >= a.n_out) continue;
+    u32x4 v = *reinterpret_cast<const u32x4*>(stg + row * ROWB + ((chunk ^ (row & (CPR - 1))) << 4));
+    const int64_t off = static_cast<int64_t>(orow) * out_row_bytes + static_cast<int64_t>(cb + chunk * 8) * sizeof(T);
+    if (a.residual != nullptr) {
+      const u32x4 r = *reinterpret_cast<const u32x4*>(a.residual + off);
+      T* pv = reinterpret_cast<T*>(&v);
+      const T* pr = reinterpret_cast<const T*>(&r);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) pv[e] = static_cast<T>(to_f32(pv[e]) + to_f32(pr[e]));
+    }
+    *reinterpret_cast<u32x4*>(a.out + off) = v;
+  }
+}
+
+template <typename T>
+int launch_wide2(const ConvArgs& base, hipStream_t stream) {
+  ConvArgs a = base;
+  a.ny = a.cout / 256;
+  const int64_t blocks = ceil_div(a.ntiles, 2) * a.ny;
+  if (blocks == 0) return HI3D_OK;
+  HI3D_REQUIRE(blocks < (int64_t(1) << 31), "too many tiles");
+  hipLaunchKernelGGL(conv_wide2_kernel<T>, dim3(static_cast<unsigned>(blocks)), dim3(512), 0, stream, a);
+  HI3D_LAUNCH_CHECK();
+  return HI3D_OK;
+}
+
 template <typename T, int BM, int BN, int WGM>
 int launch_pipe(const ConvArgs& base, hipStream_t stream) {
   ConvArgs a = base;
@@ -1279,6 +1559,8 @@ int launch_mfma(const ConvArgs& base, hipStream_t stream) {
     // 8 waves for the large tiles; 128-byte K steps for 128-channel tiles, whose gathers
     // are the larger share of their loads (measured: C128 0.46 vs 0.49 ms, C256 8.8 vs
     // 8.9 ms)
+    if (a.kvol <= kMaxPipelinedKvol && rb % 128 == 0 && rb >= 256 && rb <= 1024 && a.cout % 256 == 0)
+      return launch_wide2<T>(a, stream);
     if (a.kvol <= kMaxPipelinedKvol && ring_rows && a.cout % 256 == 0) return launch_ring<T, 256, 8>(a, stream);
     // few-offset tables (the strided pair): 128-row tiles in a 48..64 KB ring, so that two
     // or three workgroups share a CU and cover each other's tile start and end
