@@ -202,10 +202,14 @@ __global__ __launch_bounds__(256) void probe_kernel(const int4* __restrict__ coo
 }
 
 // Dense-grid variant for grids of at most kDenseMaxCells cells: one int32 cell per grid
-// position holds its row (-1 empty). Row ids land by CAS (a second claim is a duplicate,
-// as in the hash), and the lookups of a block's rows read neighbouring cells, nine short
-// z-runs per row, instead of random hash slots.
+// position holds its row (-1 empty). Every row stores its id in its cell (plain stores,
+// the last of two equal coordinates wins) and the lookup flags a duplicate where a row's
+// own cell holds another row; the lookups of a row read nine short z-runs of cells
+// instead of random hash slots.
 constexpr int64_t kDenseMaxCells = int64_t(1) << 31;
+// cells before and after the grid in its buffer (the 12-byte z-runs read one past each
+// end); 16 keep the grid 64-byte aligned
+constexpr int64_t kDensePad = 16;
 
 __global__ void dense_scatter_kernel(const int4* __restrict__ coords, int64_t n, Grid g, int32_t* __restrict__ cells,
                                      int32_t* __restrict__ status) {
@@ -216,8 +220,33 @@ __global__ void dense_scatter_kernel(const int4* __restrict__ coords, int64_t n,
     atomicOr(status, HI3D_MAP_RANGE);
     return;
   }
-  const int32_t prev = atomicCAS(&cells[g.key(c.x, c.y, c.z, c.w)], -1, static_cast<int32_t>(i));
-  if (prev != -1) atomicOr(status, HI3D_MAP_DUPLICATE);
+  cells[g.key(c.x, c.y, c.z, c.w)] = static_cast<int32_t>(i);
+}
+
+// Kept-grid path: rows are visited in cell order (a radix sort of the top kOrderBits bits
+// of their cell keys), so the scatter, the lookups of neighbouring rows and the restore
+// touch neighbouring cells.
+// An out-of-range row is flagged, gets key 0 and the row id ~i (negative), and never
+// touches the grid.
+constexpr int kOrderBits = 16;
+
+__global__ void cell_key_kernel(const int4* __restrict__ coords, int64_t n, Grid g, uint32_t* __restrict__ keys,
+                                int32_t* __restrict__ rows, int32_t* __restrict__ status) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int4 c = coords[i];
+  const bool in = g.inside(c.x, c.y, c.z, c.w);
+  keys[i] = in ? static_cast<uint32_t>(g.key(c.x, c.y, c.z, c.w)) : 0u;
+  rows[i] = in ? static_cast<int32_t>(i) : ~static_cast<int32_t>(i);
+  if (!in) atomicOr(status, HI3D_MAP_RANGE);
+}
+
+// The sorted rows store their ids in their cells.
+__global__ void sorted_scatter_kernel(const uint32_t* __restrict__ keys, const int32_t* __restrict__ rows, int64_t n,
+                                      int32_t* __restrict__ cells) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n || rows[i] < 0) return;
+  cells[keys[i]] = rows[i];
 }
 
 // Puts back the -1 of every cell the scatter may have claimed (out-of-range rows claim
@@ -229,9 +258,21 @@ __global__ void dense_restore_kernel(const int4* __restrict__ coords, int64_t n,
   if (g.inside(c.x, c.y, c.z, c.w)) cells[g.key(c.x, c.y, c.z, c.w)] = -1;
 }
 
+// Puts back the -1 of every cell the sorted rows claimed.
+__global__ void sorted_restore_kernel(const uint32_t* __restrict__ keys, const int32_t* __restrict__ rows, int64_t n,
+                                      int32_t* __restrict__ cells) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n || rows[i] < 0) return;
+  cells[keys[i]] = -1;
+}
+
+// perm (optional): the block's rows are perm[row0 ..] instead of row0 .. (rows in cell
+// order look up neighbouring cells; a negative entry p stands for the row ~p)
 __global__ __launch_bounds__(256) void dense_lookup_kernel(const int4* __restrict__ coords, int64_t n, Grid g,
                                                            int ksize, const int32_t* __restrict__ cells,
-                                                           int32_t* __restrict__ nbr, int32_t* __restrict__ counts) {
+                                                           const int32_t* __restrict__ perm,
+                                                           int32_t* __restrict__ nbr, int32_t* __restrict__ counts,
+                                                           int32_t* __restrict__ status) {
   __shared__ int32_t cnt[kMaxKvol];
   const int kvol = ksize * ksize * ksize;
   const int half = ksize / 2;
@@ -245,10 +286,17 @@ __global__ __launch_bounds__(256) void dense_lookup_kernel(const int4* __restric
   for (int j = threadIdx.x; j < cells_n; j += blockDim.x) {
     const int r = j / kvol;
     const int k = j - r * kvol;
-    const int64_t o = row0 + r;
+    int64_t o = row0 + r;
+    if (perm != nullptr) {
+      const int32_t p = perm[row0 + r];
+      o = p >= 0 ? p : ~p;
+    }
     int32_t found;
     if (k == center) {
       found = static_cast<int32_t>(o);
+      const int4 c = coords[o];
+      if (g.inside(c.x, c.y, c.z, c.w) && cells[g.key(c.x, c.y, c.z, c.w)] != found)
+        atomicOr(status, HI3D_MAP_DUPLICATE);
     } else {
       const int4 c = coords[o];
       const int x = c.y + k / (ksize * ksize) - half;
@@ -266,6 +314,110 @@ __global__ __launch_bounds__(256) void dense_lookup_kernel(const int4* __restric
   __syncthreads();
   for (int k = threadIdx.x; k < kvol; k += blockDim.x)
     if (cnt[k]) atomicAdd(&counts[k], cnt[k]);
+}
+
+// The 3x3x3 lookup with one row per thread: the row's nine z-runs of three cells are
+// nine independent 12-byte loads in flight together (a run starts one cell before the
+// row's z, so the grid keeps a pad cell before and after; runs whose column lies outside
+// the grid load at cell 0, and cells outside the grid are discarded), the counts
+// are summed per wave with ballots, and the block's [256, 27] rows are staged in LDS so
+// that the table is written in runs of whole rows. kPerm: the rows are perm[i] (rows in
+// cell order, a negative entry p standing for the out-of-range row ~p), with their
+// cells decoded from the sorted keys; the blocks then take the row chunks XCD by XCD
+// (block b runs on XCD b % 8 and takes chunk (b % 8) * per + b / 8), so each XCD's L2
+// sees a contiguous run of cells. Else the rows are i.
+constexpr int kLookup3Rows = 256;
+constexpr int kXcds = 8;
+typedef int32_t ZRun __attribute__((ext_vector_type(3), aligned(4)));
+
+template <bool kPerm>
+__global__ __launch_bounds__(kLookup3Rows) void dense_lookup3_kernel(const int4* __restrict__ coords, int64_t n,
+                                                                    Grid g, const int32_t* __restrict__ cells,
+                                                                    const int32_t* __restrict__ perm,
+                                                                    const uint32_t* __restrict__ skeys, int per,
+                                                                    int32_t* __restrict__ nbr,
+                                                                    int32_t* __restrict__ counts,
+                                                                    int32_t* __restrict__ status) {
+  __shared__ int32_t stage[kLookup3Rows * 27];
+  __shared__ int32_t orow[kLookup3Rows];
+  __shared__ int32_t cnt[27];
+  const int t = threadIdx.x;
+  if (t < 27) cnt[t] = 0;
+  const int64_t chunk = kPerm ? static_cast<int64_t>(blockIdx.x % kXcds) * per + blockIdx.x / kXcds : blockIdx.x;
+  const int64_t row0 = chunk * kLookup3Rows;
+  if (row0 >= n) return;  // the XCD order's spare blocks (before any barrier)
+  const int64_t i = row0 + t;
+  const bool live = i < n;
+  const int32_t absent = static_cast<int32_t>(n);
+  int32_t o = 0;
+  int4 c = make_int4(0, -2, -2, -2);  // a dead lane sees no cell inside the grid
+  if (live) {
+    if (kPerm) {
+      const int32_t p = perm[i];
+      if (p >= 0) {
+        o = p;
+        uint32_t key = skeys[i];
+        c.w = static_cast<int>(key % static_cast<uint32_t>(g.sz));
+        key /= static_cast<uint32_t>(g.sz);
+        c.z = static_cast<int>(key % static_cast<uint32_t>(g.sy));
+        key /= static_cast<uint32_t>(g.sy);
+        c.y = static_cast<int>(key % static_cast<uint32_t>(g.sx));
+        c.x = static_cast<int>(key / static_cast<uint32_t>(g.sx));
+      } else {
+        o = ~p;
+        c = coords[o];
+      }
+    } else {
+      o = static_cast<int32_t>(i);
+      c = coords[o];
+    }
+  }
+  orow[t] = o;
+  const bool bin = static_cast<unsigned>(c.x) < static_cast<unsigned>(g.batch);
+  bool okx[3], oky[3], okz[3];
+#pragma unroll
+  for (int d = 0; d < 3; ++d) {
+    okx[d] = bin && static_cast<unsigned>(c.y + d - 1) < static_cast<unsigned>(g.sx);
+    oky[d] = static_cast<unsigned>(c.z + d - 1) < static_cast<unsigned>(g.sy);
+    okz[d] = static_cast<unsigned>(c.w + d - 1) < static_cast<unsigned>(g.sz);
+  }
+  // key of the row's own cell; the neighbours are fixed strides away
+  const int64_t base = ((static_cast<int64_t>(c.x) * g.sx + c.y) * g.sy + c.z) * g.sz + c.w;
+  const int64_t sxs = static_cast<int64_t>(g.sy) * g.sz;
+  int32_t f[27];
+#pragma unroll
+  for (int q = 0; q < 9; ++q) {
+    const int dx = q / 3, dy = q % 3;
+    const bool col = okx[dx] && oky[dy];
+    const int64_t start = col ? base + (dx - 1) * sxs + (dy - 1) * g.sz - 1 : 0;
+    const ZRun v = *reinterpret_cast<const ZRun*>(cells + start);
+    f[q * 3 + 0] = col && okz[0] ? v.x : -1;
+    f[q * 3 + 1] = col && okz[1] ? v.y : -1;
+    f[q * 3 + 2] = col && okz[2] ? v.z : -1;
+  }
+  if (live && f[13] != o && okx[1] && oky[1] && okz[1]) atomicOr(status, HI3D_MAP_DUPLICATE);
+  const int lane = t & 63;
+  __syncthreads();  // cnt cleared
+#pragma unroll
+  for (int k = 0; k < 27; ++k) {
+    int32_t v = f[k] >= 0 ? f[k] : absent;
+    if (k == 13) v = live ? o : absent;
+    const uint64_t hit = __ballot(v != absent);
+    if (lane == 0 && hit != 0) atomicAdd(&cnt[k], static_cast<int32_t>(__popcll(hit)));
+    stage[t * 27 + k] = v;
+  }
+  __syncthreads();
+  const int rows = static_cast<int>(n - row0 < kLookup3Rows ? n - row0 : kLookup3Rows);
+  if (kPerm) {
+    for (int e = t; e < rows * 27; e += kLookup3Rows) {
+      const int r = e / 27;
+      nbr[static_cast<int64_t>(orow[r]) * 27 + (e - r * 27)] = stage[e];
+    }
+  } else {
+    int32_t* dst = nbr + row0 * 27;
+    for (int e = t; e < rows * 27; e += kLookup3Rows) dst[e] = stage[e];
+  }
+  if (t < 27 && cnt[t] != 0) atomicAdd(&counts[t], cnt[t]);
 }
 
 int64_t default_capacity(int64_t n) {
@@ -706,7 +858,18 @@ int hi3d_kmap_dense_workspace(int32_t batch_size, int32_t sx, int32_t sy, int32_
   HI3D_REQUIRE(sx > 0 && sy > 0 && sz > 0 && batch_size > 0, "spatial_shape and batch_size must be positive");
   const int64_t cells = static_cast<int64_t>(batch_size) * sx * sy * sz;
   HI3D_REQUIRE(cells <= kDenseMaxCells, "dense map grid of %lld cells exceeds 2^31", static_cast<long long>(cells));
-  *bytes = align_up(cells * 4, 256);
+  *bytes = align_up((cells + 2 * kDensePad) * 4, 256);
+  return HI3D_OK;
+}
+
+int hi3d_kmap_dense_order_workspace(int64_t n, int64_t* bytes) {
+  HI3D_REQUIRE(bytes != nullptr, "bytes_host is NULL");
+  HI3D_REQUIRE(n >= 0 && n < (int64_t(1) << 31) - 1, "bad voxel count");
+  size_t sort_bytes = 0;
+  hipcub::DoubleBuffer<uint32_t> kb(nullptr, nullptr);
+  hipcub::DoubleBuffer<int32_t> vb(nullptr, nullptr);
+  hipcub::DeviceRadixSort::SortPairs(nullptr, sort_bytes, kb, vb, static_cast<int>(std::max<int64_t>(n, 1)), 0, 32);
+  *bytes = 4 * align_up(n * 4, 256) + align_up(static_cast<int64_t>(sort_bytes), 256);
   return HI3D_OK;
 }
 
@@ -714,11 +877,30 @@ int hi3d_kmap_dense_workspace(int32_t batch_size, int32_t sx, int32_t sy, int32_
 
 namespace {
 
+void launch_dense_lookup(const int4* c4, int64_t n, Grid g, int ksize, const int32_t* cells, const int32_t* perm,
+                         const uint32_t* skeys, int32_t* nbr, int32_t* counts, int32_t* status, hipStream_t stream) {
+  if (ksize == 3) {
+    const int64_t chunks = ceil_div(n, kLookup3Rows);
+    if (perm != nullptr) {
+      const int64_t per = ceil_div(chunks, kXcds);
+      hipLaunchKernelGGL(dense_lookup3_kernel<true>, dim3(static_cast<unsigned>(per * kXcds)), dim3(kLookup3Rows), 0,
+                         stream, c4, n, g, cells, perm, skeys, static_cast<int>(per), nbr, counts, status);
+    } else {
+      hipLaunchKernelGGL(dense_lookup3_kernel<false>, dim3(static_cast<unsigned>(chunks)), dim3(kLookup3Rows), 0,
+                         stream, c4, n, g, cells, perm, skeys, 0, nbr, counts, status);
+    }
+    return;
+  }
+  hipLaunchKernelGGL(dense_lookup_kernel, dim3(static_cast<unsigned>(ceil_div(n, kProbeRows))), dim3(256), 0, stream,
+                     c4, n, g, ksize, cells, perm, nbr, counts, status);
+}
+
 // kept: the grid arrives with every cell -1 and is left that way (the scatter's cells
-// are put back after the lookup), instead of being cleared whole on entry.
+// are put back after the lookup), instead of being cleared whole on entry. order (kept
+// only, may be NULL): workspace for visiting the rows in cell order.
 int kmap_subm_dense(const int32_t* coords, int64_t n, int32_t sx, int32_t sy, int32_t sz, int32_t batch_size,
                     int32_t ksize, void* workspace, int64_t workspace_bytes, int32_t* nbr, int32_t* counts,
-                    int32_t* status, void* stream_, bool kept) {
+                    int32_t* status, void* stream_, bool kept, void* order = nullptr, int64_t order_bytes = 0) {
   hipStream_t stream = as_stream(stream_);
   HI3D_REQUIRE(n >= 0, "n must be non-negative");
   HI3D_REQUIRE(ksize >= 1 && ksize % 2 == 1 && ksize * ksize * ksize <= kMaxKvol,
@@ -738,7 +920,7 @@ int kmap_subm_dense(const int32_t* coords, int64_t n, int32_t sx, int32_t sy, in
   HI3D_REQUIRE(workspace_bytes >= need, "workspace too small: %lld < %lld bytes",
                static_cast<long long>(workspace_bytes), static_cast<long long>(need));
   Grid g{sx, sy, sz, batch_size};
-  auto* cells = static_cast<int32_t*>(workspace);
+  auto* cells = static_cast<int32_t*>(workspace) + kDensePad;
   if (!kept) {
     // clear the grid with 16-byte stores (the workspace is 256-byte aligned)
     const int64_t ncells = static_cast<int64_t>(batch_size) * sx * sy * sz;
@@ -746,10 +928,41 @@ int kmap_subm_dense(const int32_t* coords, int64_t n, int32_t sx, int32_t sy, in
     launch_fill<int32_t>(cells + (ncells & ~int64_t(3)), ncells & 3, -1, stream);
   }
   const int4* c4 = reinterpret_cast<const int4*>(coords);
+  if (kept && order != nullptr) {
+    int64_t order_need = 0;
+    rc = hi3d_kmap_dense_order_workspace(n, &order_need);
+    if (rc != HI3D_OK) return rc;
+    HI3D_REQUIRE(order_bytes >= order_need, "order workspace too small: %lld < %lld bytes",
+                 static_cast<long long>(order_bytes), static_cast<long long>(order_need));
+    const int64_t slab = align_up(n * 4, 256);
+    char* w = static_cast<char*>(order);
+    auto* k0 = reinterpret_cast<uint32_t*>(w);
+    auto* k1 = reinterpret_cast<uint32_t*>(w + slab);
+    auto* r0 = reinterpret_cast<int32_t*>(w + 2 * slab);
+    auto* r1 = reinterpret_cast<int32_t*>(w + 3 * slab);
+    void* temp = w + 4 * slab;
+    size_t temp_bytes = static_cast<size_t>(order_bytes - 4 * slab);
+    const dim3 grid1(static_cast<unsigned>(ceil_div(n, 256)));
+    hipLaunchKernelGGL(cell_key_kernel, grid1, dim3(256), 0, stream, c4, n, g, k0, r0, status);
+    const int64_t ncells = static_cast<int64_t>(batch_size) * sx * sy * sz;
+    int key_bits = 1;
+    while (key_bits < 32 && (int64_t(1) << key_bits) < ncells) ++key_bits;
+    // two radix passes over the key's top 16 bits (batch, x, y bands) give the lookups
+    // their locality; the keys move whole, so every row still knows its cell
+    const int low_bit = key_bits > kOrderBits ? key_bits - kOrderBits : 0;
+    hipcub::DoubleBuffer<uint32_t> kb(k0, k1);
+    hipcub::DoubleBuffer<int32_t> vb(r0, r1);
+    HI3D_HIP_CHECK(
+        hipcub::DeviceRadixSort::SortPairs(temp, temp_bytes, kb, vb, static_cast<int>(n), low_bit, key_bits, stream));
+    hipLaunchKernelGGL(sorted_scatter_kernel, grid1, dim3(256), 0, stream, kb.Current(), vb.Current(), n, cells);
+    launch_dense_lookup(c4, n, g, ksize, cells, vb.Current(), kb.Current(), nbr, counts, status, stream);
+    hipLaunchKernelGGL(sorted_restore_kernel, grid1, dim3(256), 0, stream, kb.Current(), vb.Current(), n, cells);
+    HI3D_LAUNCH_CHECK();
+    return HI3D_OK;
+  }
   hipLaunchKernelGGL(dense_scatter_kernel, dim3(static_cast<unsigned>(ceil_div(n, 256))), dim3(256), 0, stream, c4, n,
                      g, cells, status);
-  hipLaunchKernelGGL(dense_lookup_kernel, dim3(static_cast<unsigned>(ceil_div(n, kProbeRows))), dim3(256), 0, stream,
-                     c4, n, g, ksize, cells, nbr, counts);
+  launch_dense_lookup(c4, n, g, ksize, cells, nullptr, nullptr, nbr, counts, status, stream);
   if (kept)
     hipLaunchKernelGGL(dense_restore_kernel, dim3(static_cast<unsigned>(ceil_div(n, 256))), dim3(256), 0, stream, c4,
                        n, g, cells);
@@ -769,10 +982,10 @@ int hi3d_kmap_subm_dense(const int32_t* coords, int64_t n, int32_t sx, int32_t s
 }
 
 int hi3d_kmap_subm_dense_kept(const int32_t* coords, int64_t n, int32_t sx, int32_t sy, int32_t sz,
-                              int32_t batch_size, int32_t ksize, void* grid, int64_t grid_bytes, int32_t* nbr,
-                              int32_t* counts, int32_t* status, void* stream) {
+                              int32_t batch_size, int32_t ksize, void* grid, int64_t grid_bytes, void* order,
+                              int64_t order_bytes, int32_t* nbr, int32_t* counts, int32_t* status, void* stream) {
   return kmap_subm_dense(coords, n, sx, sy, sz, batch_size, ksize, grid, grid_bytes, nbr, counts, status, stream,
-                         true);
+                         true, order, order_bytes);
 }
 
 int hi3d_kmap_pairs_workspace(int64_t n, int32_t kvol, int64_t* bytes) {

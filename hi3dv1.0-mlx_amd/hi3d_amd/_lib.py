@@ -49,7 +49,8 @@ _SIGNATURES = {
     "hi3d_gather_conv_simple": [_p, _i64, _i32, _p, _p, _i32, _i32, _p, _i64, _p, _i32, _i32, _p, _p],
     "hi3d_kmap_dense_workspace": [_i32, _i32, _i32, _i32, _p],
     "hi3d_kmap_subm_dense": [_p, _i64, _i32, _i32, _i32, _i32, _i32, _p, _i64, _p, _p, _p, _p],
-    "hi3d_kmap_subm_dense_kept": [_p, _i64, _i32, _i32, _i32, _i32, _i32, _p, _i64, _p, _p, _p, _p],
+    "hi3d_kmap_dense_order_workspace": [_i64, _p],
+    "hi3d_kmap_subm_dense_kept": [_p, _i64, _i32, _i32, _i32, _i32, _i32, _p, _i64, _p, _i64, _p, _p, _p, _p],
     "hi3d_parent_table": [_p, _i64, _i32, _p, _i64, _p, _p],
     "hi3d_gather_rows": [_p, _i64, _i32, _p, _i64, _p, _p],
     "hi3d_stride2_up_supported": [_i32, _i32, _i32],

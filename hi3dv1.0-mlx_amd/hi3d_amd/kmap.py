@@ -39,6 +39,14 @@ the grid stays -1 outside a call, and a call touches only its rows' cells) inste
 clearing a per-call grid of 4 bytes per cell. The kept grid holds its memory until
 :func:`release_dense_grids` (4 GiB for a 1024^3 grid)."""
 
+KMAP_DENSE_ORDER_MIN_BYTES: int | None = 256 << 20
+"""With a kept grid of more than this many bytes, visit the rows in cell order (a radix
+sort of their cell keys) so that neighbouring rows store, read and restore neighbouring
+cells whatever order the coordinates arrive in; ``None`` never sorts. Below it the grid
+stays in the GPU's 256 MB last-level cache and the sort costs more than it saves (config
+5, 4.4M randomly ordered voxels at 1024^3: 1.01 ms sorted against 1.19 ms; config 2,
+543k voxels at 256^3: 0.22 against 0.14 ms)."""
+
 KMAP_DENSE_KEEP_BYTES: int = 8 << 30
 """Kept dense grids beyond this many bytes in total are freed, least recently used
 first (the grid of the current build always stays)."""
@@ -270,9 +278,14 @@ def build_kernel_map(
         nbytes = _lib.query("hi3d_kmap_dense_workspace", int(batch_size), sx, sy, sz)
         if KMAP_DENSE_KEEP:
             grid = _kept_grid(device, cells, nbytes)
+            order, order_bytes = None, 0
+            if KMAP_DENSE_ORDER_MIN_BYTES is not None and nbytes > KMAP_DENSE_ORDER_MIN_BYTES and n:
+                order = _lib.workspace(_lib.query("hi3d_kmap_dense_order_workspace", n), device)
+                order_bytes = order.numel()
             _lib.call(
                 "hi3d_kmap_subm_dense_kept",
                 _lib.ptr(coords), n, sx, sy, sz, int(batch_size), int(ksize), _lib.ptr(grid), grid.numel() * 4,
+                _lib.ptr(order), order_bytes,
                 _lib.ptr(table), _lib.ptr(counts), _lib.ptr(status), _lib.stream(device),
             )
         else:

@@ -89,7 +89,7 @@ int hi3d_kmap_subm_noalloc(const int32_t* coords_dev, int64_t n, int32_t sx, int
                            int32_t* status_dev, void* stream);
 
 /* Workspace bytes of hi3d_kmap_subm_dense: one int32 cell per grid position
- * (batch_size*sx*sy*sz <= 2^31). */
+ * (batch_size*sx*sy*sz <= 2^31) and 16 pad cells before and after the grid. */
 int hi3d_kmap_dense_workspace(int32_t batch_size, int32_t sx, int32_t sy, int32_t sz, int64_t* bytes_host);
 
 /* The submanifold kernel map of hi3d_kmap_subm (same table, counts and status flags;
@@ -101,15 +101,23 @@ int hi3d_kmap_subm_dense(const int32_t* coords_dev, int64_t n, int32_t sx, int32
                          int32_t batch_size, int32_t ksize, void* workspace_dev, int64_t workspace_bytes,
                          int32_t* nbr_dev, int32_t* counts_dev, int32_t* status_dev, void* stream);
 
+/* Workspace bytes of the row ordering of hi3d_kmap_subm_dense_kept for n voxels (cell
+ * keys, row ids and a radix sort). */
+int hi3d_kmap_dense_order_workspace(int64_t n, int64_t* bytes_host);
+
 /* hi3d_kmap_subm_dense over a grid that persists between calls: grid_dev (its size
  * from hi3d_kmap_dense_workspace) holds -1 in every cell on entry and is left so on
  * return (the cells the rows claim are put back after the lookup), so a call costs
  * O(n) instead of clearing 4 bytes per grid cell (4 GiB at 1024^3). The caller fills a
- * new grid with -1 once; calls sharing a grid must not overlap. Same reference
- * interface as hi3d_kmap_subm_dense. */
+ * new grid with -1 once; calls sharing a grid must not overlap. order_dev (NULL, or
+ * hi3d_kmap_dense_order_workspace bytes) makes the store, lookup and restore visit the
+ * rows sorted by the top 16 bits of their cell keys, so neighbouring rows read
+ * neighbouring cells whatever the input order; the table, counts and flags are the same
+ * either way. Same reference interface as hi3d_kmap_subm_dense. */
 int hi3d_kmap_subm_dense_kept(const int32_t* coords_dev, int64_t n, int32_t sx, int32_t sy, int32_t sz,
-                              int32_t batch_size, int32_t ksize, void* grid_dev, int64_t grid_bytes, int32_t* nbr_dev,
-                              int32_t* counts_dev, int32_t* status_dev, void* stream);
+                              int32_t batch_size, int32_t ksize, void* grid_dev, int64_t grid_bytes, void* order_dev,
+                              int64_t order_bytes, int32_t* nbr_dev, int32_t* counts_dev, int32_t* status_dev,
+                              void* stream);
 
 /* Workspace bytes of hi3d_kmap_pairs. */
 int hi3d_kmap_pairs_workspace(int64_t n, int32_t kvol, int64_t* bytes_host);

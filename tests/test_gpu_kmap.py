@@ -74,8 +74,15 @@ def test_errors_duplicate_range_overflow(cuda):
     from hi3d_amd import kmap
 
     idx = np.array([[0, 1, 1, 1], [0, 2, 2, 2], [0, 1, 1, 1]], np.int32)
-    with pytest.raises(ValueError, match="duplicate"):
-        kmap.build_kernel_map(torch.as_tensor(idx).to(cuda), [4, 4, 4])
+    for ksize in (1, 3, 5):
+        with pytest.raises(ValueError, match="duplicate"):
+            kmap.build_kernel_map(torch.as_tensor(idx).to(cuda), [4, 4, 4], ksize=ksize)
+    rng = np.random.default_rng(2)
+    many = _rand_indices(rng, 9, 0.4)
+    many = np.concatenate([many, many[::50]])
+    for ksize in (3, 5):
+        with pytest.raises(ValueError, match="duplicate"):
+            kmap.build_kernel_map(torch.as_tensor(many).to(cuda), [9, 9, 9], ksize=ksize)
     idx = np.array([[0, 1, 1, 1], [0, 4, 2, 2]], np.int32)
     with pytest.raises(ValueError, match="outside"):
         kmap.build_kernel_map(torch.as_tensor(idx).to(cuda), [4, 4, 4])
@@ -331,17 +338,30 @@ def test_dense_and_hash_maps_agree(cuda, ksize, batch, n_side, density):
         kmap.KMAP_DENSE_MAX_CELLS = old
 
 
-def test_kept_dense_grid_stays_clear(cuda):
-    """The dense map over a grid kept between calls: each build equals the oracle and the
-    per-call grid's map, and leaves every cell of the kept grid at -1 again, also after a
-    build that reports duplicate or out-of-range coordinates; two different sets in a row
-    on the same grid both come out exact (no cell of the first survives into the second)."""
+@pytest.mark.parametrize("ordered", [True, False])
+def test_kept_dense_grid_stays_clear(cuda, ordered):
+    """The dense map over a grid kept between calls, with the rows visited in cell order
+    or in input order: each build of a shuffled set equals the oracle and the per-call
+    grid's map, and leaves every cell of the kept grid at -1 again, also after a build
+    that reports duplicate or out-of-range coordinates; two different sets in a row on the
+    same grid both come out exact (no cell of the first survives into the second)."""
     from hi3d_amd import kmap
 
     rng = np.random.default_rng(42)
     side = 24
     kmap.release_dense_grids()
     sets = [_rand_indices(rng, side, 0.2, batch=2), _rand_indices(rng, side, 0.05, batch=2)]
+    old_order = kmap.KMAP_DENSE_ORDER_MIN_BYTES
+    kmap.KMAP_DENSE_ORDER_MIN_BYTES = 0 if ordered else None
+    try:
+        _kept_grid_sets(cuda, kmap, sets, side)
+    finally:
+        kmap.KMAP_DENSE_ORDER_MIN_BYTES = old_order
+    kmap.release_dense_grids()
+    assert not kmap._DENSE_GRIDS
+
+
+def _kept_grid_sets(cuda, kmap, sets, side):
     for idx in sets:
         t = torch.as_tensor(idx).to(cuda)
         kept = kmap.build_kernel_map(t, [side] * 3, 2)
@@ -363,5 +383,3 @@ def test_kept_dense_grid_stays_clear(cuda):
         with pytest.raises(ValueError, match="outside"):
             kmap.build_kernel_map(bad, [side] * 3, 2)
         assert bool((grid == -1).all())
-    kmap.release_dense_grids()
-    assert not kmap._DENSE_GRIDS
