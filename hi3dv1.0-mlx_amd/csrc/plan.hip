@@ -34,15 +34,24 @@ __device__ __forceinline__ uint64_t spread3(uint32_t v) {
   return x;
 }
 
-__global__ void morton_kernel(const int4* __restrict__ coords, int64_t n,
-                              unsigned long long* __restrict__ keys, int32_t* __restrict__ rows) {
+// key = batch above the 3 * coord_bits interleaved bits of x, y, z (x highest); K is
+// uint32_t when the sorted bits fit 32.
+template <typename K>
+__global__ void morton_kernel(const int4* __restrict__ coords, int64_t n, int coord_bits, K* __restrict__ keys,
+                              int32_t* __restrict__ rows) {
   int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= n) return;
   int4 c = coords[i];
   uint64_t m = (spread3(static_cast<uint32_t>(c.y)) << 2) | (spread3(static_cast<uint32_t>(c.z)) << 1) |
                spread3(static_cast<uint32_t>(c.w));
-  keys[i] = (static_cast<uint64_t>(static_cast<uint32_t>(c.x) & 0x7f) << 57) | m;
+  keys[i] = static_cast<K>((static_cast<uint64_t>(static_cast<uint32_t>(c.x) & 0x7f) << (3 * coord_bits)) | m);
   rows[i] = static_cast<int32_t>(i);
+}
+
+// Bits of the Morton key to sort on: (coord_bits, batch_bits), 0 = the full 19 and 7.
+int morton_sort_bits(int coord_bits, int batch_bits, int* cb) {
+  *cb = coord_bits > 0 ? coord_bits : 19;
+  return 3 * *cb + (batch_bits > 0 || coord_bits > 0 ? batch_bits : 7);
 }
 
 __global__ void iota_kernel(int32_t* __restrict__ rows, int64_t n) {
@@ -64,20 +73,25 @@ __device__ __forceinline__ void stage_rows(const int32_t* __restrict__ table, co
     const int64_t p = p0 + row;
     return p < n_out ? table[static_cast<int64_t>(order[p]) * kvol + k] : absent;
   };
-  // eight independent loads in flight per thread before their LDS stores
-  constexpr int U = 8;
-  int e = threadIdx.x;
-  for (; e + (U - 1) * bd < total; e += U * bd) {
+  // fourteen independent loads in flight per thread before their LDS stores (two rounds
+  // cover the 27 entries per thread of a 27-offset tile)
+  constexpr int U = 14;
+  for (int base = threadIdx.x; base < total; base += U * bd) {
     int32_t v[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) v[u] = fetch(e + u * bd);
+    for (int u = 0; u < U; ++u) {
+      const int e = base + u * bd;
+      v[u] = e < total ? fetch(e) : 0;
+    }
 #pragma unroll
-    for (int u = 0; u < U; ++u) lds[e + u * bd] = v[u];
+    for (int u = 0; u < U; ++u) {
+      const int e = base + u * bd;
+      if (e < total) lds[e] = v[u];
+    }
   }
-  for (; e < total; e += bd) lds[e] = fetch(e);
 }
 
-// key = (window << 32) | presence mask, for rows taken in Morton order.
+// key = (window << 27) | presence-mask key, for rows taken in Morton order.
 constexpr int kMaskRows = 256;
 // Sort key of a 3x3x3 presence mask: its bits reordered so that the 8 corner offsets
 // are the most significant, then the 12 edges, the 6 faces and the centre. On surfaces
@@ -94,26 +108,50 @@ __device__ __forceinline__ uint32_t subm_mask_key(uint32_t mask) {
   return key;
 }
 
-__global__ __launch_bounds__(kMaskRows) void mask_keys_kernel(const int32_t* __restrict__ table, int64_t n_out,
-                                                              int kvol, int64_t n_in,
-                                                              const int32_t* __restrict__ order, int64_t window,
-                                                              unsigned long long* __restrict__ keys,
-                                                              int32_t* __restrict__ rows) {
+// The presence-mask sort key of every row, in row order (the table read as one
+// contiguous block per kMaskRows rows). kvol <= 32.
+__global__ __launch_bounds__(kMaskRows) void row_mask_kernel(const int32_t* __restrict__ table, int64_t n_out,
+                                                             int kvol, int64_t n_in, uint32_t* __restrict__ masks) {
   __shared__ int32_t staged[kMaskRows * 32];
   const int64_t p0 = static_cast<int64_t>(blockIdx.x) * kMaskRows;
-  const int64_t p = p0 + threadIdx.x;
-  uint32_t mask = 0;
-  if (kvol <= 32) {
-    stage_rows(table, order, p0, n_out, kvol, kMaskRows, static_cast<int32_t>(n_in), staged);
-    __syncthreads();
-    const int32_t* t = staged + threadIdx.x * kvol;
-    for (int k = 0; k < kvol; ++k)
-      if (static_cast<uint64_t>(static_cast<uint32_t>(t[k])) < static_cast<uint64_t>(n_in)) mask |= 1u << k;
+  const int rows = static_cast<int>(n_out - p0 < kMaskRows ? n_out - p0 : kMaskRows);
+  const int32_t* src = table + p0 * kvol;
+  const int total = rows * kvol;
+  // fourteen independent loads in flight per thread before their LDS stores
+  constexpr int U = 14;
+  for (int base = threadIdx.x; base < total; base += U * kMaskRows) {
+    int32_t v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int e = base + u * kMaskRows;
+      v[u] = e < total ? src[e] : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int e = base + u * kMaskRows;
+      if (e < total) staged[e] = v[u];
+    }
   }
+  __syncthreads();
+  if (static_cast<int>(threadIdx.x) >= rows) return;
+  const int32_t* t = staged + threadIdx.x * kvol;
+  uint32_t mask = 0;
+  for (int k = 0; k < kvol; ++k)
+    if (static_cast<uint64_t>(static_cast<uint32_t>(t[k])) < static_cast<uint64_t>(n_in)) mask |= 1u << k;
+  masks[p0 + threadIdx.x] = kvol == 27 ? subm_mask_key(mask) : mask;
+}
+
+// masks: the rows' mask keys in row order (NULL: no mask, kvol > 32).
+template <typename K>
+__global__ void mask_keys_kernel(const uint32_t* __restrict__ masks, int64_t n_out, int mask_bits,
+                                 const int32_t* __restrict__ order, int64_t window, K* __restrict__ keys,
+                                 int32_t* __restrict__ rows) {
+  const int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (p >= n_out) return;
+  const int32_t row = order[p];
   const uint64_t w = window > 0 ? static_cast<uint64_t>(p / window) : 0;
-  keys[p] = (w << 32) | (kvol == 27 ? subm_mask_key(mask) : mask);
-  rows[p] = order[p];
+  keys[p] = static_cast<K>((w << mask_bits) | (masks != nullptr ? masks[row] : 0u));
+  rows[p] = row;
 }
 
 // One block of kTileRows threads per tile: output rows, transposed gather indices and
@@ -247,11 +285,37 @@ __global__ __launch_bounds__(kHaloRows) void halo_tile_kernel(const int32_t* __r
 }
 
 size_t sort_temp_bytes(int64_t n) {
-  size_t bytes = 0;
+  const int m = static_cast<int>(std::max<int64_t>(n, 1));
+  size_t bytes64 = 0, bytes32 = 0;
   hipcub::DoubleBuffer<unsigned long long> kb(nullptr, nullptr);
+  hipcub::DoubleBuffer<uint32_t> kb32(nullptr, nullptr);
   hipcub::DoubleBuffer<int32_t> vb(nullptr, nullptr);
-  hipcub::DeviceRadixSort::SortPairs(nullptr, bytes, kb, vb, static_cast<int>(std::max<int64_t>(n, 1)), 0, 64);
-  return bytes;
+  hipcub::DeviceRadixSort::SortPairs(nullptr, bytes64, kb, vb, m, 0, 64);
+  hipcub::DeviceRadixSort::SortPairs(nullptr, bytes32, kb32, vb, m, 0, 32);
+  return std::max(bytes64, bytes32);
+}
+
+// Sorts (keys, rows) on key bits [0, bits) with 32-bit keys when they fit, else 64-bit
+// ones; kbuf0 / kbuf1 hold n 64-bit keys each, rows start in r0. fill(k) launches the
+// kernel that writes the keys into k (uint32_t* or unsigned long long*) and the rows
+// into r0. *sorted receives the sorted rows (r0 or r1).
+template <typename Fill>
+hipError_t sort_rows(void* temp, size_t temp_bytes, unsigned long long* kbuf0, unsigned long long* kbuf1, int32_t* r0,
+                     int32_t* r1, int n, int bits, hipStream_t stream, Fill fill, const int32_t** sorted) {
+  hipcub::DoubleBuffer<int32_t> vb(r0, r1);
+  hipError_t e;
+  if (bits <= 32) {
+    auto* k0 = reinterpret_cast<uint32_t*>(kbuf0);
+    fill(k0);
+    hipcub::DoubleBuffer<uint32_t> kb(k0, reinterpret_cast<uint32_t*>(kbuf1));
+    e = hipcub::DeviceRadixSort::SortPairs(temp, temp_bytes, kb, vb, n, 0, std::max(bits, 1), stream);
+  } else {
+    fill(kbuf0);
+    hipcub::DoubleBuffer<unsigned long long> kb(kbuf0, kbuf1);
+    e = hipcub::DeviceRadixSort::SortPairs(temp, temp_bytes, kb, vb, n, 0, bits, stream);
+  }
+  *sorted = vb.Current();
+  return e;
 }
 
 }  // namespace
@@ -267,19 +331,21 @@ int hi3d_conv_plan_workspace(int64_t n_out, int64_t* bytes) {
   HI3D_REQUIRE(bytes != nullptr, "bytes_host is NULL");
   HI3D_REQUIRE(n_out >= 0 && n_out < (int64_t(1) << 31) - 1, "bad n_out");
   const int64_t m = std::max<int64_t>(n_out, 1);
-  *bytes = 2 * align_up(m * 8, 256) + 2 * align_up(m * 4, 256) + align_up(static_cast<int64_t>(sort_temp_bytes(m)), 256) + 256;
+  *bytes = 2 * align_up(m * 8, 256) + 3 * align_up(m * 4, 256) + align_up(static_cast<int64_t>(sort_temp_bytes(m)), 256) + 256;
   return HI3D_OK;
 }
 
 int hi3d_conv_plan(const int32_t* table, int64_t n_out, int32_t kvol, int64_t n_in, const int32_t* coords,
-                   int64_t window_rows, void* workspace, int64_t workspace_bytes, int32_t* rows, int32_t* gidx,
-                   uint32_t* tile_mask, void* stream_) {
+                   int32_t coord_bits, int32_t batch_bits, int64_t window_rows, void* workspace,
+                   int64_t workspace_bytes, int32_t* rows, int32_t* gidx, uint32_t* tile_mask, void* stream_) {
   hipStream_t stream = as_stream(stream_);
   int64_t need = 0;
   int rc = hi3d_conv_plan_workspace(n_out, &need);
   if (rc != HI3D_OK) return rc;
   HI3D_REQUIRE(kvol >= 1 && kvol <= 1024, "kvol out of range: %d", kvol);
   HI3D_REQUIRE(n_in >= 0 && n_in < (int64_t(1) << 31) - 1, "bad n_in");
+  HI3D_REQUIRE(coord_bits >= 0 && coord_bits <= 19 && batch_bits >= 0 && batch_bits <= 7,
+               "coord_bits must be in [0, 19] and batch_bits in [0, 7]");
   if (n_out == 0) return HI3D_OK;
   HI3D_REQUIRE(table && rows && gidx && tile_mask && workspace, "null pointer argument");
   HI3D_REQUIRE(workspace_bytes >= need, "workspace too small");
@@ -288,18 +354,20 @@ int hi3d_conv_plan(const int32_t* table, int64_t n_out, int32_t kvol, int64_t n_
   auto* k1 = ws.take<unsigned long long>(n_out);
   auto* r0 = ws.take<int32_t>(n_out);
   auto* r1 = ws.take<int32_t>(n_out);
+  auto* masks = ws.take<uint32_t>(n_out);
   size_t temp_bytes = sort_temp_bytes(n_out);
   void* temp = ws.take<char>(static_cast<int64_t>(temp_bytes));
   const unsigned blocks = static_cast<unsigned>(ceil_div(n_out, 256));
   const int n = static_cast<int>(n_out);
   const int32_t* order = nullptr;
   if (coords) {
-    hipLaunchKernelGGL(morton_kernel, dim3(blocks), dim3(256), 0, stream, reinterpret_cast<const int4*>(coords),
-                       n_out, k0, r0);
-    hipcub::DoubleBuffer<unsigned long long> kb(k0, k1);
-    hipcub::DoubleBuffer<int32_t> vb(r0, r1);
-    HI3D_HIP_CHECK(hipcub::DeviceRadixSort::SortPairs(temp, temp_bytes, kb, vb, n, 0, 64, stream));
-    order = vb.Current();
+    int cb = 0;
+    const int morton_bits = morton_sort_bits(coord_bits, batch_bits, &cb);
+    const int4* c4 = reinterpret_cast<const int4*>(coords);
+    HI3D_HIP_CHECK(sort_rows(
+        temp, temp_bytes, k0, k1, r0, r1, n, morton_bits, stream,
+        [&](auto* k) { hipLaunchKernelGGL(morton_kernel, dim3(blocks), dim3(256), 0, stream, c4, n_out, cb, k, r0); },
+        &order));
   } else {
     hipLaunchKernelGGL(iota_kernel, dim3(blocks), dim3(256), 0, stream, r0, n_out);
     order = r0;
@@ -307,24 +375,26 @@ int hi3d_conv_plan(const int32_t* table, int64_t n_out, int32_t kvol, int64_t n_
   // second key: (window, mask); the sort is stable, so Morton order survives inside
   int32_t* ord_in = const_cast<int32_t*>(order);
   int32_t* ord_alt = (ord_in == r0) ? r1 : r0;
-  hipLaunchKernelGGL(mask_keys_kernel, dim3(static_cast<unsigned>(ceil_div(n_out, kMaskRows))), dim3(kMaskRows), 0,
-                     stream, table, n_out, kvol, n_in, ord_in,
-                     window_rows, k0, ord_alt);
-  int64_t windows = window_rows > 0 ? ceil_div(n_out, window_rows) : 1;
-  int end_bit = 32;
-  while (end_bit < 64 && (int64_t(1) << (end_bit - 32)) < windows) ++end_bit;
-  const int begin_bit = 0;
   const int mask_bits = kvol <= 32 ? kvol : 0;
-  const int32_t* final_order = ord_alt;
-  if (mask_bits > 0 || windows > 1) {
-    // mask occupies bits [0, kvol); windows bits [32, end_bit)
-    hipcub::DoubleBuffer<unsigned long long> kb(k0, k1);
-    hipcub::DoubleBuffer<int32_t> vb(ord_alt, ord_in);
-    if (windows > 1 || mask_bits > 0) {
-      const int eb = windows > 1 ? end_bit : std::max(mask_bits, 1);
-      HI3D_HIP_CHECK(hipcub::DeviceRadixSort::SortPairs(temp, temp_bytes, kb, vb, n, begin_bit, eb, stream));
-    }
-    final_order = vb.Current();
+  if (mask_bits > 0)
+    hipLaunchKernelGGL(row_mask_kernel, dim3(static_cast<unsigned>(ceil_div(n_out, kMaskRows))), dim3(kMaskRows), 0,
+                       stream, table, n_out, kvol, n_in, masks);
+  const int64_t windows = window_rows > 0 ? ceil_div(n_out, window_rows) : 1;
+  int window_bits = 0;
+  while ((int64_t(1) << window_bits) < windows) ++window_bits;
+  const uint32_t* mk = mask_bits > 0 ? masks : nullptr;
+  const int32_t* final_order = nullptr;
+  auto fill = [&](auto* k) {
+    hipLaunchKernelGGL(mask_keys_kernel, dim3(blocks), dim3(256), 0, stream, mk, n_out, mask_bits, ord_in,
+                       window_rows, k, ord_alt);
+  };
+  if (mask_bits + window_bits > 0) {
+    // mask in bits [0, mask_bits), window above it
+    HI3D_HIP_CHECK(sort_rows(temp, temp_bytes, k0, k1, ord_alt, ord_in, n, mask_bits + window_bits, stream, fill,
+                             &final_order));
+  } else {
+    fill(reinterpret_cast<uint32_t*>(k0));
+    final_order = ord_alt;
   }
   const int64_t ntiles = ceil_div(n_out, kTileRows);
   hipLaunchKernelGGL(tile_kernel, dim3(static_cast<unsigned>(ntiles)), dim3(kTileRows), 0, stream, table, n_out,
@@ -339,14 +409,17 @@ int hi3d_halo_plan_workspace(int64_t n_out, int64_t* bytes) {
 }
 
 int hi3d_halo_plan(const int32_t* table, int64_t n_out, int32_t kvol, int64_t n_in, const int32_t* coords,
-                   void* workspace, int64_t workspace_bytes, int32_t* rows, int32_t* halo, int32_t* hcount,
-                   uint16_t* loff, uint32_t* bmask, int32_t* overflow, void* stream_) {
+                   int32_t coord_bits, int32_t batch_bits, void* workspace, int64_t workspace_bytes, int32_t* rows,
+                   int32_t* halo, int32_t* hcount, uint16_t* loff, uint32_t* bmask, int32_t* overflow,
+                   void* stream_) {
   hipStream_t stream = as_stream(stream_);
   int64_t need = 0;
   int rc = hi3d_halo_plan_workspace(n_out, &need);
   if (rc != HI3D_OK) return rc;
   HI3D_REQUIRE(kvol == kHaloKvol, "halo plans cover 27-offset maps (got %d offsets)", kvol);
   HI3D_REQUIRE(n_in >= 0 && n_in < (int64_t(1) << 31) - 1, "bad n_in");
+  HI3D_REQUIRE(coord_bits >= 0 && coord_bits <= 19 && batch_bits >= 0 && batch_bits <= 7,
+               "coord_bits must be in [0, 19] and batch_bits in [0, 7]");
   HI3D_REQUIRE(overflow != nullptr, "null pointer argument");
   launch_fill(overflow, 1, int32_t(0), stream);
   if (n_out == 0) return HI3D_OK;
@@ -362,12 +435,13 @@ int hi3d_halo_plan(const int32_t* table, int64_t n_out, int32_t kvol, int64_t n_
   const unsigned blocks = static_cast<unsigned>(ceil_div(n_out, 256));
   const int32_t* order = r0;
   if (coords) {
-    hipLaunchKernelGGL(morton_kernel, dim3(blocks), dim3(256), 0, stream, reinterpret_cast<const int4*>(coords),
-                       n_out, k0, r0);
-    hipcub::DoubleBuffer<unsigned long long> kb(k0, k1);
-    hipcub::DoubleBuffer<int32_t> vb(r0, r1);
-    HI3D_HIP_CHECK(hipcub::DeviceRadixSort::SortPairs(temp, temp_bytes, kb, vb, static_cast<int>(n_out), 0, 64, stream));
-    order = vb.Current();
+    int cb = 0;
+    const int morton_bits = morton_sort_bits(coord_bits, batch_bits, &cb);
+    const int4* c4 = reinterpret_cast<const int4*>(coords);
+    HI3D_HIP_CHECK(sort_rows(
+        temp, temp_bytes, k0, k1, r0, r1, static_cast<int>(n_out), morton_bits, stream,
+        [&](auto* k) { hipLaunchKernelGGL(morton_kernel, dim3(blocks), dim3(256), 0, stream, c4, n_out, cb, k, r0); },
+        &order));
   } else {
     hipLaunchKernelGGL(iota_kernel, dim3(blocks), dim3(256), 0, stream, r0, n_out);
   }

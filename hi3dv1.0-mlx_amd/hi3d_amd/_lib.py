@@ -44,7 +44,7 @@ _SIGNATURES = {
     "hi3d_child_neighbour_table": [_p, _p, _i64, _p, _i64, _p, _p, _p, _p, _p],
     "hi3d_conv_tile_rows": [],
     "hi3d_conv_plan_workspace": [_i64, _p],
-    "hi3d_conv_plan": [_p, _i64, _i32, _i64, _p, _i64, _p, _i64, _p, _p, _p, _p],
+    "hi3d_conv_plan": [_p, _i64, _i32, _i64, _p, _i32, _i32, _i64, _p, _i64, _p, _p, _p, _p],
     "hi3d_gather_conv": [_p, _i64, _i32, _p, _p, _i32, _i32, _p, _p, _p, _i64, _p, _i32, _i32, _p, _p],
     "hi3d_gather_conv_simple": [_p, _i64, _i32, _p, _p, _i32, _i32, _p, _i64, _p, _i32, _i32, _p, _p],
     "hi3d_kmap_dense_workspace": [_i32, _i32, _i32, _i32, _p],
@@ -65,7 +65,7 @@ _SIGNATURES = {
     "hi3d_halo_tile_rows": [],
     "hi3d_halo_capacity": [],
     "hi3d_halo_plan_workspace": [_i64, _p],
-    "hi3d_halo_plan": [_p, _i64, _i32, _i64, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _p],
+    "hi3d_halo_plan": [_p, _i64, _i32, _i64, _p, _i32, _i32, _p, _i64, _p, _p, _p, _p, _p, _p, _p],
     "hi3d_halo_conv": [_p, _i64, _i32, _p, _p, _i32, _p, _p, _p, _i64, _p, _i32, _i32, _p, _p],
     "hi3d_w8a8_quantize": [_p, _i64, _i32, _p, _p, _p, _p],
     "hi3d_w8a8_gemm": [_p, _p, _p, _p, _p, _i64, _i32, _i32, _p, _p, _p],

@@ -118,9 +118,24 @@ class HaloPlan:
         return int(self.hcount.shape[0])
 
 
-def build_halo_plan(table: torch.Tensor, n_in: int, coords: torch.Tensor | None = None) -> HaloPlan | None:
+def morton_bits(spatial_shape: Sequence[int], batch_size: int) -> tuple[int, int]:
+    """``(coord_bits, batch_bits)`` of the Morton sort for coordinates inside
+    ``spatial_shape`` and batch indices below ``batch_size``: the plan sorts on
+    ``3 * coord_bits + batch_bits`` key bits instead of 64 (four radix passes instead of
+    eight at 1024^3)."""
+    coord_bits = max(1, (max(int(v) for v in spatial_shape) - 1).bit_length())
+    batch_bits = (int(batch_size) - 1).bit_length()
+    if coord_bits > 19 or batch_bits > 7:
+        return (0, 0)
+    return (coord_bits, batch_bits)
+
+
+def build_halo_plan(
+    table: torch.Tensor, n_in: int, coords: torch.Tensor | None = None, bits: tuple[int, int] | None = None
+) -> HaloPlan | None:
     """Halo plan of ``table [n_out, 27]``, or None when a tile's halo exceeds the
-    kernel's capacity (callers then use the tile plan)."""
+    kernel's capacity (callers then use the tile plan). ``bits``: :func:`morton_bits` of
+    the coordinates' grid (None: the full 64-bit Morton key)."""
     device = _lib.require_gpu(table, coords)
     table = table.to(torch.int32).contiguous()
     n_out, kvol = int(table.shape[0]), int(table.shape[1])
@@ -142,7 +157,8 @@ def build_halo_plan(table: torch.Tensor, n_in: int, coords: torch.Tensor | None 
     ws = _lib.workspace(_lib.query("hi3d_halo_plan_workspace", n_out), device)
     _lib.call(
         "hi3d_halo_plan",
-        _lib.ptr(table), n_out, kvol, int(n_in), _lib.ptr(coords), _lib.ptr(ws), ws.numel(), _lib.ptr(rows),
+        _lib.ptr(table), n_out, kvol, int(n_in), _lib.ptr(coords), *(bits or (0, 0)), _lib.ptr(ws), ws.numel(),
+        _lib.ptr(rows),
         _lib.ptr(halo), _lib.ptr(hcount), _lib.ptr(loff), _lib.ptr(bmask), _lib.ptr(overflow), _lib.stream(device),
     )
     if int(overflow.item()) != 0:
@@ -164,6 +180,7 @@ class ConvPlan:
     kvol: int
     table: torch.Tensor
     coords: torch.Tensor | None = None
+    bits: tuple[int, int] | None = None
     _halo: list = field(default_factory=list, repr=False)
 
     @property
@@ -175,14 +192,20 @@ class ConvPlan:
         or a tile's halo does not fit)."""
         if not self._halo:
             ok = self.kvol == 27 and self.n_out == self.n_in
-            self._halo.append(build_halo_plan(self.table, self.n_in, self.coords) if ok else None)
+            self._halo.append(build_halo_plan(self.table, self.n_in, self.coords, self.bits) if ok else None)
         return self._halo[0]
 
 
 def build_plan(
-    table: torch.Tensor, n_in: int, coords: torch.Tensor | None = None, window_rows: int | None = None
+    table: torch.Tensor,
+    n_in: int,
+    coords: torch.Tensor | None = None,
+    window_rows: int | None = None,
+    bits: tuple[int, int] | None = None,
 ) -> ConvPlan:
-    """Plan a gather convolution over ``table [n_out, kvol]`` (entries >= n_in absent)."""
+    """Plan a gather convolution over ``table [n_out, kvol]`` (entries >= n_in absent).
+    ``bits``: :func:`morton_bits` of the coordinates' grid (None: the full 64-bit Morton
+    key; coordinates beyond the bits still give a valid plan, in a coarser order)."""
     device = _lib.require_gpu(table, coords)
     table = table.to(torch.int32).contiguous()
     n_out, kvol = int(table.shape[0]), int(table.shape[1])
@@ -202,10 +225,10 @@ def build_plan(
     ws = _lib.workspace(_lib.query("hi3d_conv_plan_workspace", n_out), device)
     _lib.call(
         "hi3d_conv_plan",
-        _lib.ptr(table), n_out, kvol, int(n_in), _lib.ptr(coords), int(window_rows),
+        _lib.ptr(table), n_out, kvol, int(n_in), _lib.ptr(coords), *(bits or (0, 0)), int(window_rows),
         _lib.ptr(ws), ws.numel(), _lib.ptr(rows), _lib.ptr(gidx), _lib.ptr(tile_mask), _lib.stream(device),
     )
-    return ConvPlan(rows, gidx, tile_mask, n_out, int(n_in), kvol, table, coords)
+    return ConvPlan(rows, gidx, tile_mask, n_out, int(n_in), kvol, table, coords, bits)
 
 
 @dataclass
@@ -240,7 +263,9 @@ class KernelMap:
     def plan(self, window_rows: int | None = None) -> ConvPlan:
         key = window_rows
         if key not in self._plans:
-            self._plans[key] = build_plan(self.table, self.n, self.indices, window_rows)
+            self._plans[key] = build_plan(
+                self.table, self.n, self.indices, window_rows, morton_bits(self.spatial_shape, self.batch_size)
+            )
         return self._plans[key]
 
 
@@ -378,12 +403,14 @@ class Stride2Structure:
 
     def down_plan(self) -> ConvPlan:
         if "down" not in self._plans:
-            self._plans["down"] = build_plan(self.down, self.n_fine, self.low)
+            bits = morton_bits(self.out_spatial_shape, 128)  # batch indices fit 7 bits
+            self._plans["down"] = build_plan(self.down, self.n_fine, self.low, bits=bits)
         return self._plans["down"]
 
     def up_plan(self) -> ConvPlan:
         if "up" not in self._plans:
-            self._plans["up"] = build_plan(self.up, self.n_coarse, self.fine_indices)
+            bits = morton_bits(self.spatial_shape, 128)
+            self._plans["up"] = build_plan(self.up, self.n_coarse, self.fine_indices, bits=bits)
         return self._plans["up"]
 
 

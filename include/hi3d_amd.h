@@ -204,14 +204,18 @@ int hi3d_conv_plan_workspace(int64_t n_out, int64_t* bytes_host);
  * are absent): output rows are ordered by Morton code of coords_dev (NULL = row
  * order), then grouped by their neighbour-presence mask within windows of
  * window_rows rows (0 = one window), and cut into tiles of hi3d_conv_tile_rows() rows.
+ * coord_bits (<= 19) and batch_bits (<= 7) bound the coordinates and batch indices
+ * (< 2^bits) so that the Morton sort runs over 3 * coord_bits + batch_bits key bits;
+ * 0 and 0 sort the full 64-bit key. Coordinates beyond the bits still give a valid
+ * plan, in a coarser order.
  * Outputs: rows_dev [ntiles*T] (output row per tile slot, -1 past n_out),
  * gidx_dev [ntiles, kvol, T] (input row per tile slot and offset, n_in if absent) and
  * tile_mask_dev [ntiles] (offsets present in the tile; kvol <= 32, else all ones).
  * Built once per coordinate set and reused by every convolution over it, like the
  * reference's indice_dict cache (src/sparc3d/ops/sparse_backend.py:52-56,124-127). */
 int hi3d_conv_plan(const int32_t* table_dev, int64_t n_out, int32_t kvol, int64_t n_in,
-                   const int32_t* coords_dev, int64_t window_rows, void* workspace_dev,
-                   int64_t workspace_bytes, int32_t* rows_dev, int32_t* gidx_dev,
+                   const int32_t* coords_dev, int32_t coord_bits, int32_t batch_bits, int64_t window_rows,
+                   void* workspace_dev, int64_t workspace_bytes, int32_t* rows_dev, int32_t* gidx_dev,
                    uint32_t* tile_mask_dev, void* stream);
 
 /* Gather-MFMA convolution: out[o] = act(bias + sum_k in[table[o,k]] . W[:, k, :]^T)
@@ -314,7 +318,8 @@ int32_t hi3d_halo_capacity(void);
 int hi3d_halo_plan_workspace(int64_t n_out, int64_t* bytes_host);
 
 /* Halo plan of a 27-offset submanifold table_dev [n_out, 27] (entries >= n_in absent):
- * output rows in Morton order of coords_dev (NULL = row order), cut into tiles of
+ * output rows in Morton order of coords_dev (NULL = row order; coord_bits and batch_bits as
+ * for hi3d_conv_plan), cut into tiles of
  * hi3d_halo_tile_rows() rows. Per tile: rows_dev [ntiles*256] (output row per slot, -1
  * past n_out), halo_dev [ntiles, 768] (sorted unique input rows touched by the tile,
  * n_in where unused), hcount_dev [ntiles], loff_dev [ntiles*256, 32] (halo position of
@@ -324,9 +329,9 @@ int hi3d_halo_plan_workspace(int64_t n_out, int64_t* bytes_host);
  * Same role as hi3d_conv_plan: built once per coordinate set and cached with the map
  * (src/sparc3d/ops/sparse_backend.py:52-56,124-127). */
 int hi3d_halo_plan(const int32_t* table_dev, int64_t n_out, int32_t kvol, int64_t n_in,
-                   const int32_t* coords_dev, void* workspace_dev, int64_t workspace_bytes,
-                   int32_t* rows_dev, int32_t* halo_dev, int32_t* hcount_dev, uint16_t* loff_dev,
-                   uint32_t* bmask_dev, int32_t* overflow_dev, void* stream);
+                   const int32_t* coords_dev, int32_t coord_bits, int32_t batch_bits, void* workspace_dev,
+                   int64_t workspace_bytes, int32_t* rows_dev, int32_t* halo_dev, int32_t* hcount_dev,
+                   uint16_t* loff_dev, uint32_t* bmask_dev, int32_t* overflow_dev, void* stream);
 
 /* The submanifold 3x3x3 convolution of hi3d_gather_conv over a halo plan: each tile's
  * halo is gathered into LDS once per 64-byte K step and shared by all 27 offsets. fp16
