@@ -128,7 +128,8 @@ def bench_subm(name: str, grid: int, cin: int, cout: int, dtype, steps: int, war
     hash_wall, hash_ev = timed(lambda: kmap.build_kernel_map(coords, [grid] * 3, 1, capacity=0, check=False), 5, 2)
     _, fresh_ev = timed(dense_fresh(lambda: kmap.build_kernel_map(coords, [grid] * 3, 1, check=False)), 5, 2)
     km = kmap.build_kernel_map(coords, [grid] * 3, 1)
-    plan_wall, plan_ev = timed(lambda: kmap.build_plan(km.table, km.n, km.indices), 3, 1)
+    bits = kmap.morton_bits(km.spatial_shape, km.batch_size)  # as KernelMap.plan() builds it
+    plan_wall, plan_ev = timed(lambda: kmap.build_plan(km.table, km.n, km.indices, None, bits), 3, 1)
     plan = km.plan()
     pairs = int(km.counts.sum())
     out = torch.empty((n, cout), dtype=dtype, device=dev)
@@ -253,7 +254,8 @@ def bench_block(steps: int, warmup: int, settle_s: float = 0.0):
     hash_wall, hash_ev = timed(lambda: kmap.build_kernel_map(coords, [1024] * 3, 1, capacity=0, check=False), 3, 1)
     _, fresh_ev = timed(dense_fresh(lambda: kmap.build_kernel_map(coords, [1024] * 3, 1, check=False)), 3, 1)
     km = kmap.build_kernel_map(coords, [1024] * 3, 1)
-    plan_wall, plan_ev = timed(lambda: kmap.build_plan(km.table, km.n, km.indices), 3, 1)
+    bits = kmap.morton_bits(km.spatial_shape, km.batch_size)  # as KernelMap.plan() builds it
+    plan_wall, plan_ev = timed(lambda: kmap.build_plan(km.table, km.n, km.indices, None, bits), 3, 1)
     plan = km.plan()
     pairs = int(km.counts.sum())
     x = torch.as_tensor(workloads.normal((n, c), 1.0, 52, np.float16)).to(dev)

@@ -59,23 +59,22 @@ __global__ void iota_kernel(int32_t* __restrict__ rows, int64_t n) {
   if (i < n) rows[i] = static_cast<int32_t>(i);
 }
 
-// The table rows order[p0 .. p0 + nrows) into LDS as [row][kvol] (absent past n_out):
-// consecutive threads read consecutive entries of a row, so a wave's loads touch a few
-// rows' contiguous entries instead of one entry of 64 scattered rows.
-__device__ __forceinline__ void stage_rows(const int32_t* __restrict__ table, const int32_t* __restrict__ order,
-                                           int64_t p0, int64_t n_out, int kvol, int nrows, int32_t absent,
-                                           int32_t* __restrict__ lds) {
+// The table rows srow[0 .. nrows) (srow in LDS; -1 = absent row) into LDS as
+// [row][kvol], kvol <= 32, nrows <= blockDim.x: consecutive threads read consecutive
+// entries of a row, so a wave's loads touch a few rows' contiguous entries instead of
+// one entry of 64 scattered rows.
+__device__ __forceinline__ void stage_rows(const int32_t* __restrict__ table, const int32_t* __restrict__ srow,
+                                           int kvol, int nrows, int32_t absent, int32_t* __restrict__ lds) {
   const int total = nrows * kvol;
   const int bd = blockDim.x;
   auto fetch = [&](int e) -> int32_t {
     const int row = e / kvol;
     const int k = e - row * kvol;
-    const int64_t p = p0 + row;
-    return p < n_out ? table[static_cast<int64_t>(order[p]) * kvol + k] : absent;
+    const int32_t src = srow[row];
+    return src >= 0 ? table[static_cast<int64_t>(src) * kvol + k] : absent;
   };
-  // fourteen independent loads in flight per thread before their LDS stores (two rounds
-  // cover the 27 entries per thread of a 27-offset tile)
-  constexpr int U = 14;
+  // all of a thread's (at most 32) loads in flight before their LDS stores
+  constexpr int U = 32;
   for (int base = threadIdx.x; base < total; base += U * bd) {
     int32_t v[U];
 #pragma unroll
@@ -164,6 +163,7 @@ __global__ __launch_bounds__(kTileRows) void tile_kernel(const int32_t* __restri
                                                          uint32_t* __restrict__ tile_mask) {
   __shared__ uint32_t wave_mask[kTileRows / 64];
   __shared__ int32_t staged[kTileRows * 32];
+  __shared__ int32_t srow[kTileRows];
   const int64_t tile = blockIdx.x;
   const int r = threadIdx.x;
   const int64_t p = tile * kTileRows + r;
@@ -173,7 +173,9 @@ __global__ __launch_bounds__(kTileRows) void tile_kernel(const int32_t* __restri
   int32_t* g = gidx + tile * kvol * kTileRows + r;
   const int32_t absent = static_cast<int32_t>(n_in);
   if (kvol <= 32) {
-    stage_rows(table, order, tile * kTileRows, n_out, kvol, kTileRows, absent, staged);
+    srow[r] = row;
+    __syncthreads();
+    stage_rows(table, srow, kvol, kTileRows, absent, staged);
     __syncthreads();
     const int32_t* t = staged + r * kvol;
     for (int k = 0; k < kvol; ++k) {
