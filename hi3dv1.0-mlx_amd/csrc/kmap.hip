@@ -14,7 +14,6 @@
 // 2^32 - 1) and its row share one 64-bit slot, so one 64-bit CAS inserts both; wider keys
 // use a 64-bit key array plus a row array. Probing writes each (row, offset) cell of the
 // table exactly once, so the table does not depend on insertion order.
-#include <hipcub/hipcub.hpp>
 
 #include <algorithm>
 #include <cstdarg>
@@ -22,6 +21,7 @@
 #include <mutex>
 
 #include "common.h"
+#include "radix.h"
 
 namespace hi3d {
 
@@ -452,18 +452,31 @@ __global__ __launch_bounds__(256) void pair_count_kernel(const int32_t* __restri
 __global__ __launch_bounds__(1024) void pair_scan_kernel(int32_t* __restrict__ block_counts,
                                                          int64_t nblocks,
                                                          int64_t* __restrict__ totals) {
-  typedef hipcub::BlockScan<int64_t, 1024> Scan;
-  __shared__ typename Scan::TempStorage tmp;
+  __shared__ int64_t wsum[16];
   __shared__ int64_t carry;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   int32_t* row = block_counts + static_cast<int64_t>(blockIdx.x) * nblocks;
   if (threadIdx.x == 0) carry = 0;
   __syncthreads();
   for (int64_t base = 0; base < nblocks; base += 1024) {
-    int64_t idx = base + threadIdx.x;
-    int64_t v = idx < nblocks ? row[idx] : 0;
-    int64_t excl, agg;
-    Scan(tmp).ExclusiveSum(v, excl, agg);
-    if (idx < nblocks) row[idx] = static_cast<int32_t>(carry + excl);
+    const int64_t idx = base + threadIdx.x;
+    const int64_t v = idx < nblocks ? row[idx] : 0;
+    int64_t x = v;  // inclusive scan within the wave, then across the 16 waves
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int64_t y = __shfl_up(x, d, 64);
+      if (lane >= d) x += y;
+    }
+    if (lane == 63) wsum[w] = x;
+    __syncthreads();
+    int64_t off = 0, agg = 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int64_t p = wsum[i];
+      off += i < w ? p : 0;
+      agg += p;
+    }
+    if (idx < nblocks) row[idx] = static_cast<int32_t>(carry + off + x - v);
     __syncthreads();
     if (threadIdx.x == 0) carry += agg;
     __syncthreads();
@@ -865,11 +878,7 @@ int hi3d_kmap_dense_workspace(int32_t batch_size, int32_t sx, int32_t sy, int32_
 int hi3d_kmap_dense_order_workspace(int64_t n, int64_t* bytes) {
   HI3D_REQUIRE(bytes != nullptr, "bytes_host is NULL");
   HI3D_REQUIRE(n >= 0 && n < (int64_t(1) << 31) - 1, "bad voxel count");
-  size_t sort_bytes = 0;
-  hipcub::DoubleBuffer<uint32_t> kb(nullptr, nullptr);
-  hipcub::DoubleBuffer<int32_t> vb(nullptr, nullptr);
-  hipcub::DeviceRadixSort::SortPairs(nullptr, sort_bytes, kb, vb, static_cast<int>(std::max<int64_t>(n, 1)), 0, 32);
-  *bytes = 4 * align_up(n * 4, 256) + align_up(static_cast<int64_t>(sort_bytes), 256);
+  *bytes = 4 * align_up(n * 4, 256) + radix::temp_bytes(n);
   return HI3D_OK;
 }
 
@@ -941,7 +950,7 @@ int kmap_subm_dense(const int32_t* coords, int64_t n, int32_t sx, int32_t sy, in
     auto* r0 = reinterpret_cast<int32_t*>(w + 2 * slab);
     auto* r1 = reinterpret_cast<int32_t*>(w + 3 * slab);
     void* temp = w + 4 * slab;
-    size_t temp_bytes = static_cast<size_t>(order_bytes - 4 * slab);
+    const int64_t temp_bytes = order_bytes - 4 * slab;
     const dim3 grid1(static_cast<unsigned>(ceil_div(n, 256)));
     hipLaunchKernelGGL(cell_key_kernel, grid1, dim3(256), 0, stream, c4, n, g, k0, r0, status);
     const int64_t ncells = static_cast<int64_t>(batch_size) * sx * sy * sz;
@@ -950,13 +959,10 @@ int kmap_subm_dense(const int32_t* coords, int64_t n, int32_t sx, int32_t sy, in
     // two radix passes over the key's top 16 bits (batch, x, y bands) give the lookups
     // their locality; the keys move whole, so every row still knows its cell
     const int low_bit = key_bits > kOrderBits ? key_bits - kOrderBits : 0;
-    hipcub::DoubleBuffer<uint32_t> kb(k0, k1);
-    hipcub::DoubleBuffer<int32_t> vb(r0, r1);
-    HI3D_HIP_CHECK(
-        hipcub::DeviceRadixSort::SortPairs(temp, temp_bytes, kb, vb, static_cast<int>(n), low_bit, key_bits, stream));
-    hipLaunchKernelGGL(sorted_scatter_kernel, grid1, dim3(256), 0, stream, kb.Current(), vb.Current(), n, cells);
-    launch_dense_lookup(c4, n, g, ksize, cells, vb.Current(), kb.Current(), nbr, counts, status, stream);
-    hipLaunchKernelGGL(sorted_restore_kernel, grid1, dim3(256), 0, stream, kb.Current(), vb.Current(), n, cells);
+    HI3D_HIP_CHECK(radix::sort_pairs(temp, temp_bytes, k0, k1, r0, r1, n, low_bit, key_bits, stream));
+    hipLaunchKernelGGL(sorted_scatter_kernel, grid1, dim3(256), 0, stream, k0, r0, n, cells);
+    launch_dense_lookup(c4, n, g, ksize, cells, r0, k0, nbr, counts, status, stream);
+    hipLaunchKernelGGL(sorted_restore_kernel, grid1, dim3(256), 0, stream, k0, r0, n, cells);
     HI3D_LAUNCH_CHECK();
     return HI3D_OK;
   }
@@ -1024,21 +1030,11 @@ int hi3d_kmap_pairs(const int32_t* nbr, int64_t n, int32_t kvol, void* workspace
   return HI3D_OK;
 }
 
-static size_t downsample_sort_bytes(int64_t n) {
-  size_t sort_bytes = 0, scan_bytes = 0;
-  hipcub::DoubleBuffer<unsigned long long> kb(nullptr, nullptr);
-  hipcub::DoubleBuffer<int32_t> vb(nullptr, nullptr);
-  hipcub::DeviceRadixSort::SortPairs(nullptr, sort_bytes, kb, vb, static_cast<int>(n), 0, 64);
-  hipcub::DeviceScan::InclusiveSum(nullptr, scan_bytes, static_cast<int32_t*>(nullptr),
-                                   static_cast<int32_t*>(nullptr), static_cast<int>(n));
-  return std::max(sort_bytes, scan_bytes);
-}
-
 int hi3d_downsample_workspace(int64_t n, int64_t* bytes) {
   HI3D_REQUIRE(bytes != nullptr, "bytes_host is NULL");
   HI3D_REQUIRE(n >= 0 && n < (int64_t(1) << 31) - 1, "bad n");
   const int64_t m = std::max<int64_t>(n, 1);
-  *bytes = 2 * align_up(m * 8, 256) + 3 * align_up(m * 4, 256) + align_up(static_cast<int64_t>(downsample_sort_bytes(m)), 256) + 256;
+  *bytes = 2 * align_up(m * 8, 256) + 3 * align_up(m * 4, 256) + radix::temp_bytes(m) + 256;
   return HI3D_OK;
 }
 
@@ -1067,24 +1063,25 @@ int hi3d_downsample_structure(const int32_t* coords, int64_t n, int32_t sx, int3
   auto* r0 = ws.take<int32_t>(n);
   auto* r1 = ws.take<int32_t>(n);
   auto* ids = ws.take<int32_t>(n);
-  size_t temp_bytes = downsample_sort_bytes(n);
-  void* temp = ws.take<char>(static_cast<int64_t>(temp_bytes));
+  const int64_t temp_bytes = radix::temp_bytes(n);
+  void* temp = ws.take<char>(temp_bytes);
   const unsigned blocks = static_cast<unsigned>(ceil_div(n, 256));
   const int4* c4 = reinterpret_cast<const int4*>(coords);
   const uint64_t space = static_cast<uint64_t>(batch_size) * hx * hy * hz * 8;  // cells x slots
   HI3D_REQUIRE(space < (uint64_t(1) << 62), "grid too large for 64-bit keys");
   hipLaunchKernelGGL(half_keys_kernel, dim3(blocks), dim3(256), 0, stream, c4, n, batch_size, sx, sy, sz, hx, hy, hz,
                      k0, r0, status);
-  hipcub::DoubleBuffer<unsigned long long> kb(k0, k1);
-  hipcub::DoubleBuffer<int32_t> vb(r0, r1);
   int end_bit = 1;
   while (end_bit < 64 && (1ull << end_bit) < space) ++end_bit;
-  HI3D_HIP_CHECK(hipcub::DeviceRadixSort::SortPairs(temp, temp_bytes, kb, vb, static_cast<int>(n), 0, end_bit, stream));
-  const unsigned long long* sk = kb.Current();
-  const int32_t* sr = vb.Current();
+  unsigned long long* ka = k0;
+  unsigned long long* kalt = k1;
+  int32_t* ra = r0;
+  int32_t* ralt = r1;
+  HI3D_HIP_CHECK(radix::sort_pairs(temp, temp_bytes, ka, kalt, ra, ralt, n, 0, end_bit, stream));
+  const unsigned long long* sk = ka;
+  const int32_t* sr = ra;
   hipLaunchKernelGGL(run_heads_kernel, dim3(blocks), dim3(256), 0, stream, sk, n, ids, status);
-  size_t scan_bytes = temp_bytes;
-  HI3D_HIP_CHECK(hipcub::DeviceScan::InclusiveSum(temp, scan_bytes, ids, ids, static_cast<int>(n), stream));
+  HI3D_HIP_CHECK(radix::scan(temp, temp_bytes, ids, ids, n, true, stream));
   hipLaunchKernelGGL(coarse_emit_kernel, dim3(blocks), dim3(256), 0, stream, sk, sr, ids, n, hx, hy, hz, c4,
                      reinterpret_cast<int4*>(low), inverse, counts, slot, n_low);
   hipLaunchKernelGGL(coarse_counts_kernel, dim3(blocks), dim3(256), 0, stream, ids, n, sk, counts);
@@ -1145,10 +1142,7 @@ int hi3d_child_table_workspace(int64_t n_parents, int64_t* bytes) {
   HI3D_REQUIRE(bytes != nullptr, "bytes_host is NULL");
   HI3D_REQUIRE(n_parents >= 0 && n_parents * 8 < (int64_t(1) << 31) - 16, "bad n_parents");
   const int64_t m = std::max<int64_t>(n_parents * 8, 1);
-  size_t scan_bytes = 0;
-  hipcub::DeviceScan::ExclusiveSum(nullptr, scan_bytes, static_cast<int32_t*>(nullptr),
-                                   static_cast<int32_t*>(nullptr), static_cast<int>(m));
-  *bytes = 2 * align_up(m * 4, 256) + align_up((m + 8) * 4, 256) + align_up(static_cast<int64_t>(scan_bytes), 256);
+  *bytes = 2 * align_up(m * 4, 256) + align_up((m + 8) * 4, 256) + radix::temp_bytes(m);
   return HI3D_OK;
 }
 
@@ -1172,12 +1166,11 @@ int hi3d_child_neighbour_table(const int32_t* parent_table, const uint8_t* mask,
   int32_t* flags = ws.take<int32_t>(m);
   int32_t* excl = ws.take<int32_t>(m);
   int32_t* lookup = ws.take<int32_t>(m + 8);
-  size_t scan_bytes = 0;
-  hipcub::DeviceScan::ExclusiveSum(nullptr, scan_bytes, flags, excl, static_cast<int>(m));
-  void* temp = ws.take<char>(static_cast<int64_t>(scan_bytes));
+  const int64_t scan_bytes = radix::temp_bytes(m);
+  void* temp = ws.take<char>(scan_bytes);
   const unsigned blocks = static_cast<unsigned>(ceil_div(m, 256));
   hipLaunchKernelGGL(mask_to_int_kernel, dim3(blocks), dim3(256), 0, stream, mask, m, flags);
-  HI3D_HIP_CHECK(hipcub::DeviceScan::ExclusiveSum(temp, scan_bytes, flags, excl, static_cast<int>(m), stream));
+  HI3D_HIP_CHECK(radix::scan(temp, scan_bytes, flags, excl, m, false, stream));
   hipLaunchKernelGGL(child_index_kernel, dim3(blocks), dim3(256), 0, stream, mask, excl, m, lookup, parent, slot,
                      n_children);
   static const ChildTables tables = make_child_tables();

@@ -9,12 +9,11 @@
 // output rows, the transposed gather indices [kvol][kTileRows] (one contiguous run per
 // offset) and the union mask. Output rows are written once each: the "scatter" is a
 // permuted row store, no atomics.
-#include <hipcub/hipcub.hpp>
-
 #include <algorithm>
 
 #include "common.h"
 #include "conv_tile.h"
+#include "radix.h"
 
 namespace hi3d {
 namespace {
@@ -217,13 +216,12 @@ __global__ __launch_bounds__(kHaloRows) void halo_tile_kernel(const int32_t* __r
                                                               int32_t* __restrict__ halo, int32_t* __restrict__ hcount,
                                                               uint16_t* __restrict__ loff, uint32_t* __restrict__ bmask,
                                                               int32_t* __restrict__ overflow) {
-  using Sort = hipcub::BlockRadixSort<uint32_t, kHaloRows, kHaloKvol, uint32_t>;
-  using Scan = hipcub::BlockScan<int, kHaloRows>;
-  __shared__ union {
-    typename Sort::TempStorage sort;
-    typename Scan::TempStorage scan;
-  } tmp;
+  static_assert(kHaloRows == radix::kThreads, "the block sort runs one thread per tile row");
   __shared__ uint32_t sorted[kHaloRows * kHaloKvol];
+  __shared__ uint32_t sorted_vals[kHaloRows * kHaloKvol];
+  __shared__ int32_t wcount[radix::kWaves][radix::kBins];
+  __shared__ int32_t lstart[radix::kBins];
+  __shared__ int32_t part[radix::kWaves];
   const int64_t tile = blockIdx.x;
   const int r = threadIdx.x;
   const int64_t p = tile * kHaloRows + r;
@@ -249,11 +247,13 @@ __global__ __launch_bounds__(kHaloRows) void halo_tile_kernel(const int32_t* __r
 #pragma unroll
   for (int d = 16; d >= 1; d >>= 1) mask |= __shfl_xor(mask, d, 64);
   if ((r & 31) == 0) bmask[tile * (kHaloRows / 32) + (r >> 5)] = mask;
-  Sort(tmp.sort).Sort(keys, vals, 0, key_bits);  // blocked: thread r holds sorted ranks r*27 .. r*27+26
-  __syncthreads();
+  radix::block_sort_pairs(keys, vals, key_bits, sorted, sorted_vals, wcount, lstart, part);
+  // thread r takes sorted ranks r*27 .. r*27+26
 #pragma unroll
-  for (int i = 0; i < kHaloKvol; ++i) sorted[r * kHaloKvol + i] = keys[i];
-  __syncthreads();
+  for (int i = 0; i < kHaloKvol; ++i) {
+    keys[i] = sorted[r * kHaloKvol + i];
+    vals[i] = sorted_vals[r * kHaloKvol + i];
+  }
   int heads = 0;
 #pragma unroll
   for (int i = 0; i < kHaloKvol; ++i) {
@@ -261,8 +261,8 @@ __global__ __launch_bounds__(kHaloRows) void halo_tile_kernel(const int32_t* __r
     const uint32_t prev = pos > 0 ? sorted[pos - 1] : 0xffffffffu;
     heads += (keys[i] < absent && keys[i] != prev) ? 1 : 0;
   }
-  int base = 0, total = 0;
-  Scan(tmp.scan).ExclusiveSum(heads, base, total);
+  int total = 0;
+  const int base = radix::block_exclusive(heads, part, &total);
   uint16_t* lt = loff + tile * kHaloRows * 32;
   int32_t* ht = halo + tile * kHaloMax;
   int run = base - 1;  // halo position of the current run
@@ -286,37 +286,26 @@ __global__ __launch_bounds__(kHaloRows) void halo_tile_kernel(const int32_t* __r
   }
 }
 
-size_t sort_temp_bytes(int64_t n) {
-  const int m = static_cast<int>(std::max<int64_t>(n, 1));
-  size_t bytes64 = 0, bytes32 = 0;
-  hipcub::DoubleBuffer<unsigned long long> kb(nullptr, nullptr);
-  hipcub::DoubleBuffer<uint32_t> kb32(nullptr, nullptr);
-  hipcub::DoubleBuffer<int32_t> vb(nullptr, nullptr);
-  hipcub::DeviceRadixSort::SortPairs(nullptr, bytes64, kb, vb, m, 0, 64);
-  hipcub::DeviceRadixSort::SortPairs(nullptr, bytes32, kb32, vb, m, 0, 32);
-  return std::max(bytes64, bytes32);
-}
+int64_t sort_temp_bytes(int64_t n) { return radix::temp_bytes(std::max<int64_t>(n, 1)); }
 
 // Sorts (keys, rows) on key bits [0, bits) with 32-bit keys when they fit, else 64-bit
 // ones; kbuf0 / kbuf1 hold n 64-bit keys each, rows start in r0. fill(k) launches the
 // kernel that writes the keys into k (uint32_t* or unsigned long long*) and the rows
 // into r0. *sorted receives the sorted rows (r0 or r1).
 template <typename Fill>
-hipError_t sort_rows(void* temp, size_t temp_bytes, unsigned long long* kbuf0, unsigned long long* kbuf1, int32_t* r0,
+hipError_t sort_rows(void* temp, int64_t temp_bytes, unsigned long long* kbuf0, unsigned long long* kbuf1, int32_t* r0,
                      int32_t* r1, int n, int bits, hipStream_t stream, Fill fill, const int32_t** sorted) {
-  hipcub::DoubleBuffer<int32_t> vb(r0, r1);
   hipError_t e;
   if (bits <= 32) {
     auto* k0 = reinterpret_cast<uint32_t*>(kbuf0);
+    auto* k1 = reinterpret_cast<uint32_t*>(kbuf1);
     fill(k0);
-    hipcub::DoubleBuffer<uint32_t> kb(k0, reinterpret_cast<uint32_t*>(kbuf1));
-    e = hipcub::DeviceRadixSort::SortPairs(temp, temp_bytes, kb, vb, n, 0, std::max(bits, 1), stream);
+    e = radix::sort_pairs(temp, temp_bytes, k0, k1, r0, r1, n, 0, std::max(bits, 1), stream);
   } else {
     fill(kbuf0);
-    hipcub::DoubleBuffer<unsigned long long> kb(kbuf0, kbuf1);
-    e = hipcub::DeviceRadixSort::SortPairs(temp, temp_bytes, kb, vb, n, 0, bits, stream);
+    e = radix::sort_pairs(temp, temp_bytes, kbuf0, kbuf1, r0, r1, n, 0, bits, stream);
   }
-  *sorted = vb.Current();
+  *sorted = r0;
   return e;
 }
 
@@ -333,7 +322,7 @@ int hi3d_conv_plan_workspace(int64_t n_out, int64_t* bytes) {
   HI3D_REQUIRE(bytes != nullptr, "bytes_host is NULL");
   HI3D_REQUIRE(n_out >= 0 && n_out < (int64_t(1) << 31) - 1, "bad n_out");
   const int64_t m = std::max<int64_t>(n_out, 1);
-  *bytes = 2 * align_up(m * 8, 256) + 3 * align_up(m * 4, 256) + align_up(static_cast<int64_t>(sort_temp_bytes(m)), 256) + 256;
+  *bytes = 2 * align_up(m * 8, 256) + 3 * align_up(m * 4, 256) + sort_temp_bytes(m) + 256;
   return HI3D_OK;
 }
 
@@ -357,8 +346,8 @@ int hi3d_conv_plan(const int32_t* table, int64_t n_out, int32_t kvol, int64_t n_
   auto* r0 = ws.take<int32_t>(n_out);
   auto* r1 = ws.take<int32_t>(n_out);
   auto* masks = ws.take<uint32_t>(n_out);
-  size_t temp_bytes = sort_temp_bytes(n_out);
-  void* temp = ws.take<char>(static_cast<int64_t>(temp_bytes));
+  const int64_t temp_bytes = sort_temp_bytes(n_out);
+  void* temp = ws.take<char>(temp_bytes);
   const unsigned blocks = static_cast<unsigned>(ceil_div(n_out, 256));
   const int n = static_cast<int>(n_out);
   const int32_t* order = nullptr;
@@ -432,8 +421,8 @@ int hi3d_halo_plan(const int32_t* table, int64_t n_out, int32_t kvol, int64_t n_
   auto* k1 = ws.take<unsigned long long>(n_out);
   auto* r0 = ws.take<int32_t>(n_out);
   auto* r1 = ws.take<int32_t>(n_out);
-  size_t temp_bytes = sort_temp_bytes(n_out);
-  void* temp = ws.take<char>(static_cast<int64_t>(temp_bytes));
+  const int64_t temp_bytes = sort_temp_bytes(n_out);
+  void* temp = ws.take<char>(temp_bytes);
   const unsigned blocks = static_cast<unsigned>(ceil_div(n_out, 256));
   const int32_t* order = r0;
   if (coords) {

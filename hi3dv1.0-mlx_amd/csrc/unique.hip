@@ -9,11 +9,10 @@
 // sorted index; counts are differences of first indices. Results equal
 // np.unique(keys, return_inverse=True, return_counts=True) bit for bit.
 
-#include <hipcub/hipcub.hpp>
-
 #include <algorithm>
 
 #include "common.h"
+#include "radix.h"
 
 namespace hi3d {
 namespace {
@@ -127,21 +126,6 @@ __global__ void row_bounds_kernel(const T* __restrict__ rows, int64_t n, int d, 
   }
 }
 
-size_t unique_sort_bytes(int64_t n) {
-  size_t bytes = 0;
-  hipcub::DoubleBuffer<unsigned long long> kb(nullptr, nullptr);
-  hipcub::DoubleBuffer<int32_t> vb(nullptr, nullptr);
-  hipcub::DeviceRadixSort::SortPairs(nullptr, bytes, kb, vb, static_cast<int>(std::max<int64_t>(n, 1)), 0, 64);
-  return bytes;
-}
-
-size_t unique_scan_bytes(int64_t n) {
-  size_t bytes = 0;
-  hipcub::DeviceScan::InclusiveSum(nullptr, bytes, static_cast<int32_t*>(nullptr), static_cast<int32_t*>(nullptr),
-                                   static_cast<int>(std::max<int64_t>(n, 1)));
-  return bytes;
-}
-
 }  // namespace
 }  // namespace hi3d
 
@@ -151,8 +135,7 @@ extern "C" int hi3d_unique_keys_workspace(int64_t n, int64_t* bytes) {
   HI3D_REQUIRE(bytes != nullptr, "bytes_host is NULL");
   HI3D_REQUIRE(n >= 0 && n < (int64_t(1) << 31) - 1, "n out of range: %lld", static_cast<long long>(n));
   const int64_t m = std::max<int64_t>(n, 1);
-  *bytes = 2 * align_up(m * 8, 256) + 5 * align_up(m * 4, 256) +
-           align_up(static_cast<int64_t>(std::max(unique_sort_bytes(m), unique_scan_bytes(m))), 256) + 256;
+  *bytes = 2 * align_up(m * 8, 256) + 5 * align_up(m * 4, 256) + radix::temp_bytes(m) + 256;
   return HI3D_OK;
 }
 
@@ -180,22 +163,23 @@ extern "C" int hi3d_unique_keys(const int64_t* keys, int64_t n, int32_t key_bits
   auto* head = ws.take<int32_t>(n);
   auto* run = ws.take<int32_t>(n);
   auto* first = ws.take<int32_t>(n);
-  size_t temp_bytes = std::max(unique_sort_bytes(n), unique_scan_bytes(n));
-  void* temp = ws.take<char>(static_cast<int64_t>(temp_bytes));
+  const int64_t temp_bytes = radix::temp_bytes(n);
+  void* temp = ws.take<char>(temp_bytes);
   const unsigned blocks = static_cast<unsigned>(ceil_div(n, 256));
-  const int ni = static_cast<int>(n);
   // keys within [0, 2^key_bits) sort on those bits as they are; any int64 sorts on all
   // 64 bits with the sign bit flipped
   const unsigned long long flip = key_bits == 0 ? kSignFlip : 0ull;
   const int end_bit = key_bits == 0 ? 64 : key_bits;
   hipLaunchKernelGGL(unique_prep_kernel, dim3(blocks), dim3(256), 0, stream, keys, n, flip, k0, p0);
-  hipcub::DoubleBuffer<unsigned long long> kb(k0, k1);
-  hipcub::DoubleBuffer<int32_t> vb(p0, p1);
-  HI3D_HIP_CHECK(hipcub::DeviceRadixSort::SortPairs(temp, temp_bytes, kb, vb, ni, 0, end_bit, stream));
-  const unsigned long long* sk = kb.Current();
-  const int32_t* pos = vb.Current();
+  unsigned long long* ka = k0;
+  unsigned long long* kalt = k1;
+  int32_t* pa = p0;
+  int32_t* palt = p1;
+  HI3D_HIP_CHECK(radix::sort_pairs(temp, temp_bytes, ka, kalt, pa, palt, n, 0, end_bit, stream));
+  const unsigned long long* sk = ka;
+  const int32_t* pos = pa;
   hipLaunchKernelGGL(unique_heads_kernel, dim3(blocks), dim3(256), 0, stream, sk, n, head);
-  HI3D_HIP_CHECK(hipcub::DeviceScan::InclusiveSum(temp, temp_bytes, head, run, ni, stream));
+  HI3D_HIP_CHECK(radix::scan(temp, temp_bytes, head, run, n, true, stream));
   hipLaunchKernelGGL(unique_scatter_kernel, dim3(blocks), dim3(256), 0, stream, sk, pos, head, run, n, flip, uniq,
                      inverse, first, n_unique);
   if (counts)

@@ -50,6 +50,9 @@ _SIGNATURES = {
     "hi3d_kmap_dense_workspace": [_i32, _i32, _i32, _i32, _p],
     "hi3d_kmap_subm_dense": [_p, _i64, _i32, _i32, _i32, _i32, _i32, _p, _i64, _p, _p, _p, _p],
     "hi3d_kmap_dense_order_workspace": [_i64, _p],
+    "hi3d_sort_pairs_workspace": [_i64, _p],
+    "hi3d_sort_pairs": [_p, _p, _p, _p, _i64, _i32, _i32, _i32, _p, _i64, _p, _p],
+    "hi3d_scan": [_p, _p, _i64, _i32, _p, _i64, _p],
     "hi3d_kmap_subm_dense_kept": [_p, _i64, _i32, _i32, _i32, _i32, _i32, _p, _i64, _p, _i64, _p, _p, _p, _p],
     "hi3d_parent_table": [_p, _i64, _i32, _p, _i64, _p, _p],
     "hi3d_gather_rows": [_p, _i64, _i32, _p, _i64, _p, _p],

@@ -268,6 +268,27 @@ int hi3d_parent_table(const int32_t* table_dev, int64_t n, int32_t kvol, const i
 int hi3d_gather_rows(const void* in_dev, int64_t n_in, int32_t row_bytes, const int32_t* index_dev, int64_t n,
                      void* out_dev, void* stream);
 
+/* ------------------------------------------------------------- sort and scan -- */
+
+/* Workspace bytes of hi3d_sort_pairs and hi3d_scan for n elements. */
+int hi3d_sort_pairs_workspace(int64_t n, int64_t* bytes_host);
+
+/* Stable LSD radix sort (8-bit digits) of n (key, int32 value) pairs by key bits
+ * [begin_bit, end_bit): keys_dev (uint32 for key_bytes 4, uint64 for 8) and vals_dev
+ * hold the input, keys_alt_dev / vals_alt_dev are scratch of the same sizes; the sorted
+ * pairs end in the alternate buffers when *in_alt_host is 1 (an odd number of 8-bit
+ * passes), else in keys_dev / vals_dev. The sort behind the kernel-map, plan, stride-2
+ * and unique builds (the reference sorts with torch.sort / torch.unique /
+ * mx.argsort, src/hi3d_mac/fast_unique.py:25-56). */
+int hi3d_sort_pairs(void* keys_dev, void* keys_alt_dev, int32_t* vals_dev, int32_t* vals_alt_dev, int64_t n,
+                    int32_t key_bytes, int32_t begin_bit, int32_t end_bit, void* workspace_dev,
+                    int64_t workspace_bytes, int32_t* in_alt_host, void* stream);
+
+/* out_dev[i] = sum of in_dev[0 .. i) (inclusive = 0) or in_dev[0 .. i] (inclusive = 1),
+ * int32; out_dev may be in_dev. Workspace from hi3d_sort_pairs_workspace. */
+int hi3d_scan(const int32_t* in_dev, int32_t* out_dev, int64_t n, int32_t inclusive, void* workspace_dev,
+              int64_t workspace_bytes, void* stream);
+
 /* Workspace bytes of hi3d_unique_keys. */
 int hi3d_unique_keys_workspace(int64_t n, int64_t* bytes_host);
 
