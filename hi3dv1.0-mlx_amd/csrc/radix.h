@@ -3,7 +3,8 @@
 // runs three kernels over tiles of kTile elements:
 //   upsweep    each tile's digit counts, stored digit-major ([digit][tile]);
 //   scan       one workgroup per digit turns its row of tile counts into exclusive
-//              prefixes and writes the digit's total;
+//              prefixes and writes the digit's total (skipped for at most kDirect
+//              tiles: the downsweep then sums the rows itself);
 //   downsweep  each tile ranks its keys stably within the tile (wave-wide ballots
 //              match the lanes of equal digit, a running count per wave and digit
 //              keeps element order), places them in LDS in digit order and writes
@@ -29,6 +30,7 @@ constexpr int kItems = 16;
 constexpr int kTile = kThreads * kItems;
 constexpr int kBins = 256;
 constexpr int kWaves = kThreads / 64;
+constexpr int kDirect = 32;  // tile counts up to which the downsweep sums the rows
 static_assert(kBins == kThreads, "one thread per digit in the per-digit steps");
 
 inline int64_t tiles(int64_t n) { return std::max<int64_t>(ceil_div(n, kTile), 1); }
@@ -96,7 +98,7 @@ __global__ __launch_bounds__(kThreads) void upsweep_kernel(const K* __restrict__
 __global__ __launch_bounds__(kThreads) void row_scan_kernel(int32_t* __restrict__ counts, int64_t len,
                                                             int32_t* __restrict__ totals) {
   __shared__ int32_t part[kWaves];
-  int32_t* row = counts + static_cast<int64_t>(blockIdx.x) * len;
+  int32_t* const row = counts + static_cast<int64_t>(blockIdx.x) * len;
   // thread t owns the contiguous segment [t * per, (t + 1) * per)
   const int64_t per = (len + kThreads - 1) / kThreads;
   const int64_t lo = std::min<int64_t>(threadIdx.x * per, len), hi = std::min<int64_t>(lo + per, len);
@@ -132,9 +134,23 @@ __global__ __launch_bounds__(kThreads) void downsweep_kernel(const K* __restrict
 #pragma unroll
   for (int i = 0; i < kWaves; ++i) wcount[i][t] = 0;
   {
+    // totals == nullptr: counts are raw (at most kDirect tiles), so sum the row here
+    int32_t tot, pre;
+    if (totals != nullptr) {
+      tot = totals[t];
+      pre = counts[static_cast<int64_t>(t) * ntiles + blockIdx.x];
+    } else {
+      tot = 0;
+      pre = 0;
+      for (int b = 0; b < static_cast<int>(ntiles); ++b) {
+        const int32_t c = counts[t * ntiles + b];
+        tot += c;
+        pre += b < static_cast<int>(blockIdx.x) ? c : 0;
+      }
+    }
     int32_t all;
-    const int32_t ex = block_exclusive(totals[t], part, &all);
-    gbase[t] = ex + counts[static_cast<int64_t>(t) * ntiles + blockIdx.x];
+    const int32_t ex = block_exclusive(tot, part, &all);
+    gbase[t] = ex + pre;
   }
   // wave w holds tile elements w * 64 * kItems + 64 i + lane (element order = (w, i, lane));
   // past n a key of all ones, whose digit is the largest, so it ranks after every valid one
@@ -291,9 +307,11 @@ hipError_t sort_pairs(void* temp, int64_t temp_size, K*& keys, K*& keys_alt, int
     const int nbits = std::min(8, end_bit - shift);
     const uint32_t dmask = (1u << nbits) - 1u;
     hipLaunchKernelGGL(upsweep_kernel<K>, grid, dim3(kThreads), 0, stream, keys, n, shift, dmask, counts, nt);
-    hipLaunchKernelGGL(row_scan_kernel, dim3(kBins), dim3(kThreads), 0, stream, counts, nt, totals);
+    const bool direct = nt <= kDirect;
+    if (!direct)
+      hipLaunchKernelGGL(row_scan_kernel, dim3(kBins), dim3(kThreads), 0, stream, counts, nt, totals);
     hipLaunchKernelGGL(downsweep_kernel<K>, grid, dim3(kThreads), 0, stream, keys, vals, keys_alt, vals_alt, n,
-                       shift, nbits, counts, nt, totals);
+                       shift, nbits, counts, nt, direct ? nullptr : totals);
     std::swap(keys, keys_alt);
     std::swap(vals, vals_alt);
   }
