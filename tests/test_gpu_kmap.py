@@ -310,8 +310,9 @@ def test_gather_neighbours_matches_take(cuda, dtype, c):
 @pytest.mark.parametrize("ksize,batch,n_side,density", [(3, 1, 20, 0.2), (3, 3, 16, 0.5), (5, 2, 12, 0.3),
                                                         (3, 1, 64, 0.01)])
 def test_dense_and_hash_maps_agree(cuda, ksize, batch, n_side, density):
-    """The dense-grid map and the hash map give the same table and counts bit for bit,
-    and both equal the oracle; both flag duplicates and out-of-range coordinates."""
+    """The dense-grid map (rows in input order and in cell order) and the hash map give
+    the same table and counts bit for bit, and equal the oracle; all flag duplicates and
+    out-of-range coordinates."""
     from hi3d_amd import kmap
 
     rng = np.random.default_rng(n_side * 10 + batch)
@@ -336,6 +337,20 @@ def test_dense_and_hash_maps_agree(cuda, ksize, batch, n_side, density):
         assert torch.equal(kmap.build_kernel_map(t, [n_side] * 3, batch, ksize).table, dense.table)
     finally:
         kmap.KMAP_DENSE_MAX_CELLS = old
+    # the kept grid with the rows in cell order (forced on this small grid): same map and
+    # the same errors, for this kernel size too
+    old_order = kmap.KMAP_DENSE_ORDER_MIN_BYTES
+    try:
+        kmap.KMAP_DENSE_ORDER_MIN_BYTES = 0
+        ordered = kmap.build_kernel_map(t, [n_side] * 3, batch, ksize)
+        assert torch.equal(ordered.table, dense.table) and torch.equal(ordered.counts, dense.counts)
+        with pytest.raises(ValueError, match="duplicate"):
+            kmap.build_kernel_map(dup, [n_side] * 3, batch, ksize)
+        with pytest.raises(ValueError, match="outside"):
+            kmap.build_kernel_map(bad, [n_side] * 3, batch, ksize)
+        assert torch.equal(kmap.build_kernel_map(t, [n_side] * 3, batch, ksize).table, dense.table)
+    finally:
+        kmap.KMAP_DENSE_ORDER_MIN_BYTES = old_order
 
 
 @pytest.mark.parametrize("ordered", [True, False])
