@@ -149,6 +149,8 @@ def bench_subm(name: str, grid: int, cin: int, cout: int, dtype, steps: int, war
         "conv_kernel_ms": ev,
         "voxels_per_s": n / (wall * 1e-3),
         "eff_tflops": flops / (ev * 1e-3) / 1e12,
+        # dense MFMA peak of the compute type (fp32 157.3, fp16 2500 TFLOP/s)
+        "mfma_frac": flops / (ev * 1e-3) / 1e12 / (2500.0 if dtype == torch.float16 else 157.3),
         "conv_alg_bytes": conv_bytes,
         "map_ms": map_wall,
         "map_dense_ms": map_ev,

@@ -954,6 +954,192 @@ int launch_ring(const ConvArgs& base, hipStream_t stream) {
   return HI3D_OK;
 }
 
+// ------------------------------------------------------ fp32 16-row block kernel --
+// fp32 rows of 64 channels into 64-channel output slices, for sets too small to fill
+// the chip with 128-row tiles. A workgroup takes 16 NW plan rows and each wave one
+// 16-row block, whose 16 x 64 output block it accumulates in 16 registers with
+// v_mfma_f32_16x16x4f32: the weights are the A operand and the gathered rows B, so a
+// lane ends with four consecutive output channels of its own row. A wave runs the
+// MFMAs of only the offsets present in its 16 rows (1.15 products per present pair on
+// the 45k-voxel C64 shell, against 1.59 for a 128-row tile's union); the workgroup
+// walks the union of its blocks' offsets in step, so that each offset's 16 KB weight
+// slice is loaded into LDS once (NSLOT slices in flight), while each wave gathers its
+// rows straight into registers one offset ahead. The dispatch uses two slices and
+// four-wave workgroups: on that shell 71 us against 110 us for the 128-row ring tile;
+// three slices (two workgroups per CU instead of four) 100 us, 32- or 128-row
+// workgroups 81-84 us. Its time is the busiest CU's MFMA work: every workgroup is
+// resident from the start, and per-wave timestamps put each CU's end in proportion to
+// the offsets its waves run (correlation 0.97).
+//
+// K order: lane (i, h) = (lane % 16, lane / 16) loads 16 bytes of its row, channels
+// 16 s + 4 h .. + 3, and MFMA j of step s takes channel 16 s + 4 h + j from both
+// operands, so the 16 (s, j) MFMAs cover each channel once.
+constexpr int kBlockRows = 16;
+constexpr int kBlockCin = 64;
+constexpr int kBlockCout = 64;
+constexpr int kBlockSlice = kBlockCout * kBlockCin * 4;  // one offset's weight slice, bytes
+
+template <int NW, int NSLOT>
+__global__ __launch_bounds__(NW * 64) void conv_block_f32_kernel(ConvArgs a) {
+  constexpr int R = kBlockRows * NW;                // plan rows per workgroup
+  constexpr int DW = kBlockSlice / (1024 * NW);     // 1 KB weight DMAs per wave and offset
+  constexpr int KV = kMaxPipelinedKvol;
+  static_assert(DW * NW * 1024 == kBlockSlice && kTileRows % R == 0, "shape");
+  static_assert(NSLOT == 2 || NSLOT == 3, "two or three weight slices in flight");
+  // weight slices (row c = output channel, 256 bytes; 16-byte chunk q of row c at
+  // position q ^ (c % 16)), then the blocks' gather rows [k][R] (-1: absent), then masks
+  __shared__ __attribute__((aligned(16))) char smem[NSLOT * kBlockSlice + KV * R * 4 + NW * 4];
+  int32_t* const gl = reinterpret_cast<int32_t*>(smem + NSLOT * kBlockSlice);
+  uint32_t* const smask = reinterpret_cast<uint32_t*>(gl + KV * R);
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int i = lane & 15, h = lane >> 4;
+  const int64_t item = xcd_remap(blockIdx.x, static_cast<int64_t>(gridDim.x));
+  const int64_t tile = item / a.ny;
+  const int n0 = static_cast<int>(item - tile * a.ny) * kBlockCout;
+  const int kvol = a.kvol;
+  const uint64_t n_in = static_cast<uint64_t>(a.n_in);
+  const int brow = wave * kBlockRows + i;  // this lane's row in the workgroup
+  const int64_t p = tile * R + brow;       // its plan row (< ntiles * 128: R divides 128)
+  const int32_t orow = a.rows[p];
+  const int32_t* gsrc = a.gidx + (p / kTileRows) * kvol * kTileRows + (p % kTileRows);
+
+  // the block's gather rows into LDS and its offset mask
+  // (all loads issued before the first use: offsets past kvol reread offset 0)
+  int32_t g[KV];
+#pragma unroll
+  for (int k = 0; k < KV; ++k) g[k] = gsrc[(k < kvol ? k : 0) * kTileRows];
+  uint32_t wmask = 0;
+#pragma unroll
+  for (int k = 0; k < KV; ++k) {
+    const bool ok = k < kvol && static_cast<uint64_t>(static_cast<uint32_t>(g[k])) < n_in;
+    if (__builtin_amdgcn_ballot_w64(ok) != 0) wmask |= 1u << k;
+    if (h == 0) gl[k * R + brow] = ok ? g[k] : -1;
+  }
+  if (lane == 0) smask[wave] = wmask;
+  __syncthreads();
+  uint32_t uni = 0;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) uni |= smask[w];
+  uni = __builtin_amdgcn_readfirstlane(uni);
+  const int n = __popc(uni);
+
+  // DMA u of this wave fills slice bytes [1024 m, +1024), m = wave + NW u: row
+  // c = 4 m + lane / 16, position lane % 16, i.e. logical chunk (lane % 16) ^ (c % 16)
+  auto issue_w = [&](int k, int slot) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < DW; ++u) {
+      const int m = wave + NW * u;
+      const int c = 4 * m + (lane >> 4);
+      const int q = (lane & 15) ^ (c & 15);
+      lds_dma16(a.weight + (static_cast<int64_t>(n0 + c) * kvol + k) * (kBlockCin * 4) + q * 16,
+                smem + slot * kBlockSlice + m * 1024);
+    }
+  };
+  // gathered rows through global (not flat) loads, which LDS waits do not cover
+  using GRow = const __attribute__((address_space(1))) f32x4;
+  const char* const zrow = reinterpret_cast<const char*>(g_zero_row) + h * 16;
+  auto issue_x = [&](int k, f32x4 (&x)[4]) __attribute__((always_inline)) {
+    const int32_t gk = gl[k * R + brow];
+    const char* src = gk >= 0 ? a.in + static_cast<int64_t>(gk) * (kBlockCin * 4) + h * 16 : zrow;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) x[s] = *(GRow*)(src + 64 * s);
+  };
+  f32x4 acc[4];
+#pragma unroll
+  for (int cb = 0; cb < 4; ++cb) acc[cb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  auto compute = [&](int slot, const f32x4 (&x)[4]) __attribute__((always_inline)) {
+    const char* sb = smem + slot * kBlockSlice + i * 256;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      f32x4 wf[4];
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb)
+        wf[cb] = *reinterpret_cast<const f32x4*>(sb + cb * (16 * 256) + (((4 * s + h) ^ i) << 4));
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb) acc[cb] = __builtin_amdgcn_mfma_f32_16x16x4f32(wf[cb][j], x[s][j], acc[cb], 0, 0, 0);
+    }
+  };
+
+  if (n > 0) {
+    // offsets of ordinals ord, ord + 1, ord + 2 (the later ones meaningless past n)
+    uint32_t rest = uni;
+    auto pop = [&]() __attribute__((always_inline)) {
+      const int k = rest ? __builtin_ctz(rest) : 0;
+      rest &= rest - 1u;
+      return k;
+    };
+    int kc = pop(), kx = pop(), kw = pop();
+    f32x4 xa[4], xb[4];
+    // prologue, in issue order: W(0), X(0), then W(1) with three slices
+    issue_w(kc, 0);
+    issue_x(kc, xa);
+    if constexpr (NSLOT == 3) {
+      if (n > 1) issue_w(kx, 1);
+    }
+    int slot = 0;
+    // iteration ord: wait for W(ord) and X(ord) (with three slices W(ord + 1), issued
+    // after them, may stay in flight), so that after the barrier every wave's share of
+    // slice ord is in LDS and slice ord - 1 is no longer read; then X(ord + 1) and the
+    // next slice, then the MFMAs of ord when this block has the offset
+    auto body = [&](int ord, const f32x4 (&xc)[4], f32x4 (&xn)[4]) __attribute__((always_inline)) {
+      if (NSLOT == 3 && ord + 1 < n) wait_vmcnt<DW>();
+      else wait_vmcnt<0>();
+      raw_barrier();
+      if (ord + 1 < n) issue_x(kx, xn);
+      if constexpr (NSLOT == 3) {
+        if (ord + 2 < n) issue_w(kw, slot == 0 ? 2 : slot - 1);
+      } else {
+        if (ord + 1 < n) issue_w(kx, slot ^ 1);
+      }
+      if ((wmask >> kc) & 1u) compute(slot, xc);
+      slot = NSLOT == 3 ? (slot == 2 ? 0 : slot + 1) : (slot ^ 1);
+      kc = kx;
+      kx = kw;
+      kw = pop();
+    };
+    for (int ord = 0; ord < n; ord += 2) {
+      body(ord, xa, xb);
+      if (ord + 1 < n) body(ord + 1, xb, xa);
+    }
+  }
+
+  // epilogue: lane (i, h) holds output channels n0 + 16 cb + 4 h .. + 3 of its row
+  if (orow < 0 || orow >= a.n_out) return;
+  const float* bias = static_cast<const float*>(a.bias);
+  const int64_t obase = static_cast<int64_t>(orow) * a.cout * 4;
+#pragma unroll
+  for (int cb = 0; cb < 4; ++cb) {
+    const int col = n0 + 16 * cb + 4 * h;
+    f32x4 v = acc[cb];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float x = v[e] + (bias != nullptr ? bias[col + e] : 0.0f);
+      if (a.act == HI3D_ACT_SILU) x = silu(x);
+      v[e] = x;
+    }
+    const int64_t off = obase + col * 4;
+    if (a.residual != nullptr) v += *reinterpret_cast<const f32x4*>(a.residual + off);
+    *reinterpret_cast<f32x4*>(a.out + off) = v;
+  }
+}
+
+template <int NW, int NSLOT>
+int launch_block_f32(const ConvArgs& base, hipStream_t stream) {
+  ConvArgs a = base;
+  a.ny = a.cout / kBlockCout;
+  const int64_t blocks = ceil_div(a.n_out, kBlockRows * NW) * a.ny;
+  if (blocks == 0) return HI3D_OK;
+  HI3D_REQUIRE(blocks < (int64_t(1) << 31), "too many tiles");
+  hipLaunchKernelGGL((conv_block_f32_kernel<NW, NSLOT>), dim3(static_cast<unsigned>(blocks)), dim3(NW * 64), 0, stream,
+                     a);
+  HI3D_LAUNCH_CHECK();
+  return HI3D_OK;
+}
+
 // ------------------------------------------------------ wide-step ring kernel --
 // The ring kernel's scheme with 128-byte K steps: each gathered row is fetched as one
 // 128-byte request per stage instead of two 64-byte ones, halving the gather requests
@@ -1577,6 +1763,9 @@ int launch_mfma(const ConvArgs& base, hipStream_t stream) {
     // fp32 (four 32x32x2 MFMAs per fragment): 128-row tiles so that small sets still
     // spread over every CU (the 45k-voxel C64 shell makes 353 of them)
     const int rb = a.cin * 4;
+    // 64 -> 64 channels: 16-row blocks that skip the offsets absent from their rows
+    if (a.kvol <= kMaxPipelinedKvol && a.cin == kBlockCin && a.cout == kBlockCout)
+      return launch_block_f32<4, 2>(a, stream);
     if (a.kvol <= kMaxPipelinedKvol && rb % 64 == 0 && rb >= 256 && rb <= kRingMaxRowBytes) {
       if (a.cout == 64) return launch_ring<T, 64, 4, 128>(a, stream);
       // 128 x 128 tiles (several column tiles for wider outputs): the largest fp32 tile

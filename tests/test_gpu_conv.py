@@ -236,6 +236,41 @@ def test_halo_conv_matches_float64_and_tile_plan(cuda, dtype, cin, cout, density
     assert oconv.rel_err(y.float().cpu().numpy(), y2.float().cpu().numpy().astype(np.float64)) <= GATE[dtype]
 
 
+@pytest.mark.parametrize("side,density,batch,kvol,act,res", [
+    (24, 0.15, 2, 27, "silu", True), (24, 0.004, 2, 27, None, False), (20, 0.5, 1, 27, None, True),
+    (24, 0.2, 2, 8, "silu", False), (30, 0.05, 3, 27, None, False),
+])
+def test_fp32_block_kernel(cuda, side, density, batch, kvol, act, res):
+    """The fp32 64 -> 64 kernel of 16-row blocks (each wave runs only the offsets present
+    in its rows, the workgroup walks their union): against float64 with SiLU and the
+    residual, isolated voxels (blocks whose only offset is the centre), a dense set
+    (every offset present), a few-offset table, and set sizes that end in a partial
+    workgroup; and bitwise independent of the plan's tile order (each row sums its
+    offsets in increasing order whatever block it lands in)."""
+    from hi3d_amd import conv, kmap
+
+    rng = np.random.default_rng(side * 100 + kvol + int(density * 1000))
+    idx = _rand_indices(rng, side, density, batch=batch)
+    n = len(idx)
+    if kvol == 27:
+        table = kmap.build_kernel_map(torch.as_tensor(idx).to(cuda), [side] * 3, batch).table
+    else:
+        t = rng.integers(0, n + 1, (n - 5, kvol)).astype(np.int32)
+        t[rng.random(t.shape) < 0.6] = n
+        table = torch.as_tensor(t).to(cuda)
+    x, w, b = _case(rng, n, 64, 64, torch.float32, kvol)
+    r = torch.as_tensor(rng.standard_normal((int(table.shape[0]), 64), dtype=np.float32)) if res else None
+    xd, wd, bd = x.to(cuda), w.to(cuda), b.to(cuda)
+    rd = None if r is None else r.to(cuda)
+    y = conv.gather_conv(xd, kmap.build_plan(table, n), wd, bd, act=act, residual=rd)
+    ref = oconv.gather_conv_f64(x.numpy(), table.cpu().numpy(), w.numpy(), b.numpy(), act=act,
+                                residual=None if r is None else r.numpy())
+    assert y.dtype == torch.float32 and y.shape == (int(table.shape[0]), 64)
+    assert oconv.rel_err(y.cpu().numpy(), ref) <= GATE[torch.float32]
+    y2 = conv.gather_conv(xd, kmap.build_plan(table, n, window_rows=64), wd, bd, act=act, residual=rd)
+    assert torch.equal(y, y2)
+
+
 def test_plan_choice_does_not_change_results(cuda):
     """Within a kernel family the output is bitwise independent of the plan: the tile-plan
     kernels accumulate each row's present (offset, K-block) products in the same order
