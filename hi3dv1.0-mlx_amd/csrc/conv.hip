@@ -955,21 +955,21 @@ int launch_ring(const ConvArgs& base, hipStream_t stream) {
 }
 
 // ------------------------------------------------------ fp32 16-row block kernel --
-// fp32 rows of 64 channels into 64-channel output slices, for sets too small to fill
+// fp32 rows of 64 channels into CO-channel output slices, for sets too small to fill
 // the chip with 128-row tiles. A workgroup takes 16 NW plan rows and each wave one
-// 16-row block, whose 16 x 64 output block it accumulates in 16 registers with
+// 16-row block, whose 16 x CO output block it accumulates in CO / 4 registers with
 // v_mfma_f32_16x16x4f32: the weights are the A operand and the gathered rows B, so a
 // lane ends with four consecutive output channels of its own row. A wave runs the
 // MFMAs of only the offsets present in its 16 rows (1.15 products per present pair on
 // the 45k-voxel C64 shell, against 1.59 for a 128-row tile's union); the workgroup
-// walks the union of its blocks' offsets in step, so that each offset's 16 KB weight
-// slice is loaded into LDS once (NSLOT slices in flight), while each wave gathers its
-// rows straight into registers one offset ahead. The dispatch uses two slices and
-// four-wave workgroups: on that shell 71 us against 110 us for the 128-row ring tile;
-// three slices (two workgroups per CU instead of four) 100 us, 32- or 128-row
-// workgroups 81-84 us. Its time is the busiest CU's MFMA work: every workgroup is
-// resident from the start, and per-wave timestamps put each CU's end in proportion to
-// the offsets its waves run (correlation 0.97).
+// walks the union of its blocks' offsets in step, so that each offset's weight slice
+// (CO x 256 bytes) is loaded into LDS once (NSLOT slices in flight), while each wave
+// gathers its rows straight into registers one offset ahead. On that shell: 70 us for
+// eight waves, two slices and 32 channels, against 110 us for the 128-row ring tile
+// (four waves over 64 channels 72 us, three slices 78-100 us, 16 channels 88 us).
+// Every workgroup is resident from the start, and per-wave timestamps put each CU's
+// end in proportion to the offsets its waves run (correlation 0.97): the time is the
+// busiest SIMD's MFMA work, 1.5 times the mean, as the blocks run 6 to 27 offsets.
 //
 // K order: lane (i, h) = (lane % 16, lane / 16) loads 16 bytes of its row, channels
 // 16 s + 4 h .. + 3, and MFMA j of step s takes channel 16 s + 4 h + j from both
@@ -977,19 +977,20 @@ int launch_ring(const ConvArgs& base, hipStream_t stream) {
 constexpr int kBlockRows = 16;
 constexpr int kBlockCin = 64;
 constexpr int kBlockCout = 64;
-constexpr int kBlockSlice = kBlockCout * kBlockCin * 4;  // one offset's weight slice, bytes
 
-template <int NW, int NSLOT>
+template <int NW, int NSLOT, int CO>
 __global__ __launch_bounds__(NW * 64) void conv_block_f32_kernel(ConvArgs a) {
   constexpr int R = kBlockRows * NW;                // plan rows per workgroup
-  constexpr int DW = kBlockSlice / (1024 * NW);     // 1 KB weight DMAs per wave and offset
+  constexpr int SLICE = CO * kBlockCin * 4;         // one offset's weights for the CO output channels, bytes
+  constexpr int NCB = CO / 16;                      // 16-channel output blocks
+  constexpr int DW = SLICE / (1024 * NW);           // 1 KB weight DMAs per wave and offset
   constexpr int KV = kMaxPipelinedKvol;
-  static_assert(DW * NW * 1024 == kBlockSlice && kTileRows % R == 0, "shape");
+  static_assert(DW * NW * 1024 == SLICE && kTileRows % R == 0 && (CO == 16 || CO == 32 || CO == 64), "shape");
   static_assert(NSLOT == 2 || NSLOT == 3, "two or three weight slices in flight");
   // weight slices (row c = output channel, 256 bytes; 16-byte chunk q of row c at
   // position q ^ (c % 16)), then the blocks' gather rows [k][R] (-1: absent), then masks
-  __shared__ __attribute__((aligned(16))) char smem[NSLOT * kBlockSlice + KV * R * 4 + NW * 4];
-  int32_t* const gl = reinterpret_cast<int32_t*>(smem + NSLOT * kBlockSlice);
+  __shared__ __attribute__((aligned(16))) char smem[NSLOT * SLICE + KV * R * 4 + NW * 4];
+  int32_t* const gl = reinterpret_cast<int32_t*>(smem + NSLOT * SLICE);
   uint32_t* const smask = reinterpret_cast<uint32_t*>(gl + KV * R);
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -997,7 +998,7 @@ __global__ __launch_bounds__(NW * 64) void conv_block_f32_kernel(ConvArgs a) {
   const int i = lane & 15, h = lane >> 4;
   const int64_t item = xcd_remap(blockIdx.x, static_cast<int64_t>(gridDim.x));
   const int64_t tile = item / a.ny;
-  const int n0 = static_cast<int>(item - tile * a.ny) * kBlockCout;
+  const int n0 = static_cast<int>(item - tile * a.ny) * CO;
   const int kvol = a.kvol;
   const uint64_t n_in = static_cast<uint64_t>(a.n_in);
   const int brow = wave * kBlockRows + i;  // this lane's row in the workgroup
@@ -1034,7 +1035,7 @@ __global__ __launch_bounds__(NW * 64) void conv_block_f32_kernel(ConvArgs a) {
       const int c = 4 * m + (lane >> 4);
       const int q = (lane & 15) ^ (c & 15);
       lds_dma16(a.weight + (static_cast<int64_t>(n0 + c) * kvol + k) * (kBlockCin * 4) + q * 16,
-                smem + slot * kBlockSlice + m * 1024);
+                smem + slot * SLICE + m * 1024);
     }
   };
   // gathered rows through global (not flat) loads, which LDS waits do not cover
@@ -1046,21 +1047,21 @@ __global__ __launch_bounds__(NW * 64) void conv_block_f32_kernel(ConvArgs a) {
 #pragma unroll
     for (int s = 0; s < 4; ++s) x[s] = *(GRow*)(src + 64 * s);
   };
-  f32x4 acc[4];
+  f32x4 acc[NCB];
 #pragma unroll
-  for (int cb = 0; cb < 4; ++cb) acc[cb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int cb = 0; cb < NCB; ++cb) acc[cb] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   auto compute = [&](int slot, const f32x4 (&x)[4]) __attribute__((always_inline)) {
-    const char* sb = smem + slot * kBlockSlice + i * 256;
+    const char* sb = smem + slot * SLICE + i * 256;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      f32x4 wf[4];
+      f32x4 wf[NCB];
 #pragma unroll
-      for (int cb = 0; cb < 4; ++cb)
+      for (int cb = 0; cb < NCB; ++cb)
         wf[cb] = *reinterpret_cast<const f32x4*>(sb + cb * (16 * 256) + (((4 * s + h) ^ i) << 4));
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int cb = 0; cb < 4; ++cb) acc[cb] = __builtin_amdgcn_mfma_f32_16x16x4f32(wf[cb][j], x[s][j], acc[cb], 0, 0, 0);
+        for (int cb = 0; cb < NCB; ++cb) acc[cb] = __builtin_amdgcn_mfma_f32_16x16x4f32(wf[cb][j], x[s][j], acc[cb], 0, 0, 0);
     }
   };
 
@@ -1112,7 +1113,7 @@ __global__ __launch_bounds__(NW * 64) void conv_block_f32_kernel(ConvArgs a) {
   const float* bias = static_cast<const float*>(a.bias);
   const int64_t obase = static_cast<int64_t>(orow) * a.cout * 4;
 #pragma unroll
-  for (int cb = 0; cb < 4; ++cb) {
+  for (int cb = 0; cb < NCB; ++cb) {
     const int col = n0 + 16 * cb + 4 * h;
     f32x4 v = acc[cb];
 #pragma unroll
@@ -1127,14 +1128,14 @@ __global__ __launch_bounds__(NW * 64) void conv_block_f32_kernel(ConvArgs a) {
   }
 }
 
-template <int NW, int NSLOT>
+template <int NW, int NSLOT, int CO>
 int launch_block_f32(const ConvArgs& base, hipStream_t stream) {
   ConvArgs a = base;
-  a.ny = a.cout / kBlockCout;
+  a.ny = a.cout / CO;
   const int64_t blocks = ceil_div(a.n_out, kBlockRows * NW) * a.ny;
   if (blocks == 0) return HI3D_OK;
   HI3D_REQUIRE(blocks < (int64_t(1) << 31), "too many tiles");
-  hipLaunchKernelGGL((conv_block_f32_kernel<NW, NSLOT>), dim3(static_cast<unsigned>(blocks)), dim3(NW * 64), 0, stream,
+  hipLaunchKernelGGL((conv_block_f32_kernel<NW, NSLOT, CO>), dim3(static_cast<unsigned>(blocks)), dim3(NW * 64), 0, stream,
                      a);
   HI3D_LAUNCH_CHECK();
   return HI3D_OK;
@@ -1763,9 +1764,11 @@ int launch_mfma(const ConvArgs& base, hipStream_t stream) {
     // fp32 (four 32x32x2 MFMAs per fragment): 128-row tiles so that small sets still
     // spread over every CU (the 45k-voxel C64 shell makes 353 of them)
     const int rb = a.cin * 4;
-    // 64 -> 64 channels: 16-row blocks that skip the offsets absent from their rows
+    // 64 -> 64 channels: 16-row blocks that skip the offsets absent from their rows;
+    // 128-row workgroups over half the output channels (config 1: 0.070 ms; 64-row
+    // workgroups over all 64 channels 0.072, 128-row ones 0.082)
     if (a.kvol <= kMaxPipelinedKvol && a.cin == kBlockCin && a.cout == kBlockCout)
-      return launch_block_f32<4, 2>(a, stream);
+      return launch_block_f32<8, 2, 32>(a, stream);
     if (a.kvol <= kMaxPipelinedKvol && rb % 64 == 0 && rb >= 256 && rb <= kRingMaxRowBytes) {
       if (a.cout == 64) return launch_ring<T, 64, 4, 128>(a, stream);
       // 128 x 128 tiles (several column tiles for wider outputs): the largest fp32 tile
