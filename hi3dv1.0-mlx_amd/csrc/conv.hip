@@ -968,8 +968,9 @@ int launch_ring(const ConvArgs& base, hipStream_t stream) {
 // eight waves, two slices and 32 channels, against 110 us for the 128-row ring tile
 // (four waves over 64 channels 72 us, three slices 78-100 us, 16 channels 88 us).
 // Every workgroup is resident from the start, and per-wave timestamps put each CU's
-// end in proportion to the offsets its waves run (correlation 0.97): the time is the
-// busiest SIMD's MFMA work, 1.5 times the mean, as the blocks run 6 to 27 offsets.
+// end in proportion to the offsets its waves run (correlation 0.97, 0.36 us per
+// wave-offset); dealing the tiles or a workgroup's blocks in other orders (across the
+// XCDs, heaviest first, heavy with light on one SIMD) left the time unchanged.
 //
 // K order: lane (i, h) = (lane % 16, lane / 16) loads 16 bytes of its row, channels
 // 16 s + 4 h .. + 3, and MFMA j of step s takes channel 16 s + 4 h + j from both
