@@ -1336,7 +1336,10 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_wide_kernel(ConvArgs a) {
     group(G2{});
     if constexpr (MODE == 0) {
       advance();
-      wait_vmcnt<L + 1>();
+      // with one K stage per offset the next stage enters an offset and reads the
+      // indices this stage requested: they must land before the barrier
+      if (KB == 1) wait_vmcnt<L>();
+      else wait_vmcnt<L + 1>();
       raw_barrier();
     } else if constexpr (MODE == 1) {
       wait_vmcnt<0>();
@@ -1345,7 +1348,7 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_wide_kernel(ConvArgs a) {
     group(G3{});
   };
 
-  if (S > 0) {  // S = taps * KB >= 2
+  if (S > 0) {  // S = taps * KB (1 only for one tap of a 128-byte row)
     ck = mask ? __builtin_ctz(mask) : 0;
     rest = mask & (mask - 1u);
     ckb = 0;
@@ -1355,27 +1358,40 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_wide_kernel(ConvArgs a) {
     raw_barrier();
     enter_offset();
     // prologue: the next offset's indices (offset 0's again without a successor), then
-    // stages 0 and 1 (one offset: KB >= 2)
+    // stages 0 and 1 (with S = 1, stage 1 rereads stage 0's rows into slot 1, unused;
+    // the epilogue's wait retires it)
     issue_idx(rest ? __builtin_ctz(rest) : ck, 1);
 #pragma unroll
     for (int st = 0; st < NS - 1; ++st) {
 #pragma unroll
       for (int u = 0; u < L; ++u) issue_load(st, u);
       advance();
+      if (st == 0 && KB == 1) {
+        // stage 1 is the next offset's: its indices (requested before stage 0's
+        // loads) land, then its sources, and the request for the offset after it
+        wait_vmcnt<L>();
+        raw_barrier();
+        enter_offset();
+        issue_idx(rest ? __builtin_ctz(rest) : ck, (cord + 1) & 1);
+      }
     }
     wait_vmcnt<L>();
     raw_barrier();
 #pragma unroll
     for (int i = 0; i < NF; ++i) frag_one(0, G0{}, i);
 
-    int slot = 0;
-    for (int s = 0; s + 2 < S; ++s) {
-      stage(slot, I0{});
-      slot = slot == NS - 1 ? 0 : slot + 1;
+    if (S == 1) {
+      stage(0, I2{});
+    } else {
+      int slot = 0;
+      for (int s = 0; s + 2 < S; ++s) {
+        stage(slot, I0{});
+        slot = slot == NS - 1 ? 0 : slot + 1;
+      }
+      // the last two stages, S - 2 and S - 1
+      stage(slot, I1{});
+      stage(slot == NS - 1 ? 0 : slot + 1, I2{});
     }
-    // the last two stages, S - 2 and S - 1
-    stage(slot, I1{});
-    stage(slot == NS - 1 ? 0 : slot + 1, I2{});
   }
 
   // epilogue: each wave stages its 64 x (NB * 32) block
@@ -1752,6 +1768,10 @@ int launch_mfma(const ConvArgs& base, hipStream_t stream) {
     if (a.kvol <= kMaxPipelinedKvol && ring_rows && a.cout % 256 == 0) return launch_ring<T, 256, 8>(a, stream);
     // few-offset tables (the strided pair): 128-row tiles in a 48..64 KB ring, so that two
     // or three workgroups share a CU and cover each other's tile start and end
+    // 128-byte rows into 128 outputs (the stride-2 down-convolution): one 128-byte
+    // request per gathered row, one K stage per offset (0.060 against 0.062 ms for the
+    // 128-row ring tile)
+    if (few && rb == 128 && a.cout == 128) return launch_wide<T, 128, 8>(a, stream);
     if (few) return a.cout == 64 ? launch_ring<T, 64, 4, 128>(a, stream) : launch_ring<T, 128, 4, 128>(a, stream);
     if (a.kvol <= kMaxPipelinedKvol && ring_rows && a.cout % 128 == 0) {
       if (rb % 128 == 0) return launch_wide<T, 128, 8>(a, stream);

@@ -271,6 +271,39 @@ def test_fp32_block_kernel(cuda, side, density, batch, kvol, act, res):
     assert torch.equal(y, y2)
 
 
+@pytest.mark.parametrize("dtype,mode", [
+    (torch.float16, "one"), (torch.float16, "mixed"), (torch.bfloat16, "mixed"), (torch.float16, "blocks"),
+])
+def test_wide_kernel_128_byte_rows(cuda, dtype, mode):
+    """Few-offset tables of 128-byte rows into 128 outputs (the stride-2
+    down-convolution's shape) run the 128-byte-step wide kernel, where a tile with one
+    offset has a single K stage: every tile one offset ("one"), random tables ("mixed"),
+    and tiles of one offset, of two and of none in one launch ("blocks"), with partial
+    tiles at the end; against float64."""
+    from hi3d_amd import conv, kmap
+
+    rng = np.random.default_rng({"one": 1, "mixed": 2, "blocks": 3}[mode] + (10 if dtype == torch.bfloat16 else 0))
+    n_in, n_out = 3001, 1300
+    t = np.full((n_out, 8), n_in, np.int32)
+    if mode == "one":
+        t[:, 5] = rng.integers(0, n_in, n_out)
+    elif mode == "mixed":
+        t = rng.integers(0, n_in + 1, (n_out, 8)).astype(np.int32)
+        t[rng.random(t.shape) < 0.6] = n_in
+    else:
+        t[:512, 3] = rng.integers(0, n_in, 512)
+        t[512:1024, 1] = rng.integers(0, n_in, 512)
+        t[512:1024, 6] = rng.integers(0, n_in, 512)
+    x = torch.as_tensor(rng.standard_normal((n_in, 64), dtype=np.float32)).to(dtype)
+    w = torch.as_tensor(rng.standard_normal((128, 8, 64), dtype=np.float32) / np.sqrt(8 * 64)).to(dtype)
+    b = torch.as_tensor(rng.standard_normal(128, dtype=np.float32) * 0.1).to(dtype)
+    table = torch.as_tensor(t).to(cuda)
+    y = conv.gather_conv(x.to(cuda), kmap.build_plan(table, n_in), w.to(cuda), b.to(cuda))
+    ref = oconv.gather_conv_f64(x.float().numpy(), t, w.float().numpy(), b.float().numpy())
+    assert y.dtype == dtype and y.shape == (n_out, 128)
+    assert oconv.rel_err(y.float().cpu().numpy(), ref) <= GATE[dtype]
+
+
 def test_plan_choice_does_not_change_results(cuda):
     """Within a kernel family the output is bitwise independent of the plan: the tile-plan
     kernels accumulate each row's present (offset, K-block) products in the same order
