@@ -1187,9 +1187,11 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_wide_kernel(ConvArgs a) {
   static_assert(STAGE == 49152 && LG * (KG - 1) == L && LG <= NM && LA * 8 * NW == BM, "stage shape");
   static_assert(sizeof(T) == 2, "16-bit elements (the epilogue packs four channels into 8 bytes)");
   static_assert(BM * BN * 2 <= NS * STAGE, "output tile must fit the ring");
-  __shared__ __attribute__((aligned(16))) char smem[NS * STAGE + 3 * IDX + 256];
+  // gather-index ring: two slots (one offset ahead), four with one K stage per offset
+  // (two offsets ahead, so that a request has a whole stage to land)
+  __shared__ __attribute__((aligned(16))) char smem[NS * STAGE + 5 * IDX + 256];
   char* const idx_ring = smem + NS * STAGE;
-  char* const rows_lds = idx_ring + 2 * IDX;  // the tile's output rows
+  char* const rows_lds = idx_ring + 4 * IDX;  // the tile's output rows
   char* const idx_dummy = rows_lds + IDX;     // target of the index DMA of stages entering no offset
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -1208,6 +1210,8 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_wide_kernel(ConvArgs a) {
   mask &= (1u << kvol) - 1u;
   const int rb = a.cin * static_cast<int>(sizeof(T));
   const int KB = rb >> 7;
+  const int islots = KB == 1 ? 3 : 1;  // index-ring slot mask
+  const int ahead = KB == 1 ? 2 : 1;   // offsets between an index request and its use
   const int taps = __popc(mask);
   const int S = taps * KB;
   const uint64_t n_in = static_cast<uint64_t>(a.n_in);
@@ -1242,12 +1246,18 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_wide_kernel(ConvArgs a) {
   int ck, ckb, cord;
   const char* src[LA];
   auto enter_offset = [&]() {
-    const int32_t* gi = reinterpret_cast<const int32_t*>(idx_ring + (cord & 1) * IDX);
+    const int32_t* gi = reinterpret_cast<const int32_t*>(idx_ring + (cord & islots) * IDX);
     int32_t g[LA];
 #pragma unroll
     for (int j = 0; j < LA; ++j) g[j] = gi[r0 + 8 * NW * j];
 #pragma unroll
     for (int j = 0; j < LA; ++j) src[j] = gather_src(a.in, g[j], n_in, rb, coff, zrow);
+  };
+  // offset whose indices are requested on entering an offset: the next one, or with one
+  // K stage per offset the one after it (the current one again past the last)
+  auto ahead_offset = [&]() {
+    const uint32_t r = KB == 1 ? rest & (rest - 1u) : rest;
+    return r ? __builtin_ctz(r) : ck;
   };
   auto advance = [&]() {
     if (++ckb == KB) {
@@ -1306,7 +1316,7 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_wide_kernel(ConvArgs a) {
       if (ckb == 0) {
         wait_lgkm0();
         enter_offset();
-        issue_idx(rest ? __builtin_ctz(rest) : ck, (cord + 1) & 1);
+        issue_idx(ahead_offset(), (cord + ahead) & islots);
       } else {
         lds_dma4(a.gidx + lane, idx_dummy);
       }
@@ -1336,10 +1346,7 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_wide_kernel(ConvArgs a) {
     group(G2{});
     if constexpr (MODE == 0) {
       advance();
-      // with one K stage per offset the next stage enters an offset and reads the
-      // indices this stage requested: they must land before the barrier
-      if (KB == 1) wait_vmcnt<L>();
-      else wait_vmcnt<L + 1>();
+      wait_vmcnt<L + 1>();
       raw_barrier();
     } else if constexpr (MODE == 1) {
       wait_vmcnt<0>();
@@ -1354,28 +1361,29 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_wide_kernel(ConvArgs a) {
     ckb = 0;
     cord = 0;
     issue_idx(ck, 0);
+    if (KB == 1) issue_idx(rest ? __builtin_ctz(rest) : ck, 1);
     wait_vmcnt<0>();
     raw_barrier();
     enter_offset();
     // prologue: the next offset's indices (offset 0's again without a successor), then
     // stages 0 and 1 (with S = 1, stage 1 rereads stage 0's rows into slot 1, unused;
     // the epilogue's wait retires it)
-    issue_idx(rest ? __builtin_ctz(rest) : ck, 1);
+    issue_idx(ahead_offset(), ahead);
 #pragma unroll
     for (int st = 0; st < NS - 1; ++st) {
 #pragma unroll
       for (int u = 0; u < L; ++u) issue_load(st, u);
       advance();
       if (st == 0 && KB == 1) {
-        // stage 1 is the next offset's: its indices (requested before stage 0's
-        // loads) land, then its sources, and the request for the offset after it
-        wait_vmcnt<L>();
-        raw_barrier();
+        // stage 1 is the second offset's, whose indices came with the first's
         enter_offset();
-        issue_idx(rest ? __builtin_ctz(rest) : ck, (cord + 1) & 1);
+        issue_idx(ahead_offset(), (cord + 2) & 3);
       }
     }
-    wait_vmcnt<L>();
+    // stage 0's loads land (with one K stage per offset also the third offset's
+    // indices, requested before them; the fourth's may stay in flight)
+    if (KB == 1) wait_vmcnt<L + 1>();
+    else wait_vmcnt<L>();
     raw_barrier();
 #pragma unroll
     for (int i = 0; i < NF; ++i) frag_one(0, G0{}, i);
@@ -1769,7 +1777,7 @@ int launch_mfma(const ConvArgs& base, hipStream_t stream) {
     // few-offset tables (the strided pair): 128-row tiles in a 48..64 KB ring, so that two
     // or three workgroups share a CU and cover each other's tile start and end
     // 128-byte rows into 128 outputs (the stride-2 down-convolution): one 128-byte
-    // request per gathered row, one K stage per offset (0.060 against 0.062 ms for the
+    // request per gathered row, one K stage per offset (0.057 against 0.062 ms for the
     // 128-row ring tile)
     if (few && rb == 128 && a.cout == 128) return launch_wide<T, 128, 8>(a, stream);
     if (few) return a.cout == 64 ? launch_ring<T, 64, 4, 128>(a, stream) : launch_ring<T, 128, 4, 128>(a, stream);
