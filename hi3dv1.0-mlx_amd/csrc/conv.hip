@@ -1178,7 +1178,7 @@ constexpr int kWideDepth = 3;
 
 __device__ __forceinline__ int wide_off(int row, int chunk) { return row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4); }
 
-template <typename T, int BN, int NW>
+template <typename T, int BN, int NW, bool K1>
 __global__ __launch_bounds__(NW * 64, 1) void conv_wide_kernel(ConvArgs a) {
   using Sh = WideShape<BN, NW>;
   constexpr int NS = kWideDepth, BM = Sh::BM, LA = Sh::LA, LB = Sh::LB, SUB = Sh::SUB, L = Sh::L;
@@ -1187,11 +1187,13 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_wide_kernel(ConvArgs a) {
   static_assert(STAGE == 49152 && LG * (KG - 1) == L && LG <= NM && LA * 8 * NW == BM, "stage shape");
   static_assert(sizeof(T) == 2, "16-bit elements (the epilogue packs four channels into 8 bytes)");
   static_assert(BM * BN * 2 <= NS * STAGE, "output tile must fit the ring");
-  // gather-index ring: two slots (one offset ahead), four with one K stage per offset
-  // (two offsets ahead, so that a request has a whole stage to land)
-  __shared__ __attribute__((aligned(16))) char smem[NS * STAGE + 5 * IDX + 256];
+  // gather-index ring: two slots (one offset ahead), or with K1 (128-byte rows, one K
+  // stage per offset) four, two offsets ahead, so that a request has a whole stage to land
+  constexpr int ISLOTS = K1 ? 4 : 2;
+  constexpr int AHEAD = K1 ? 2 : 1;  // offsets between an index request and its use
+  __shared__ __attribute__((aligned(16))) char smem[NS * STAGE + (ISLOTS + 1) * IDX + 256];
   char* const idx_ring = smem + NS * STAGE;
-  char* const rows_lds = idx_ring + 4 * IDX;  // the tile's output rows
+  char* const rows_lds = idx_ring + ISLOTS * IDX;  // the tile's output rows
   char* const idx_dummy = rows_lds + IDX;     // target of the index DMA of stages entering no offset
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -1210,8 +1212,6 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_wide_kernel(ConvArgs a) {
   mask &= (1u << kvol) - 1u;
   const int rb = a.cin * static_cast<int>(sizeof(T));
   const int KB = rb >> 7;
-  const int islots = KB == 1 ? 3 : 1;  // index-ring slot mask
-  const int ahead = KB == 1 ? 2 : 1;   // offsets between an index request and its use
   const int taps = __popc(mask);
   const int S = taps * KB;
   const uint64_t n_in = static_cast<uint64_t>(a.n_in);
@@ -1246,7 +1246,7 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_wide_kernel(ConvArgs a) {
   int ck, ckb, cord;
   const char* src[LA];
   auto enter_offset = [&]() {
-    const int32_t* gi = reinterpret_cast<const int32_t*>(idx_ring + (cord & islots) * IDX);
+    const int32_t* gi = reinterpret_cast<const int32_t*>(idx_ring + (cord & (ISLOTS - 1)) * IDX);
     int32_t g[LA];
 #pragma unroll
     for (int j = 0; j < LA; ++j) g[j] = gi[r0 + 8 * NW * j];
@@ -1256,7 +1256,7 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_wide_kernel(ConvArgs a) {
   // offset whose indices are requested on entering an offset: the next one, or with one
   // K stage per offset the one after it (the current one again past the last)
   auto ahead_offset = [&]() {
-    const uint32_t r = KB == 1 ? rest & (rest - 1u) : rest;
+    const uint32_t r = K1 ? rest & (rest - 1u) : rest;
     return r ? __builtin_ctz(r) : ck;
   };
   auto advance = [&]() {
@@ -1316,7 +1316,7 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_wide_kernel(ConvArgs a) {
       if (ckb == 0) {
         wait_lgkm0();
         enter_offset();
-        issue_idx(ahead_offset(), (cord + ahead) & islots);
+        issue_idx(ahead_offset(), (cord + AHEAD) & (ISLOTS - 1));
       } else {
         lds_dma4(a.gidx + lane, idx_dummy);
       }
@@ -1361,20 +1361,20 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_wide_kernel(ConvArgs a) {
     ckb = 0;
     cord = 0;
     issue_idx(ck, 0);
-    if (KB == 1) issue_idx(rest ? __builtin_ctz(rest) : ck, 1);
+    if constexpr (K1) issue_idx(rest ? __builtin_ctz(rest) : ck, 1);
     wait_vmcnt<0>();
     raw_barrier();
     enter_offset();
     // prologue: the next offset's indices (offset 0's again without a successor), then
     // stages 0 and 1 (with S = 1, stage 1 rereads stage 0's rows into slot 1, unused;
     // the epilogue's wait retires it)
-    issue_idx(ahead_offset(), ahead);
+    issue_idx(ahead_offset(), AHEAD);
 #pragma unroll
     for (int st = 0; st < NS - 1; ++st) {
 #pragma unroll
       for (int u = 0; u < L; ++u) issue_load(st, u);
       advance();
-      if (st == 0 && KB == 1) {
+      if (K1 && st == 0) {
         // stage 1 is the second offset's, whose indices came with the first's
         enter_offset();
         issue_idx(ahead_offset(), (cord + 2) & 3);
@@ -1382,13 +1382,13 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_wide_kernel(ConvArgs a) {
     }
     // stage 0's loads land (with one K stage per offset also the third offset's
     // indices, requested before them; the fourth's may stay in flight)
-    if (KB == 1) wait_vmcnt<L + 1>();
+    if constexpr (K1) wait_vmcnt<L + 1>();
     else wait_vmcnt<L>();
     raw_barrier();
 #pragma unroll
     for (int i = 0; i < NF; ++i) frag_one(0, G0{}, i);
 
-    if (S == 1) {
+    if (K1 && S == 1) {
       stage(0, I2{});
     } else {
       int slot = 0;
@@ -1457,14 +1457,16 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_wide_kernel(ConvArgs a) {
   }
 }
 
-template <typename T, int BN, int NW>
+template <typename T, int BN, int NW, bool K1 = false>
 int launch_wide(const ConvArgs& base, hipStream_t stream) {
+  // the one-stage form (K1) takes 128-byte rows and the other form longer ones
+  HI3D_REQUIRE(K1 == (base.cin * static_cast<int>(sizeof(T)) == 128), "wide kernel: row length and form disagree");
   ConvArgs a = base;
   a.ny = a.cout / BN;
   const int64_t blocks = ceil_div(a.ntiles, WideShape<BN, NW>::SUB) * a.ny;
   if (blocks == 0) return HI3D_OK;
   HI3D_REQUIRE(blocks < (int64_t(1) << 31), "too many tiles");
-  hipLaunchKernelGGL((conv_wide_kernel<T, BN, NW>), dim3(static_cast<unsigned>(blocks)), dim3(NW * 64), 0, stream, a);
+  hipLaunchKernelGGL((conv_wide_kernel<T, BN, NW, K1>), dim3(static_cast<unsigned>(blocks)), dim3(NW * 64), 0, stream, a);
   HI3D_LAUNCH_CHECK();
   return HI3D_OK;
 }
@@ -1777,9 +1779,9 @@ int launch_mfma(const ConvArgs& base, hipStream_t stream) {
     // few-offset tables (the strided pair): 128-row tiles in a 48..64 KB ring, so that two
     // or three workgroups share a CU and cover each other's tile start and end
     // 128-byte rows into 128 outputs (the stride-2 down-convolution): one 128-byte
-    // request per gathered row, one K stage per offset (0.057 against 0.062 ms for the
-    // 128-row ring tile)
-    if (few && rb == 128 && a.cout == 128) return launch_wide<T, 128, 8>(a, stream);
+    // request per gathered row, one K stage per offset (0.058-0.062 against 0.064 ms
+    // for the 128-row ring tile on one box)
+    if (few && rb == 128 && a.cout == 128) return launch_wide<T, 128, 8, true>(a, stream);
     if (few) return a.cout == 64 ? launch_ring<T, 64, 4, 128>(a, stream) : launch_ring<T, 128, 4, 128>(a, stream);
     if (a.kvol <= kMaxPipelinedKvol && ring_rows && a.cout % 128 == 0) {
       if (rb % 128 == 0) return launch_wide<T, 128, 8>(a, stream);
