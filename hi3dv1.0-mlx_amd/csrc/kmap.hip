@@ -371,6 +371,10 @@ __global__ __launch_bounds__(kLookup3Rows) void dense_lookup3_kernel(const int4*
       o = static_cast<int32_t>(i);
       c = coords[o];
     }
+    // An out-of-range row (flagged by the scatter or the key kernel) reads no cell: its
+    // z-runs are checked per column only, so a z far outside the grid would otherwise
+    // address cells far outside the buffer.
+    if (!g.inside(c.x, c.y, c.z, c.w)) c = make_int4(0, -2, -2, -2);
   }
   orow[t] = o;
   const bool bin = static_cast<unsigned>(c.x) < static_cast<unsigned>(g.batch);

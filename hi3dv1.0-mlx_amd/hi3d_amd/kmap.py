@@ -51,7 +51,16 @@ KMAP_DENSE_KEEP_BYTES: int = 8 << 30
 """Kept dense grids beyond this many bytes in total are freed, least recently used
 first (the grid of the current build always stays)."""
 
-_DENSE_GRIDS: dict[tuple[int, int], torch.Tensor] = {}
+@dataclass
+class _KeptGrid:
+    """A dense grid kept between builds (every cell -1 outside a build) and the event
+    recorded on the stream of its last build, after that build's restore."""
+
+    grid: torch.Tensor
+    done: torch.cuda.Event | None = None
+
+
+_DENSE_GRIDS: dict[tuple[int, int], _KeptGrid] = {}
 
 
 def release_dense_grids() -> None:
@@ -59,18 +68,39 @@ def release_dense_grids() -> None:
     _DENSE_GRIDS.clear()
 
 
-def _kept_grid(device: torch.device, cells: int, nbytes: int) -> torch.Tensor:
+def _kept_grid(device: torch.device, cells: int, nbytes: int) -> tuple[tuple[int, int], _KeptGrid]:
     key = (device.index if device.index is not None else torch.cuda.current_device(), cells)
-    grid = _DENSE_GRIDS.pop(key, None)
-    if grid is None:
-        held = sum(g.numel() * 4 for g in _DENSE_GRIDS.values())
+    entry = _DENSE_GRIDS.pop(key, None)
+    if entry is None:
+        held = sum(e.grid.numel() * 4 for e in _DENSE_GRIDS.values())
         for k in list(_DENSE_GRIDS):
             if held + nbytes <= KMAP_DENSE_KEEP_BYTES:
                 break
-            held -= _DENSE_GRIDS.pop(k).numel() * 4
-        grid = torch.full((nbytes // 4,), -1, dtype=torch.int32, device=device)
-    _DENSE_GRIDS[key] = grid  # most recently used last
-    return grid
+            held -= _DENSE_GRIDS.pop(k).grid.numel() * 4
+        entry = _KeptGrid(torch.full((nbytes // 4,), -1, dtype=torch.int32, device=device))
+    _DENSE_GRIDS[key] = entry  # most recently used last
+    return key, entry
+
+
+def _build_on_kept_grid(key: tuple[int, int], entry: _KeptGrid, device: torch.device, launch) -> None:
+    """Run ``launch(grid)`` (one kept-grid build) on the current stream of ``device``.
+
+    The build stores its rows in the grid's cells and puts them back, so two builds must
+    not overlap on one grid: the current stream first waits for the previous build's
+    event (a no-op on the same stream), and records its own after the launch. A launch
+    that raises drops the grid, since its cells may no longer all be -1."""
+    current = torch.cuda.current_stream(device)
+    if entry.done is not None:
+        current.wait_event(entry.done)
+    entry.grid.record_stream(current)  # freeing the grid waits for this stream's work too
+    try:
+        launch(entry.grid)
+    except BaseException:
+        _DENSE_GRIDS.pop(key, None)
+        raise
+    done = torch.cuda.Event()
+    done.record(current)
+    entry.done = done
 
 PLAN_GLOBAL_ROWS = 1 << 21
 PLAN_SMALL_WINDOW = 0
@@ -280,8 +310,8 @@ def build_kernel_map(
     """Submanifold kernel map of ``indices [N, 4]`` ``(batch, x, y, z)``: through a dense
     grid of rows when the grid has at most ``KMAP_DENSE_MAX_CELLS`` cells and no hash
     ``capacity`` is asked for (kept between calls when ``KMAP_DENSE_KEEP``), else
-    through the voxel hash (same table either way). Builds that share a kept grid must
-    not overlap: run them on one stream.
+    through the voxel hash (same table either way). Builds on a kept grid are ordered
+    across streams by an event recorded after each one.
 
     With ``check`` the device status word is read (one sync): duplicate or out-of-range
     coordinates raise ``ValueError``, a full hash table raises ``RuntimeError``.
@@ -302,17 +332,21 @@ def build_kernel_map(
     if capacity is None and cells <= KMAP_DENSE_MAX_CELLS:
         nbytes = _lib.query("hi3d_kmap_dense_workspace", int(batch_size), sx, sy, sz)
         if KMAP_DENSE_KEEP:
-            grid = _kept_grid(device, cells, nbytes)
+            key, entry = _kept_grid(device, cells, nbytes)
             order, order_bytes = None, 0
             if KMAP_DENSE_ORDER_MIN_BYTES is not None and nbytes > KMAP_DENSE_ORDER_MIN_BYTES and n:
                 order = _lib.workspace(_lib.query("hi3d_kmap_dense_order_workspace", n), device)
                 order_bytes = order.numel()
-            _lib.call(
-                "hi3d_kmap_subm_dense_kept",
-                _lib.ptr(coords), n, sx, sy, sz, int(batch_size), int(ksize), _lib.ptr(grid), grid.numel() * 4,
-                _lib.ptr(order), order_bytes,
-                _lib.ptr(table), _lib.ptr(counts), _lib.ptr(status), _lib.stream(device),
-            )
+
+            def launch(grid: torch.Tensor) -> None:
+                _lib.call(
+                    "hi3d_kmap_subm_dense_kept",
+                    _lib.ptr(coords), n, sx, sy, sz, int(batch_size), int(ksize), _lib.ptr(grid), grid.numel() * 4,
+                    _lib.ptr(order), order_bytes,
+                    _lib.ptr(table), _lib.ptr(counts), _lib.ptr(status), _lib.stream(device),
+                )
+
+            _build_on_kept_grid(key, entry, device, launch)
         else:
             ws = _lib.workspace(nbytes, device)
             _lib.call(

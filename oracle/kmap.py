@@ -111,6 +111,43 @@ def neighbour_rows(indices: np.ndarray, spatial_shape, rows: np.ndarray, ksize: 
     return table
 
 
+def neighbour_table_sorted(indices: np.ndarray, spatial_shape, ksize: int = 3) -> np.ndarray:
+    """``[N, ks^3]`` table (sentinel N) by the same sorted-key ``searchsorted`` lookup as
+    :func:`subm_pairs` (src/hi3d_mac/torch_backend/sparse_conv.py:115-149), with the
+    queries taken in key order: the packed key is linear in the coordinates, so the
+    shifted keys of the key-sorted rows are the sorted keys plus one constant, and the
+    search runs over sorted needles (minutes become seconds at millions of voxels).
+    Writes the table directly instead of per-offset lists."""
+    coords = np.asarray(indices, dtype=np.int64)
+    shape = np.array([int(v) for v in spatial_shape], dtype=np.int64)
+    n = coords.shape[0]
+    kvol = ksize**3
+    table = np.full((n, kvol), n, dtype=np.int32)
+    if n == 0:
+        return table
+    keys = voxel_keys(coords, shape)
+    order = np.argsort(keys, kind="stable")
+    sorted_keys = keys[order]
+    sorted_xyz = [coords[order, 1 + a] for a in range(3)]
+    half = ksize // 2
+    in_sorted = np.full((n, kvol), n, dtype=np.int32)  # rows in key order, then permuted once
+    for k, r in enumerate(itertools.product(range(ksize), repeat=3)):
+        d = [int(v) - half for v in r]
+        delta = (d[0] * int(shape[1]) + d[1]) * int(shape[2]) + d[2]
+        inside = np.ones(n, dtype=bool)
+        for a in range(3):
+            if d[a] < 0:
+                inside &= sorted_xyz[a] >= -d[a]
+            elif d[a] > 0:
+                inside &= sorted_xyz[a] < shape[a] - d[a]
+        query = sorted_keys + delta
+        pos = np.minimum(np.searchsorted(sorted_keys, query), n - 1)
+        found = inside & (sorted_keys[pos] == query)
+        in_sorted[found, k] = order[pos[found]]
+    table[order] = in_sorted
+    return table
+
+
 def neighbour_table_dense(coords: np.ndarray) -> np.ndarray:
     """Dense-grid ``neighbour_table`` (src/hi3d_mac/mlx_backend/sparse.py:29-43): a padded
     index grid of extent ``max + 3``, 27 fancy gathers. ``coords`` is ``[N, 3]``."""

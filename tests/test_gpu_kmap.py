@@ -145,8 +145,10 @@ def test_workload_maps_bit_exact(cuda, name):
 
 
 def test_large_shell_map_properties(cuda):
-    """The 1024^3 workload (~4.4M voxels): exact on sampled rows, and over all rows the
-    size-independent properties: neighbour coordinates, symmetry, count symmetry."""
+    """The 1024^3 workload (~4.4M voxels): the whole table equals the oracle's (the
+    sort + searchsorted lookup over key-ordered rows, every row and offset), and over all
+    rows the size-independent properties: neighbour coordinates, symmetry, count
+    symmetry."""
     from hi3d_amd import kmap, workloads
 
     idx = workloads.coords_for("resblock_c256_fp16", device=cuda)
@@ -154,9 +156,8 @@ def test_large_shell_map_properties(cuda):
     coords = torch.as_tensor(idx).to(cuda)
     km = kmap.build_kernel_map(coords, [1024] * 3, 1)
     table = km.table
-    rows = np.random.default_rng(0).choice(n, 4096, replace=False)
-    assert np.array_equal(table[torch.as_tensor(rows, device=cuda)].cpu().numpy(),
-                          okmap.neighbour_rows(idx, [1024] * 3, rows))
+    print(f"comparing the full {n} x 27 table with the oracle", flush=True)
+    assert np.array_equal(table.cpu().numpy(), okmap.neighbour_table_sorted(idx, [1024] * 3))
     offs = torch.as_tensor(okmap.kernel_offsets(3) - 1, device=cuda, dtype=torch.int32)
     present = table != n
     for k in range(27):
@@ -307,6 +308,12 @@ def test_gather_neighbours_matches_take(cuda, dtype, c):
     assert torch.equal(got, padded[level.table[5:77].long()])
 
 
+# (column, value for a grid of side n) of coordinates outside the grid: one cell past an
+# edge, and z (whose cells the 3x3x3 lookup loads as runs) far outside on either side
+_OUT_OF_RANGE = [(2, lambda n: n), (3, lambda n: 1 << 30), (3, lambda n: -(1 << 30)), (3, lambda n: n + 40),
+                 (3, lambda n: -1)]
+
+
 @pytest.mark.parametrize("ksize,batch,n_side,density", [(3, 1, 20, 0.2), (3, 3, 16, 0.5), (5, 2, 12, 0.3),
                                                         (3, 1, 64, 0.01)])
 def test_dense_and_hash_maps_agree(cuda, ksize, batch, n_side, density):
@@ -327,10 +334,11 @@ def test_dense_and_hash_maps_agree(cuda, ksize, batch, n_side, density):
     for cap in (None, 1 << 16):
         with pytest.raises(ValueError, match="duplicate"):
             kmap.build_kernel_map(dup, [n_side] * 3, batch, ksize, capacity=cap)
-        bad = t.clone()
-        bad[5, 2] = n_side
-        with pytest.raises(ValueError, match="outside"):
-            kmap.build_kernel_map(bad, [n_side] * 3, batch, ksize, capacity=cap)
+        for col, value in _OUT_OF_RANGE:
+            bad = t.clone()
+            bad[5, col] = value(n_side)
+            with pytest.raises(ValueError, match="outside"):
+                kmap.build_kernel_map(bad, [n_side] * 3, batch, ksize, capacity=cap)
     old = kmap.KMAP_DENSE_MAX_CELLS
     try:
         kmap.KMAP_DENSE_MAX_CELLS = 0  # the hash without a capacity
@@ -346,8 +354,11 @@ def test_dense_and_hash_maps_agree(cuda, ksize, batch, n_side, density):
         assert torch.equal(ordered.table, dense.table) and torch.equal(ordered.counts, dense.counts)
         with pytest.raises(ValueError, match="duplicate"):
             kmap.build_kernel_map(dup, [n_side] * 3, batch, ksize)
-        with pytest.raises(ValueError, match="outside"):
-            kmap.build_kernel_map(bad, [n_side] * 3, batch, ksize)
+        for col, value in _OUT_OF_RANGE:
+            bad = t.clone()
+            bad[5, col] = value(n_side)
+            with pytest.raises(ValueError, match="outside"):
+                kmap.build_kernel_map(bad, [n_side] * 3, batch, ksize)
         assert torch.equal(kmap.build_kernel_map(t, [n_side] * 3, batch, ksize).table, dense.table)
     finally:
         kmap.KMAP_DENSE_ORDER_MIN_BYTES = old_order
@@ -388,13 +399,55 @@ def _kept_grid_sets(cuda, kmap, sets, side):
         finally:
             kmap.KMAP_DENSE_KEEP = old
         assert torch.equal(kept.table, fresh.table) and torch.equal(kept.counts, fresh.counts)
-        (grid,) = kmap._DENSE_GRIDS.values()
+        (entry,) = kmap._DENSE_GRIDS.values()
+        grid = entry.grid
         assert int(grid.numel()) >= 2 * side**3 and bool((grid == -1).all())
         dup = torch.cat([t, t[7:9]])
         with pytest.raises(ValueError, match="duplicate"):
             kmap.build_kernel_map(dup, [side] * 3, 2)
-        bad = t.clone()
-        bad[3, 1] = side
-        with pytest.raises(ValueError, match="outside"):
-            kmap.build_kernel_map(bad, [side] * 3, 2)
+        for col, value in [(1, lambda n: n)] + _OUT_OF_RANGE:
+            bad = t.clone()
+            bad[3, col] = value(side)
+            with pytest.raises(ValueError, match="outside"):
+                kmap.build_kernel_map(bad, [side] * 3, 2)
         assert bool((grid == -1).all())
+
+
+def test_kept_dense_grid_across_streams_and_errors(cuda, monkeypatch):
+    """Builds on one kept grid from two streams in a row give the oracle's map each time
+    (the second stream waits for the first build's restore), and a build whose call
+    raises drops the kept grid, so the next build starts from a fresh one."""
+    from hi3d_amd import _lib, kmap
+
+    rng = np.random.default_rng(7)
+    side = 32
+    kmap.release_dense_grids()
+    sets = [_rand_indices(rng, side, 0.15), _rand_indices(rng, side, 0.3)]
+    streams = [torch.cuda.Stream(cuda), torch.cuda.Stream(cuda)]
+    tables = []
+    for idx, s in zip(sets, streams):
+        t = torch.as_tensor(idx).to(cuda)
+        torch.cuda.current_stream(cuda).synchronize()
+        with torch.cuda.stream(s):
+            tables.append(kmap.build_kernel_map(t, [side] * 3, 1, check=False).table)
+    torch.cuda.synchronize(cuda)
+    for idx, table in zip(sets, tables):
+        assert np.array_equal(table.cpu().numpy(), okmap.neighbour_table(idx, [side] * 3))
+    (entry,) = kmap._DENSE_GRIDS.values()
+    assert bool((entry.grid == -1).all())
+
+    real_call = _lib.call
+
+    def failing(name, *args):
+        if name == "hi3d_kmap_subm_dense_kept":
+            raise _lib.Hi3dError("planted failure")
+        return real_call(name, *args)
+
+    monkeypatch.setattr(_lib, "call", failing)
+    with pytest.raises(_lib.Hi3dError, match="planted"):
+        kmap.build_kernel_map(torch.as_tensor(sets[0]).to(cuda), [side] * 3, 1)
+    assert not kmap._DENSE_GRIDS
+    monkeypatch.setattr(_lib, "call", real_call)
+    again = kmap.build_kernel_map(torch.as_tensor(sets[1]).to(cuda), [side] * 3, 1)
+    assert np.array_equal(again.table.cpu().numpy(), okmap.neighbour_table(sets[1], [side] * 3))
+    kmap.release_dense_grids()

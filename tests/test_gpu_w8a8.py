@@ -53,7 +53,7 @@ def test_reference_shapes_bit_exact(cuda, rows, cols, width):
     integer = np.asarray(q, np.int64) @ np.asarray(w, np.int64).T
     expected = integer.astype(np.float32) * sa[:, None] * sw[None, :] + bias.astype(np.float32)
     assert np.isfinite(result).all()
-    np.testing.assert_allclose(result, expected, rtol=5e-4, atol=2e-6 + 1e-3 * np.abs(expected).max())
+    np.testing.assert_allclose(result, expected, rtol=5e-4, atol=2e-6)
 
 
 @pytest.mark.parametrize("rotation", ["h64", "none"])

@@ -7,6 +7,8 @@ Pinning map (oracle function -> checks here):
   kmap.subm_pairs / neighbour_table   -> brute_force_table, neighbour_table_dense, the
                                          layout invariants of tests/test_backends.py:53-67
   kmap.neighbour_table_dense          -> brute_force_table
+  kmap.neighbour_rows / neighbour_table_sorted -> brute_force_table (corners, faces, batch
+                                         2, ksize 5, keys above 2^62) and neighbour_table
   kmap.pairs_from_table/table_from_pairs -> round trip + subm_pairs lists
   kmap.stride2_structure / downsample_structure -> brute-force parents and slots
   kmap.child_neighbour_table          -> dense-grid table of the children
@@ -24,6 +26,13 @@ Pinning map (oracle function -> checks here):
   norm.adaln_projection              -> closed forms (zero weight, identity halves, SiLU
                                          from math.exp), torch linear + chunk(2)
   norm.residual_block_f64            -> explicit float64 composition
+  vae.group_stats_f64 / group_norm_swish / gather_group_norm_swish -> numpy per-group
+                                         moments, u / (1 + exp(-u)), element-wise block
+  vae.conv_gn_swish_f64 / resnet_f64 / occupancy_f64 -> per-group GroupNorm + dense
+                                         F.conv3d(padding=1) over the scattered grid
+  vae.children_f64 / child_coords / upsample_f64 -> s*I slot weights, per-child products,
+                                         SerializedUnpooling's masked view, inv_grid_coord,
+                                         brute-force child table
 """
 
 from __future__ import annotations
@@ -69,6 +78,62 @@ def test_dense_grid_table_matches_brute_force():
     assert np.array_equal(dense, okmap.brute_force_table(idx, [9, 9, 9], 3))
     # the extent-agnostic dense grid agrees with the bounded sort-based map
     assert np.array_equal(dense, okmap.neighbour_table(idx, [9, 9, 9], 3))
+
+
+def _with_edges(idx, side, batch):
+    """``idx`` plus every corner, one voxel on each face centre and the grid centre of
+    every batch element (deduplicated)."""
+    extra = []
+    for b in range(batch):
+        for x in (0, side - 1):
+            for y in (0, side - 1):
+                for z in (0, side - 1):
+                    extra.append((b, x, y, z))
+        m = side // 2
+        for face in ((0, m, m), (side - 1, m, m), (m, 0, m), (m, side - 1, m), (m, m, 0), (m, m, side - 1),
+                     (m, m, m)):
+            extra.append((b, *face))
+    allrows = np.concatenate([idx, np.array(extra, np.int32)])
+    return np.unique(allrows, axis=0)
+
+
+@pytest.mark.parametrize("ksize,batch", [(3, 1), (3, 2), (5, 2)])
+def test_neighbour_rows_and_sorted_table_match_brute_force(ksize, batch):
+    """``neighbour_rows`` (the sampled-row lookup) and ``neighbour_table_sorted`` (the
+    full-size table) against the dictionary brute force and the pair-list table, on sets
+    with voxels on every corner and face of the grid, two batch elements and ksize 5;
+    sampled rows in any order and with repeats."""
+    rng = np.random.default_rng(40 + ksize + batch)
+    side = 8
+    idx = _with_edges(_rand_indices(rng, side, 0.25, batch=batch), side, batch)
+    idx = idx[rng.permutation(len(idx))]
+    brute = okmap.brute_force_table(idx, [side] * 3, ksize)
+    assert np.array_equal(okmap.neighbour_table(idx, [side] * 3, ksize), brute)
+    assert np.array_equal(okmap.neighbour_table_sorted(idx, [side] * 3, ksize), brute)
+    rows = np.concatenate([rng.permutation(len(idx)), rng.integers(0, len(idx), 17)])
+    assert np.array_equal(okmap.neighbour_rows(idx, [side] * 3, rows, ksize), brute[rows])
+
+
+def test_neighbour_rows_and_sorted_table_with_64bit_keys():
+    """Grids whose packed keys exceed 2^62: clusters of voxels near the far corners of a
+    [2e6, 2e6, 1e6] grid with two batch elements (keys below 2^63), so keys differ in
+    their high bits; both lookups against the brute force, which packs no keys."""
+    rng = np.random.default_rng(44)
+    shape = [2_000_000, 2_000_000, 1_000_000]
+    parts = []
+    for corner in ((0, 0, 0), (shape[0] - 6, shape[1] - 6, shape[2] - 6), (shape[0] - 6, 0, shape[2] - 6),
+                   (1 << 20, 1 << 19, 1 << 18)):
+        xyz = np.argwhere(rng.random((6, 6, 6)) < 0.4) + np.array(corner)
+        for b in range(2):
+            parts.append(np.concatenate([np.full((len(xyz), 1), b), xyz], 1))
+    idx = np.concatenate(parts).astype(np.int64)
+    idx = idx[rng.permutation(len(idx))]
+    keys = okmap.voxel_keys(idx, shape)
+    assert int(keys.max()) > (1 << 62) and int(keys.min()) >= 0
+    brute = okmap.brute_force_table(idx, shape, 3)
+    assert np.array_equal(okmap.neighbour_table_sorted(idx, shape), brute)
+    assert np.array_equal(okmap.neighbour_rows(idx, shape, np.arange(len(idx))), brute)
+    assert np.array_equal(okmap.neighbour_table(idx, shape), brute)
 
 
 def test_pair_layout_invariants():
@@ -499,6 +564,128 @@ def test_vae_children_oracle_slot_layout():
         assert np.allclose(got[i], w[s * c:(s + 1) * c] @ x[parent[i]], rtol=1e-13, atol=1e-13)
     feat = x @ w.T
     assert np.array_equal(feat.reshape(p * 8, c)[mask.reshape(-1)], got)
+
+
+def _vae_params(rng, name, cin, cout, res_conv=False, head=False):
+    """Random decoder parameters under the reference's key names (vae.py:166-218,
+    270-271): GroupNorm ``weights``/``bias`` and conv ``weight [27 Cin, Cout]``/``bias``."""
+    p = {}
+    pairs = [("cls_head.fc.0", "cls_head.fc.2", cin, cout)] if head else \
+        [("block.0", "block.2", cin, cout), ("block.3", "block.5", cout, cout)]
+    for norm, conv, ci, co in pairs:
+        p[f"{name}.{norm}.weights"] = rng.uniform(0.5, 1.5, ci)
+        p[f"{name}.{norm}.bias"] = rng.normal(0, 0.3, ci)
+        p[f"{name}.{conv}.weight"] = rng.normal(0, 1 / np.sqrt(27 * ci), (27 * ci, co))
+        p[f"{name}.{conv}.bias"] = rng.normal(0, 0.1, co)
+    if res_conv:
+        p[f"{name}.res_conv.weight"] = rng.normal(0, 1 / np.sqrt(cin), (cout, cin))
+        p[f"{name}.res_conv.bias"] = rng.normal(0, 0.1, cout)
+    return p
+
+
+def _independent_gn_swish(x, weight, bias, eps=1e-6):
+    """GroupNorm + swish written out per group: per-group sums with the reference's
+    divisor ``n * width + eps`` (vae.py:153-164), then ``u / (1 + exp(-u))``."""
+    from oracle import vae as ovae
+
+    n, c = x.shape
+    g = ovae.groups_for(c)
+    w = c // g
+    u = np.empty_like(x)
+    for k in range(g):
+        blk = x[:, k * w:(k + 1) * w]
+        cnt = n * w + eps
+        mean = blk.sum() / cnt
+        var = (blk * blk).sum() / cnt - mean * mean
+        u[:, k * w:(k + 1) * w] = (blk - mean) / np.sqrt(var + eps)
+    u = u * weight + bias
+    return u / (1.0 + np.exp(-u))
+
+
+def _dense_conv_wt(a, xyz, weight_t, bias, side):
+    """3x3x3 convolution of the rows ``a`` at ``xyz`` by ``F.conv3d(padding=1)`` over the
+    scattered dense grid, with ``W_t`` row ``k Cin + ci`` (k = 9 kx + 3 ky + kz) as tap
+    ``(kx, ky, kz)`` of input channel ci (sparse.py:185-189)."""
+    cin = a.shape[1]
+    cout = weight_t.shape[1]
+    vol = torch.zeros((1, cin, side, side, side), dtype=torch.float64)
+    x, y, z = (torch.as_tensor(xyz[:, i]).long() for i in range(3))
+    vol[0, :, x, y, z] = torch.as_tensor(a).T
+    w = torch.as_tensor(weight_t).reshape(3, 3, 3, cin, cout).permute(4, 3, 0, 1, 2)
+    out = F.conv3d(vol, w, padding=1)[0][:, x, y, z].T.numpy()
+    return out + bias
+
+
+def test_vae_compositions_against_dense_conv3d():
+    """conv_gn_swish_f64, resnet_f64 (identity and projected shortcuts) and occupancy_f64
+    against an independent composition: per-group GroupNorm with the reference's
+    divisor, ``u / (1 + exp(-u))`` and a dense ``F.conv3d(padding=1)`` over the scattered
+    grid (src/hi3d_mac/mlx_backend/vae.py:141-218, 270-271;
+    tests/test_mlx_kernels.py:63-76,124-150)."""
+    from oracle import vae as ovae
+
+    rng = np.random.default_rng(60)
+    side = 9
+    idx = _rand_indices(rng, side, 0.3)
+    idx = idx[rng.permutation(len(idx))]
+    xyz = idx[:, 1:]
+    table = okmap.neighbour_table(idx, [side] * 3)
+    n = len(idx)
+    for cin, cout, res in ((16, 16, False), (16, 32, True)):
+        p = _vae_params(rng, "blk", cin, cout, res_conv=res)
+        x = rng.normal(0.4, 1.7, (n, cin))
+        f = lambda k: p[f"blk.{k}"]
+        a = _independent_gn_swish(x, f("block.0.weights"), f("block.0.bias"))
+        h = _dense_conv_wt(a, xyz, f("block.2.weight"), f("block.2.bias"), side)
+        got = ovae.conv_gn_swish_f64(x, table, f("block.0.weights"), f("block.0.bias"), f("block.2.weight"),
+                                     f("block.2.bias"))
+        assert np.allclose(got, h, rtol=1e-10, atol=1e-10)
+        shortcut = x @ f("res_conv.weight").T + f("res_conv.bias") if res else x
+        want = shortcut + _dense_conv_wt(_independent_gn_swish(h, f("block.3.weights"), f("block.3.bias")), xyz,
+                                         f("block.5.weight"), f("block.5.bias"), side)
+        assert np.allclose(ovae.resnet_f64(x, table, p, "blk"), want, rtol=1e-10, atol=1e-10)
+    head = _vae_params(rng, "up", 16, 8, head=True)
+    x = rng.normal(size=(n, 16))
+    want = _dense_conv_wt(_independent_gn_swish(x, head["up.cls_head.fc.0.weights"], head["up.cls_head.fc.0.bias"]),
+                          xyz, head["up.cls_head.fc.2.weight"], head["up.cls_head.fc.2.bias"], side)
+    assert np.allclose(ovae.occupancy_f64(x, table, head, "up"), want, rtol=1e-10, atol=1e-10)
+
+
+def test_vae_upsample_oracle_against_brute_force_children():
+    """upsample_f64 against an independent construction: the mask ``logits > 0`` of the
+    dense-conv occupancy, the kept children enumerated parent-major and slot-minor, each
+    child's features as its slot's ``[C, C]`` block times its parent's row, coordinates
+    ``2 p + (s>>2&1, s>>1&1, s&1)``, and the children's table by dictionary brute force
+    over their own coordinates (vae.py:220-244,316-327; blocks.py:526-543)."""
+    from oracle import vae as ovae
+
+    rng = np.random.default_rng(61)
+    side, c = 7, 8
+    idx = _rand_indices(rng, side, 0.3)
+    idx = idx[rng.permutation(len(idx))]
+    xyz = idx[:, 1:]
+    table = okmap.neighbour_table(idx, [side] * 3)
+    n = len(idx)
+    p = _vae_params(rng, "up", c, 8, head=True)
+    p["up.proj.weight"] = rng.normal(0, 1 / np.sqrt(c), (8 * c, c))
+    x = rng.normal(size=(n, c))
+    logits = _dense_conv_wt(_independent_gn_swish(x, p["up.cls_head.fc.0.weights"], p["up.cls_head.fc.0.bias"]),
+                            xyz, p["up.cls_head.fc.2.weight"], p["up.cls_head.fc.2.bias"], side)
+    feats, ccoords, ctable, parent, slot, mask = ovae.upsample_f64(x, xyz, table, p, "up")
+    assert np.array_equal(mask, logits > 0) and 0 < mask.sum() < mask.size
+    kept = [(i, s) for i in range(n) for s in range(8) if logits[i, s] > 0]
+    assert parent.tolist() == [i for i, _ in kept] and slot.tolist() == [s for _, s in kept]
+    w = p["up.proj.weight"]
+    for j, (i, s) in enumerate(kept):
+        assert np.allclose(feats[j], w[s * c:(s + 1) * c] @ x[i], rtol=1e-12, atol=1e-12)
+        bits = np.array([(s >> 2) & 1, (s >> 1) & 1, s & 1])
+        assert np.array_equal(ccoords[j], 2 * xyz[i] + bits)
+    cidx = np.concatenate([np.zeros((len(kept), 1), np.int64), ccoords], 1)
+    assert np.array_equal(ctable, okmap.brute_force_table(cidx, [2 * side] * 3, 3))
+    # a given mask is used as is
+    given = rng.random((n, 8)) < 0.3
+    out = ovae.upsample_f64(x, xyz, table, p, "up", mask=given)
+    assert np.array_equal(out[5], given) and len(out[3]) == int(given.sum())
 
 
 def test_vae_child_coords_match_unpooling_grid():
