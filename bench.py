@@ -311,6 +311,52 @@ def bench_block(steps: int, warmup: int, settle_s: float = 0.0):
     }
 
 
+def bench_resblock3d(steps: int, warmup: int):
+    """The transformer's own residual block (``SparseResBlock3d(256, 2112)``: norm1 +
+    SiLU, conv 256 -> 128, norm2 + modulate + SiLU, conv 128 -> 128 + SiLU, linear
+    128 -> 256 + the input) on the 1024^3 shells, fp16, one batch element; the kernel
+    map and plans are built before the timed passes (cached on the rows, as the
+    reference's ``indice_dict``)."""
+    import numpy as np
+    import torch
+
+    from hi3d_amd import workloads
+    from hi3d_amd.nn import SparseTensor
+    from hi3d_amd.resblock import SparseResBlock3d
+
+    dev = torch.device("cuda:0")
+    idx = coords_of("resblock_c256_fp16", dev)
+    n = len(idx)
+    c, d = 256, 2112
+    torch.manual_seed(61)
+    m = SparseResBlock3d(c, d)
+    with torch.no_grad():  # the released init zeroes the linear; give it weights to move
+        m.linear.weight.normal_(0, 1 / np.sqrt(m.hidden_channels))
+    m = m.half().to(dev)
+    x = SparseTensor(torch.as_tensor(workloads.normal((n, c), 1.0, 62, np.float16)).to(dev),
+                     torch.as_tensor(idx).to(dev))
+    emb = torch.as_tensor(workloads.normal((1, d), 1.0, 63, np.float16)).to(dev)
+    with torch.no_grad():
+        m(x, emb)  # kernel map + plans
+        torch.cuda.synchronize()
+        wall, ev = timed(lambda: m(x, emb), steps, warmup)
+    km = x.backend_data().find_indice_pair("subm3").kmap
+    pairs = int(km.counts.sum())
+    h = m.hidden_channels
+    flops = 2.0 * pairs * (c * h + h * h) + 2.0 * n * h * c
+    return {
+        "workload": "sparse_resblock3d_c256_fp16",
+        "voxels": n,
+        "pairs": pairs,
+        "channels": c,
+        "hidden": h,
+        "block_ms": ev,
+        "block_wall_ms": wall,
+        "voxels_per_s": n / (ev * 1e-3),
+        "eff_tflops": flops / (ev * 1e-3) / 1e12,
+    }
+
+
 def bench_vae(steps: int, warmup: int):
     """VAE decoder residual block (GroupNorm + swish -> conv, twice, + shortcut) at the
     finest decoder stage's width, C128 fp16, on the 512^3 fine shells, with its kernels
@@ -527,7 +573,7 @@ def cpu_baseline_w8a8(rows: int):
 
 
 WORKLOADS = ("resblock", "subm3_c128_fp16", "subm3_c64_fp32", "stride2", "w8a8", "vae_resnet", "vae_upsample",
-             "transformer_io", "unique")
+             "transformer_io", "resblock3d", "unique")
 
 
 def main() -> int:
@@ -606,6 +652,9 @@ def main() -> int:
         elif name == "transformer_io":
             log("transformer I/O resampling C256 fp16, 1024^3 shells")
             extra["transformer_io_c256_fp16"] = bench_geometry(half_steps, half_warm)
+        elif name == "resblock3d":
+            log("transformer SparseResBlock3d C256 (hidden 128, emb 2112) fp16, 1024^3 shells")
+            extra["sparse_resblock3d_c256_fp16"] = bench_resblock3d(half_steps, half_warm)
         elif name == "unique":
             log("unique cube corners of the 1024^3 shells")
             extra["unique_corners_1024"] = bench_unique(max(5, args.steps // 10), 2)

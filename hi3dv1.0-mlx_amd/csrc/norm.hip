@@ -10,11 +10,22 @@
 namespace hi3d {
 namespace {
 
+// SiLU of an fp16 value as the reference's fp16 ``x * sigmoid(x)``
+// (src/hi3d_mac/mlx_backend/transformer.py:172-173): the sigmoid rounded to fp16, then
+// the product rounded to fp16.
+__device__ __forceinline__ _Float16 silu_h(_Float16 h) {
+#pragma clang fp contract(off)
+  const float x = static_cast<float>(h);
+  const _Float16 sig = static_cast<_Float16>(1.0f / (1.0f + __expf(-x)));
+  return static_cast<_Float16>(x * static_cast<float>(sig));
+}
+
 // G lanes per row, CPL 8-element chunks per lane (chunk g + i G), held in registers;
 // fp32 two-pass statistics; y = (x - mean) * inv [* w + b]; h = fp16(y); modulate
-// h = fp16(fp16(h * scale) + shift) (two roundings, no FMA). The per-channel vectors of a
-// lane's chunks are loaded once; blocks stride over groups of 256 / G rows.
-template <int G, int CPL, bool kAffine, bool kModulate>
+// h = fp16(fp16(h * scale) + shift) (two roundings, no FMA); kSilu: h = silu(h) in fp16.
+// The per-channel vectors of a lane's chunks are loaded once; blocks stride over groups
+// of 256 / G rows.
+template <int G, int CPL, bool kAffine, bool kModulate, bool kSilu = false>
 __global__ __launch_bounds__(256) void ln_kernel(const _Float16* __restrict__ x, int64_t rows, int c, float eps,
                                                  const float* __restrict__ weight, const float* __restrict__ bias,
                                                  const _Float16* __restrict__ scale,
@@ -97,6 +108,7 @@ __global__ __launch_bounds__(256) void ln_kernel(const _Float16* __restrict__ x,
           const _Float16 p = static_cast<_Float16>(static_cast<float>(h) * static_cast<float>(sv[i][e]));
           h = static_cast<_Float16>(static_cast<float>(p) + static_cast<float>(hv[i][e]));
         }
+        if constexpr (kSilu) h = silu_h(h);
         o[e] = h;
       }
       __builtin_nontemporal_store(o, reinterpret_cast<f16x8*>(orow + ch * 8));
@@ -109,7 +121,7 @@ __global__ __launch_bounds__(256) void ln_generic_kernel(const _Float16* __restr
                                                          const float* __restrict__ weight,
                                                          const float* __restrict__ bias,
                                                          const _Float16* __restrict__ scale,
-                                                         const _Float16* __restrict__ shift,
+                                                         const _Float16* __restrict__ shift, int act,
                                                          _Float16* __restrict__ out) {
 #pragma clang fp contract(off)
   const int lane = threadIdx.x & 63;
@@ -136,6 +148,7 @@ __global__ __launch_bounds__(256) void ln_generic_kernel(const _Float16* __restr
       const _Float16 p = static_cast<_Float16>(static_cast<float>(h) * static_cast<float>(scale[i]));
       h = static_cast<_Float16>(static_cast<float>(p) + static_cast<float>(shift[i]));
     }
+    if (act == HI3D_ACT_SILU) h = silu_h(h);
     orow[i] = h;
   }
 }
@@ -165,7 +178,7 @@ __global__ __launch_bounds__(256) void adaln_kernel(const float* __restrict__ w,
   else shift[j - half] = yh;
 }
 
-template <int G, int CPL>
+template <int G, int CPL, bool kSilu>
 void launch_ln(const _Float16* x, int64_t rows, int c, float eps, const float* w, const float* b, const _Float16* sc,
                const _Float16* sh, _Float16* out, hipStream_t stream) {
   constexpr int RPB = 256 / G;
@@ -174,13 +187,57 @@ void launch_ln(const _Float16* x, int64_t rows, int c, float eps, const float* w
   const int64_t cap = static_cast<int64_t>(cus > 0 ? cus : 256) * 16;  // a few strides per block
   const dim3 grid(static_cast<unsigned>(groups < cap ? groups : cap));
   if (w != nullptr && sc != nullptr)
-    hipLaunchKernelGGL((ln_kernel<G, CPL, true, true>), grid, dim3(256), 0, stream, x, rows, c, eps, w, b, sc, sh, out);
+    hipLaunchKernelGGL((ln_kernel<G, CPL, true, true, kSilu>), grid, dim3(256), 0, stream, x, rows, c, eps, w, b, sc, sh,
+                       out);
   else if (w != nullptr)
-    hipLaunchKernelGGL((ln_kernel<G, CPL, true, false>), grid, dim3(256), 0, stream, x, rows, c, eps, w, b, sc, sh, out);
+    hipLaunchKernelGGL((ln_kernel<G, CPL, true, false, kSilu>), grid, dim3(256), 0, stream, x, rows, c, eps, w, b, sc,
+                       sh, out);
   else if (sc != nullptr)
-    hipLaunchKernelGGL((ln_kernel<G, CPL, false, true>), grid, dim3(256), 0, stream, x, rows, c, eps, w, b, sc, sh, out);
+    hipLaunchKernelGGL((ln_kernel<G, CPL, false, true, kSilu>), grid, dim3(256), 0, stream, x, rows, c, eps, w, b, sc,
+                       sh, out);
   else
-    hipLaunchKernelGGL((ln_kernel<G, CPL, false, false>), grid, dim3(256), 0, stream, x, rows, c, eps, w, b, sc, sh, out);
+    hipLaunchKernelGGL((ln_kernel<G, CPL, false, false, kSilu>), grid, dim3(256), 0, stream, x, rows, c, eps, w, b, sc,
+                       sh, out);
+}
+
+template <bool kSilu>
+void launch_ln_width(const _Float16* xh, int64_t rows, int c, float eps, const float* weight, const float* bias,
+                     const _Float16* sc, const _Float16* sh, _Float16* o, hipStream_t stream) {
+  const int chunks = c / 8;
+  if (chunks <= 4) launch_ln<4, 1, kSilu>(xh, rows, c, eps, weight, bias, sc, sh, o, stream);
+  else if (chunks <= 8) launch_ln<8, 1, kSilu>(xh, rows, c, eps, weight, bias, sc, sh, o, stream);
+  else if (chunks <= 16) launch_ln<8, 2, kSilu>(xh, rows, c, eps, weight, bias, sc, sh, o, stream);
+  else if (chunks <= 32) launch_ln<8, 4, kSilu>(xh, rows, c, eps, weight, bias, sc, sh, o, stream);
+  else if (chunks <= 64) launch_ln<16, 4, kSilu>(xh, rows, c, eps, weight, bias, sc, sh, o, stream);
+  else if (chunks <= 128) launch_ln<32, 4, kSilu>(xh, rows, c, eps, weight, bias, sc, sh, o, stream);
+  else if (chunks <= 256) launch_ln<64, 4, kSilu>(xh, rows, c, eps, weight, bias, sc, sh, o, stream);
+  else launch_ln<64, 8, kSilu>(xh, rows, c, eps, weight, bias, sc, sh, o, stream);
+}
+
+int layer_norm(const void* x, int64_t rows, int32_t c, float eps, const float* weight, const float* bias,
+               const void* scale, const void* shift, int32_t act, void* out, hipStream_t stream) {
+  HI3D_REQUIRE(rows >= 0 && c > 0, "bad sizes");
+  HI3D_REQUIRE((weight == nullptr) == (bias == nullptr), "weight and bias must be given together");
+  HI3D_REQUIRE((scale == nullptr) == (shift == nullptr), "scale and shift must be given together");
+  HI3D_REQUIRE(act == HI3D_ACT_NONE || act == HI3D_ACT_SILU, "unknown activation %d", act);
+  if (rows == 0) return HI3D_OK;
+  HI3D_REQUIRE(x && out, "null pointer argument");
+  const auto* xh = static_cast<const _Float16*>(x);
+  const auto* sc = static_cast<const _Float16*>(scale);
+  const auto* sh = static_cast<const _Float16*>(shift);
+  auto* o = static_cast<_Float16*>(out);
+  const uintptr_t vec = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(out) |
+                        reinterpret_cast<uintptr_t>(weight) | reinterpret_cast<uintptr_t>(bias) |
+                        reinterpret_cast<uintptr_t>(scale) | reinterpret_cast<uintptr_t>(shift);
+  if (c % 8 == 0 && (vec & 15) == 0 && c / 8 <= 64 * 8) {
+    if (act == HI3D_ACT_SILU) launch_ln_width<true>(xh, rows, c, eps, weight, bias, sc, sh, o, stream);
+    else launch_ln_width<false>(xh, rows, c, eps, weight, bias, sc, sh, o, stream);
+  } else {
+    hipLaunchKernelGGL(ln_generic_kernel, dim3(static_cast<unsigned>(ceil_div(rows, 4))), dim3(256), 0, stream, xh, rows,
+                       c, eps, weight, bias, sc, sh, act, o);
+  }
+  HI3D_LAUNCH_CHECK();
+  return HI3D_OK;
 }
 
 }  // namespace
@@ -191,36 +248,13 @@ using namespace hi3d;
 extern "C" {
 
 int hi3d_layer_norm_modulate(const void* x, int64_t rows, int32_t c, float eps, const float* weight, const float* bias,
-                             const void* scale, const void* shift, void* out, void* stream_) {
-  hipStream_t stream = as_stream(stream_);
-  HI3D_REQUIRE(rows >= 0 && c > 0, "bad sizes");
-  HI3D_REQUIRE((weight == nullptr) == (bias == nullptr), "weight and bias must be given together");
-  HI3D_REQUIRE((scale == nullptr) == (shift == nullptr), "scale and shift must be given together");
-  if (rows == 0) return HI3D_OK;
-  HI3D_REQUIRE(x && out, "null pointer argument");
-  const auto* xh = static_cast<const _Float16*>(x);
-  const auto* sc = static_cast<const _Float16*>(scale);
-  const auto* sh = static_cast<const _Float16*>(shift);
-  auto* o = static_cast<_Float16*>(out);
-  const uintptr_t vec = reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(out) |
-                        reinterpret_cast<uintptr_t>(weight) | reinterpret_cast<uintptr_t>(bias) |
-                        reinterpret_cast<uintptr_t>(scale) | reinterpret_cast<uintptr_t>(shift);
-  const int chunks = c / 8;
-  if (c % 8 == 0 && (vec & 15) == 0 && chunks <= 64 * 8) {
-    if (chunks <= 4) launch_ln<4, 1>(xh, rows, c, eps, weight, bias, sc, sh, o, stream);
-    else if (chunks <= 8) launch_ln<8, 1>(xh, rows, c, eps, weight, bias, sc, sh, o, stream);
-    else if (chunks <= 16) launch_ln<8, 2>(xh, rows, c, eps, weight, bias, sc, sh, o, stream);
-    else if (chunks <= 32) launch_ln<8, 4>(xh, rows, c, eps, weight, bias, sc, sh, o, stream);
-    else if (chunks <= 64) launch_ln<16, 4>(xh, rows, c, eps, weight, bias, sc, sh, o, stream);
-    else if (chunks <= 128) launch_ln<32, 4>(xh, rows, c, eps, weight, bias, sc, sh, o, stream);
-    else if (chunks <= 256) launch_ln<64, 4>(xh, rows, c, eps, weight, bias, sc, sh, o, stream);
-    else launch_ln<64, 8>(xh, rows, c, eps, weight, bias, sc, sh, o, stream);
-  } else {
-    hipLaunchKernelGGL(ln_generic_kernel, dim3(static_cast<unsigned>(ceil_div(rows, 4))), dim3(256), 0, stream, xh, rows,
-                       c, eps, weight, bias, sc, sh, o);
-  }
-  HI3D_LAUNCH_CHECK();
-  return HI3D_OK;
+                             const void* scale, const void* shift, void* out, void* stream) {
+  return layer_norm(x, rows, c, eps, weight, bias, scale, shift, HI3D_ACT_NONE, out, as_stream(stream));
+}
+
+int hi3d_layer_norm_act(const void* x, int64_t rows, int32_t c, float eps, const float* weight, const float* bias,
+                        const void* scale, const void* shift, int32_t act, void* out, void* stream) {
+  return layer_norm(x, rows, c, eps, weight, bias, scale, shift, act, out, as_stream(stream));
 }
 
 int hi3d_adaln_projection(const float* w, const float* b, const float* cond, int32_t n_out, int32_t n_in,

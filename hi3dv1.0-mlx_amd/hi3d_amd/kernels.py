@@ -20,8 +20,13 @@ def layer_norm_modulate(
     bias: torch.Tensor | None = None,
     scale: torch.Tensor | None = None,
     shift: torch.Tensor | None = None,
+    act: str | None = None,
 ) -> torch.Tensor:
-    """``LayerNorm32`` of fp16 rows, then optionally ``fp16(fp16(h * scale) + shift)``."""
+    """``LayerNorm32`` of fp16 rows, then optionally ``fp16(fp16(h * scale) + shift)``,
+    then optionally (``act="silu"``) the fp16 SiLU ``h * sigmoid(h)`` of the reference's
+    res blocks (src/hi3d_mac/mlx_backend/transformer.py:172-173, 418-433)."""
+    if act not in (None, "none", "silu"):
+        raise ValueError(f"unknown activation {act!r}")
     if x.dtype != torch.float16:
         raise ValueError("layer_norm_modulate takes fp16 rows")
     device = _lib.require_gpu(x, weight, bias, scale, shift)
@@ -41,9 +46,9 @@ def layer_norm_modulate(
             raise ValueError(f"per-channel parameters must have {c} entries")
     out = torch.empty_like(xc)
     _lib.call(
-        "hi3d_layer_norm_modulate",
-        _lib.ptr(xc), rows, c, float(eps), _lib.ptr(w), _lib.ptr(b), _lib.ptr(sc), _lib.ptr(sh), _lib.ptr(out),
-        _lib.stream(device),
+        "hi3d_layer_norm_act",
+        _lib.ptr(xc), rows, c, float(eps), _lib.ptr(w), _lib.ptr(b), _lib.ptr(sc), _lib.ptr(sh),
+        _lib.ACT_SILU if act == "silu" else _lib.ACT_NONE, _lib.ptr(out), _lib.stream(device),
     )
     return out
 

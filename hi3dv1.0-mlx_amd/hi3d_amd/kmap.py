@@ -261,6 +261,22 @@ def build_plan(
     return ConvPlan(rows, gidx, tile_mask, n_out, int(n_in), kvol, table, coords, bits)
 
 
+def identity_plan(n: int, device: torch.device) -> ConvPlan:
+    """Plan of the one-offset identity table (output row i gathers input row i): the
+    gather convolution over it is a row-wise linear layer ``out = x @ W[:, 0, :].T + b``
+    with the convolutions' epilogues (bias, SiLU, residual). Rows stay in order, so the
+    plan is built without sorting."""
+    t = int(_lib.lib().hi3d_conv_tile_rows())
+    ntiles = (int(n) + t - 1) // t
+    slots = torch.arange(ntiles * t, dtype=torch.int32, device=device)
+    past = slots >= n
+    rows = slots.masked_fill(past, -1)
+    gidx = slots.masked_fill(past, int(n))
+    tile_mask = torch.ones(ntiles, dtype=torch.int32, device=device)
+    table = slots[:n].reshape(-1, 1).clone()
+    return ConvPlan(rows, gidx, tile_mask, int(n), int(n), 1, table)
+
+
 @dataclass
 class KernelMap:
     """Submanifold kernel map of one coordinate set (built once, reused by every
@@ -289,6 +305,12 @@ class KernelMap:
         if self._pairs is None:
             self._pairs = pair_lists(self.table)
         return self._pairs
+
+    def identity_plan(self) -> ConvPlan:
+        """The row-wise (one-offset identity) plan over this map's rows, cached."""
+        if "identity" not in self._plans:
+            self._plans["identity"] = identity_plan(self.n, self.table.device)
+        return self._plans["identity"]
 
     def plan(self, window_rows: int | None = None) -> ConvPlan:
         key = window_rows

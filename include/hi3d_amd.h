@@ -434,6 +434,17 @@ int hi3d_layer_norm_modulate(const void* x_dev, int64_t rows, int32_t c, float e
                              const void* scale_dev, const void* shift_dev, void* out_dev,
                              void* stream);
 
+/* The same LayerNorm (+ affine, + modulate) followed by SiLU on the fp16 result when
+ * act = HI3D_ACT_SILU (sigmoid rounded to fp16, then the product): the res-block steps
+ * norm1 -> SiLU and norm2 -> modulate -> SiLU in one pass.
+ * Replaces: layer_norm32 + silu of _resblock / _resblock_tail
+ * (src/hi3d_mac/mlx_backend/transformer.py:160-173,418-433); norm1/norm2 + F.silu of
+ * SparseResBlock3d.forward (src/sparc3d/models/transformers/sparc3d_transformer.py:136-141). */
+int hi3d_layer_norm_act(const void* x_dev, int64_t rows, int32_t c, float eps,
+                        const float* weight_dev, const float* bias_dev,
+                        const void* scale_dev, const void* shift_dev, int32_t act,
+                        void* out_dev, void* stream);
+
 /* adaLN projection: y = W . (silu(cond) if apply_silu else cond) + b in fp32
  * (W [n_out, n_in] fp32, cond [n_in], b [n_out] or NULL), then
  * scale1p_dev = fp16(1 + fp16(y[:n_out/2])) and shift_dev = fp16(y[n_out/2:])

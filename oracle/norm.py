@@ -79,3 +79,49 @@ def residual_block_f64(x, table, cond, proj_w, proj_b, w1, b1, w2, b2, eps=1e-6,
     h1 = gather_conv_f64(h2, compact(need2)[t[need1]], w1, b1, act="silu")
     out = gather_conv_f64(h1, compact(need1)[t[rows]], w2, b2)
     return out + np.asarray(x[rows]).astype(np.float64)
+
+
+def silu_f16(h) -> np.ndarray:
+    """fp16 ``x * sigmoid(x)`` of the reference's res blocks
+    (src/hi3d_mac/mlx_backend/transformer.py:172-173): the sigmoid rounded to fp16, then
+    the product rounded to fp16."""
+    hf = np.asarray(h).astype(np.float16).astype(np.float32)
+    sig = (np.float32(1.0) / (np.float32(1.0) + np.exp(-hf))).astype(np.float16)
+    return (hf * sig.astype(np.float32)).astype(np.float16)
+
+
+def res_block3d_f64(x, table, embedding, p: dict, spans=None, eps: float = 1e-6) -> np.ndarray:
+    """``SparseResBlock3d.forward`` after its resampling, in float64
+    (src/sparc3d/models/transformers/sparc3d_transformer.py:132-144;
+    src/hi3d_mac/mlx_backend/transformer.py:413-437) over the rows' ``[N, 27]`` table:
+    ``scale, shift = Linear(SiLU(emb))`` per batch element, ``h = silu(LN(x) w1 + b1)``,
+    ``h = conv1(h)``, ``h = silu(LN(h) (1 + scale) + shift)``, ``h = silu(conv2(h))``,
+    ``linear(h) + skip(x)``. ``p`` holds the module's state-dict names
+    (``conv*.conv.weight`` in spconv's ``[Cout, 3, 3, 3, Cin]``); ``spans`` are the batch
+    elements' row ranges (one element when None)."""
+    f = lambda k: np.asarray(p[k], np.float64)
+    x64 = np.asarray(x, np.float64)
+    emb = np.asarray(embedding, np.float64).reshape(-1, f("emb_layers.1.weight").shape[1])
+    spans = spans or [slice(0, x64.shape[0])]
+    silu = lambda v: v / (1.0 + np.exp(-v))
+
+    def ln(v):
+        mean = v.mean(axis=1, keepdims=True)
+        var = ((v - mean) ** 2).mean(axis=1, keepdims=True)
+        return (v - mean) / np.sqrt(var + eps)
+
+    def taps(name):
+        w = f(name)
+        return w.reshape(w.shape[0], -1, w.shape[-1])
+
+    h = silu(ln(x64) * f("norm1.weight") + f("norm1.bias"))
+    h = gather_conv_f64(h, table, taps("conv1.conv.weight"), f("conv1.conv.bias"))
+    hidden = h.shape[1]
+    h2 = np.empty_like(h)
+    for b, span in enumerate(spans):
+        y = f("emb_layers.1.weight") @ silu(emb[b]) + f("emb_layers.1.bias")
+        scale, shift = y[:hidden], y[hidden:]
+        h2[span] = ln(h[span]) * (1.0 + scale) + shift
+    h = gather_conv_f64(silu(h2), table, taps("conv2.conv.weight"), f("conv2.conv.bias"), act="silu")
+    skip = x64 @ f("skip_connection.weight").T + f("skip_connection.bias") if "skip_connection.weight" in p else x64
+    return h @ f("linear.weight").T + f("linear.bias") + skip

@@ -1,0 +1,151 @@
+"""The transformer's sparse residual block (``resblock.SparseResBlock3d``) on the GPU
+against the float64 composition of the reference's block (oracle ``res_block3d_f64``),
+with and without the skip projection, with two batch elements of their own embeddings,
+and with the paired factor-2 downsample / upsample in front.
+
+Gate (fp16): max|y - y_ref| / rms(y_ref) <= 1e-2. The fused LayerNorm + SiLU kernel is
+checked on its own at the LayerNorm gate (more than 99.9 % bit-equal to the oracle's
+fp16 steps, all within atol 1e-2 / rtol 1e-3).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import conv as oconv
+from oracle import kmap as okmap
+from oracle import norm as onorm
+
+pytestmark = pytest.mark.gpu
+
+
+def _indices(rng, side, density, batches):
+    """Batch-grouped coordinates (rows of one element contiguous, shuffled inside)."""
+    parts = []
+    for b in range(batches):
+        xyz = np.argwhere(rng.random((side,) * 3) < density)
+        xyz = xyz[rng.permutation(len(xyz))]
+        parts.append(np.concatenate([np.full((len(xyz), 1), b), xyz], 1))
+    return np.concatenate(parts).astype(np.int32)
+
+
+def _spans(idx):
+    spans, start = [], 0
+    for b in range(int(idx[:, 0].max()) + 1):
+        count = int((idx[:, 0] == b).sum())
+        spans.append(slice(start, start + count))
+        start += count
+    return spans
+
+
+def _block(rng, cuda, channels, emb, out=None, **kw):
+    """A block with every parameter random (the zero-initialised linear too), in fp16,
+    and its state dict as float64 arrays for the oracle."""
+    from hi3d_amd.resblock import SparseResBlock3d
+
+    m = SparseResBlock3d(channels, emb, out_channels=out, **kw)
+    with torch.no_grad():
+        for name, p in m.named_parameters():
+            if name.startswith("norm1.weight"):
+                p.copy_(torch.as_tensor(rng.uniform(0.5, 1.5, p.shape)))
+            elif name.endswith("bias"):
+                p.copy_(torch.as_tensor(rng.normal(0, 0.1, p.shape)))
+            else:
+                fan_in = int(np.prod(p.shape[1:]))
+                p.copy_(torch.as_tensor(rng.normal(0, 1 / np.sqrt(fan_in), p.shape)))
+    m = m.half().to(cuda)
+    params = {k: v.detach().float().cpu().numpy().astype(np.float64) for k, v in m.state_dict().items()}
+    return m, params
+
+
+def _sparse(cuda, idx, x):
+    from hi3d_amd.nn import SparseTensor
+
+    return SparseTensor(torch.as_tensor(x).to(cuda), torch.as_tensor(idx).to(cuda))
+
+
+@pytest.mark.parametrize("c", [64, 256, 2112, 40])
+def test_layer_norm_silu_kernel(cuda, c):
+    """LayerNorm + affine + SiLU and LayerNorm + modulate + SiLU against the oracle's
+    fp16 steps (LN as layer_norm_modulate, then silu_f16)."""
+    from hi3d_amd import kernels
+
+    rng = np.random.default_rng(c)
+    x = (rng.standard_normal((300, c)) * 2 + 0.3).astype(np.float16)
+    w = rng.uniform(0.5, 1.5, c).astype(np.float32)
+    b = rng.normal(0, 0.3, c).astype(np.float32)
+    scale = (1 + 0.2 * rng.standard_normal(c)).astype(np.float16)
+    shift = (0.2 * rng.standard_normal(c)).astype(np.float16)
+    xt = torch.as_tensor(x).to(cuda)
+    for kw in ({"weight": w, "bias": b}, {"scale": scale, "shift": shift}):
+        got = kernels.layer_norm_modulate(xt, 1e-6, act="silu", **{k: torch.as_tensor(v).to(cuda)
+                                                                     for k, v in kw.items()}).cpu().numpy()
+        ref = onorm.silu_f16(onorm.layer_norm_modulate(x, 1e-6, **kw))
+        assert float(np.mean(got == ref)) > 0.999
+        np.testing.assert_allclose(got.astype(np.float32), ref.astype(np.float32), atol=1e-2, rtol=1e-3)
+
+
+@pytest.mark.parametrize("channels,out,batches", [(64, None, 1), (64, 128, 2), (256, None, 1)])
+def test_res_block_matches_float64(cuda, channels, out, batches):
+    rng = np.random.default_rng(channels + batches)
+    side = 18
+    idx = _indices(rng, side, 0.15, batches)
+    x = rng.standard_normal((len(idx), channels)).astype(np.float16)
+    emb = rng.standard_normal((batches, 96)).astype(np.float16)
+    m, p = _block(rng, cuda, channels, 96, out)
+    st = _sparse(cuda, idx, x)
+    y = m(st, torch.as_tensor(emb).to(cuda))
+    assert y.feats.dtype == torch.float16 and tuple(y.feats.shape) == (len(idx), out or channels)
+    assert torch.equal(y.coords, st.coords)
+    table = okmap.neighbour_table(idx, [side] * 3)
+    ref = onorm.res_block3d_f64(x, table, emb.astype(np.float64), p, _spans(idx))
+    assert oconv.rel_err(y.feats.float().cpu().numpy(), ref) <= 1e-2
+    # a second pass over the same rows reuses the cached maps and gives the same bits
+    again = m(st.replace(torch.as_tensor(x).to(cuda)), torch.as_tensor(emb).to(cuda))
+    assert torch.equal(again.feats, y.feats)
+
+
+def test_res_block_downsample_then_upsample(cuda):
+    """A downsampling block (mean of each coarse cell's rows with the reference's
+    ``count + 1`` divisor, then the block on the coarse rows) followed by its paired
+    upsampling block (parent rows copied back to the fine rows, then the block)."""
+    rng = np.random.default_rng(77)
+    side = 20
+    idx = _indices(rng, side, 0.12, 2)
+    x = rng.standard_normal((len(idx), 64)).astype(np.float16)
+    emb = rng.standard_normal((2, 32)).astype(np.float16)
+    down, pd = _block(rng, cuda, 64, 32, 128, downsample=True)
+    up, pu = _block(rng, cuda, 128, 32, 64, upsample=True)
+    st = _sparse(cuda, idx, x)
+    coarse = down(st, torch.as_tensor(emb).to(cuda))
+    low, inverse, counts, slot, table_down, table_up = okmap.stride2_structure(idx)
+    assert np.array_equal(coarse.coords.cpu().numpy(), low)
+    pooled = oconv.gather_mean(x.astype(np.float64), table_down, extra=1)
+    ref_c = onorm.res_block3d_f64(pooled, okmap.neighbour_table(low, [side // 2] * 3), emb.astype(np.float64), pd,
+                                  _spans(low))
+    got_c = coarse.feats.float().cpu().numpy()
+    assert oconv.rel_err(got_c, ref_c) <= 1e-2
+    fine = up(coarse, torch.as_tensor(emb).to(cuda))
+    assert torch.equal(fine.coords, st.coords)
+    x_up = got_c[inverse]
+    ref_f = onorm.res_block3d_f64(x_up, okmap.neighbour_table(idx, [side] * 3), emb.astype(np.float64), pu,
+                                  _spans(idx))
+    assert oconv.rel_err(fine.feats.float().cpu().numpy(), ref_f) <= 1e-2
+
+
+def test_res_block_errors(cuda):
+    from hi3d_amd.resblock import SparseResBlock3d
+
+    with pytest.raises(ValueError, match="cannot downsample and upsample"):
+        SparseResBlock3d(8, 8, downsample=True, upsample=True)
+    rng = np.random.default_rng(5)
+    idx = _indices(rng, 8, 0.3, 1)
+    m = SparseResBlock3d(16, 8).to(cuda)
+    with pytest.raises(NotImplementedError, match="fp16"):
+        m(_sparse(cuda, idx, rng.standard_normal((len(idx), 16)).astype(np.float32)), torch.zeros(8, device=cuda))
+    m = m.half()
+    with pytest.raises(ValueError, match="embedding"):
+        m(_sparse(cuda, idx, rng.standard_normal((len(idx), 16)).astype(np.float16)),
+          torch.zeros((2, 8), device=cuda, dtype=torch.float16))

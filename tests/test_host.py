@@ -227,3 +227,25 @@ def test_bench_main_calls_defined_functions():
     called = {node.func.id for node in ast.walk(main) if isinstance(node, ast.Call) and isinstance(node.func, ast.Name)}
     wanted = {name for name in called if name.startswith(("bench_", "cpu_baseline", "measured_traffic"))}
     assert wanted and wanted <= defined, sorted(wanted - defined)
+
+
+def test_res_block_state_dict_names_match_the_reference():
+    """``resblock.SparseResBlock3d`` keeps the reference module's parameter names and
+    shapes (src/sparc3d/models/transformers/sparc3d_transformer.py:109-129), so its state
+    dict loads unchanged; the linear starts at zero (``zero_module``)."""
+    from hi3d_amd.resblock import SparseResBlock3d
+
+    m = SparseResBlock3d(256, 2112, out_channels=512)
+    shapes = {k: tuple(v.shape) for k, v in m.state_dict().items()}
+    assert shapes == {
+        "norm1.weight": (256,), "norm1.bias": (256,),
+        "conv1.conv.weight": (256, 3, 3, 3, 256), "conv1.conv.bias": (256,),
+        "conv2.conv.weight": (256, 3, 3, 3, 256), "conv2.conv.bias": (256,),
+        "linear.weight": (512, 256), "linear.bias": (512,),
+        "emb_layers.1.weight": (512, 2112), "emb_layers.1.bias": (512,),
+        "skip_connection.weight": (512, 256), "skip_connection.bias": (512,),
+    }
+    assert not m.linear.weight.any() and not m.linear.bias.any()
+    plain = SparseResBlock3d(256, 2112)
+    assert "skip_connection.weight" not in plain.state_dict() and plain.hidden_channels == 128
+    assert SparseResBlock3d(64, 8, downsample=True).updown is not None

@@ -26,6 +26,9 @@ Pinning map (oracle function -> checks here):
   norm.adaln_projection              -> closed forms (zero weight, identity halves, SiLU
                                          from math.exp), torch linear + chunk(2)
   norm.residual_block_f64            -> explicit float64 composition
+  norm.silu_f16                       -> float64 u / (1 + exp(-u)) within two roundings
+  norm.res_block3d_f64                -> torch float64 modules (F.layer_norm, F.silu,
+                                         F.linear, chunk) + dense F.conv3d per batch
   vae.group_stats_f64 / group_norm_swish / gather_group_norm_swish -> numpy per-group
                                          moments, u / (1 + exp(-u)), element-wise block
   vae.conv_gn_swish_f64 / resnet_f64 / occupancy_f64 -> per-group GroupNorm + dense
@@ -463,6 +466,71 @@ def test_residual_block_composition():
     h1 = h1 / (1 + np.exp(-h1))
     ref = oconv.dense_subm_conv3d(idx, h1, w2, b2, [8, 8, 8]) + x.astype(np.float64)
     assert np.allclose(full, ref, atol=1e-10)
+
+
+def test_silu_f16_against_float64():
+    """fp16 SiLU within two fp16 roundings of ``u / (1 + exp(-u))`` (relative half-ulps
+    of the product and the sigmoid, plus the sigmoid's absolute subnormal half-ulp
+    2^-25 times |u|); exact at 0."""
+    u = np.linspace(-12, 12, 4001).astype(np.float16)
+    got = onorm.silu_f16(u).astype(np.float64)
+    u64 = u.astype(np.float64)
+    want = u64 / (1 + np.exp(-u64))
+    assert np.all(np.abs(got - want) <= 2 * 2.0**-11 * np.abs(want) + np.abs(u64) * 2.0**-25 + 2.0**-25)
+    assert onorm.silu_f16(np.array([0.0]))[0] == 0
+
+
+@pytest.mark.parametrize("cin,cout,batches", [(16, None, 1), (8, 16, 2)])
+def test_res_block3d_oracle_against_torch_modules(cin, cout, batches):
+    """res_block3d_f64 against the block written with torch's own float64 operators: a
+    dense ``F.conv3d(padding=1)`` per batch element for the submanifold convolutions
+    (the reference's conv oracle, tests/test_backends.py:32-50), ``F.layer_norm``,
+    ``F.silu``, ``F.linear`` and ``chunk(2)`` of the embedding projection
+    (sparc3d_transformer.py:132-144)."""
+    rng = np.random.default_rng(70 + cin)
+    side = 8
+    idx = _rand_indices(rng, side, 0.3, batch=batches)
+    spans, start = [], 0
+    for b in range(batches):
+        count = int((idx[:, 0] == b).sum())
+        spans.append(slice(start, start + count))
+        start += count
+    n = len(idx)
+    cout = cout or cin
+    hidden = cout // 2
+    p = {
+        "norm1.weight": rng.uniform(0.5, 1.5, cin), "norm1.bias": rng.normal(0, 0.2, cin),
+        "conv1.conv.weight": rng.normal(0, 0.1, (hidden, 3, 3, 3, cin)), "conv1.conv.bias": rng.normal(0, 0.1, hidden),
+        "conv2.conv.weight": rng.normal(0, 0.1, (hidden, 3, 3, 3, hidden)),
+        "conv2.conv.bias": rng.normal(0, 0.1, hidden),
+        "linear.weight": rng.normal(0, 0.3, (cout, hidden)), "linear.bias": rng.normal(0, 0.1, cout),
+        "emb_layers.1.weight": rng.normal(0, 0.3, (2 * hidden, 12)), "emb_layers.1.bias": rng.normal(0, 0.1, 2 * hidden),
+    }
+    if cout != cin:
+        p["skip_connection.weight"] = rng.normal(0, 0.3, (cout, cin))
+        p["skip_connection.bias"] = rng.normal(0, 0.1, cout)
+    x = rng.normal(0.3, 1.2, (n, cin))
+    emb = rng.normal(size=(batches, 12))
+    table = okmap.neighbour_table(idx, [side] * 3)
+    got = onorm.res_block3d_f64(x, table, emb, p, spans)
+
+    t = {k: torch.as_tensor(v) for k, v in p.items()}
+
+    def conv(v, w, b):
+        return torch.as_tensor(oconv.dense_subm_conv3d(idx, v.numpy(), w.numpy(), b.numpy(), [side] * 3))
+
+    xt = torch.as_tensor(x)
+    y = F.linear(F.silu(torch.as_tensor(emb)), t["emb_layers.1.weight"], t["emb_layers.1.bias"])
+    scale, shift = y.chunk(2, dim=1)
+    h = F.silu(F.layer_norm(xt, (cin,), t["norm1.weight"], t["norm1.bias"], eps=1e-6))
+    h = conv(h, t["conv1.conv.weight"], t["conv1.conv.bias"])
+    h = F.layer_norm(h, (hidden,), eps=1e-6)
+    batch = torch.as_tensor(idx[:, 0]).long()
+    h = F.silu(h * (1 + scale[batch]) + shift[batch])
+    h = F.silu(conv(h, t["conv2.conv.weight"], t["conv2.conv.bias"]))
+    skip = F.linear(xt, t["skip_connection.weight"], t["skip_connection.bias"]) if cout != cin else xt
+    want = (F.linear(h, t["linear.weight"], t["linear.bias"]) + skip).numpy()
+    assert np.allclose(got, want, rtol=1e-10, atol=1e-10)
 
 
 def test_cpu_baseline_runs_on_a_sample():
