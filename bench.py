@@ -95,6 +95,24 @@ def timed(fn, steps: int, warmup: int):
     return wall, ev
 
 
+def timed_batch(fn, steps: int, warmup: int) -> float:
+    """Mean ms per call over `steps` back-to-back calls between two events: the GPU stays
+    busy while the host queues the next launch, so a short kernel is timed without the
+    host's per-call overhead (events around each call would include it)."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
 def dense_fresh(fn):
     """Run a kernel-map build with a dense grid cleared inside the call (not kept)."""
     from hi3d_amd import kmap
@@ -181,9 +199,14 @@ def bench_stride2(steps: int, warmup: int):
     wu = torch.as_tensor(workloads.normal((64, 8, 128), 1.0 / np.sqrt(8 * 128), 33, np.float16)).to(dev)
     y = torch.empty((nc, 128), dtype=torch.float16, device=dev)
     z = torch.empty((nf, 64), dtype=torch.float16, device=dev)
+    s.up_order()  # the sorted up convolution's plan, built with the structure's other plans
     d_wall, d_ev = timed(lambda: conv.gather_conv(x, dp, wd, None, out=y), steps, warmup)
     u_wall, u_ev = timed(lambda: conv.stride2_up(y, s, wu, None, out=z), steps, warmup)
     ug_wall, ug_ev = timed(lambda: conv.gather_conv(y, up, wu, None, out=z), steps, warmup)
+    # kernel time: back-to-back launches between two events
+    d_k = timed_batch(lambda: conv.gather_conv(x, dp, wd, None, out=y), 4 * steps, warmup)
+    u_k = timed_batch(lambda: conv.stride2_up(y, s, wu, None, out=z), 4 * steps, warmup)
+    u_k_rows = timed_batch(lambda: conv.stride2_up(y, s, wu, None, out=z, sorted_rows=False), 4 * steps, warmup)
     flops = 2.0 * nf * 64 * 128
     bytes_conv = 2 * (nf * 64 + nc * 128 + 8 * 64 * 128) + 5 * nf
     return {
@@ -194,10 +217,17 @@ def bench_stride2(steps: int, warmup: int):
         "down_ms": d_wall,
         "up_ms": u_wall,
         "up_gather_ms": ug_wall,
-        "down_tflops": flops / (d_ev * 1e-3) / 1e12,
-        "up_tflops": flops / (u_ev * 1e-3) / 1e12,
-        "down_gbs_alg": bytes_conv / (d_ev * 1e-3) / 1e9,
-        "up_gbs_alg": bytes_conv / (u_ev * 1e-3) / 1e9,
+        "down_kernel_ms": d_k,
+        "up_kernel_ms": u_k,
+        "up_kernel_row_order_ms": u_k_rows,
+        "down_call_gbs_alg": bytes_conv / (d_ev * 1e-3) / 1e9,
+        "up_call_gbs_alg": bytes_conv / (u_ev * 1e-3) / 1e9,
+        "down_tflops": flops / (d_k * 1e-3) / 1e12,
+        "up_tflops": flops / (u_k * 1e-3) / 1e12,
+        "down_gbs_alg": bytes_conv / (d_k * 1e-3) / 1e9,
+        "up_gbs_alg": bytes_conv / (u_k * 1e-3) / 1e9,
+        "down_hbm_frac": bytes_conv / (d_k * 1e-3) / 1e9 / PEAK_HBM_GBS,
+        "up_hbm_frac": bytes_conv / (u_k * 1e-3) / 1e9 / PEAK_HBM_GBS,
         "voxels_per_s": nf / ((d_wall + u_wall) * 1e-3),
     }
 

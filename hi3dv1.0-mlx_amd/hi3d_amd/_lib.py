@@ -58,6 +58,10 @@ _SIGNATURES = {
     "hi3d_gather_rows": [_p, _i64, _i32, _p, _i64, _p, _p],
     "hi3d_stride2_up_supported": [_i32, _i32, _i32],
     "hi3d_stride2_up_conv": [_p, _i64, _i32, _p, _p, _i32, _p, _i64, _i32, _p, _p],
+    "hi3d_stride2_up_tile_rows": [],
+    "hi3d_stride2_up_plan_workspace": [_i64, _p],
+    "hi3d_stride2_up_plan": [_p, _i64, _i64, _i32, _p, _i64, _p, _p, _p],
+    "hi3d_stride2_up_conv_sorted": [_p, _i64, _i32, _p, _p, _i32, _p, _p, _i64, _i32, _p, _p],
     "hi3d_unique_keys_workspace": [_i64, _p],
     "hi3d_unique_keys": [_p, _i64, _i32, _p, _i64, _p, _p, _p, _p, _p],
     "hi3d_pack_rows": [_p, _i32, _i64, _i32, _p, _p, _p, _p],
@@ -81,6 +85,7 @@ _SIGNATURES = {
     "hi3d_gather_gn_swish": [_p, _i32, _i64, _i32, _p, _i64, _p, _p, _p, _p, _p, _i32, _p],
 }
 _RESTYPES = {"hi3d_last_error": ctypes.c_char_p, "hi3d_version": ctypes.c_char_p, "hi3d_conv_tile_rows": _i32,
+             "hi3d_stride2_up_tile_rows": _i32,
              "hi3d_halo_tile_rows": _i32, "hi3d_halo_capacity": _i32}
 
 _LIB: ctypes.CDLL | None = None

@@ -228,11 +228,19 @@ def stride2_up_supported(dtype: torch.dtype, cin: int, cout: int) -> bool:
     return bool(_lib.lib().hi3d_stride2_up_supported(int(cin), int(cout), _lib.DTYPES[dtype]))
 
 
+UP_SORTED = True
+"""Run the transposed stride-2 convolution over the coarse rows sorted by their
+children's slot mask (``hi3d_stride2_up_conv_sorted``, which skips the products of
+slots a tile lacks) instead of in row order; the outputs are the same bits."""
+
+
 def stride2_up(features: torch.Tensor, structure, weight: torch.Tensor, bias: torch.Tensor | None = None,
-               out: torch.Tensor | None = None) -> torch.Tensor:
+               out: torch.Tensor | None = None, sorted_rows: bool | None = None) -> torch.Tensor:
     """Transpose of the 2x2x2 / stride-2 convolution onto the fine set of ``structure``
     (a :class:`~hi3d_amd.kmap.Stride2Structure`): ``out[i] = b + W[:, slot(i), :] @
     features[parent(i)]`` with ``W [Cout, 8, Cin]`` (or spconv's ``[Cout, 2, 2, 2, Cin]``).
+    ``sorted_rows`` (default ``UP_SORTED``): walk the coarse rows in the structure's
+    mask order (``Stride2Structure.up_order``).
     Shapes the parent-major kernel takes (fp16 / bf16, Cin 64 or 128, Cout 64) read each
     coarse row once and write each fine row once; the others run the gather convolution
     over the structure's up table."""
@@ -253,6 +261,12 @@ def stride2_up(features: torch.Tensor, structure, weight: torch.Tensor, bias: to
         x = x.clone()
     b = None if bias is None else bias.to(features.dtype).contiguous()
     y = _output(out, n_f, cout, features.dtype, device)
+    if UP_SORTED if sorted_rows is None else sorted_rows:
+        order, down_sorted = structure.up_order()
+        _lib.call("hi3d_stride2_up_conv_sorted", _lib.ptr(x), n_c, cin, _lib.ptr(w), _lib.ptr(b), cout,
+                  _lib.ptr(order), _lib.ptr(down_sorted), n_f, _lib.DTYPES[features.dtype], _lib.ptr(y),
+                  _lib.stream(device))
+        return y
     _lib.call("hi3d_stride2_up_conv", _lib.ptr(x), n_c, cin, _lib.ptr(w), _lib.ptr(b), cout,
               _lib.ptr(structure.down), n_f, _lib.DTYPES[features.dtype], _lib.ptr(y), _lib.stream(device))
     return y

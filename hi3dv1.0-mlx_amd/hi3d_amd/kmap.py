@@ -102,6 +102,11 @@ def _build_on_kept_grid(key: tuple[int, int], entry: _KeptGrid, device: torch.de
     done.record(current)
     entry.done = done
 
+UP_ORDER_WINDOW_LOG2: int = 31
+"""Windows (log2 rows) of the sorted up convolution's mask sort: 31 sorts every coarse
+row by its children's slot mask at once (the tiles then share masks best; the rows it
+gathers stay inside the coarse set, which the last-level cache holds)."""
+
 PLAN_GLOBAL_ROWS = 1 << 21
 PLAN_SMALL_WINDOW = 0
 PLAN_LARGE_WINDOW = 1 << 19
@@ -462,6 +467,26 @@ class Stride2Structure:
             bits = morton_bits(self.out_spatial_shape, 128)  # batch indices fit 7 bits
             self._plans["down"] = build_plan(self.down, self.n_fine, self.low, bits=bits)
         return self._plans["down"]
+
+    def up_order(self, window_log2: int | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+        """``(order, down_sorted)`` of the sorted parent-major up convolution: coarse
+        rows sorted by the slot mask of their children (within windows of
+        ``2**window_log2`` rows; ``None``: ``UP_ORDER_WINDOW_LOG2``), padded to whole
+        tiles (``hi3d_stride2_up_plan``)."""
+        w = UP_ORDER_WINDOW_LOG2 if window_log2 is None else int(window_log2)
+        key = ("up_order", w)
+        if key not in self._plans:
+            device = self.down.device
+            n_c, n_f = self.n_coarse, self.n_fine
+            t = int(_lib.lib().hi3d_stride2_up_tile_rows())
+            npad = (n_c + t - 1) // t * t
+            order = torch.empty(max(npad, 1), dtype=torch.int32, device=device)
+            down_sorted = torch.empty((max(npad, 1), 8), dtype=torch.int32, device=device)
+            ws = _lib.workspace(_lib.query("hi3d_stride2_up_plan_workspace", n_c), device)
+            _lib.call("hi3d_stride2_up_plan", _lib.ptr(self.down), n_c, n_f, w, _lib.ptr(ws), ws.numel(),
+                      _lib.ptr(order), _lib.ptr(down_sorted), _lib.stream(device))
+            self._plans[key] = (order, down_sorted)
+        return self._plans[key]
 
     def up_plan(self) -> ConvPlan:
         if "up" not in self._plans:

@@ -178,6 +178,32 @@ int hi3d_stride2_up_conv(const void* in_dev, int64_t n_c, int32_t cin, const voi
                          const void* bias_dev, int32_t cout, const int32_t* down_dev, int64_t n_f,
                          int32_t dtype, void* out_dev, void* stream);
 
+/* Coarse rows per tile of the parent-major up convolution (32): the sorted form's
+ * order and child table hold whole tiles, ceil(n_c / 32) * 32 rows. */
+int hi3d_stride2_up_tile_rows(void);
+
+/* Workspace bytes of hi3d_stride2_up_plan. */
+int hi3d_stride2_up_plan_workspace(int64_t n_c, int64_t* bytes_host);
+
+/* Plan of the sorted up convolution: a stable radix sort of the coarse rows by
+ * (row >> window_log2, 8-bit mask of the slots holding a child), so the rows of a tile
+ * mostly share one mask. order_dev [ceil(n_c/32)*32] receives the coarse row of each
+ * position (padding: n_c - 1), down_sorted_dev [same, 8] the permuted rows of down_dev
+ * (padding: every slot n_f). window_log2 = 31 sorts all rows as one window.
+ * (No reference function, as for hi3d_stride2_up_conv.) */
+int hi3d_stride2_up_plan(const int32_t* down_dev, int64_t n_c, int64_t n_f, int32_t window_log2,
+                         void* workspace_dev, int64_t workspace_bytes, int32_t* order_dev,
+                         int32_t* down_sorted_dev, void* stream);
+
+/* hi3d_stride2_up_conv over the plan's order: the tile at positions 32 t .. 32 t + 31
+ * reads coarse rows order_dev[...] and writes the children of down_sorted_dev; a slot no
+ * row of a tile has skips its products. The same outputs as hi3d_stride2_up_conv, bit
+ * for bit. (No reference function, as for hi3d_stride2_up_conv.) */
+int hi3d_stride2_up_conv_sorted(const void* in_dev, int64_t n_c, int32_t cin, const void* weight_dev,
+                                const void* bias_dev, int32_t cout, const int32_t* order_dev,
+                                const int32_t* down_sorted_dev, int64_t n_f, int32_t dtype,
+                                void* out_dev, void* stream);
+
 /* Workspace bytes of hi3d_child_neighbour_table. */
 int hi3d_child_table_workspace(int64_t n_parents, int64_t* bytes_host);
 

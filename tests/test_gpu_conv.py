@@ -459,6 +459,9 @@ def test_stride2_up_parent_major(cuda, dtype, cin, n_side, density, with_bias):
     assert oconv.rel_err(z.float().cpu().numpy(), ref) <= GATE[dtype]
     out = torch.full_like(z, float("nan"))
     assert conv.stride2_up(y, s, w, b, out=out) is out and torch.equal(out, z)
+    # rows in the mask-sorted order (the default) and in row order: the same bits
+    assert torch.equal(conv.stride2_up(y, s, w, b, sorted_rows=False), z)
+    assert torch.equal(conv.stride2_up(y, s, w, b, sorted_rows=True), z)
 
 
 def test_stride2_up_workload_fp16(cuda):
@@ -473,6 +476,41 @@ def test_stride2_up_workload_fp16(cuda):
     z = conv.stride2_up(y, s, w, None, out=torch.full((s.n_fine, 64), float("nan"), dtype=torch.float16, device=cuda))
     assert bool(torch.isfinite(z).all())
     assert torch.equal(z, conv.gather_conv(y, s.up_plan(), w))
+    for sorted_rows in (False, True):
+        again = torch.full((s.n_fine, 64), float("nan"), dtype=torch.float16, device=cuda)
+        assert torch.equal(conv.stride2_up(y, s, w, None, out=again, sorted_rows=sorted_rows), z)
     rows = np.random.default_rng(3).choice(s.n_fine, 4096, replace=False)
     ref = oconv.gather_conv_f64(y.float().cpu().numpy(), s.up.cpu().numpy(), w.float().cpu().numpy(), rows=rows)
     assert oconv.rel_err(z.float().cpu().numpy()[rows], ref) <= 1e-2
+
+
+@pytest.mark.parametrize("window_log2", [31, 4, 0])
+def test_stride2_up_order_plan(cuda, window_log2):
+    """The sorted up convolution's plan: ``order`` is a permutation of the coarse rows
+    (padded with row n_c - 1 to whole 32-row tiles), stable-sorted by (row window, slot
+    mask of the row's children); ``down_sorted`` is ``down[order]`` with absent padding;
+    the convolution over it equals the row-order kernel bit for bit."""
+    from hi3d_amd import conv, kmap
+
+    rng = np.random.default_rng(90 + window_log2)
+    idx = _rand_indices(rng, 21, 0.25, batch=2)
+    s = kmap.stride2_structure(torch.as_tensor(idx).to(cuda), [21] * 3, 2)
+    order, down_sorted = s.up_order(window_log2)
+    n_c, n_f = s.n_coarse, s.n_fine
+    down = s.down.cpu().numpy()
+    mask = ((down < n_f) * (1 << np.arange(8))).sum(1)
+    key = ((np.arange(n_c) >> window_log2) << 8) | mask
+    want = np.argsort(key, kind="stable")
+    npad = (n_c + 31) // 32 * 32
+    o = order.cpu().numpy()
+    assert o.shape == (npad,) and np.array_equal(o[:n_c], want) and np.all(o[n_c:] == n_c - 1)
+    ds = down_sorted.cpu().numpy()
+    assert np.array_equal(ds[:n_c], down[want]) and np.all(ds[n_c:] == n_f)
+    y = torch.as_tensor(rng.standard_normal((n_c, 128), dtype=np.float32)).half().to(cuda)
+    w = torch.as_tensor(rng.standard_normal((64, 8, 128), dtype=np.float32) / 32).half().to(cuda)
+    old = kmap.UP_ORDER_WINDOW_LOG2
+    try:
+        kmap.UP_ORDER_WINDOW_LOG2 = window_log2
+        assert torch.equal(conv.stride2_up(y, s, w, sorted_rows=True), conv.stride2_up(y, s, w, sorted_rows=False))
+    finally:
+        kmap.UP_ORDER_WINDOW_LOG2 = old
