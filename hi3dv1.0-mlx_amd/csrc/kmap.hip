@@ -14,6 +14,13 @@
 // 2^32 - 1) and its row share one 64-bit slot, so one 64-bit CAS inserts both; wider keys
 // use a 64-bit key array plus a row array. Probing writes each (row, offset) cell of the
 // table exactly once, so the table does not depend on insertion order.
+//
+// Slots keep locality: a voxel's home slot is 8 * mix64(its 2x2x2 brick) + its corner in
+// the brick, so the eight cells of a brick share one 64-byte run of slots and a row's 26
+// neighbours fall in at most 8 such runs. With a workspace for it, the rows are first
+// sorted by the top 16 bits of their cell keys (batch, x, bands of y), and the insert and
+// the probe walk them in that order (in chunks taken XCD by XCD), so neighbouring rows
+// touch the same runs while they sit in L2.
 
 #include <algorithm>
 #include <cstdarg>
@@ -72,13 +79,34 @@ struct Grid {
   __device__ __forceinline__ uint64_t key(int b, int x, int y, int z) const {
     return ((static_cast<uint64_t>(b) * sx + x) * sy + y) * sz + z;
   }
+  // the cell's 2x2x2 brick (packed like the cell key over the halved extents) and its
+  // corner in the brick
+  __device__ __forceinline__ uint64_t brick(int b, int x, int y, int z) const {
+    const uint64_t hx = (static_cast<uint64_t>(sx) + 1) >> 1, hy = (static_cast<uint64_t>(sy) + 1) >> 1,
+                   hz = (static_cast<uint64_t>(sz) + 1) >> 1;
+    return ((static_cast<uint64_t>(b) * hx + (x >> 1)) * hy + (y >> 1)) * hz + (z >> 1);
+  }
+  __device__ __forceinline__ int corner(int x, int y, int z) const {
+    return ((x & 1) << 2) | ((y & 1) << 1) | (z & 1);
+  }
+  // voxel-slot home: the cell's corner within a run of 8 slots per brick
+  __device__ __forceinline__ uint64_t home(int b, int x, int y, int z, uint64_t mask) const {
+    return ((mix64(brick(b, x, y, z)) << 3) | static_cast<uint64_t>(corner(x, y, z))) & mask;
+  }
 };
 
-__global__ void insert32_kernel(const int4* __restrict__ coords, int64_t n, Grid g,
+// perm (optional): visit rows perm[0 ..] (cell order; a negative entry stands for an
+// out-of-range row, already flagged) instead of 0 ..
+__global__ void insert32_kernel(const int4* __restrict__ coords, int64_t n, Grid g, const int32_t* __restrict__ perm,
                                 unsigned long long* __restrict__ slots, uint64_t mask,
                                 int32_t* __restrict__ status) {
   int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= n) return;
+  if (perm != nullptr) {
+    const int32_t p = perm[i];
+    if (p < 0) return;
+    i = p;
+  }
   int4 c = coords[i];
   if (!g.inside(c.x, c.y, c.z, c.w)) {
     atomicOr(status, HI3D_MAP_RANGE);
@@ -86,7 +114,7 @@ __global__ void insert32_kernel(const int4* __restrict__ coords, int64_t n, Grid
   }
   uint32_t key = static_cast<uint32_t>(g.key(c.x, c.y, c.z, c.w));
   unsigned long long packed = (static_cast<unsigned long long>(key) << 32) | static_cast<uint32_t>(i);
-  uint64_t h = mix64(key) & mask;
+  uint64_t h = g.home(c.x, c.y, c.z, c.w, mask);
   for (uint64_t probe = 0; probe <= mask; ++probe) {
     unsigned long long prev = atomicCAS(&slots[h], kEmpty, packed);
     if (prev == kEmpty) return;
@@ -99,18 +127,23 @@ __global__ void insert32_kernel(const int4* __restrict__ coords, int64_t n, Grid
   atomicOr(status, HI3D_MAP_OVERFLOW);
 }
 
-__global__ void insert64_kernel(const int4* __restrict__ coords, int64_t n, Grid g,
+__global__ void insert64_kernel(const int4* __restrict__ coords, int64_t n, Grid g, const int32_t* __restrict__ perm,
                                 unsigned long long* __restrict__ keys, int32_t* __restrict__ vals,
                                 uint64_t mask, int32_t* __restrict__ status) {
   int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= n) return;
+  if (perm != nullptr) {
+    const int32_t p = perm[i];
+    if (p < 0) return;
+    i = p;
+  }
   int4 c = coords[i];
   if (!g.inside(c.x, c.y, c.z, c.w)) {
     atomicOr(status, HI3D_MAP_RANGE);
     return;
   }
   unsigned long long key = g.key(c.x, c.y, c.z, c.w);
-  uint64_t h = mix64(key) & mask;
+  uint64_t h = g.home(c.x, c.y, c.z, c.w, mask);
   for (uint64_t probe = 0; probe <= mask; ++probe) {
     unsigned long long prev = atomicCAS(&keys[h], kEmpty, key);
     if (prev == kEmpty) {
@@ -127,8 +160,7 @@ __global__ void insert64_kernel(const int4* __restrict__ coords, int64_t n, Grid
 }
 
 __device__ __forceinline__ int32_t lookup32(const unsigned long long* __restrict__ slots,
-                                            uint64_t mask, uint32_t key, int32_t absent) {
-  uint64_t h = mix64(key) & mask;
+                                            uint64_t mask, uint64_t h, uint32_t key, int32_t absent) {
   for (uint64_t probe = 0; probe <= mask; ++probe) {
     unsigned long long s = slots[h];
     if (s == kEmpty) return absent;
@@ -139,9 +171,8 @@ __device__ __forceinline__ int32_t lookup32(const unsigned long long* __restrict
 }
 
 __device__ __forceinline__ int32_t lookup64(const unsigned long long* __restrict__ keys,
-                                            const int32_t* __restrict__ vals, uint64_t mask,
+                                            const int32_t* __restrict__ vals, uint64_t mask, uint64_t h,
                                             unsigned long long key, int32_t absent) {
-  uint64_t h = mix64(key) & mask;
   for (uint64_t probe = 0; probe <= mask; ++probe) {
     unsigned long long s = keys[h];
     if (s == kEmpty) return absent;
@@ -151,50 +182,254 @@ __device__ __forceinline__ int32_t lookup64(const unsigned long long* __restrict
   return absent;
 }
 
-// One block handles kRows rows x kvol offsets; flat (row, offset) order makes the table
-// writes coalesced. Counts are reduced in LDS, then one atomic per offset per block.
+// One block handles kProbeRows rows x kvol offsets; flat (row, offset) order makes the
+// table writes coalesced. The block's rows and coordinates are staged in LDS once; each
+// thread then takes its cells kProbeBatch at a time, issuing the home-slot loads of all
+// of them before resolving any (independent loads in flight instead of one dependent
+// chain per cell); a key found past its home slot continues the linear probe there.
+// Counts are reduced in LDS, then one atomic per offset per block.
 constexpr int kProbeRows = 64;
+constexpr int kProbeBatch = 8;
 
+// perm (optional): the block's rows are perm[row0 ..] (cell order; a negative entry p
+// stands for the out-of-range row ~p), with the row chunks taken XCD by XCD (block b
+// runs on XCD b % 8 and takes chunk (b % 8) * per + b / 8), so each XCD's L2 sees a
+// contiguous run of cells.
 template <bool kKey64>
 __global__ __launch_bounds__(256) void probe_kernel(const int4* __restrict__ coords, int64_t n,
-                                                    Grid g, int ksize,
+                                                    Grid g, int ksize, const int32_t* __restrict__ perm, int per,
                                                     const unsigned long long* __restrict__ slots,
                                                     const int32_t* __restrict__ vals, uint64_t mask,
                                                     int32_t* __restrict__ nbr,
                                                     int32_t* __restrict__ counts) {
   __shared__ int32_t cnt[kMaxKvol];
+  __shared__ int4 sc[kProbeRows];
+  __shared__ int32_t so[kProbeRows];
   const int kvol = ksize * ksize * ksize;
   const int half = ksize / 2;
   const int center = kvol / 2;
-  for (int k = threadIdx.x; k < kvol; k += blockDim.x) cnt[k] = 0;
-  __syncthreads();
-  const int64_t row0 = static_cast<int64_t>(blockIdx.x) * kProbeRows;
+  const int64_t chunk = perm != nullptr ? static_cast<int64_t>(blockIdx.x % 8) * per + blockIdx.x / 8 : blockIdx.x;
+  const int64_t row0 = chunk * kProbeRows;
+  if (row0 >= n) return;  // the XCD order's spare blocks (before any barrier)
   const int rows = static_cast<int>(n - row0 < kProbeRows ? n - row0 : kProbeRows);
+  for (int k = threadIdx.x; k < kvol; k += blockDim.x) cnt[k] = 0;
+  if (threadIdx.x < rows) {
+    int64_t o = row0 + threadIdx.x;
+    if (perm != nullptr) {
+      const int32_t p = perm[o];
+      o = p >= 0 ? p : ~p;
+    }
+    so[threadIdx.x] = static_cast<int32_t>(o);
+    sc[threadIdx.x] = coords[o];
+  }
+  __syncthreads();
   const int cells = rows * kvol;
   const int32_t absent = static_cast<int32_t>(n);
-  for (int j = threadIdx.x; j < cells; j += blockDim.x) {
-    const int r = j / kvol;
-    const int k = j - r * kvol;
-    const int64_t o = row0 + r;
-    int32_t found;
-    if (k == center) {
-      found = static_cast<int32_t>(o);
-    } else {
-      int4 c = coords[o];
-      const int dx = k / (ksize * ksize) - half;
-      const int dy = (k / ksize) % ksize - half;
-      const int dz = k % ksize - half;
-      const int x = c.y + dx, y = c.z + dy, z = c.w + dz;
-      if (!g.inside(c.x, x, y, z)) {
-        found = absent;
-      } else if (kKey64) {
-        found = lookup64(slots, vals, mask, g.key(c.x, x, y, z), absent);
-      } else {
-        found = lookup32(slots, mask, static_cast<uint32_t>(g.key(c.x, x, y, z)), absent);
+  for (int base = threadIdx.x; base < cells; base += blockDim.x * kProbeBatch) {
+    uint64_t h[kProbeBatch], key[kProbeBatch];
+    unsigned long long v[kProbeBatch];
+    bool look[kProbeBatch];
+#pragma unroll
+    for (int u = 0; u < kProbeBatch; ++u) {
+      const int j = base + u * blockDim.x;
+      look[u] = false;
+      h[u] = 0;
+      key[u] = 0;
+      if (j < cells) {
+        const int r = j / kvol;
+        const int k = j - r * kvol;
+        const int4 c = sc[r];
+        const int x = c.y + k / (ksize * ksize) - half;
+        const int y = c.z + (k / ksize) % ksize - half;
+        const int z = c.w + k % ksize - half;
+        if (k != center && g.inside(c.x, x, y, z)) {
+          look[u] = true;
+          h[u] = g.home(c.x, x, y, z, mask);
+          key[u] = g.key(c.x, x, y, z);
+        }
       }
     }
-    nbr[o * kvol + k] = found;
-    if (found != absent) atomicAdd(&cnt[k], 1);
+#pragma unroll
+    for (int u = 0; u < kProbeBatch; ++u) v[u] = look[u] ? slots[h[u]] : kEmpty;
+#pragma unroll
+    for (int u = 0; u < kProbeBatch; ++u) {
+      const int j = base + u * blockDim.x;
+      if (j >= cells) continue;
+      const int r = j / kvol;
+      const int k = j - r * kvol;
+      const int32_t o = so[r];
+      int32_t found = absent;
+      if (k == center) {
+        found = o;
+      } else if (look[u]) {
+        // the home slot's value is in v; an empty slot ends the probe, a match ends it
+        // with the row, another key moves on to the next slots
+        if (kKey64) {
+          if (v[u] == key[u]) found = vals[h[u]];
+          else if (v[u] != kEmpty)
+            found = lookup64(slots, vals, mask, (h[u] + 1) & mask, key[u], absent);
+        } else {
+          const uint32_t k32 = static_cast<uint32_t>(key[u]);
+          if (static_cast<uint32_t>(v[u] >> 32) == k32 && v[u] != kEmpty)
+            found = static_cast<int32_t>(static_cast<uint32_t>(v[u]));
+          else if (v[u] != kEmpty)
+            found = lookup32(slots, mask, (h[u] + 1) & mask, k32, absent);
+        }
+      }
+      nbr[static_cast<int64_t>(o) * kvol + k] = found;
+      if (found != absent) atomicAdd(&cnt[k], 1);
+    }
+  }
+  __syncthreads();
+  for (int k = threadIdx.x; k < kvol; k += blockDim.x)
+    if (cnt[k]) atomicAdd(&counts[k], cnt[k]);
+}
+
+// ------------------------------------------------------------- brick hash --
+// The map build's hash (hi3d_kmap_subm): one bucket per occupied 2x2x2 brick, open
+// addressing with linear probing over buckets. A bucket is its brick key (keys[]), an
+// 8-bit occupancy mask (masks[]) and the rows of its 8 cells (rows[8 h ..], valid where
+// the mask bit is set, so only keys and masks are cleared per build). A row's 26
+// neighbours lie in 8 bricks, so every lookup reads one bucket (longer probes are rare at
+// the default capacity of one bucket per voxel) and neighbouring rows read the same ones.
+constexpr unsigned long long kEmptyBrick = ~0ull;
+
+struct BrickTable {
+  unsigned long long* keys;
+  uint32_t* masks;
+  int32_t* rows;
+  uint64_t mask;
+};
+
+// perm (optional): rows perm[0 ..] in cell order (a negative entry stands for an
+// out-of-range row, already flagged)
+__global__ void brick_insert_kernel(const int4* __restrict__ coords, int64_t n, Grid g,
+                                    const int32_t* __restrict__ perm, BrickTable t, int32_t* __restrict__ status) {
+  int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  if (perm != nullptr) {
+    const int32_t p = perm[i];
+    if (p < 0) return;
+    i = p;
+  }
+  const int4 c = coords[i];
+  if (!g.inside(c.x, c.y, c.z, c.w)) {
+    atomicOr(status, HI3D_MAP_RANGE);
+    return;
+  }
+  const unsigned long long bk = g.brick(c.x, c.y, c.z, c.w);
+  uint64_t h = mix64(bk) & t.mask;
+  for (uint64_t probe = 0; probe <= t.mask; ++probe) {
+    const unsigned long long prev = atomicCAS(&t.keys[h], kEmptyBrick, bk);
+    if (prev == kEmptyBrick || prev == bk) {
+      const int cn = g.corner(c.y, c.z, c.w);
+      t.rows[h * 8 + cn] = static_cast<int32_t>(i);
+      const uint32_t old = atomicOr(&t.masks[h], 1u << cn);
+      if (old & (1u << cn)) atomicOr(status, HI3D_MAP_DUPLICATE);
+      return;
+    }
+    h = (h + 1) & t.mask;
+  }
+  atomicOr(status, HI3D_MAP_OVERFLOW);
+}
+
+// bucket of brick bk from slot h on (h's key already known to differ), or -1
+__device__ __forceinline__ int64_t brick_find(const BrickTable& t, uint64_t h, unsigned long long bk) {
+  for (uint64_t probe = 0; probe <= t.mask; ++probe) {
+    const unsigned long long k = t.keys[h];
+    if (k == bk) return static_cast<int64_t>(h);
+    if (k == kEmptyBrick) return -1;
+    h = (h + 1) & t.mask;
+  }
+  return -1;
+}
+
+// One block: kProbeRows rows x kvol offsets, rows staged in LDS, each thread's cells
+// kProbeBatch at a time: first every cell's bucket key (one independent load each), then
+// the buckets' masks and rows (again independent loads).
+__global__ __launch_bounds__(256) void brick_probe_kernel(const int4* __restrict__ coords, int64_t n, Grid g,
+                                                          int ksize, const int32_t* __restrict__ perm, int per,
+                                                          BrickTable t, int32_t* __restrict__ nbr,
+                                                          int32_t* __restrict__ counts) {
+  __shared__ int32_t cnt[kMaxKvol];
+  __shared__ int4 sc[kProbeRows];
+  __shared__ int32_t so[kProbeRows];
+  const int kvol = ksize * ksize * ksize;
+  const int half = ksize / 2;
+  const int center = kvol / 2;
+  const int64_t chunk = perm != nullptr ? static_cast<int64_t>(blockIdx.x % 8) * per + blockIdx.x / 8 : blockIdx.x;
+  const int64_t row0 = chunk * kProbeRows;
+  if (row0 >= n) return;  // the XCD order's spare blocks (before any barrier)
+  const int rows = static_cast<int>(n - row0 < kProbeRows ? n - row0 : kProbeRows);
+  for (int k = threadIdx.x; k < kvol; k += blockDim.x) cnt[k] = 0;
+  if (threadIdx.x < rows) {
+    int64_t o = row0 + threadIdx.x;
+    if (perm != nullptr) {
+      const int32_t p = perm[o];
+      o = p >= 0 ? p : ~p;
+    }
+    so[threadIdx.x] = static_cast<int32_t>(o);
+    sc[threadIdx.x] = coords[o];
+  }
+  __syncthreads();
+  const int cells = rows * kvol;
+  const int32_t absent = static_cast<int32_t>(n);
+  for (int base = threadIdx.x; base < cells; base += blockDim.x * kProbeBatch) {
+    unsigned long long bk[kProbeBatch], kv[kProbeBatch];
+    uint64_t h[kProbeBatch];
+    int cn[kProbeBatch];
+    bool look[kProbeBatch];
+#pragma unroll
+    for (int u = 0; u < kProbeBatch; ++u) {
+      const int j = base + u * blockDim.x;
+      look[u] = false;
+      bk[u] = kEmptyBrick;
+      h[u] = 0;
+      cn[u] = 0;
+      if (j < cells) {
+        const int r = j / kvol;
+        const int k = j - r * kvol;
+        const int4 c = sc[r];
+        const int x = c.y + k / (ksize * ksize) - half;
+        const int y = c.z + (k / ksize) % ksize - half;
+        const int z = c.w + k % ksize - half;
+        if (k != center && g.inside(c.x, x, y, z)) {
+          look[u] = true;
+          bk[u] = g.brick(c.x, x, y, z);
+          h[u] = mix64(bk[u]) & t.mask;
+          cn[u] = g.corner(x, y, z);
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kProbeBatch; ++u) kv[u] = look[u] ? t.keys[h[u]] : kEmptyBrick;
+    int64_t hb[kProbeBatch];
+#pragma unroll
+    for (int u = 0; u < kProbeBatch; ++u) {
+      hb[u] = -1;
+      if (look[u]) {
+        if (kv[u] == bk[u]) hb[u] = static_cast<int64_t>(h[u]);
+        else if (kv[u] != kEmptyBrick) hb[u] = brick_find(t, (h[u] + 1) & t.mask, bk[u]);
+      }
+    }
+    uint32_t m[kProbeBatch];
+    int32_t rv[kProbeBatch];
+#pragma unroll
+    for (int u = 0; u < kProbeBatch; ++u) {
+      m[u] = hb[u] >= 0 ? t.masks[hb[u]] : 0u;
+      rv[u] = hb[u] >= 0 ? t.rows[hb[u] * 8 + cn[u]] : absent;
+    }
+#pragma unroll
+    for (int u = 0; u < kProbeBatch; ++u) {
+      const int j = base + u * blockDim.x;
+      if (j >= cells) continue;
+      const int r = j / kvol;
+      const int k = j - r * kvol;
+      const int32_t o = so[r];
+      const int32_t found = k == center ? o : ((m[u] >> cn[u]) & 1u) ? rv[u] : absent;
+      nbr[static_cast<int64_t>(o) * kvol + k] = found;
+      if (found != absent) atomicAdd(&cnt[k], 1);
+    }
   }
   __syncthreads();
   for (int k = threadIdx.x; k < kvol; k += blockDim.x)
@@ -237,6 +472,20 @@ __global__ void cell_key_kernel(const int4* __restrict__ coords, int64_t n, Grid
   const int4 c = coords[i];
   const bool in = g.inside(c.x, c.y, c.z, c.w);
   keys[i] = in ? static_cast<uint32_t>(g.key(c.x, c.y, c.z, c.w)) : 0u;
+  rows[i] = in ? static_cast<int32_t>(i) : ~static_cast<int32_t>(i);
+  if (!in) atomicOr(status, HI3D_MAP_RANGE);
+}
+
+// Hash path's cell order: the top 32 bits of the row's cell key (the key shifted right
+// by `shift`); an out-of-range row is flagged, gets key 0 and the row id ~i.
+__global__ void order_key_kernel(const int4* __restrict__ coords, int64_t n, Grid g, int shift,
+                                 uint32_t* __restrict__ keys, int32_t* __restrict__ rows,
+                                 int32_t* __restrict__ status) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int4 c = coords[i];
+  const bool in = g.inside(c.x, c.y, c.z, c.w);
+  keys[i] = in ? static_cast<uint32_t>(g.key(c.x, c.y, c.z, c.w) >> shift) : 0u;
   rows[i] = in ? static_cast<int32_t>(i) : ~static_cast<int32_t>(i);
   if (!in) atomicOr(status, HI3D_MAP_RANGE);
 }
@@ -427,6 +676,14 @@ __global__ __launch_bounds__(kLookup3Rows) void dense_lookup3_kernel(const int4*
 int64_t default_capacity(int64_t n) {
   int64_t cap = 64;
   while (cap < 2 * n) cap <<= 1;
+  return cap;
+}
+
+// Default bucket count of the brick hash: one per voxel (a set whose voxels all sit in
+// distinct bricks fills half of it; shells fill ~15 %).
+int64_t brick_capacity(int64_t n) {
+  int64_t cap = 64;
+  while (cap < n) cap <<= 1;
   return cap;
 }
 
@@ -778,12 +1035,28 @@ const char* hi3d_last_error(void) { return g_last_error.c_str(); }
 
 const char* hi3d_version(void) { return "hi3d_amd 0.1 gfx950"; }
 
+// Bytes of the cell-order sort that precedes a hash build: keys and rows (two slabs
+// each) and the radix sort's counts.
+static int64_t hash_order_bytes(int64_t n) {
+  return 4 * align_up(std::max<int64_t>(n, 1) * 4, 256) + radix::temp_bytes(std::max<int64_t>(n, 1));
+}
+
+// Bytes of a brick table of `cap` buckets: keys, masks, then 8 rows per bucket.
+static int64_t brick_table_bytes(int64_t cap) {
+  return align_up(cap * 8, 256) + align_up(cap * 4, 256) + align_up(cap * 32, 256);
+}
+
+// Brick tables above this size are built and probed in cell order (below it the table
+// stays in the last-level cache and the sort costs more than it saves).
+constexpr int64_t kBrickOrderMinBytes = int64_t(64) << 20;
+
 int hi3d_kmap_workspace(int64_t n, int64_t capacity, int32_t key64, int64_t* bytes) {
   HI3D_REQUIRE(bytes != nullptr, "bytes_host is NULL");
   HI3D_REQUIRE(n >= 0, "n must be non-negative");
-  int64_t cap = capacity > 0 ? capacity : default_capacity(n);
+  (void)key64;  // bricks always use 64-bit keys
+  int64_t cap = capacity > 0 ? capacity : brick_capacity(n);
   HI3D_REQUIRE((cap & (cap - 1)) == 0, "capacity must be a power of two");
-  *bytes = key64 ? align_up(cap * 8, 256) + cap * 4 + 256 : cap * 8 + 256;
+  *bytes = brick_table_bytes(cap) + hash_order_bytes(n);
   return HI3D_OK;
 }
 
@@ -803,25 +1076,73 @@ static int kmap_subm_begin(const int32_t* coords, int64_t n, int32_t sx, int32_t
   return HI3D_OK;
 }
 
-// Hash build + probe over a table of `cap` slots at `table` (cap * 8 bytes of slots, then
-// for 64-bit keys cap * 4 bytes of rows at the next 256-byte boundary).
+// Voxel-slot hash build + probe over a table of `cap` slots at `table` (cap * 8 bytes of
+// slots, then for 64-bit keys cap * 4 bytes of rows at the next 256-byte boundary), rows
+// in input order: the allocation-free map's table, which fits its fixed array.
 static int kmap_subm_hash(const int32_t* coords, int64_t n, Grid g, int32_t ksize, bool key64, int64_t cap,
                           char* table, int32_t* nbr, int32_t* counts, int32_t* status, hipStream_t stream) {
   const uint64_t mask = static_cast<uint64_t>(cap - 1);
   auto* slots = reinterpret_cast<unsigned long long*>(table);
   int32_t* vals = key64 ? reinterpret_cast<int32_t*>(table + align_up(cap * 8, 256)) : nullptr;
-  launch_fill<unsigned long long>(slots, cap, kEmpty, stream);
   const unsigned blocks = static_cast<unsigned>(ceil_div(n, 256));
   const int4* c4 = reinterpret_cast<const int4*>(coords);
+  launch_fill<unsigned long long>(slots, cap, kEmpty, stream);
+  const dim3 pgrid(static_cast<unsigned>(ceil_div(n, kProbeRows)));
   if (key64) {
-    hipLaunchKernelGGL(insert64_kernel, dim3(blocks), dim3(256), 0, stream, c4, n, g, slots, vals, mask, status);
-    hipLaunchKernelGGL(probe_kernel<true>, dim3(static_cast<unsigned>(ceil_div(n, kProbeRows))), dim3(256), 0,
-                       stream, c4, n, g, ksize, slots, vals, mask, nbr, counts);
+    hipLaunchKernelGGL(insert64_kernel, dim3(blocks), dim3(256), 0, stream, c4, n, g, nullptr, slots, vals, mask,
+                       status);
+    hipLaunchKernelGGL(probe_kernel<true>, pgrid, dim3(256), 0, stream, c4, n, g, ksize, nullptr, 0, slots, vals, mask,
+                       nbr, counts);
   } else {
-    hipLaunchKernelGGL(insert32_kernel, dim3(blocks), dim3(256), 0, stream, c4, n, g, slots, mask, status);
-    hipLaunchKernelGGL(probe_kernel<false>, dim3(static_cast<unsigned>(ceil_div(n, kProbeRows))), dim3(256), 0,
-                       stream, c4, n, g, ksize, slots, nullptr, mask, nbr, counts);
+    hipLaunchKernelGGL(insert32_kernel, dim3(blocks), dim3(256), 0, stream, c4, n, g, nullptr, slots, mask, status);
+    hipLaunchKernelGGL(probe_kernel<false>, pgrid, dim3(256), 0, stream, c4, n, g, ksize, nullptr, 0, slots, nullptr,
+                       mask, nbr, counts);
   }
+  HI3D_LAUNCH_CHECK();
+  return HI3D_OK;
+}
+
+// Brick-hash build + probe (hi3d_kmap_subm's map) over `cap` buckets at `ws`, with the
+// cell-order sort when the table is large.
+static int kmap_subm_brick(const int32_t* coords, int64_t n, Grid g, int32_t ksize, int64_t cap, char* ws,
+                           int32_t* nbr, int32_t* counts, int32_t* status, hipStream_t stream) {
+  BrickTable t;
+  t.keys = reinterpret_cast<unsigned long long*>(ws);
+  t.masks = reinterpret_cast<uint32_t*>(ws + align_up(cap * 8, 256));
+  t.rows = reinterpret_cast<int32_t*>(ws + align_up(cap * 8, 256) + align_up(cap * 4, 256));
+  t.mask = static_cast<uint64_t>(cap - 1);
+  char* order = ws + brick_table_bytes(cap);
+  const unsigned blocks = static_cast<unsigned>(ceil_div(n, 256));
+  const int4* c4 = reinterpret_cast<const int4*>(coords);
+  const int32_t* perm = nullptr;
+  int per = 0;
+  int64_t probe_blocks = ceil_div(n, kProbeRows);
+  if (brick_table_bytes(cap) > kBrickOrderMinBytes) {
+    const int64_t slab = align_up(n * 4, 256);
+    auto* k0 = reinterpret_cast<uint32_t*>(order);
+    auto* k1 = reinterpret_cast<uint32_t*>(order + slab);
+    auto* r0 = reinterpret_cast<int32_t*>(order + 2 * slab);
+    auto* r1 = reinterpret_cast<int32_t*>(order + 3 * slab);
+    const uint64_t cells = static_cast<uint64_t>(g.batch) * g.sx * g.sy * g.sz;
+    int key_bits = 1;
+    while (key_bits < 64 && (uint64_t(1) << key_bits) < cells) ++key_bits;
+    const int shift = key_bits > 32 ? key_bits - 32 : 0;
+    const int kb = key_bits - shift;
+    hipLaunchKernelGGL(order_key_kernel, dim3(blocks), dim3(256), 0, stream, c4, n, g, shift, k0, r0, status);
+    // two radix passes over the key's top 16 bits (batch, x, y bands)
+    HI3D_HIP_CHECK(radix::sort_pairs(order + 4 * slab, radix::temp_bytes(n), k0, k1, r0, r1, n,
+                                     kb > 16 ? kb - 16 : 0, kb, stream));
+    perm = r0;
+    per = static_cast<int>(ceil_div(probe_blocks, kXcds));
+    probe_blocks = static_cast<int64_t>(per) * kXcds;
+  }
+  launch_fill<unsigned long long>(t.keys, cap, kEmptyBrick, stream);
+  launch_fill<uint32_t>(t.masks, cap, 0u, stream);
+  hipLaunchKernelGGL(brick_insert_kernel, dim3(blocks), dim3(256), 0, stream, c4, n, g, perm, t, status);
+  // (one row per thread, its 8 buckets' keys, masks and rows in registers, measured
+  // slower on the config-5 shells: 1.74 against 1.60 ms for the whole build)
+  hipLaunchKernelGGL(brick_probe_kernel, dim3(static_cast<unsigned>(probe_blocks)), dim3(256), 0, stream, c4, n, g,
+                     ksize, perm, per, t, nbr, counts);
   HI3D_LAUNCH_CHECK();
   return HI3D_OK;
 }
@@ -834,16 +1155,14 @@ int hi3d_kmap_subm(const int32_t* coords, int64_t n, int32_t sx, int32_t sy, int
   int rc = kmap_subm_begin(coords, n, sx, sy, sz, batch_size, ksize, nbr, counts, status, stream);
   if (rc != HI3D_OK || n == 0) return rc;
   HI3D_REQUIRE(workspace != nullptr, "null pointer argument");
-  const uint64_t space = static_cast<uint64_t>(batch_size) * sx * sy * sz;
-  const bool key64 = space >= 0xFFFFFFFFull;
-  int64_t cap = capacity > 0 ? capacity : default_capacity(n);
+  const int64_t cap = capacity > 0 ? capacity : brick_capacity(n);
   int64_t need = 0;
-  rc = hi3d_kmap_workspace(n, cap, key64, &need);
+  rc = hi3d_kmap_workspace(n, cap, 1, &need);
   if (rc != HI3D_OK) return rc;
   HI3D_REQUIRE(workspace_bytes >= need, "workspace too small: %lld < %lld bytes",
                static_cast<long long>(workspace_bytes), static_cast<long long>(need));
-  return kmap_subm_hash(coords, n, Grid{sx, sy, sz, batch_size}, ksize, key64, cap, static_cast<char*>(workspace), nbr,
-                        counts, status, stream);
+  return kmap_subm_brick(coords, n, Grid{sx, sy, sz, batch_size}, ksize, cap, static_cast<char*>(workspace), nbr,
+                         counts, status, stream);
 }
 
 // The same map with the hash table in `scratch`, a device array of this library (no

@@ -29,9 +29,10 @@ window C64 0.243 / C128 0.554 ms against 0.257 / 0.575 ms at 2^18; on the 4.4M-v
 C256 shells 2^19 is best (7.09 ms; 7.28 at 2^18, 7.22-7.25 at 2^20 .. one window)."""
 KMAP_DENSE_MAX_CELLS: int = 1 << 31
 """Grids of at most this many cells (batch * sx * sy * sz) build their map through a
-dense grid of rows instead of the hash; ``0`` always hashes. The dense map is the faster
-one on every measured set (config-5 shells, 4.4M voxels at 1024^3: 2.12 ms with a grid
-cleared per call against 2.47 ms hashed; 400k voxels at 256^3: 0.176 against 0.278 ms)."""
+dense grid of rows instead of the brick hash; ``0`` always hashes. The dense map is the
+faster one on every measured set (config-5 shells, 4.4M voxels at 1024^3: 0.76 ms on the
+kept grid against 1.60 ms hashed; 543k voxels at 256^3: 0.13 against 0.29 ms), so the
+hash is the path for grids above the limit (and for callers that ask for a capacity)."""
 
 KMAP_DENSE_KEEP: bool = True
 """Keep one dense grid per (device, cell count) between calls (``hi3d_kmap_subm_dense_kept``:
@@ -337,7 +338,7 @@ def build_kernel_map(
     """Submanifold kernel map of ``indices [N, 4]`` ``(batch, x, y, z)``: through a dense
     grid of rows when the grid has at most ``KMAP_DENSE_MAX_CELLS`` cells and no hash
     ``capacity`` is asked for (kept between calls when ``KMAP_DENSE_KEEP``), else
-    through the voxel hash (same table either way). Builds on a kept grid are ordered
+    through the brick hash (same table either way). Builds on a kept grid are ordered
     across streams by an event recorded after each one.
 
     With ``check`` the device status word is read (one sync): duplicate or out-of-range

@@ -56,15 +56,20 @@ const char* hi3d_version(void);
 
 /* ------------------------------------------------------------------ kernel maps -- */
 
-/* Workspace bytes of hi3d_kmap_subm for n voxels; capacity 0 = default (power of two
- * >= 2n). key64 != 0 when batch*sx*sy*sz >= 2^32 - 1 (64-bit voxel keys). */
+/* Workspace bytes of hi3d_kmap_subm for n voxels: the brick hash of `capacity` buckets
+ * (a power of two; 0 = default, the power of two >= n) plus the cell-order sort. key64 is
+ * accepted for the ABI's sake and ignored (brick keys are 64-bit). */
 int hi3d_kmap_workspace(int64_t n, int64_t capacity, int32_t key64, int64_t* bytes_host);
 
-/* Submanifold kernel map: inserts every voxel's packed key
- * ((b*sx + x)*sy + y)*sz + z into an open-addressing hash (linear probing, one CAS per
- * insert) and probes the ksize^3 neighbourhood of each voxel, writing the dense
- * neighbour table nbr_dev [n, ksize^3] (sentinel n) and per-offset non-sentinel counts
- * counts_dev [ksize^3]. Neighbours outside [0, spatial_shape) are absent.
+/* Submanifold kernel map through a brick hash: every voxel claims (one 64-bit CAS) the
+ * bucket of its 2x2x2 brick, keyed by the brick's packed coordinates (as
+ * ((b*sx + x)*sy + y)*sz + z over the halved extents; open addressing, linear probing
+ * over buckets), and sets its corner's bit and row; the ksize^3 neighbourhood of each
+ * voxel is then read bucket by bucket, writing the dense neighbour table
+ * nbr_dev [n, ksize^3] (sentinel n) and per-offset non-sentinel counts counts_dev
+ * [ksize^3]. Neighbours outside [0, spatial_shape) are absent. Large tables are built
+ * and probed in cell order. status_dev flags DUPLICATE, RANGE and OVERFLOW (capacity
+ * smaller than the occupied bricks).
  * Replaces: _voxel_keys + subm_pairs (src/hi3d_mac/torch_backend/sparse_conv.py:109-149)
  * and neighbour_table (src/hi3d_mac/mlx_backend/sparse.py:29-43). */
 int hi3d_kmap_subm(const int32_t* coords_dev, int64_t n, int32_t sx, int32_t sy, int32_t sz,
@@ -77,8 +82,9 @@ int hi3d_kmap_subm(const int32_t* coords_dev, int64_t n, int32_t sx, int32_t sy,
 #define HI3D_KMAP_NOALLOC_BYTES (128ll << 20)
 
 /* hi3d_kmap_subm without allocation or workspace: the same table, counts and status
- * (identical for every coordinate set), with the hash table in a fixed device array of
- * HI3D_KMAP_NOALLOC_BYTES. No counterpart in the reference: for callers that cannot
+ * (identical for every coordinate set), through a voxel-slot hash (one 64-bit slot per
+ * voxel, 2n slots, each voxel's home slot its corner in an 8-slot run of its 2x2x2
+ * brick) in a fixed device array of HI3D_KMAP_NOALLOC_BYTES. No counterpart in the reference: for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops, harnesses
  * that forbid hipMalloc). Takes up to 2^23 voxels with 32-bit keys and 2^22 with 64-bit
  * keys (batch*sx*sy*sz >= 2^32 - 1); larger sets return HI3D_ERR_INVALID before any

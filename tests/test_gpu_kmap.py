@@ -89,8 +89,8 @@ def test_errors_duplicate_range_overflow(cuda):
     rng = np.random.default_rng(1)
     idx = _rand_indices(rng, 8, 0.5)
     assert len(idx) > 64
-    with pytest.raises(RuntimeError, match="overflow"):
-        kmap.build_kernel_map(torch.as_tensor(idx).to(cuda), [8, 8, 8], capacity=64)
+    with pytest.raises(RuntimeError, match="overflow"):  # 16 buckets for the 8^3 grid's 64 bricks
+        kmap.build_kernel_map(torch.as_tensor(idx).to(cuda), [8, 8, 8], capacity=16)
 
 
 def test_stride2_structure_errors(cuda):
