@@ -785,14 +785,21 @@ __global__ __launch_bounds__(256) void pair_write_kernel(const int32_t* __restri
   }
 }
 
-// ------------------------------------------------------------ stride-2 structure --
-// Sort key of fine row i: its coarse cell's packed code times 8 plus its slot, so the
-// rows of one coarse cell sort together and two rows with the same coordinate sort next
-// to each other. Coordinates outside [0, batch) x [0, sx) x [0, sy) x [0, sz) raise the
-// range flag and take key 0 (the result is then discarded by the caller).
-__global__ void half_keys_kernel(const int4* __restrict__ coords, int64_t n, int32_t batch, int32_t sx, int32_t sy,
-                                 int32_t sz, int32_t hx, int32_t hy, int32_t hz, unsigned long long* __restrict__ keys,
-                                 int32_t* __restrict__ rows, int32_t* __restrict__ status) {
+// ------------------------------------------------ resampling (stride-f) structure --
+// Factor (fx, fy, fz) per axis, F = fx fy fz slots per coarse cell (2, 2, 2 for the
+// stride-2 pair). Sort key of fine row i: its coarse cell's packed code times F plus its
+// slot ((x % fx) fy + y % fy) fz + z % fz, so the rows of one coarse cell sort together
+// and two rows with the same coordinate sort next to each other. Coordinates outside
+// [0, batch) x [0, sx) x [0, sy) x [0, sz) raise the range flag and take key 0 (the
+// result is then discarded by the caller).
+struct Factor {
+  int32_t fx, fy, fz, hx, hy, hz;  // factors and coarse extents
+  __device__ __forceinline__ uint64_t slots() const { return static_cast<uint64_t>(fx) * fy * fz; }
+};
+
+__global__ void factor_keys_kernel(const int4* __restrict__ coords, int64_t n, int32_t batch, int32_t sx, int32_t sy,
+                                   int32_t sz, Factor f, unsigned long long* __restrict__ keys,
+                                   int32_t* __restrict__ rows, int32_t* __restrict__ status) {
   int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= n) return;
   int4 c = coords[i];
@@ -802,49 +809,50 @@ __global__ void half_keys_kernel(const int4* __restrict__ coords, int64_t n, int
     c = make_int4(0, 0, 0, 0);
   }
   const unsigned long long cell =
-      ((static_cast<unsigned long long>(c.x) * hx + (c.y >> 1)) * hy + (c.z >> 1)) * hz + (c.w >> 1);
-  keys[i] = cell * 8 + static_cast<unsigned long long>(((c.y & 1) << 2) | ((c.z & 1) << 1) | (c.w & 1));
+      ((static_cast<unsigned long long>(c.x) * f.hx + c.y / f.fx) * f.hy + c.z / f.fy) * f.hz + c.w / f.fz;
+  const unsigned long long slot =
+      (static_cast<unsigned long long>(c.y % f.fx) * f.fy + c.z % f.fy) * f.fz + c.w % f.fz;
+  keys[i] = cell * f.slots() + slot;
   rows[i] = static_cast<int32_t>(i);
 }
 
 // heads[i] = 1 where sorted position i starts a coarse cell; equal neighbouring keys
 // (same cell and slot) are a repeated coordinate
-__global__ void run_heads_kernel(const unsigned long long* __restrict__ keys, int64_t n,
+__global__ void run_heads_kernel(const unsigned long long* __restrict__ keys, int64_t n, uint64_t slots,
                                  int32_t* __restrict__ heads, int32_t* __restrict__ status) {
   int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= n) return;
   const unsigned long long k = keys[i];
   const unsigned long long prev = i > 0 ? keys[i - 1] : ~k;
-  heads[i] = (i == 0 || (k >> 3) != (prev >> 3)) ? 1 : 0;
+  heads[i] = (i == 0 || k / slots != prev / slots) ? 1 : 0;
   if (i > 0 && k == prev && status) atomicOr(status, HI3D_MAP_DUPLICATE);
 }
 
 // After the inclusive scan, ids[i] - 1 is the coarse row of sorted position i.
 __global__ void coarse_emit_kernel(const unsigned long long* __restrict__ keys,
                                    const int32_t* __restrict__ rows,
-                                   const int32_t* __restrict__ ids, int64_t n, int32_t hx,
-                                   int32_t hy, int32_t hz, const int4* __restrict__ coords,
+                                   const int32_t* __restrict__ ids, int64_t n, Factor f,
                                    int4* __restrict__ low, int32_t* __restrict__ inverse,
                                    int32_t* __restrict__ counts, uint8_t* __restrict__ slot,
                                    int64_t* __restrict__ n_low) {
   int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= n) return;
+  const uint64_t slots = f.slots();
   const int32_t c = ids[i] - 1;
   const int32_t r = rows[i];
   inverse[r] = c;
-  int4 f = coords[r];
-  slot[r] = static_cast<uint8_t>(((f.y & 1) << 2) | ((f.z & 1) << 1) | (f.w & 1));
-  const bool head = (i == 0) || (keys[i] >> 3) != (keys[i - 1] >> 3);
-  const bool tail = (i == n - 1) || (keys[i] >> 3) != (keys[i + 1] >> 3);
+  slot[r] = static_cast<uint8_t>(keys[i] % slots);
+  const bool head = (i == 0) || keys[i] / slots != keys[i - 1] / slots;
+  const bool tail = (i == n - 1) || keys[i] / slots != keys[i + 1] / slots;
   if (head) {
-    unsigned long long k = keys[i] >> 3;
+    unsigned long long k = keys[i] / slots;
     int4 l;
-    l.w = static_cast<int>(k % hz);
-    k /= hz;
-    l.z = static_cast<int>(k % hy);
-    k /= hy;
-    l.y = static_cast<int>(k % hx);
-    l.x = static_cast<int>(k / hx);
+    l.w = static_cast<int>(k % f.hz);
+    k /= f.hz;
+    l.z = static_cast<int>(k % f.hy);
+    k /= f.hy;
+    l.y = static_cast<int>(k % f.hx);
+    l.x = static_cast<int>(k / f.hx);
     low[c] = l;
     // run length = position of this run's tail - head + 1, written by the tail below
   }
@@ -857,15 +865,23 @@ __global__ void coarse_emit_kernel(const unsigned long long* __restrict__ keys,
 }
 
 __global__ void coarse_counts_kernel(const int32_t* __restrict__ ids, int64_t n,
-                                     const unsigned long long* __restrict__ keys,
+                                     const unsigned long long* __restrict__ keys, uint64_t slots,
                                      int32_t* __restrict__ counts) {
   int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= n) return;
-  const bool head = (i == 0) || (keys[i] >> 3) != (keys[i - 1] >> 3);
+  const bool head = (i == 0) || keys[i] / slots != keys[i - 1] / slots;
   if (head) {
     const int32_t c = ids[i] - 1;
     counts[c] = counts[c] - static_cast<int32_t>(i) + 1;  // tail - head + 1
   }
+}
+
+// down[inverse[i] * F + slot[i]] = i (the table arrives filled with the absent value n)
+__global__ void factor_down_kernel(const int32_t* __restrict__ inverse, const uint8_t* __restrict__ slot, int64_t n,
+                                   int32_t slots, int32_t* __restrict__ down) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  down[static_cast<int64_t>(inverse[i]) * slots + slot[i]] = static_cast<int32_t>(i);
 }
 
 // parent_table[o, k] = inverse[table[o, k]] for present entries, n_low for absent ones
@@ -1361,15 +1377,18 @@ int hi3d_downsample_workspace(int64_t n, int64_t* bytes) {
   return HI3D_OK;
 }
 
-int hi3d_downsample_structure(const int32_t* coords, int64_t n, int32_t sx, int32_t sy, int32_t sz,
-                              int32_t batch_size, void* workspace, int64_t workspace_bytes, int32_t* low,
-                              int32_t* inverse, int32_t* counts, uint8_t* slot, int64_t* n_low, int32_t* status,
-                              void* stream_) {
-  hipStream_t stream = as_stream(stream_);
+// The coarse structure of a resampling by factor (fx, fy, fz) (workspace as
+// hi3d_downsample_workspace).
+static int resample_structure(const int32_t* coords, int64_t n, int32_t sx, int32_t sy, int32_t sz,
+                              int32_t batch_size, int32_t fx, int32_t fy, int32_t fz, void* workspace,
+                              int64_t workspace_bytes, int32_t* low, int32_t* inverse, int32_t* counts,
+                              uint8_t* slot, int64_t* n_low, int32_t* status, hipStream_t stream) {
   int64_t need = 0;
   int rc = hi3d_downsample_workspace(n, &need);
   if (rc != HI3D_OK) return rc;
   HI3D_REQUIRE(n_low != nullptr, "n_low_dev is NULL");
+  HI3D_REQUIRE(fx > 0 && fy > 0 && fz > 0 && static_cast<int64_t>(fx) * fy * fz <= 256,
+               "factors must be positive with a product of at most 256, got (%d, %d, %d)", fx, fy, fz);
   if (status) launch_fill<int32_t>(status, 1, 0, stream);
   if (n == 0) {
     launch_fill<int64_t>(n_low, 1, 0, stream);
@@ -1379,7 +1398,8 @@ int hi3d_downsample_structure(const int32_t* coords, int64_t n, int32_t sx, int3
   HI3D_REQUIRE(coords && low && inverse && counts && slot && workspace, "null pointer argument");
   HI3D_REQUIRE(workspace_bytes >= need, "workspace too small");
   HI3D_REQUIRE(sx > 0 && sy > 0 && sz > 0 && batch_size > 0, "spatial_shape and batch_size must be positive");
-  const int32_t hx = (sx + 1) / 2, hy = (sy + 1) / 2, hz = (sz + 1) / 2;
+  const Factor f{fx, fy, fz, (sx + fx - 1) / fx, (sy + fy - 1) / fy, (sz + fz - 1) / fz};
+  const uint64_t slots = static_cast<uint64_t>(fx) * fy * fz;
   Workspace ws(workspace, workspace_bytes);
   auto* k0 = ws.take<unsigned long long>(n);
   auto* k1 = ws.take<unsigned long long>(n);
@@ -1390,10 +1410,11 @@ int hi3d_downsample_structure(const int32_t* coords, int64_t n, int32_t sx, int3
   void* temp = ws.take<char>(temp_bytes);
   const unsigned blocks = static_cast<unsigned>(ceil_div(n, 256));
   const int4* c4 = reinterpret_cast<const int4*>(coords);
-  const uint64_t space = static_cast<uint64_t>(batch_size) * hx * hy * hz * 8;  // cells x slots
-  HI3D_REQUIRE(space < (uint64_t(1) << 62), "grid too large for 64-bit keys");
-  hipLaunchKernelGGL(half_keys_kernel, dim3(blocks), dim3(256), 0, stream, c4, n, batch_size, sx, sy, sz, hx, hy, hz,
-                     k0, r0, status);
+  const double space_d = static_cast<double>(batch_size) * f.hx * f.hy * f.hz * static_cast<double>(slots);
+  HI3D_REQUIRE(space_d < 4.0e18, "grid too large for 64-bit keys");
+  const uint64_t space = static_cast<uint64_t>(batch_size) * f.hx * f.hy * f.hz * slots;  // cells x slots
+  hipLaunchKernelGGL(factor_keys_kernel, dim3(blocks), dim3(256), 0, stream, c4, n, batch_size, sx, sy, sz, f, k0, r0,
+                     status);
   int end_bit = 1;
   while (end_bit < 64 && (1ull << end_bit) < space) ++end_bit;
   unsigned long long* ka = k0;
@@ -1403,11 +1424,43 @@ int hi3d_downsample_structure(const int32_t* coords, int64_t n, int32_t sx, int3
   HI3D_HIP_CHECK(radix::sort_pairs(temp, temp_bytes, ka, kalt, ra, ralt, n, 0, end_bit, stream));
   const unsigned long long* sk = ka;
   const int32_t* sr = ra;
-  hipLaunchKernelGGL(run_heads_kernel, dim3(blocks), dim3(256), 0, stream, sk, n, ids, status);
+  hipLaunchKernelGGL(run_heads_kernel, dim3(blocks), dim3(256), 0, stream, sk, n, slots, ids, status);
   HI3D_HIP_CHECK(radix::scan(temp, temp_bytes, ids, ids, n, true, stream));
-  hipLaunchKernelGGL(coarse_emit_kernel, dim3(blocks), dim3(256), 0, stream, sk, sr, ids, n, hx, hy, hz, c4,
+  hipLaunchKernelGGL(coarse_emit_kernel, dim3(blocks), dim3(256), 0, stream, sk, sr, ids, n, f,
                      reinterpret_cast<int4*>(low), inverse, counts, slot, n_low);
-  hipLaunchKernelGGL(coarse_counts_kernel, dim3(blocks), dim3(256), 0, stream, ids, n, sk, counts);
+  hipLaunchKernelGGL(coarse_counts_kernel, dim3(blocks), dim3(256), 0, stream, ids, n, sk, slots, counts);
+  HI3D_LAUNCH_CHECK();
+  return HI3D_OK;
+}
+
+int hi3d_downsample_structure(const int32_t* coords, int64_t n, int32_t sx, int32_t sy, int32_t sz,
+                              int32_t batch_size, void* workspace, int64_t workspace_bytes, int32_t* low,
+                              int32_t* inverse, int32_t* counts, uint8_t* slot, int64_t* n_low, int32_t* status,
+                              void* stream) {
+  return resample_structure(coords, n, sx, sy, sz, batch_size, 2, 2, 2, workspace, workspace_bytes, low, inverse,
+                            counts, slot, n_low, status, as_stream(stream));
+}
+
+int hi3d_resample_structure(const int32_t* coords, int64_t n, int32_t sx, int32_t sy, int32_t sz, int32_t batch_size,
+                            int32_t fx, int32_t fy, int32_t fz, void* workspace, int64_t workspace_bytes, int32_t* low,
+                            int32_t* inverse, int32_t* counts, uint8_t* slot, int64_t* n_low, int32_t* status,
+                            void* stream) {
+  return resample_structure(coords, n, sx, sy, sz, batch_size, fx, fy, fz, workspace, workspace_bytes, low, inverse,
+                            counts, slot, n_low, status, as_stream(stream));
+}
+
+int hi3d_resample_down_table(const int32_t* inverse, const uint8_t* slot, int64_t n, int64_t n_low, int32_t slots,
+                             int32_t* down, void* stream_) {
+  hipStream_t stream = as_stream(stream_);
+  HI3D_REQUIRE(n >= 0 && n_low >= 0 && slots >= 1 && slots <= 256, "bad sizes");
+  if (n_low == 0) return HI3D_OK;
+  HI3D_REQUIRE(down != nullptr, "null pointer argument");
+  launch_fill<int32_t>(down, n_low * slots, static_cast<int32_t>(n), stream);
+  if (n > 0) {
+    HI3D_REQUIRE(inverse && slot, "null pointer argument");
+    hipLaunchKernelGGL(factor_down_kernel, dim3(static_cast<unsigned>(ceil_div(n, 256))), dim3(256), 0, stream,
+                       inverse, slot, n, slots, down);
+  }
   HI3D_LAUNCH_CHECK();
   return HI3D_OK;
 }

@@ -40,6 +40,9 @@ _SIGNATURES = {
     "hi3d_downsample_workspace": [_i64, _p],
     "hi3d_downsample_structure": [_p, _i64, _i32, _i32, _i32, _i32, _p, _i64, _p, _p, _p, _p, _p, _p, _p],
     "hi3d_stride2_tables": [_p, _p, _i64, _i64, _p, _p, _p],
+    "hi3d_resample_structure": [_p, _i64, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p, _i64, _p, _p, _p, _p, _p, _p,
+                                _p],
+    "hi3d_resample_down_table": [_p, _p, _i64, _i64, _i32, _p, _p],
     "hi3d_child_table_workspace": [_i64, _p],
     "hi3d_child_neighbour_table": [_p, _p, _i64, _p, _i64, _p, _p, _p, _p, _p],
     "hi3d_conv_tile_rows": [],

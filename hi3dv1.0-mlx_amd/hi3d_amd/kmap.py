@@ -533,6 +533,59 @@ def stride2_structure(indices: torch.Tensor, spatial_shape: Sequence[int], batch
     return Stride2Structure(low, inverse, counts, slot, down, up, coords, [sx, sy, sz], out_shape)
 
 
+@dataclass
+class ResampleStructure:
+    """Coarse set of a downsampling by any per-axis factor and its mean-pool table."""
+
+    low: torch.Tensor  # [Nc, 4] int32 (batch, x // fx, y // fy, z // fz), lexicographic
+    inverse: torch.Tensor  # [Nf] int32
+    counts: torch.Tensor  # [Nc] int32
+    slot: torch.Tensor  # [Nf] uint8: ((x % fx) fy + y % fy) fz + z % fz
+    down: torch.Tensor  # [Nc, fx fy fz] fine row per slot (sentinel Nf)
+    factor: tuple[int, int, int]
+
+
+def resample_structure(indices: torch.Tensor, spatial_shape: Sequence[int], factor: Sequence[int],
+                       batch_size: int | None = None) -> ResampleStructure:
+    """Coarse set of ``indices [N, 4]`` downsampled by ``factor`` (one positive value per
+    axis, product at most 256): the coordinates divided by the factor, sorted unique in
+    lexicographic ``(batch, x, y, z)`` order (src/sparc3d/nn/sparse/spatial.py:36-72),
+    each fine row's parent and slot, and the ``[Nc, fx fy fz]`` table of the mean pool.
+    Raises ``ValueError`` for coordinates outside ``spatial_shape`` / ``batch_size`` and
+    for repeated coordinates."""
+    coords = _as_coords(indices)
+    device = _lib.require_gpu(coords)
+    fx, fy, fz = (int(v) for v in factor)
+    if min(fx, fy, fz) <= 0 or fx * fy * fz > 256:
+        raise ValueError(f"factors must be positive with a product of at most 256, got {(fx, fy, fz)}")
+    n = int(coords.shape[0])
+    sx, sy, sz = (int(v) for v in spatial_shape)
+    if batch_size is None:
+        batch_size = int(coords[:, 0].max()) + 1 if n else 1
+    low = torch.empty((max(n, 1), 4), dtype=torch.int32, device=device)
+    inverse = torch.empty(n, dtype=torch.int32, device=device)
+    counts = torch.empty(max(n, 1), dtype=torch.int32, device=device)
+    slot = torch.empty(n, dtype=torch.uint8, device=device)
+    n_low_t = torch.empty(2, dtype=torch.int64, device=device)  # coarse row count, then the status word
+    ws = _lib.workspace(_lib.query("hi3d_downsample_workspace", n), device)
+    stream = _lib.stream(device)
+    _lib.call(
+        "hi3d_resample_structure",
+        _lib.ptr(coords), n, sx, sy, sz, int(batch_size), fx, fy, fz, _lib.ptr(ws), ws.numel(), _lib.ptr(low),
+        _lib.ptr(inverse), _lib.ptr(counts), _lib.ptr(slot), _lib.ptr(n_low_t), _lib.ptr(n_low_t[1:]), stream,
+    )
+    n_low, flags = (int(v) for v in n_low_t.tolist())
+    flags &= 0xFFFFFFFF
+    if flags & _lib.MAP_RANGE:
+        raise ValueError(f"coordinates outside spatial_shape {[sx, sy, sz]} or batch {batch_size}")
+    if flags & _lib.MAP_DUPLICATE:
+        raise ValueError("duplicate coordinates: every active voxel must appear once")
+    slots = fx * fy * fz
+    down = torch.empty((n_low, slots), dtype=torch.int32, device=device)
+    _lib.call("hi3d_resample_down_table", _lib.ptr(inverse), _lib.ptr(slot), n, n_low, slots, _lib.ptr(down), stream)
+    return ResampleStructure(low[:n_low], inverse, counts[:n_low], slot, down, (fx, fy, fz))
+
+
 def downsample_structure(coords: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """``(low [Nc, 3], inverse [N], counts [Nc])``: unique ``coords // 2`` in
     lexicographic ``(x, y, z)`` order, each row's parent, and children per parent."""

@@ -244,8 +244,9 @@ def _cache_keys(factor: tuple[int, ...]) -> tuple[str, str, str]:
 
 
 class SparseDownsample(nn.Module):
-    """Mean of the rows that share a coarse cell (factor 2 per axis on the GPU); the
-    fine rows' coordinates, layout and parents are kept for the paired upsample."""
+    """Mean of the rows that share a coarse cell (any positive factor per axis, product at
+    most 256); the fine rows' coordinates, layout and parents are kept for the paired
+    upsample."""
 
     def __init__(self, factor: int | Sequence[int]):
         super().__init__()
@@ -253,17 +254,16 @@ class SparseDownsample(nn.Module):
 
     def forward(self, input: SparseTensor) -> SparseTensor:
         factor = _factor_tuple(self.factor, input.coords.shape[-1] - 1)
-        if factor != (2, 2, 2):
-            raise NotImplementedError("the GPU downsample implements factor 2")
         fine = input.coords
         extent = [hi + 1 for hi in _kmap.column_bounds(fine)[1][1:]]
-        structure = _kmap.stride2_structure(fine, extent)
+        structure = _kmap.resample_structure(fine, extent, factor)
         feats = input.feats.contiguous()
         device = _lib.require_gpu(feats)
-        pooled = torch.empty((structure.n_coarse, feats.shape[1]), dtype=feats.dtype, device=device)
+        n_coarse, slots = int(structure.down.shape[0]), int(structure.down.shape[1])
+        pooled = torch.empty((n_coarse, feats.shape[1]), dtype=feats.dtype, device=device)
         _lib.call(
             "hi3d_gather_mean",
-            _lib.ptr(feats), structure.n_fine, int(feats.shape[1]), _lib.ptr(structure.down), 8, structure.n_coarse, 1,
+            _lib.ptr(feats), int(fine.shape[0]), int(feats.shape[1]), _lib.ptr(structure.down), slots, n_coarse, 1,
             _lib.DTYPES[feats.dtype], _lib.ptr(pooled), _lib.stream(device),
         )
         coarse = SparseTensor(

@@ -166,6 +166,26 @@ int hi3d_downsample_structure(const int32_t* coords_dev, int64_t n, int32_t sx, 
 int hi3d_stride2_tables(const int32_t* inverse_dev, const uint8_t* slot_dev, int64_t n,
                         int64_t n_low, int32_t* down_dev, int32_t* up_dev, void* stream);
 
+/* The coarse structure of a downsampling by (fx, fy, fz) per axis (fx fy fz <= 256), as
+ * hi3d_downsample_structure (which is this with factor 2, 2, 2; same workspace): coarse
+ * coordinates (b, x / fx, y / fy, z / fz) in lexicographic order, inverse, counts, and
+ * each fine row's slot ((x % fx) fy + y % fy) fz + z % fz.
+ * Replaces: SparseDownsample's unique of the divided coordinates
+ * (src/sparc3d/nn/sparse/spatial.py:36-50,64-72). */
+int hi3d_resample_structure(const int32_t* coords_dev, int64_t n, int32_t sx, int32_t sy, int32_t sz,
+                            int32_t batch_size, int32_t fx, int32_t fy, int32_t fz, void* workspace_dev,
+                            int64_t workspace_bytes, int32_t* low_dev, int32_t* inverse_dev,
+                            int32_t* counts_dev, uint8_t* slot_dev, int64_t* n_low_dev,
+                            int32_t* status_dev, void* stream);
+
+/* down_dev [n_low, slots]: the fine row in each slot of each coarse cell (sentinel n),
+ * from hi3d_resample_structure's inverse and slot; the gather table of the mean pool
+ * (hi3d_gather_mean with kvol = slots, extra = 1).
+ * Replaces: SparseDownsample's scatter_reduce(mean) index
+ * (src/sparc3d/nn/sparse/spatial.py:51-62). */
+int hi3d_resample_down_table(const int32_t* inverse_dev, const uint8_t* slot_dev, int64_t n, int64_t n_low,
+                             int32_t slots, int32_t* down_dev, void* stream);
+
 /* Whether hi3d_stride2_up_conv takes this shape (1) or not (0): F16 / BF16, cin 64 or
  * 128, cout 64. */
 int hi3d_stride2_up_supported(int32_t cin, int32_t cout, int32_t dtype);

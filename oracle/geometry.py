@@ -51,3 +51,21 @@ def up_conv_f64(h_low, full_table, inverse, weight, bias):
     idx = up_conv_index(full_table, inverse, h.shape[0])
     y = proj[idx].sum(axis=1)
     return y if bias is None else y + np.asarray(bias, np.float64)
+
+
+def sparse_downsample(indices, feats, factor):
+    """``SparseDownsample(factor).forward`` in float64 (src/sparc3d/nn/sparse/spatial.py:
+    34-79): the coordinates divided per axis, packed with offsets from the cumulative
+    product of the divided extents (batch most significant), ``unique`` with inverse,
+    the features' mean per coarse row onto zeros (``scatter_reduce(mean)`` with the zero
+    included: the sum over count + 1), the coarse coordinates unpacked. Returns
+    ``(coords [Nc, 4], feats [Nc, C], inverse [N])``."""
+    c = np.asarray(indices, np.int64)
+    cols = [c[:, 0]] + [c[:, a + 1] // int(f) for a, f in enumerate(factor)]
+    extents = [int(col.max()) + 1 for col in cols[1:]]
+    offsets = list(np.cumprod(extents[::-1])[::-1]) + [1]
+    codes = sum(col * int(off) for col, off in zip(cols, offsets))
+    unique, inverse = np.unique(codes, return_inverse=True)
+    inverse = inverse.reshape(-1)
+    low = np.stack([unique // offsets[0]] + [(unique // offsets[a + 1]) % extents[a] for a in range(3)], 1)
+    return low.astype(np.int32), downsample_f64(feats, inverse, len(unique)), inverse

@@ -153,3 +153,35 @@ def test_mlx_shaped_sparse_conv(cuda, dtype):
         b64 = None if bias is None else bias.double().cpu().numpy()
         ref = _dense_reference(indices, f64, w64, b64, 18)
         assert oconv.rel_err(y.double().cpu().numpy(), ref) <= gate
+
+
+@pytest.mark.parametrize("factor", [2, (3, 3, 3), (2, 3, 4), (1, 1, 1), (4, 1, 2)])
+def test_nn_sparse_downsample_any_factor(cuda, factor):
+    """``SparseDownsample(factor)`` for any per-axis factor against the oracle's
+    restatement of the reference (src/sparc3d/nn/sparse/spatial.py:34-79): coarse
+    coordinates in the reference's order, the mean over each cell's rows and one zero,
+    the scale, and the paired ``SparseUpsample`` restoring the fine rows and copying each
+    parent's row to its children; two batch elements, fp16 and fp32 features."""
+    from oracle import geometry as ogeo
+    from hi3d_amd.nn import SparseDownsample, SparseTensor, SparseUpsample
+
+    f3 = (factor,) * 3 if isinstance(factor, int) else factor
+    rng = np.random.default_rng(sum(f3) + 11)
+    parts = []
+    for b in range(2):
+        xyz = np.argwhere(rng.random((13, 11, 12)) < 0.15)
+        parts.append(np.concatenate([np.full((len(xyz), 1), b), xyz[rng.permutation(len(xyz))]], 1))
+    idx = np.concatenate(parts).astype(np.int32)
+    for dtype, tol in ((torch.float32, 1e-6), (torch.float16, 2e-3)):
+        x = rng.standard_normal((len(idx), 24)).astype(np.float32)
+        st = SparseTensor(torch.as_tensor(x).to(dtype).to(cuda), torch.as_tensor(idx).to(cuda))
+        coarse = SparseDownsample(factor)(st)
+        low, pooled, inverse = ogeo.sparse_downsample(idx, torch.as_tensor(x).to(dtype).double().numpy(), f3)
+        assert np.array_equal(coarse.coords.cpu().numpy(), low)
+        np.testing.assert_allclose(coarse.feats.double().cpu().numpy(), pooled, rtol=tol, atol=tol)
+        assert coarse.scale == f3
+        fine = SparseUpsample(factor)(coarse)
+        assert torch.equal(fine.coords, st.coords) and fine.scale == (1, 1, 1)
+        assert torch.equal(fine.feats, coarse.feats[torch.as_tensor(inverse, device=cuda)])
+    with pytest.raises(ValueError, match="factor"):
+        SparseDownsample((2, 2))(st)

@@ -33,6 +33,7 @@ Pinning map (oracle function -> checks here):
                                          moments, u / (1 + exp(-u)), element-wise block
   vae.conv_gn_swish_f64 / resnet_f64 / occupancy_f64 -> per-group GroupNorm + dense
                                          F.conv3d(padding=1) over the scattered grid
+  geometry.sparse_downsample          -> dictionary grouping by divided coordinates
   vae.children_f64 / child_coords / upsample_f64 -> s*I slot weights, per-child products,
                                          SerializedUnpooling's masked view, inv_grid_coord,
                                          brute-force child table
@@ -767,6 +768,29 @@ def test_vae_child_coords_match_unpooling_grid():
     parent = rng.integers(0, 20, 40)
     slot = rng.integers(0, 8, 40)
     assert np.array_equal(ovae.child_coords(coords, parent, slot), coords[parent] * 2 + inv_grid[slot])
+
+
+@pytest.mark.parametrize("factor", [(2, 2, 2), (3, 3, 3), (2, 3, 4), (1, 1, 1), (5, 1, 2)])
+def test_sparse_downsample_oracle_against_grouping(factor):
+    """sparse_downsample against a dictionary grouping of the rows by
+    ``(b, x // fx, y // fy, z // fz)``: coarse rows in sorted order, each one's mean over
+    its rows and one extra zero, every fine row's parent; two batch elements."""
+    from oracle import geometry as ogeo
+
+    rng = np.random.default_rng(sum(factor))
+    idx = _rand_indices(rng, 9, 0.2, batch=2)
+    idx = idx[rng.permutation(len(idx))]
+    x = rng.normal(size=(len(idx), 5))
+    low, pooled, inverse = ogeo.sparse_downsample(idx, x, factor)
+    groups = {}
+    for i, (b, px, py, pz) in enumerate(idx.tolist()):
+        groups.setdefault((b, px // factor[0], py // factor[1], pz // factor[2]), []).append(i)
+    keys = sorted(groups)
+    assert low.tolist() == [list(k) for k in keys]
+    for c, k in enumerate(keys):
+        rows = groups[k]
+        assert np.allclose(pooled[c], x[rows].sum(0) / (len(rows) + 1), rtol=1e-13, atol=1e-13)
+        assert all(inverse[r] == c for r in rows)
 
 
 def test_unique_oracle_against_numpy_and_torch():
