@@ -103,6 +103,22 @@ def test_c_argument_validation_without_launch():
     assert lib.hi3d_gather_conv_narrow(null, 0, 64, null, null, 8, 27, null, null, null, 0, null, 0, _lib.F16, null,
                                        null) == 0
     assert lib.hi3d_w8a8_quantize(null, 0, 64, null, null, null, null) == 0
+    # resampling factors: positive, product at most 256 (checked before any launch)
+    fake = ctypes.c_void_p(16)
+    for f in ((0, 2, 2), (2, -1, 2), (8, 8, 8)):
+        rc = lib.hi3d_resample_structure(null, 10, 8, 8, 8, 1, *f, null, 0, null, null, null, null, fake, null, null)
+        assert rc == _lib.ERR_INVALID and "factors" in _lib.last_error()
+    rc = lib.hi3d_resample_down_table(null, null, 10, 4, 257, null, null)
+    assert rc == _lib.ERR_INVALID
+    # the sorted transposed conv refuses what the row-order one refuses; its plan checks the window
+    rc = lib.hi3d_stride2_up_conv_sorted(null, 10, 256, null, null, 64, null, null, 30, _lib.F16, null, null)
+    assert rc == _lib.ERR_INVALID and "cin 64 or 128" in _lib.last_error()
+    rc = lib.hi3d_stride2_up_plan(fake, 10, 30, 40, null, 0, null, null, null)
+    assert rc == _lib.ERR_INVALID and "window_log2" in _lib.last_error()
+    assert lib.hi3d_stride2_up_tile_rows() == 32
+    # the LayerNorm + activation entry: unknown activation
+    rc = lib.hi3d_layer_norm_act(fake, 4, 8, 1e-6, null, null, null, null, 7, fake, null)
+    assert rc == _lib.ERR_INVALID and "activation" in _lib.last_error()
 
 
 def test_python_validation_matches_reference_errors():
