@@ -287,16 +287,16 @@ __global__ __launch_bounds__(256) void probe_kernel(const int4* __restrict__ coo
 
 // ------------------------------------------------------------- brick hash --
 // The map build's hash (hi3d_kmap_subm): one bucket per occupied 2x2x2 brick, open
-// addressing with linear probing over buckets. A bucket is its brick key (keys[]), an
-// 8-bit occupancy mask (masks[]) and the rows of its 8 cells (rows[8 h ..], valid where
-// the mask bit is set, so only keys and masks are cleared per build). A row's 26
-// neighbours lie in 8 bricks, so every lookup reads one bucket (longer probes are rare at
-// the default capacity of one bucket per voxel) and neighbouring rows read the same ones.
+// addressing with linear probing over buckets. A bucket is one 64-bit word, the brick
+// key shifted left by 8 with the occupancy mask of its 8 cells in the low byte, plus the
+// rows of its 8 cells (rows[8 h ..], valid where the mask bit is set, so only the words
+// are cleared per build). A row's 26 neighbours lie in 8 bricks; a lookup reads one word
+// (longer probes are rare at the default capacity of one bucket per voxel) and, for a
+// present neighbour only, its row. Brick keys must stay below 2^56 - 1.
 constexpr unsigned long long kEmptyBrick = ~0ull;
 
 struct BrickTable {
-  unsigned long long* keys;
-  uint32_t* masks;
+  unsigned long long* words;  // key << 8 | mask, kEmptyBrick when free
   int32_t* rows;
   uint64_t mask;
 };
@@ -320,12 +320,12 @@ __global__ void brick_insert_kernel(const int4* __restrict__ coords, int64_t n, 
   const unsigned long long bk = g.brick(c.x, c.y, c.z, c.w);
   uint64_t h = mix64(bk) & t.mask;
   for (uint64_t probe = 0; probe <= t.mask; ++probe) {
-    const unsigned long long prev = atomicCAS(&t.keys[h], kEmptyBrick, bk);
-    if (prev == kEmptyBrick || prev == bk) {
+    const unsigned long long prev = atomicCAS(&t.words[h], kEmptyBrick, bk << 8);
+    if (prev == kEmptyBrick || (prev >> 8) == bk) {
       const int cn = g.corner(c.y, c.z, c.w);
       t.rows[h * 8 + cn] = static_cast<int32_t>(i);
-      const uint32_t old = atomicOr(&t.masks[h], 1u << cn);
-      if (old & (1u << cn)) atomicOr(status, HI3D_MAP_DUPLICATE);
+      const unsigned long long old = atomicOr(&t.words[h], 1ull << cn);
+      if (old & (1ull << cn)) atomicOr(status, HI3D_MAP_DUPLICATE);
       return;
     }
     h = (h + 1) & t.mask;
@@ -336,9 +336,9 @@ __global__ void brick_insert_kernel(const int4* __restrict__ coords, int64_t n, 
 // bucket of brick bk from slot h on (h's key already known to differ), or -1
 __device__ __forceinline__ int64_t brick_find(const BrickTable& t, uint64_t h, unsigned long long bk) {
   for (uint64_t probe = 0; probe <= t.mask; ++probe) {
-    const unsigned long long k = t.keys[h];
-    if (k == bk) return static_cast<int64_t>(h);
-    if (k == kEmptyBrick) return -1;
+    const unsigned long long w = t.words[h];
+    if (w == kEmptyBrick) return -1;
+    if ((w >> 8) == bk) return static_cast<int64_t>(h);
     h = (h + 1) & t.mask;
   }
   return -1;
@@ -402,23 +402,26 @@ __global__ __launch_bounds__(256) void brick_probe_kernel(const int4* __restrict
       }
     }
 #pragma unroll
-    for (int u = 0; u < kProbeBatch; ++u) kv[u] = look[u] ? t.keys[h[u]] : kEmptyBrick;
+    for (int u = 0; u < kProbeBatch; ++u) kv[u] = look[u] ? t.words[h[u]] : kEmptyBrick;
     int64_t hb[kProbeBatch];
+    uint32_t m[kProbeBatch];
 #pragma unroll
     for (int u = 0; u < kProbeBatch; ++u) {
       hb[u] = -1;
-      if (look[u]) {
-        if (kv[u] == bk[u]) hb[u] = static_cast<int64_t>(h[u]);
-        else if (kv[u] != kEmptyBrick) hb[u] = brick_find(t, (h[u] + 1) & t.mask, bk[u]);
+      m[u] = 0u;
+      if (look[u] && kv[u] != kEmptyBrick) {
+        if ((kv[u] >> 8) == bk[u]) {
+          hb[u] = static_cast<int64_t>(h[u]);
+          m[u] = static_cast<uint32_t>(kv[u] & 0xFFu);
+        } else {
+          hb[u] = brick_find(t, (h[u] + 1) & t.mask, bk[u]);
+          if (hb[u] >= 0) m[u] = static_cast<uint32_t>(t.words[hb[u]] & 0xFFu);
+        }
       }
     }
-    uint32_t m[kProbeBatch];
     int32_t rv[kProbeBatch];
 #pragma unroll
-    for (int u = 0; u < kProbeBatch; ++u) {
-      m[u] = hb[u] >= 0 ? t.masks[hb[u]] : 0u;
-      rv[u] = hb[u] >= 0 ? t.rows[hb[u] * 8 + cn[u]] : absent;
-    }
+    for (int u = 0; u < kProbeBatch; ++u) rv[u] = ((m[u] >> cn[u]) & 1u) ? t.rows[hb[u] * 8 + cn[u]] : absent;
 #pragma unroll
     for (int u = 0; u < kProbeBatch; ++u) {
       const int j = base + u * blockDim.x;
@@ -426,7 +429,7 @@ __global__ __launch_bounds__(256) void brick_probe_kernel(const int4* __restrict
       const int r = j / kvol;
       const int k = j - r * kvol;
       const int32_t o = so[r];
-      const int32_t found = k == center ? o : ((m[u] >> cn[u]) & 1u) ? rv[u] : absent;
+      const int32_t found = k == center ? o : rv[u];
       nbr[static_cast<int64_t>(o) * kvol + k] = found;
       if (found != absent) atomicAdd(&cnt[k], 1);
     }
@@ -1057,10 +1060,8 @@ static int64_t hash_order_bytes(int64_t n) {
   return 4 * align_up(std::max<int64_t>(n, 1) * 4, 256) + radix::temp_bytes(std::max<int64_t>(n, 1));
 }
 
-// Bytes of a brick table of `cap` buckets: keys, masks, then 8 rows per bucket.
-static int64_t brick_table_bytes(int64_t cap) {
-  return align_up(cap * 8, 256) + align_up(cap * 4, 256) + align_up(cap * 32, 256);
-}
+// Bytes of a brick table of `cap` buckets: key | mask words, then 8 rows per bucket.
+static int64_t brick_table_bytes(int64_t cap) { return align_up(cap * 8, 256) + align_up(cap * 32, 256); }
 
 // Brick tables above this size are built and probed in cell order (below it the table
 // stays in the last-level cache and the sort costs more than it saves).
@@ -1123,9 +1124,8 @@ static int kmap_subm_hash(const int32_t* coords, int64_t n, Grid g, int32_t ksiz
 static int kmap_subm_brick(const int32_t* coords, int64_t n, Grid g, int32_t ksize, int64_t cap, char* ws,
                            int32_t* nbr, int32_t* counts, int32_t* status, hipStream_t stream) {
   BrickTable t;
-  t.keys = reinterpret_cast<unsigned long long*>(ws);
-  t.masks = reinterpret_cast<uint32_t*>(ws + align_up(cap * 8, 256));
-  t.rows = reinterpret_cast<int32_t*>(ws + align_up(cap * 8, 256) + align_up(cap * 4, 256));
+  t.words = reinterpret_cast<unsigned long long*>(ws);
+  t.rows = reinterpret_cast<int32_t*>(ws + align_up(cap * 8, 256));
   t.mask = static_cast<uint64_t>(cap - 1);
   char* order = ws + brick_table_bytes(cap);
   const unsigned blocks = static_cast<unsigned>(ceil_div(n, 256));
@@ -1152,8 +1152,7 @@ static int kmap_subm_brick(const int32_t* coords, int64_t n, Grid g, int32_t ksi
     per = static_cast<int>(ceil_div(probe_blocks, kXcds));
     probe_blocks = static_cast<int64_t>(per) * kXcds;
   }
-  launch_fill<unsigned long long>(t.keys, cap, kEmptyBrick, stream);
-  launch_fill<uint32_t>(t.masks, cap, 0u, stream);
+  launch_fill<unsigned long long>(t.words, cap, kEmptyBrick, stream);
   hipLaunchKernelGGL(brick_insert_kernel, dim3(blocks), dim3(256), 0, stream, c4, n, g, perm, t, status);
   // (one row per thread, its 8 buckets' keys, masks and rows in registers, measured
   // slower on the config-5 shells: 1.74 against 1.60 ms for the whole build)
@@ -1172,6 +1171,8 @@ int hi3d_kmap_subm(const int32_t* coords, int64_t n, int32_t sx, int32_t sy, int
   if (rc != HI3D_OK || n == 0) return rc;
   HI3D_REQUIRE(workspace != nullptr, "null pointer argument");
   const int64_t cap = capacity > 0 ? capacity : brick_capacity(n);
+  const double bricks = static_cast<double>(batch_size) * ((sx + 1) / 2) * ((sy + 1) / 2) * ((sz + 1) / 2);
+  HI3D_REQUIRE(bricks < 7.2e16, "grid of %.3g 2x2x2 bricks exceeds the hash's 2^56 brick keys", bricks);
   int64_t need = 0;
   rc = hi3d_kmap_workspace(n, cap, 1, &need);
   if (rc != HI3D_OK) return rc;

@@ -63,8 +63,8 @@ int hi3d_kmap_workspace(int64_t n, int64_t capacity, int32_t key64, int64_t* byt
 
 /* Submanifold kernel map through a brick hash: every voxel claims (one 64-bit CAS) the
  * bucket of its 2x2x2 brick, keyed by the brick's packed coordinates (as
- * ((b*sx + x)*sy + y)*sz + z over the halved extents; open addressing, linear probing
- * over buckets), and sets its corner's bit and row; the ksize^3 neighbourhood of each
+ * ((b*sx + x)*sy + y)*sz + z over the halved extents, below 2^56; open addressing, linear
+ * probing over buckets), and sets its corner's bit (in the key's word) and row; the ksize^3 neighbourhood of each
  * voxel is then read bucket by bucket, writing the dense neighbour table
  * nbr_dev [n, ksize^3] (sentinel n) and per-offset non-sentinel counts counts_dev
  * [ksize^3]. Neighbours outside [0, spatial_shape) are absent. Large tables are built
