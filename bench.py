@@ -14,7 +14,8 @@ searchsorted map, per-offset gather / matmul / index_add_, LayerNorm) on the hos
 for a sample of output rows. ``extra`` reports the other workloads: the fp32 sphere
 shell and the C128 shells (with kernel-map builds through the dense grid and the
 hash), the strided pair, W8A8 int8 TOPS (GEMM alone and quantise + GEMM), the VAE
-blocks, octree upsampling, transformer I/O resampling and unique cube corners, with
+blocks, octree upsampling, transformer I/O resampling, unique cube corners and the
+kernel-map builds of the 1024^3 and 256^3 shells (dense grid and brick hash), with
 CPU baselines of the fp32 shell (in full) and of W8A8 (sampled tokens).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only a,b] [--quick] [--no-cpu]
@@ -554,6 +555,38 @@ def bench_unique(steps: int, warmup: int):
     }
 
 
+def bench_kmap(steps: int, warmup: int):
+    """Submanifold 3x3x3 kernel-map builds on the 1024^3 residual-block shells and the
+    256^3 C128 shells: the dense grid (kept between builds, the default; and cleared
+    inside each build) and the brick hash, each checked equal to the dense table."""
+    import torch
+
+    from hi3d_amd import kmap
+
+    dev = torch.device("cuda:0")
+    out = {}
+    for name, grid in (("resblock_c256_fp16", 1024), ("subm3_c128_fp16", 256)):
+        coords = torch.as_tensor(coords_of(name, dev)).to(dev)
+        ref = kmap.build_kernel_map(coords, [grid] * 3, 1).table
+        dense = lambda: kmap.build_kernel_map(coords, [grid] * 3, 1, check=False)
+        brick = lambda: kmap.build_kernel_map(coords, [grid] * 3, 1, capacity=0, check=False)
+        _, dense_ms = timed(dense, steps, warmup)
+        _, fresh_ms = timed(dense_fresh(dense), steps, warmup)
+        _, hash_ms = timed(brick, steps, warmup)
+        n = int(coords.shape[0])
+        out[name] = {
+            "grid": grid,
+            "voxels": n,
+            "dense_ms": dense_ms,
+            "dense_fresh_ms": fresh_ms,
+            "brick_hash_ms": hash_ms,
+            "brick_hash_voxels_per_s": n / (hash_ms * 1e-3),
+            "hash_equal": bool(torch.equal(brick().table, ref)),
+            "dense_fresh_equal": bool(torch.equal(dense_fresh(dense)().table, ref)),
+        }
+    return out
+
+
 def cpu_threads() -> int:
     """Host threads for the CPU baselines: the process's CPU share (``OMP_NUM_THREADS``
     when the launcher sets it, as GPU hosts that split their cores per GPU do), else
@@ -603,7 +636,7 @@ def cpu_baseline_w8a8(rows: int):
 
 
 WORKLOADS = ("resblock", "subm3_c128_fp16", "subm3_c64_fp32", "stride2", "w8a8", "vae_resnet", "vae_upsample",
-             "transformer_io", "resblock3d", "unique")
+             "transformer_io", "resblock3d", "unique", "kmap")
 
 
 def main() -> int:
@@ -688,6 +721,9 @@ def main() -> int:
         elif name == "unique":
             log("unique cube corners of the 1024^3 shells")
             extra["unique_corners_1024"] = bench_unique(max(5, args.steps // 10), 2)
+        elif name == "kmap":
+            log("submanifold kernel-map builds (dense grid, brick hash), 1024^3 and 256^3 shells")
+            extra["kmap_subm3"] = bench_kmap(max(10, args.steps // 2), 3)
     if head is None:  # a partial run (profiling): the workloads' own figures only
         print(json.dumps({"partial": selected, "extra": extra}), flush=True)
         return 0
