@@ -264,6 +264,29 @@ def bench_w8a8(steps: int, warmup: int):
                 "quant_ms": q_ev, "quant_gbs": (2 * m * k + m * k + 4 * m) / (q_ev * 1e-3) / 1e9,
                 "e2e_ms": e_wall, "e2e_tops": ops / (e_wall * 1e-3) / 1e12,
             }
+        if tag == "A":
+            # shape A as the transformer block feeds it (mlp.0 after the modulated norm):
+            # norm, quantiser and GEMM in sequence against the norm fused with the
+            # quantiser, then the GEMM
+            from hi3d_amd import kernels
+
+            scale = (1 + 0.2 * torch.randn(k, device=dev, generator=g)).half()
+            shift = (0.2 * torch.randn(k, device=dev, generator=g)).half()
+            wq, sw = w8a8.quantize_weight(wf)
+            _, ln_ev = timed(lambda: kernels.layer_norm_modulate(x, 1e-6, scale=scale, shift=shift), steps, warmup)
+            _, nq_ev = timed(lambda: w8a8.norm_quantize(x, 1e-6, scale=scale, shift=shift), steps, warmup)
+            seq_wall, _ = timed(lambda: w8a8.linear(kernels.layer_norm_modulate(x, 1e-6, scale=scale, shift=shift),
+                                                    wq, sw, bias), steps, warmup)
+            fused_wall, _ = timed(lambda: w8a8.norm_linear(x, 1e-6, wq, sw, bias, scale=scale, shift=shift), steps,
+                                  warmup)
+            ops = 2.0 * m * n * k
+            res["A_norm_h64"] = {
+                "m": m, "k": k, "n": n,
+                "norm_ms": ln_ev,
+                "norm_quant_ms": nq_ev, "norm_quant_gbs": (2 * m * k + m * k + 4 * m) / (nq_ev * 1e-3) / 1e9,
+                "norm_then_linear_ms": seq_wall, "norm_linear_fused_ms": fused_wall,
+                "fused_e2e_tops": ops / (fused_wall * 1e-3) / 1e12,
+            }
     return res
 
 

@@ -7,6 +7,7 @@
 
 #include "common.h"
 #include "conv_tile.h"
+#include "quant.h"
 
 namespace hi3d {
 namespace {
@@ -19,25 +20,12 @@ namespace {
 // order, the same order as the reference's lane shuffles (bits 0..4) followed by its
 // u/v combine (bit 5):  pair (L, H) differing in bit d -> (L + H, L - H).
 // Bits 0..3 live in registers, bits 4 and 5 are lane bits 0 and 1 (quad DPP moves).
-// The reference scales the last stage by 1/8; here the values stay unscaled (8x theirs,
-// exactly: scaling by a power of two commutes with rounding away from the subnormal
-// range) and the 1/8 moves into the scale: s = fl(max(8 max|v|, 8e-8) / 127) / 8 is
-// the reference's s, and v / (8 s) is the reference's quotient, the same real number.
-// Quantisation divides with the compiler's own correctly rounded f32 division
-// sequence, its reciprocal refinement hoisted per row (t = 8 s, r = rcp(t) refined):
-//   q = v r, e = v - t q, q1 = q + e r, e1 = v - t q1, v / t = q1 + e1 r   (fma each)
-// The division's pre-scaling (v_div_scale) and fix-up only act when the quotient is
-// below 2^-126 or v below 2^-103 (t is at least 8e-8 / 127 and |v| / t at most 127),
-// where both round to 0; rows with a non-finite scale use the full division.
+// The reference scales the last stage by 1/8; here the values stay unscaled (8x theirs)
+// and the 1/8 moves into the scale (quant_divisor). Quantisation divides with the
+// compiler's own correctly rounded f32 division sequence, its reciprocal refinement
+// hoisted per row (quant_div); rows with a non-finite scale use the full division.
 // The multipliers (signs) sit in LDS, loaded once per workgroup.
 constexpr int kQuantCols = 1024;  // columns per pass
-
-__device__ __forceinline__ float dpp_xor1(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xB1, 0xF, 0xF, true));
-}
-__device__ __forceinline__ float dpp_xor2(float v) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4E, 0xF, 0xF, true));
-}
 
 template <int NP, bool kRotate, bool kFull>
 __global__ __launch_bounds__(256) void quant_kernel(const _Float16* __restrict__ x, int64_t m, int k,
@@ -108,12 +96,7 @@ __global__ __launch_bounds__(256) void quant_kernel(const _Float16* __restrict__
   auto store_pass = [&](int8_t* qr, int p, float (&v)[16], float t, float r, bool fast) {
     if (fast) {
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const float a = v[e];
-        const float q0 = a * r;
-        const float q1 = __builtin_fmaf(__builtin_fmaf(-t, q0, a), r, q0);
-        v[e] = __builtin_fmaf(__builtin_fmaf(-t, q1, a), r, q1);
-      }
+      for (int e = 0; e < 16; ++e) v[e] = quant_div(v[e], t, r);
     } else {
 #pragma unroll
       for (int e = 0; e < 16; ++e) v[e] = v[e] / t;
@@ -121,15 +104,7 @@ __global__ __launch_bounds__(256) void quant_kernel(const _Float16* __restrict__
     const int c0 = p * kQuantCols + lane * 16;
     uint32_t w[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      uint32_t packed = 0;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float rr = fminf(fmaxf(__builtin_rintf(v[4 * j + e]), -127.0f), 127.0f);
-        packed |= (static_cast<uint32_t>(static_cast<int32_t>(rr)) & 0xffu) << (8 * e);
-      }
-      w[j] = packed;
-    }
+    for (int j = 0; j < 4; ++j) w[j] = quant_pack4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
     if (c0 + 8 < k) *reinterpret_cast<uint4*>(qr + c0) = make_uint4(w[0], w[1], w[2], w[3]);
     else if (c0 < k) *reinterpret_cast<uint2*>(qr + c0) = make_uint2(w[0], w[1]);
   };
@@ -137,16 +112,12 @@ __global__ __launch_bounds__(256) void quant_kernel(const _Float16* __restrict__
   auto finish_scale = [&](int64_t row, float maximum, float& t, float& r, bool& fast) {
 #pragma unroll
     for (int d = 32; d >= 1; d >>= 1) maximum = fmaxf(maximum, __shfl_xor(maximum, d, 64));
-    if constexpr (kRotate) {
-      t = fmaxf(maximum, 1e-8f * 8.0f) / 127.0f;  // 8 s
-      if (lane == 0) scale[row] = t * 0.125f;
-    } else {
-      t = fmaxf(maximum, 1e-8f) / 127.0f;
-      if (lane == 0) scale[row] = t;
-    }
-    fast = __builtin_isfinite(t);
-    const float r0 = __builtin_amdgcn_rcpf(t);
-    r = __builtin_fmaf(__builtin_fmaf(-t, r0, 1.0f), r0, r0);
+    float s;
+    const QuantDivisor dv = quant_divisor<kRotate>(maximum, s);
+    if (lane == 0) scale[row] = s;
+    t = dv.t;
+    r = dv.r;
+    fast = dv.fast;
   };
 
   if constexpr (kHold) {

@@ -121,6 +121,80 @@ def linear(x, w, sw, bias, tile=(64, 128), multiplier=None, rotation: str = "h64
     return y.reshape(*shape, n)
 
 
+def _norm_vec(v: torch.Tensor | None, c: int, dtype: torch.dtype, what: str) -> torch.Tensor | None:
+    if v is None:
+        return None
+    t = v.to(dtype).reshape(-1).contiguous()
+    if t.numel() != c:
+        raise ValueError(f"{what} must have {c} entries")
+    if t.data_ptr() % 16:  # the kernel reads per-channel vectors as 16-byte vectors
+        t = t.clone()
+    return t
+
+
+def norm_quantize(
+    x: torch.Tensor,
+    eps: float,
+    weight: torch.Tensor | None = None,
+    bias: torch.Tensor | None = None,
+    scale: torch.Tensor | None = None,
+    shift: torch.Tensor | None = None,
+    multiplier: torch.Tensor | None = None,
+    rotation: str = "h64",
+):
+    """``quantize_activation(layer_norm_modulate(x, eps, weight, bias, scale, shift))`` in
+    one pass, bitwise equal to the two in sequence: ``(q int8 [M, K], s float32 [M])``
+    of fp16 rows ``x [..., K]``. The transformer block quantises a norm's output for
+    ``to_qkv``, ``cross_attn.to_q`` and ``mlp.0``
+    (src/hi3d_mac/mlx_backend/transformer.py:548-549, 570-571, 575-577); here the norm's
+    fp16 rows never reach memory. Rows wider than 4096 run the two kernels in sequence."""
+    if x.dtype != torch.float16:
+        raise ValueError("norm_quantize takes fp16 rows")
+    k = int(x.shape[-1])
+    if rotation == "h64" and k % 64:
+        raise ValueError("signed H64 requires width divisible by 64")
+    if k % 8:
+        raise ValueError("width must be a multiple of 8")
+    if (weight is None) != (bias is None):
+        raise ValueError("weight and bias must be given together")
+    if (scale is None) != (shift is None):
+        raise ValueError("scale and shift must be given together")
+    device = _lib.require_gpu(x, weight, bias, scale, shift)
+    if k > 4096:
+        from . import kernels
+
+        return quantize_activation(kernels.layer_norm_modulate(x, eps, weight, bias, scale, shift), multiplier, rotation)
+    x2 = x.reshape(-1, k).contiguous()
+    if x2.data_ptr() % 16:
+        x2 = x2.clone()
+    m = int(x2.shape[0])
+    w = _norm_vec(weight, k, torch.float32, "weight")
+    b = _norm_vec(bias, k, torch.float32, "bias")
+    sc = _norm_vec(scale, k, torch.float16, "scale")
+    sh = _norm_vec(shift, k, torch.float16, "shift")
+    mult = _multiplier(k, device, rotation, multiplier)
+    q = torch.empty((m, k), dtype=torch.int8, device=device)
+    s = torch.empty(m, dtype=torch.float32, device=device)
+    _lib.call("hi3d_layer_norm_quantize", _lib.ptr(x2), m, k, float(eps), _lib.ptr(w), _lib.ptr(b), _lib.ptr(sc),
+              _lib.ptr(sh), _lib.ptr(mult), _lib.ptr(q), _lib.ptr(s), _lib.stream(device))
+    return q, s
+
+
+def norm_linear(x, eps, w, sw, bias, weight=None, norm_bias=None, scale=None, shift=None, multiplier=None,
+                rotation: str = "h64"):
+    """``linear(layer_norm_modulate(x, eps, weight, norm_bias, scale, shift), w, sw, bias)``
+    with the norm and the activation quantiser fused (``norm_quantize``); the same
+    output bits as the composition."""
+    if w.dtype != torch.int8 or sw.dtype != torch.float32:
+        raise ValueError("W8A8 requires int8 weights and float32 scales")
+    if w.ndim != 2 or x.shape[-1] != w.shape[1] or tuple(sw.shape) != (w.shape[0],) or tuple(bias.shape) != (w.shape[0],):
+        raise ValueError("incompatible W8A8 projection shapes")
+    shape = tuple(x.shape[:-1])
+    n = int(w.shape[0])
+    a, sa = norm_quantize(x, eps, weight, norm_bias, scale, shift, multiplier, rotation)
+    return gemm(a, sa, w, sw, bias).reshape(*shape, n)
+
+
 def quantize_weight(weight: torch.Tensor, rotation: str = "h64", multiplier: torch.Tensor | None = None):
     """Offline weight conversion: ``(w int8 [N, K], sw float32 [N])``, symmetric per output
     row (``maxabs / 127``, round half to even), rows rotated by the same signed H64 as

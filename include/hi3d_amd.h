@@ -497,6 +497,21 @@ int hi3d_layer_norm_act(const void* x_dev, int64_t rows, int32_t c, float eps,
                         const void* scale_dev, const void* shift_dev, int32_t act,
                         void* out_dev, void* stream);
 
+/* The same LayerNorm (+ affine, + modulate) followed by the W8A8 activation quantiser
+ * of its fp16 result, in one pass (the fp16 rows are not stored): q_dev [rows, c] int8
+ * and q_scale_dev [rows] fp32, bitwise those of hi3d_layer_norm_modulate then
+ * hi3d_w8a8_quantize with the same signs_dev (signed H64 when given, c % 64 == 0;
+ * NULL = plain per-token). c a multiple of 8, at most 4096; x, the per-channel vectors
+ * and signs 16-byte aligned, q 8-byte aligned.
+ * Replaces: norm followed by w8a8.linear's quantize_activation in the transformer
+ * block (src/hi3d_mac/mlx_backend/transformer.py:548-549, 570-571, 575-577 over
+ * kernels.py:162-237 and w8a8.py:25-58, 95-102). */
+int hi3d_layer_norm_quantize(const void* x_dev, int64_t rows, int32_t c, float eps,
+                             const float* weight_dev, const float* bias_dev,
+                             const void* scale_dev, const void* shift_dev,
+                             const float* signs_dev, int8_t* q_dev, float* q_scale_dev,
+                             void* stream);
+
 /* adaLN projection: y = W . (silu(cond) if apply_silu else cond) + b in fp32
  * (W [n_out, n_in] fp32, cond [n_in], b [n_out] or NULL), then
  * scale1p_dev = fp16(1 + fp16(y[:n_out/2])) and shift_dev = fp16(y[n_out/2:])

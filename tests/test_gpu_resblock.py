@@ -68,8 +68,8 @@ def _sparse(cuda, idx, x):
 
 @pytest.mark.parametrize("c", [64, 256, 2112, 40])
 def test_layer_norm_silu_kernel(cuda, c):
-    """LayerNorm + affine + SiLU and LayerNorm + modulate + SiLU against the oracle's
-    fp16 steps (LN as layer_norm_modulate, then silu_f16)."""
+    """LayerNorm + affine + SiLU, LayerNorm + modulate + SiLU and plain LayerNorm + SiLU
+    against the oracle's fp16 steps (LN as layer_norm_modulate, then silu_f16)."""
     from hi3d_amd import kernels
 
     rng = np.random.default_rng(c)
@@ -79,7 +79,7 @@ def test_layer_norm_silu_kernel(cuda, c):
     scale = (1 + 0.2 * rng.standard_normal(c)).astype(np.float16)
     shift = (0.2 * rng.standard_normal(c)).astype(np.float16)
     xt = torch.as_tensor(x).to(cuda)
-    for kw in ({"weight": w, "bias": b}, {"scale": scale, "shift": shift}):
+    for kw in ({"weight": w, "bias": b}, {"scale": scale, "shift": shift}, {}):
         got = kernels.layer_norm_modulate(xt, 1e-6, act="silu", **{k: torch.as_tensor(v).to(cuda)
                                                                      for k, v in kw.items()}).cpu().numpy()
         ref = onorm.silu_f16(onorm.layer_norm_modulate(x, 1e-6, **kw))

@@ -294,3 +294,90 @@ def test_checkpoint_round_trip(cuda, tmp_path):
     with pytest.raises(ValueError, match="released Hi3Dv1.0-mlx-w8a8"):
         w8a8.load_checkpoint(partial, cuda)
     assert set(w8a8.load_checkpoint(partial, cuda, require_blocks=False)) == {"blocks.0.norm1.weight"}
+
+
+def _norm_params(rng, c, affine, modulate):
+    kw = {}
+    if affine:
+        kw["weight"] = rng.uniform(0.5, 1.5, c).astype(np.float32)
+        kw["bias"] = rng.normal(0, 0.3, c).astype(np.float32)
+    if modulate:
+        kw["scale"] = (1 + 0.3 * rng.standard_normal(c)).astype(np.float16)
+        kw["shift"] = (0.3 * rng.standard_normal(c)).astype(np.float16)
+    return kw
+
+
+@pytest.mark.parametrize("c,rotation", [(64, "h64"), (128, "none"), (1024, "h64"), (1024, "none"), (2112, "h64"),
+                                        (4096, "h64"), (1000, "none"), (4160, "h64")])
+def test_norm_quantize_bitwise_equals_norm_then_quantiser(cuda, c, rotation):
+    """LayerNorm (plain, affine, modulate, both) fused with the quantiser: codes and
+    scales bitwise equal to ``layer_norm_modulate`` then ``quantize_activation``, and to
+    the oracle's quantiser on the norm's fp16 rows. One lane per 8 columns from 8 to 64
+    lanes per row, two to eight chunks per lane, widths that leave lanes idle (1000,
+    2112), and the composed path above 4096. Rows include all-equal rows (a zero
+    norm), rows whose modulated values overflow fp16 (an infinite scale, compared with
+    the composition only) and tiny and huge magnitudes."""
+    from hi3d_amd import kernels, w8a8
+
+    rng = np.random.default_rng(c + len(rotation))
+    m = 777
+    x = (rng.standard_normal((m, c)) * 10.0 ** rng.uniform(-3, 3, (m, 1)) + rng.normal(0, 2, (m, 1)))
+    x[3] = 1.25  # constant row: every normalised value 0
+    x[10, : c // 3] *= 40
+    x = np.clip(x, -60000, 60000).astype(np.float16)
+    xt = torch.as_tensor(x).to(cuda)
+    for affine, modulate in ((False, False), (True, False), (False, True), (True, True)):
+        kw = {k: torch.as_tensor(v).to(cuda) for k, v in _norm_params(rng, c, affine, modulate).items()}
+        if modulate:
+            kw["scale"][c // 2] = 60000.0  # column c/2 overflows to +-inf in most rows
+        q, s = w8a8.norm_quantize(xt, 1e-6, rotation=rotation, **kw)
+        h = kernels.layer_norm_modulate(xt, 1e-6, **kw)
+        rq, rs = w8a8.quantize_activation(h, rotation=rotation)
+        assert torch.equal(q, rq) and torch.equal(s, rs), (affine, modulate)
+        # the oracle on the rows with a finite scale (its int8 cast of a NaN quotient is
+        # the platform's, not the reference's clamp)
+        fin = np.isfinite(s.cpu().numpy())
+        assert fin.sum() >= m // 2
+        oq, os_ = ow8a8.quantize_activation(h.cpu().numpy()[fin], rotation=rotation)
+        assert np.array_equal(q.cpu().numpy()[fin], oq) and np.array_equal(s.cpu().numpy()[fin], os_)
+
+
+def test_norm_quantize_custom_multiplier_and_views(cuda):
+    """A float multiplier in place of the signs, a row-sliced input and leading batch
+    dimensions give the composed bits."""
+    from hi3d_amd import kernels, w8a8
+
+    rng = np.random.default_rng(3)
+    c = 1024
+    x = torch.as_tensor(rng.standard_normal((2, 300, c)).astype(np.float16)).to(cuda)
+    mult = torch.as_tensor(rng.standard_normal(c).astype(np.float32)).to(cuda)
+    kw = {k: torch.as_tensor(v).to(cuda) for k, v in _norm_params(rng, c, False, True).items()}
+    for xin in (x, x[:, 7:]):
+        q, s = w8a8.norm_quantize(xin, 1e-6, multiplier=mult, **kw)
+        rq, rs = w8a8.quantize_activation(kernels.layer_norm_modulate(xin, 1e-6, **kw), mult)
+        assert tuple(q.shape) == (xin.numel() // c, c)
+        assert torch.equal(q, rq) and torch.equal(s, rs)
+    with pytest.raises(ValueError, match="fp16"):
+        w8a8.norm_quantize(x.float(), 1e-6)
+    with pytest.raises(ValueError, match="H64"):
+        w8a8.norm_quantize(x[..., :72], 1e-6)
+    with pytest.raises(ValueError, match="scale and shift"):
+        w8a8.norm_quantize(x, 1e-6, scale=kw["scale"])
+
+
+def test_norm_linear_workload4_shape_a(cuda):
+    """The MLP's first projection as the transformer block runs it, on config 4's shape A
+    (65,536 tokens, 1024 -> 4096): modulated norm fused with the quantiser, then the int8
+    GEMM; every output bit equals the composition of the three kernels."""
+    from hi3d_amd import kernels, w8a8
+
+    m, k, n = 65536, 1024, 4096
+    g = torch.Generator(device=cuda).manual_seed(41)
+    x = (torch.randn((m, k), device=cuda, generator=g) * 3 + 0.5).half()
+    scale = (1 + 0.2 * torch.randn(k, device=cuda, generator=g)).half()
+    shift = (0.2 * torch.randn(k, device=cuda, generator=g)).half()
+    wq, sw = w8a8.quantize_weight((torch.randn((n, k), device=cuda, generator=g) / 32).half())
+    bias = (torch.randn(n, device=cuda, generator=g) * 0.02).half()
+    fused = w8a8.norm_linear(x, 1e-6, wq, sw, bias, scale=scale, shift=shift)
+    composed = w8a8.linear(kernels.layer_norm_modulate(x, 1e-6, scale=scale, shift=shift), wq, sw, bias)
+    assert torch.equal(fused, composed)

@@ -119,6 +119,22 @@ def test_c_argument_validation_without_launch():
     # the LayerNorm + activation entry: unknown activation
     rc = lib.hi3d_layer_norm_act(fake, 4, 8, 1e-6, null, null, null, null, 7, fake, null)
     assert rc == _lib.ERR_INVALID and "activation" in _lib.last_error()
+    # the LayerNorm + quantise entry: widths, rotation, pairs of vectors, alignment
+    lnq = lib.hi3d_layer_norm_quantize
+    for c, signs, what in ((12, null, "multiple of 8"), (72, fake, "H64"), (4160, fake, "4096")):
+        rc = lnq(fake, 4, c, 1e-6, null, null, null, null, signs, fake, fake, null)
+        assert rc == _lib.ERR_INVALID and what in _lib.last_error()
+    rc = lnq(fake, 4, 64, 1e-6, fake, null, null, null, null, fake, fake, null)
+    assert rc == _lib.ERR_INVALID and "weight and bias" in _lib.last_error()
+    rc = lnq(fake, 4, 64, 1e-6, null, null, null, fake, null, fake, fake, null)
+    assert rc == _lib.ERR_INVALID and "scale and shift" in _lib.last_error()
+    rc = lnq(ctypes.c_void_p(24), 4, 64, 1e-6, null, null, null, null, null, fake, fake, null)
+    assert rc == _lib.ERR_INVALID and "aligned" in _lib.last_error()
+    rc = lnq(fake, 4, 64, 1e-6, null, null, null, null, null, ctypes.c_void_p(20), fake, null)
+    assert rc == _lib.ERR_INVALID and "aligned" in _lib.last_error()
+    rc = lnq(fake, 4, 64, 1e-6, null, null, null, null, null, null, fake, null)
+    assert rc == _lib.ERR_INVALID and "null" in _lib.last_error()
+    assert lnq(null, 0, 64, 1e-6, null, null, null, null, null, null, null, null) == 0
 
 
 def test_python_validation_matches_reference_errors():
