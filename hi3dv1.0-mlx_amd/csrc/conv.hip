@@ -47,8 +47,6 @@ __device__ __forceinline__ float to_f32(T v) {
   return static_cast<float>(v);
 }
 
-__device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
-
 template <typename T, int BN>
 __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a) {
   constexpr int BM = kTileRows;
@@ -183,7 +181,7 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a) {
       for (int v = 0; v < 16; ++v) {
         const int i = wm * 64 + mb * 32 + acc_row(lane, v);
         float x = acc[mb][nb][v] + b;
-        if (a.act == HI3D_ACT_SILU) x = silu(x);
+        if (a.act == HI3D_ACT_SILU) x = silu_f32(x);
         C[i * BN + j] = static_cast<T>(x);
       }
     }
@@ -463,7 +461,7 @@ __global__ __launch_bounds__(kPipeThreads) void conv_pipe_kernel(ConvArgs a) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           float x = acc[nb][mb][4 * q + e] + b[e];
-          if (a.act == HI3D_ACT_SILU) x = silu(x);
+          if (a.act == HI3D_ACT_SILU) x = silu_f32(x);
           h[e] = static_cast<T>(x);
         }
         if constexpr (sizeof(T) == 2) {
@@ -908,7 +906,7 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_ring_kernel(ConvArgs a) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           float x = acc[nb][mb][4 * q + e] + b[e];
-          if (a.act == HI3D_ACT_SILU) x = silu(x);
+          if (a.act == HI3D_ACT_SILU) x = silu_f32(x);
           h[e] = static_cast<T>(x);
         }
         Quad packed;
@@ -1120,7 +1118,7 @@ __global__ __launch_bounds__(NW * 64) void conv_block_f32_kernel(ConvArgs a) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       float x = v[e] + (bias != nullptr ? bias[col + e] : 0.0f);
-      if (a.act == HI3D_ACT_SILU) x = silu(x);
+      if (a.act == HI3D_ACT_SILU) x = silu_f32(x);
       v[e] = x;
     }
     const int64_t off = obase + col * 4;
@@ -1424,7 +1422,7 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_wide_kernel(ConvArgs a) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           float x = acc[nb][mb][4 * q + e] + b[e];
-          if (a.act == HI3D_ACT_SILU) x = silu(x);
+          if (a.act == HI3D_ACT_SILU) x = silu_f32(x);
           h[e] = static_cast<T>(x);
         }
         uint2 packed;
@@ -1706,7 +1704,7 @@ __global__ __launch_bounds__(512, 1) void conv_wide2_kernel(ConvArgs a) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           float x = acc[nb][mb][4 * q + e] + b[e];
-          if (a.act == HI3D_ACT_SILU) x = silu(x);
+          if (a.act == HI3D_ACT_SILU) x = silu_f32(x);
           h[e] = static_cast<T>(x);
         }
         uint2 packed;

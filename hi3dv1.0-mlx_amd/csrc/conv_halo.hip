@@ -66,8 +66,6 @@ __device__ __forceinline__ int hoff(int row, int chunk) {
   return row * 64 + ((chunk ^ ((row >> 2) & 3)) << 4);
 }
 
-__device__ __forceinline__ float hsilu(float x) { return x / (1.0f + expf(-x)); }
-
 template <typename T>
 __global__ __launch_bounds__(kHThreads, 1) void conv_halo_kernel(HaloArgs a) {
   __shared__ __attribute__((aligned(16))) char smem[2 * kHSlot + kHRingB * kHStageB];
@@ -248,7 +246,7 @@ __global__ __launch_bounds__(kHThreads, 1) void conv_halo_kernel(HaloArgs a) {
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             float x = acc[nb][mb][4 * q + e] + b[e];
-            if (a.act == HI3D_ACT_SILU) x = hsilu(x);
+            if (a.act == HI3D_ACT_SILU) x = silu_f32(x);
             h[e] = static_cast<T>(x);
           }
           uint2 packed;

@@ -216,7 +216,7 @@ __global__ __launch_bounds__(kNarrowWaves * 64) void conv_narrow_kernel(NarrowAr
       if (j >= a.cout) continue;
       float v = acc[g][i];
       if (bias) v += narrow_f32(bias[j]);
-      if (a.act == HI3D_ACT_SILU) v = v / (1.0f + expf(-v));
+      if (a.act == HI3D_ACT_SILU) v = silu_f32(v);
       T t = static_cast<T>(v);
       const int64_t at = static_cast<int64_t>(o) * a.cout + j;
       if (res) t = static_cast<T>(narrow_f32(t) + narrow_f32(res[at]));
@@ -377,7 +377,7 @@ __global__ __launch_bounds__(64) void conv_narrow_lds_kernel(NarrowArgs a) {
       if (j >= a.cout) continue;
       float v = acc[g][i];
       if (bias) v += narrow_f32(bias[j]);
-      if (a.act == HI3D_ACT_SILU) v = v / (1.0f + expf(-v));
+      if (a.act == HI3D_ACT_SILU) v = silu_f32(v);
       T t = static_cast<T>(v);
       const int64_t at = static_cast<int64_t>(o) * a.cout + j;
       if (res) t = static_cast<T>(narrow_f32(t) + narrow_f32(res[at]));
