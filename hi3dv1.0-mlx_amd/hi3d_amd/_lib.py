@@ -82,6 +82,7 @@ _SIGNATURES = {
     "hi3d_layer_norm_modulate": [_p, _i64, _i32, _f32, _p, _p, _p, _p, _p, _p],
     "hi3d_layer_norm_act": [_p, _i64, _i32, _f32, _p, _p, _p, _p, _i32, _p, _p],
     "hi3d_layer_norm_quantize": [_p, _i64, _i32, _f32, _p, _p, _p, _p, _p, _p, _p, _p],
+    "hi3d_dense_linear": [_p, _i64, _i32, _p, _p, _i32, _p, _p, _p],
     "hi3d_adaln_projection": [_p, _p, _p, _i32, _i32, _i32, _p, _p, _p],
     "hi3d_group_stats_workspace": [_i64, _i32, _p],
     "hi3d_group_stats": [_p, _i32, _i64, _i32, _i32, _f32, _p, _i64, _p, _p, _p],

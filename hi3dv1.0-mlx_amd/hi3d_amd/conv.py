@@ -220,6 +220,50 @@ def conv(
     return gather_conv_simple(features, plan.table, weight, bias, act, residual, n_in=plan.n_in, out=out)
 
 
+def dense_linear_supported(dtype: torch.dtype, cin: int, cout: int) -> bool:
+    """Whether the row-wise linear kernel takes this shape (fp16, Cin a multiple of 16 up
+    to 128, Cout 64, 128, 192 or 256)."""
+    return dtype == torch.float16 and 0 < cin <= 128 and cin % 16 == 0 and 0 < cout <= 256 and cout % 64 == 0
+
+
+def dense_linear(
+    features: torch.Tensor,
+    weight: torch.Tensor,
+    bias: torch.Tensor | None = None,
+    residual: torch.Tensor | None = None,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """``fp16(x W^T + bias)`` over fp16 rows ``x [N, Cin]`` with ``W [Cout, Cin]``, then
+    with ``residual`` ``fp16(that + residual)``: the res block's ``linear(h) +
+    skip_connection(x)`` in one pass over the rows (``hi3d_dense_linear``), with the
+    bits of :func:`conv` over the one-offset identity plan. ``out`` may be ``residual``."""
+    n, cin = int(features.shape[0]), int(features.shape[1])
+    w = weight.reshape(int(weight.shape[0]), -1)
+    cout = int(w.shape[0])
+    if int(w.shape[1]) != cin:
+        raise ValueError(f"weight takes {int(w.shape[1])} input channels, the rows hold {cin}")
+    if not dense_linear_supported(features.dtype, cin, cout):
+        raise ValueError(f"dense_linear takes fp16 rows, Cin % 16 == 0 up to 128 and Cout % 64 == 0 up to 256, "
+                         f"got {features.dtype} {cin} -> {cout}")
+    device = _lib.require_gpu(features, weight, bias, residual, out)
+    x = features.contiguous()
+    wc = w.to(torch.float16).contiguous()
+    b = None if bias is None else bias.to(torch.float16).reshape(-1).contiguous()
+    if b is not None and b.numel() != cout:
+        raise ValueError(f"bias must have {cout} entries")
+    r = None
+    if residual is not None:
+        if tuple(residual.shape) != (n, cout) or residual.dtype != torch.float16:
+            raise ValueError(f"residual must be a [{n}, {cout}] float16 tensor")
+        r = residual.contiguous()
+    o = _output(out, n, cout, torch.float16, device)
+    if o.numel() and o.data_ptr() == x.data_ptr():
+        raise ValueError("out must not alias the input rows")
+    _lib.call("hi3d_dense_linear", _lib.ptr(x), n, cin, _lib.ptr(wc), _lib.ptr(b), cout, _lib.ptr(r), _lib.ptr(o),
+              _lib.stream(device))
+    return o
+
+
 @functools.lru_cache(maxsize=None)
 def stride2_up_supported(dtype: torch.dtype, cin: int, cout: int) -> bool:
     """Whether the parent-major transposed kernel takes this shape."""

@@ -15,9 +15,10 @@ state dict loads unchanged) and forward signature
 
 Each line after the projection is one kernel: the LayerNorm kernel applies the affine
 or the modulation and the SiLU in its epilogue, conv2 applies the SiLU in its
-epilogue, and ``linear`` + ``skip_connection`` is a gather convolution over the
-one-offset identity plan whose residual epilogue adds the skip (the skip's own linear,
-when the channel count changes, is another such launch). The block runs on fp16
+epilogue, and ``linear`` + ``skip_connection`` is one row-wise linear launch whose
+residual epilogue adds the skip (``conv.dense_linear``; a gather convolution over the
+one-offset identity plan for shapes it does not take, with the same bits; the skip's own
+linear, when the channel count changes, is another such launch). The block runs on fp16
 features (the reference's fp16 torso, ``convert_to_fp16``); weights of another dtype are
 cast to fp16 for the launch.
 
@@ -122,9 +123,16 @@ class SparseResBlock3d(nn.Module):
                            for span, (s, t) in zip(x.layout, modulation)])
         h = _conv.conv(h, plan, _half(c2.weight).reshape(self.hidden_channels, 27, -1), _half(c2.bias), act="silu")
         if isinstance(self.skip_connection, nn.Linear):
-            skip = _conv.conv(feats, rows, _half(self.skip_connection.weight)[:, None, :],
-                              _half(self.skip_connection.bias))
+            sw, sb = _half(self.skip_connection.weight), _half(self.skip_connection.bias)
+            if _conv.dense_linear_supported(feats.dtype, self.channels, self.out_channels):
+                skip = _conv.dense_linear(feats, sw, sb)
+            else:
+                skip = _conv.conv(feats, rows, sw[:, None, :], sb)
         else:
             skip = feats
-        out = _conv.conv(h, rows, _half(self.linear.weight)[:, None, :], _half(self.linear.bias), residual=skip)
+        lw, lb = _half(self.linear.weight), _half(self.linear.bias)
+        if _conv.dense_linear_supported(h.dtype, self.hidden_channels, self.out_channels):
+            out = _conv.dense_linear(h, lw, lb, residual=skip)
+        else:
+            out = _conv.conv(h, rows, lw[:, None, :], lb, residual=skip)
         return x.replace(out)

@@ -512,6 +512,19 @@ int hi3d_layer_norm_quantize(const void* x_dev, int64_t rows, int32_t c, float e
                              const float* signs_dev, int8_t* q_dev, float* q_scale_dev,
                              void* stream);
 
+/* Row-wise linear layer on fp16 rows: out_dev [n, cout] = fp16(x W^T + bias), then with
+ * residual_dev fp16(out + residual) (the residual added to the rounded product and rounded
+ * again, as the convolution epilogues do; the bits of hi3d_gather_conv over the one-offset
+ * identity plan). x_dev [n, cin], w_dev [cout, cin], bias_dev [cout] or NULL, residual_dev
+ * [n, cout] or NULL (may be out_dev). cin a multiple of 16 up to 128, cout 64, 128, 192
+ * or 256; rows and weights 16-byte aligned.
+ * Replaces: the res block's linear(h) + skip_connection(x)
+ * (src/sparc3d/models/transformers/sparc3d_transformer.py:143-144;
+ * src/hi3d_mac/mlx_backend/transformer.py:426-437). */
+int hi3d_dense_linear(const void* x_dev, int64_t n, int32_t cin, const void* w_dev,
+                      const void* bias_dev, int32_t cout, const void* residual_dev,
+                      void* out_dev, void* stream);
+
 /* adaLN projection: y = W . (silu(cond) if apply_silu else cond) + b in fp32
  * (W [n_out, n_in] fp32, cond [n_in], b [n_out] or NULL), then
  * scale1p_dev = fp16(1 + fp16(y[:n_out/2])) and shift_dev = fp16(y[n_out/2:])

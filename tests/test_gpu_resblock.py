@@ -149,3 +149,45 @@ def test_res_block_errors(cuda):
     with pytest.raises(ValueError, match="embedding"):
         m(_sparse(cuda, idx, rng.standard_normal((len(idx), 16)).astype(np.float16)),
           torch.zeros((2, 8), device=cuda, dtype=torch.float16))
+
+
+@pytest.mark.parametrize("n,cin,cout,with_bias,with_res", [
+    (4429, 128, 256, True, True), (1000, 64, 128, True, False), (77, 16, 64, False, True),
+    (5000, 112, 192, True, True), (33, 128, 256, False, False), (1, 48, 64, True, True)])
+def test_dense_linear_bitwise_equals_identity_plan_conv(cuda, n, cin, cout, with_bias, with_res):
+    """The row-wise linear kernel against the gather convolution over the one-offset
+    identity plan (same MFMA sequence and rounding points): bitwise equal, ragged row
+    counts included; in place over the residual too; and against float64 at the fp16
+    gate."""
+    from hi3d_amd import conv, kmap
+
+    rng = np.random.default_rng(n + cin + cout)
+    x = torch.as_tensor(rng.standard_normal((n, cin)).astype(np.float16)).to(cuda)
+    w = torch.as_tensor((rng.standard_normal((cout, cin)) / np.sqrt(cin)).astype(np.float16)).to(cuda)
+    b = torch.as_tensor(rng.normal(0, 0.1, cout).astype(np.float16)).to(cuda) if with_bias else None
+    r = torch.as_tensor(rng.standard_normal((n, cout)).astype(np.float16)).to(cuda) if with_res else None
+    got = conv.dense_linear(x, w, b, residual=r)
+    want = conv.conv(x, kmap.identity_plan(n, x.device), w[:, None, :], b, residual=r)
+    assert torch.equal(got, want)
+    if with_res:
+        inplace = r.clone()
+        conv.dense_linear(x, w, b, residual=inplace, out=inplace)
+        assert torch.equal(inplace, want)
+    ref = x.double().cpu() @ w.double().cpu().T
+    if with_bias:
+        ref = ref + b.double().cpu()
+    if with_res:
+        ref = ref + r.double().cpu()
+    assert oconv.rel_err(got.float().cpu().numpy(), ref.numpy()) <= 1e-2
+
+
+def test_dense_linear_refuses_unsupported_shapes(cuda):
+    from hi3d_amd import conv
+
+    x = torch.zeros((8, 40), dtype=torch.float16, device=cuda)
+    with pytest.raises(ValueError, match="Cin % 16"):
+        conv.dense_linear(x, torch.zeros((64, 40), dtype=torch.float16, device=cuda))
+    with pytest.raises(ValueError, match="input channels"):
+        conv.dense_linear(x, torch.zeros((64, 48), dtype=torch.float16, device=cuda))
+    with pytest.raises(ValueError, match="Cin % 16"):
+        conv.dense_linear(x[:, :32], torch.zeros((96, 32), dtype=torch.float16, device=cuda))

@@ -135,6 +135,13 @@ def test_c_argument_validation_without_launch():
     rc = lnq(fake, 4, 64, 1e-6, null, null, null, null, null, null, fake, null)
     assert rc == _lib.ERR_INVALID and "null" in _lib.last_error()
     assert lnq(null, 0, 64, 1e-6, null, null, null, null, null, null, null, null) == 0
+    # the row-wise linear entry: channel counts and alignment
+    for cin, cout, what in ((40, 64, "cin"), (144, 64, "cin"), (64, 96, "cout"), (64, 320, "cout")):
+        rc = lib.hi3d_dense_linear(fake, 4, cin, fake, null, cout, null, fake, null)
+        assert rc == _lib.ERR_INVALID and what in _lib.last_error()
+    rc = lib.hi3d_dense_linear(ctypes.c_void_p(24), 4, 64, fake, null, 64, null, fake, null)
+    assert rc == _lib.ERR_INVALID and "aligned" in _lib.last_error()
+    assert lib.hi3d_dense_linear(null, 0, 64, null, null, 64, null, null, null) == 0
 
 
 def test_python_validation_matches_reference_errors():
