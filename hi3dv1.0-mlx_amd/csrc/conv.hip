@@ -1407,6 +1407,28 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_wide_kernel(ConvArgs a) {
   constexpr int ROWB = NB * 64, CPR = NB * 4;
   char* stg = smem + wave * (64 * ROWB);
   const int cb = n0 + wn * NB * 32;
+  const int64_t out_row_bytes = static_cast<int64_t>(a.cout) * sizeof(T);
+  // chunk i of this lane: row lane / CPR + (64 / CPR) i of the wave's rows, 16-byte chunk
+  // lane % CPR of its channels; false for rows past the plan or without an output row
+  auto chunk_at = [&](int i, int64_t& off) {
+    const int row = lane / CPR + (64 / CPR) * i;
+    const int tr = wm * 64 + row;
+    const int64_t pt = tile * SUB + tr / kTileRows;
+    const int32_t orow = pt < a.ntiles ? reinterpret_cast<const int32_t*>(rows_lds)[tr] : -1;
+    off = static_cast<int64_t>(orow) * out_row_bytes + static_cast<int64_t>(cb + (lane % CPR) * 8) * sizeof(T);
+    return orow >= 0 && orow < a.n_out;
+  };
+  // the residual's chunks are requested before the accumulators are converted and
+  // staged, so their latency overlaps that work instead of each group of stores
+  u32x4 res[CPR];
+  if (a.residual != nullptr) {
+#pragma unroll
+    for (int i = 0; i < CPR; ++i) {
+      int64_t off;
+      const bool ok = chunk_at(i, off);
+      res[i] = *reinterpret_cast<const u32x4*>(a.residual + (ok ? off : 0));
+    }
+  }
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
 #pragma unroll
@@ -1432,22 +1454,16 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_wide_kernel(ConvArgs a) {
     }
   }
   wait_lgkm0();
-  const int64_t out_row_bytes = static_cast<int64_t>(a.cout) * sizeof(T);
-#pragma unroll 4
+#pragma unroll
   for (int i = 0; i < CPR; ++i) {
     const int row = lane / CPR + (64 / CPR) * i;  // 0..63 within this wave's rows
     const int chunk = lane % CPR;
-    const int tr = wm * 64 + row;
-    const int64_t pt = tile * SUB + tr / kTileRows;
-    if (pt >= a.ntiles) continue;
-    const int32_t orow = reinterpret_cast<const int32_t*>(rows_lds)[tr];
-    if (orow < 0 || orow >= a.n_out) continue;
+    int64_t off;
+    if (!chunk_at(i, off)) continue;
     u32x4 v = *reinterpret_cast<const u32x4*>(stg + row * ROWB + ((chunk ^ (row & (CPR - 1))) << 4));
-    const int64_t off = static_cast<int64_t>(orow) * out_row_bytes + static_cast<int64_t>(cb + chunk * 8) * sizeof(T);
     if (a.residual != nullptr) {
-      const u32x4 r = *reinterpret_cast<const u32x4*>(a.residual + off);
       T* pv = reinterpret_cast<T*>(&v);
-      const T* pr = reinterpret_cast<const T*>(&r);
+      const T* pr = reinterpret_cast<const T*>(&res[i]);
 #pragma unroll
       for (int e = 0; e < 8; ++e) pv[e] = static_cast<T>(to_f32(pv[e]) + to_f32(pr[e]));
     }
@@ -1689,6 +1705,28 @@ __global__ __launch_bounds__(512, 1) void conv_wide2_kernel(ConvArgs a) {
   constexpr int ROWB = NB * 64, CPR = NB * 4;
   char* stg = smem + wave * (64 * ROWB);
   const int cb = n0 + wn * NB * 32;
+  const int64_t out_row_bytes = static_cast<int64_t>(a.cout) * sizeof(T);
+  // chunk i of this lane: row lane / CPR + (64 / CPR) i of the wave's rows, 16-byte chunk
+  // lane % CPR of its channels; false for rows past the plan or without an output row
+  auto chunk_at = [&](int i, int64_t& off) {
+    const int row = lane / CPR + (64 / CPR) * i;
+    const int tr = wm * 64 + row;
+    const int64_t pt = tile * SUB + tr / kTileRows;
+    const int32_t orow = pt < a.ntiles ? reinterpret_cast<const int32_t*>(rows_lds)[tr] : -1;
+    off = static_cast<int64_t>(orow) * out_row_bytes + static_cast<int64_t>(cb + (lane % CPR) * 8) * sizeof(T);
+    return orow >= 0 && orow < a.n_out;
+  };
+  // the residual's chunks are requested before the accumulators are converted and
+  // staged, so their latency overlaps that work instead of each group of stores
+  u32x4 res[CPR];
+  if (a.residual != nullptr) {
+#pragma unroll
+    for (int i = 0; i < CPR; ++i) {
+      int64_t off;
+      const bool ok = chunk_at(i, off);
+      res[i] = *reinterpret_cast<const u32x4*>(a.residual + (ok ? off : 0));
+    }
+  }
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
 #pragma unroll
@@ -1714,22 +1752,16 @@ __global__ __launch_bounds__(512, 1) void conv_wide2_kernel(ConvArgs a) {
     }
   }
   wait_lgkm0();
-  const int64_t out_row_bytes = static_cast<int64_t>(a.cout) * sizeof(T);
-#pragma unroll 4
+#pragma unroll
   for (int i = 0; i < CPR; ++i) {
     const int row = lane / CPR + (64 / CPR) * i;  // 0..63 within this wave's rows
     const int chunk = lane % CPR;
-    const int tr = wm * 64 + row;
-    const int64_t pt = tile * SUB + tr / kTileRows;
-    if (pt >= a.ntiles) continue;
-    const int32_t orow = reinterpret_cast<const int32_t*>(rows_lds)[tr];
-    if (orow < 0 || orow >= a.n_out) continue;
+    int64_t off;
+    if (!chunk_at(i, off)) continue;
     u32x4 v = *reinterpret_cast<const u32x4*>(stg + row * ROWB + ((chunk ^ (row & (CPR - 1))) << 4));
-    const int64_t off = static_cast<int64_t>(orow) * out_row_bytes + static_cast<int64_t>(cb + chunk * 8) * sizeof(T);
     if (a.residual != nullptr) {
-      const u32x4 r = *reinterpret_cast<const u32x4*>(a.residual + off);
       T* pv = reinterpret_cast<T*>(&v);
-      const T* pr = reinterpret_cast<const T*>(&r);
+      const T* pr = reinterpret_cast<const T*>(&res[i]);
 #pragma unroll
       for (int e = 0; e < 8; ++e) pv[e] = static_cast<T>(to_f32(pv[e]) + to_f32(pr[e]));
     }
