@@ -19,6 +19,8 @@
 
 #include "common.h"
 #include "conv_tile.h"
+#include "quant.h"
+#include "rownorm.h"
 
 namespace hi3d {
 namespace {
@@ -40,6 +42,13 @@ struct ConvArgs {
   const char* residual;
   int32_t act;
   char* out;
+  // the row norm of conv_wide_kernel<.., kLN>: LayerNorm of each 128-channel output row,
+  // then fp16(fp16(h * scale[b]) + shift[b]) and SiLU, b = the row's batch (coords[4 r])
+  const int32_t* ln_coords;
+  const void* ln_scale;  // fp16 [ln_batches, cout]
+  const void* ln_shift;  // fp16 [ln_batches, cout]
+  int32_t ln_batches;
+  float ln_eps;
 };
 
 template <typename T>
@@ -1176,7 +1185,7 @@ constexpr int kWideDepth = 3;
 
 __device__ __forceinline__ int wide_off(int row, int chunk) { return row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4); }
 
-template <typename T, int BN, int NW, bool K1>
+template <typename T, int BN, int NW, bool K1, bool kLN = false>
 __global__ __launch_bounds__(NW * 64, 1) void conv_wide_kernel(ConvArgs a) {
   using Sh = WideShape<BN, NW>;
   constexpr int NS = kWideDepth, BM = Sh::BM, LA = Sh::LA, LB = Sh::LB, SUB = Sh::SUB, L = Sh::L;
@@ -1454,6 +1463,75 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_wide_kernel(ConvArgs a) {
     }
   }
   wait_lgkm0();
+  if constexpr (kLN) {
+    // The res block's second norm on whole output rows (cout == BN == 128): each row's
+    // 16 chunks sit in the staged blocks of waves (row / 64) (chunks 0..7) and
+    // (row / 64) + 4 (chunks 8..15). Eight lanes per row, lane g holding chunks g and
+    // g + 8: the lanes, chunks, summation order and reduction partners of ln_kernel<8, 2>
+    // (the LayerNorm of 128-channel rows), so the result is bitwise the convolution
+    // followed by that kernel.
+#pragma clang fp contract(off)
+    static_assert(BN == 128 && NB == 2 && Sh::WM == 4 && NW == 8, "the row norm takes whole 128-channel rows");
+    __syncthreads();
+    const _Float16* scale = static_cast<const _Float16*>(a.ln_scale);
+    const _Float16* shift = static_cast<const _Float16*>(a.ln_shift);
+    const int g = lane & 7;
+    const float c = static_cast<float>(BN);
+    // the four passes are unrolled so that their independent chains (LDS reads, sums,
+    // lane moves, the square root and the SiLU) overlap; lane moves by DPP (the same
+    // partners as ln_kernel's shuffles)
+#pragma unroll
+    for (int pass = 0; pass < BM / (NW * 8); ++pass) {
+      const int tr = pass * (NW * 8) + wave * 8 + (lane >> 3);  // tile row
+      const int64_t pt = tile * SUB + tr / kTileRows;
+      const int32_t orow = pt < a.ntiles ? reinterpret_cast<const int32_t*>(rows_lds)[tr] : -1;
+      const bool live = orow >= 0 && orow < a.n_out;
+      const int wr = tr & 63;
+      float v[2][8];
+      float sum = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const f16x8 h = *reinterpret_cast<const f16x8*>(smem + ((tr >> 6) + 4 * i) * (64 * ROWB) + wr * ROWB +
+                                                        ((g ^ (wr & (CPR - 1))) << 4));
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          v[i][e] = static_cast<float>(h[e]);
+          sum += v[i][e];
+        }
+      }
+      sum += dpp_xor4(sum);
+      sum += dpp_xor2(sum);
+      sum += dpp_xor1(sum);
+      const float mean = sum / c;
+      float sq = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float d = v[i][e] - mean;
+          sq += d * d;
+        }
+      sq += dpp_xor4(sq);
+      sq += dpp_xor2(sq);
+      sq += dpp_xor1(sq);
+      const float inv = 1.0f / sqrtf(sq / c + a.ln_eps);
+      int b = live ? a.ln_coords[static_cast<int64_t>(orow) * 4] : 0;
+      b = b < 0 ? 0 : (b >= a.ln_batches ? a.ln_batches - 1 : b);
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int ch = g + 8 * i;
+        f16x8 o;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = static_cast<_Float16>(f32_rounded((v[i][e] - mean) * inv));
+        o = modulate8(o, *reinterpret_cast<const f16x8*>(scale + b * BN + ch * 8),
+                      *reinterpret_cast<const f16x8*>(shift + b * BN + ch * 8));
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = silu_h(o[e]);
+        if (live) *reinterpret_cast<f16x8*>(a.out + (static_cast<int64_t>(orow) * BN + ch * 8) * 2) = o;
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < CPR; ++i) {
     const int row = lane / CPR + (64 / CPR) * i;  // 0..63 within this wave's rows
@@ -1471,7 +1549,7 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_wide_kernel(ConvArgs a) {
   }
 }
 
-template <typename T, int BN, int NW, bool K1 = false>
+template <typename T, int BN, int NW, bool K1 = false, bool kLN = false>
 int launch_wide(const ConvArgs& base, hipStream_t stream) {
   // the one-stage form (K1) takes 128-byte rows and the other form longer ones
   HI3D_REQUIRE(K1 == (base.cin * static_cast<int>(sizeof(T)) == 128), "wide kernel: row length and form disagree");
@@ -1480,7 +1558,8 @@ int launch_wide(const ConvArgs& base, hipStream_t stream) {
   const int64_t blocks = ceil_div(a.ntiles, WideShape<BN, NW>::SUB) * a.ny;
   if (blocks == 0) return HI3D_OK;
   HI3D_REQUIRE(blocks < (int64_t(1) << 31), "too many tiles");
-  hipLaunchKernelGGL((conv_wide_kernel<T, BN, NW, K1>), dim3(static_cast<unsigned>(blocks)), dim3(NW * 64), 0, stream, a);
+  hipLaunchKernelGGL((conv_wide_kernel<T, BN, NW, K1, kLN>), dim3(static_cast<unsigned>(blocks)), dim3(NW * 64), 0,
+                     stream, a);
   HI3D_LAUNCH_CHECK();
   return HI3D_OK;
 }
@@ -2002,6 +2081,45 @@ int hi3d_gather_conv(const void* in, int64_t n_in, int32_t cin, const void* weig
     case HI3D_BF16: return launch_mfma<__bf16>(a, s);
     default: return launch_mfma<float>(a, s);
   }
+}
+
+int hi3d_gather_conv_ln_silu(const void* in, int64_t n_in, int32_t cin, const void* weight, const void* bias,
+                             int32_t cout, int32_t kvol, const int32_t* rows, const int32_t* gidx,
+                             const uint32_t* tile_mask, int64_t n_out, const int32_t* coords, int32_t batches,
+                             const void* scale1p, const void* shift, float eps, void* out, void* stream) {
+  const int rb = cin * 2;
+  HI3D_REQUIRE(cout == 128, "the fused row norm takes 128 output channels (got %d)", cout);
+  HI3D_REQUIRE(rb % 128 == 0 && rb >= 256 && rb <= 1024, "the fused row norm takes 128..512 fp16 input channels in "
+               "steps of 64 (got %d)", cin);
+  HI3D_REQUIRE(kvol > 0 && kvol <= kMaxPipelinedKvol, "kvol must be 1..%d", kMaxPipelinedKvol);
+  HI3D_REQUIRE(n_in >= 0 && n_out >= 0 && batches > 0, "sizes must be non-negative and batches positive");
+  if (n_out == 0) return HI3D_OK;
+  HI3D_REQUIRE(in && weight && rows && gidx && tile_mask && coords && scale1p && shift && out, "null pointer argument");
+  const uintptr_t align = reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(weight) |
+                          reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(scale1p) |
+                          reinterpret_cast<uintptr_t>(shift);
+  HI3D_REQUIRE((align & 15) == 0, "feature, weight, output, scale and shift pointers must be 16-byte aligned");
+  ConvArgs a{};
+  a.in = static_cast<const char*>(in);
+  a.n_in = n_in;
+  a.cin = cin;
+  a.weight = static_cast<const char*>(weight);
+  a.bias = bias;
+  a.cout = cout;
+  a.kvol = kvol;
+  a.rows = rows;
+  a.gidx = gidx;
+  a.tile_mask = tile_mask;
+  a.ntiles = ceil_div(n_out, kTileRows);
+  a.n_out = n_out;
+  a.act = HI3D_ACT_NONE;
+  a.out = static_cast<char*>(out);
+  a.ln_coords = coords;
+  a.ln_scale = scale1p;
+  a.ln_shift = shift;
+  a.ln_batches = batches;
+  a.ln_eps = eps;
+  return launch_wide<_Float16, 128, 8, false, true>(a, as_stream(stream));
 }
 
 int hi3d_gather_conv_simple(const void* in, int64_t n_in, int32_t cin, const void* weight, const void* bias,

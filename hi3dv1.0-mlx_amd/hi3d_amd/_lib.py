@@ -49,6 +49,8 @@ _SIGNATURES = {
     "hi3d_conv_plan_workspace": [_i64, _p],
     "hi3d_conv_plan": [_p, _i64, _i32, _i64, _p, _i32, _i32, _i64, _p, _i64, _p, _p, _p, _p],
     "hi3d_gather_conv": [_p, _i64, _i32, _p, _p, _i32, _i32, _p, _p, _p, _i64, _p, _i32, _i32, _p, _p],
+    "hi3d_gather_conv_ln_silu": [_p, _i64, _i32, _p, _p, _i32, _i32, _p, _p, _p, _i64, _p, _i32, _p, _p, _f32, _p,
+                                 _p],
     "hi3d_gather_conv_simple": [_p, _i64, _i32, _p, _p, _i32, _i32, _p, _i64, _p, _i32, _i32, _p, _p],
     "hi3d_kmap_dense_workspace": [_i32, _i32, _i32, _i32, _p],
     "hi3d_kmap_subm_dense": [_p, _i64, _i32, _i32, _i32, _i32, _i32, _p, _i64, _p, _p, _p, _p],

@@ -113,6 +113,55 @@ def gather_conv(
     return out
 
 
+def conv_ln_silu_supported(dtype: torch.dtype, cin: int, cout: int, kvol: int) -> bool:
+    """Whether the convolution with the res block's second norm fused into its epilogue
+    takes this shape (fp16, 128..512 input channels in steps of 64, 128 outputs)."""
+    return dtype == torch.float16 and cout == 128 and cin % 64 == 0 and 128 <= cin <= 512 and 0 < kvol <= 27
+
+
+def conv_ln_silu(
+    features: torch.Tensor,
+    plan: ConvPlan,
+    weight: torch.Tensor,
+    bias: torch.Tensor | None,
+    coords: torch.Tensor,
+    scale1p: torch.Tensor,
+    shift: torch.Tensor,
+    eps: float,
+) -> torch.Tensor:
+    """``silu(layer_norm(conv(x)) * scale1p[b] + shift[b])`` per output row, ``b`` the row's
+    batch (``coords[:, 0]``): the res block's ``conv1`` then ``norm2`` with its modulation
+    and SiLU in one launch (``hi3d_gather_conv_ln_silu``), bitwise :func:`gather_conv`
+    followed by ``kernels.layer_norm_modulate(..., act="silu")`` on each batch's rows.
+    ``scale1p`` and ``shift`` are fp16 ``[B, 128]``."""
+    device = _lib.require_gpu(features, weight, bias, coords, scale1p, shift, plan.gidx)
+    if features.ndim != 2 or features.shape[0] != plan.n_in:
+        raise ValueError(f"expected features [{plan.n_in}, Cin], got {tuple(features.shape)}")
+    x = features.contiguous()
+    w = _flat_weight(weight, plan.kvol)
+    cin, cout = int(x.shape[1]), int(w.shape[0])
+    if int(w.shape[2]) != cin:
+        raise ValueError(f"weight expects {int(w.shape[2])} input channels, features have {cin}")
+    if x.dtype != torch.float16 or w.dtype != torch.float16 or not conv_ln_silu_supported(x.dtype, cin, cout, plan.kvol):
+        raise ValueError(f"conv_ln_silu takes fp16 rows of 128..512 channels into 128 (got {x.dtype} {cin} -> {cout})")
+    c = coords.to(torch.int32).contiguous()
+    if tuple(c.shape) != (plan.n_out, 4):
+        raise ValueError(f"coords must be [{plan.n_out}, 4]")
+    sc = scale1p.to(torch.float16).reshape(-1, cout).contiguous()
+    sh = shift.to(torch.float16).reshape(-1, cout).contiguous()
+    if sc.shape != sh.shape or sc.shape[0] < 1:
+        raise ValueError("scale1p and shift must both be [B, 128] with B >= 1")
+    b = None if bias is None else bias.to(torch.float16).contiguous()
+    out = torch.empty((plan.n_out, cout), dtype=torch.float16, device=device)
+    _lib.call(
+        "hi3d_gather_conv_ln_silu",
+        _lib.ptr(x), plan.n_in, cin, _lib.ptr(w), _lib.ptr(b), cout, plan.kvol, _lib.ptr(plan.rows),
+        _lib.ptr(plan.gidx), _lib.ptr(plan.tile_mask), plan.n_out, _lib.ptr(c), int(sc.shape[0]), _lib.ptr(sc),
+        _lib.ptr(sh), float(eps), _lib.ptr(out), _lib.stream(device),
+    )
+    return out
+
+
 def narrow_supported(dtype: torch.dtype, cin: int, cout: int, kvol: int) -> bool:
     """Whether the narrow-output kernel takes this convolution (at most 16 outputs)."""
     if dtype not in (torch.float16, torch.bfloat16, torch.float32) or not 1 <= cout <= 16 or not 1 <= kvol <= 32:

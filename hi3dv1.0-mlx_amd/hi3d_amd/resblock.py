@@ -13,9 +13,11 @@ state dict loads unchanged) and forward signature
     h = silu(conv2(h))
     return linear(h) + skip_connection(x)
 
-Each line after the projection is one kernel: the LayerNorm kernel applies the affine
-or the modulation and the SiLU in its epilogue, conv2 applies the SiLU in its
-epilogue, and ``linear`` + ``skip_connection`` is one row-wise linear launch whose
+Each line after the projection is one kernel: the LayerNorm kernel applies norm1's
+affine and the SiLU in its epilogue; conv1 applies norm2, each row's batch modulation
+and the SiLU to its output rows in its epilogue (``conv.conv_ln_silu``, for 128 hidden
+channels; else the convolution and the LayerNorm kernel, the same bits); conv2 applies
+the SiLU in its epilogue, and ``linear`` + ``skip_connection`` is one row-wise linear launch whose
 residual epilogue adds the skip (``conv.dense_linear``; a gather convolution over the
 one-offset identity plan for shapes it does not take, with the same bits; the skip's own
 linear, when the channel count changes, is another such launch). The block runs on fp16
@@ -114,13 +116,19 @@ class SparseResBlock3d(nn.Module):
         h = layer_norm_modulate(feats, self.norm1.eps, weight=self.norm1.weight.detach(),
                                 bias=self.norm1.bias.detach(), act="silu")
         c1, c2 = self.conv1.conv, self.conv2.conv
-        h = _conv.conv(h, plan, _half(c1.weight).reshape(self.hidden_channels, 27, -1), _half(c1.bias))
-        if len(modulation) == 1:
-            scale1p, shift = modulation[0]
-            h = layer_norm_modulate(h, self.norm2.eps, scale=scale1p, shift=shift, act="silu")
+        w1 = _half(c1.weight).reshape(self.hidden_channels, 27, -1)
+        if _conv.conv_ln_silu_supported(h.dtype, self.channels, self.hidden_channels, plan.kvol) and not _conv.HALO:
+            # conv1 with norm2, the modulation of each row's batch and SiLU in its epilogue
+            h = _conv.conv_ln_silu(h, plan, w1, _half(c1.bias), x.coords, torch.stack([m[0] for m in modulation]),
+                                   torch.stack([m[1] for m in modulation]), self.norm2.eps)
         else:
-            h = torch.cat([layer_norm_modulate(h[span], self.norm2.eps, scale=s, shift=t, act="silu")
-                           for span, (s, t) in zip(x.layout, modulation)])
+            h = _conv.conv(h, plan, w1, _half(c1.bias))
+            if len(modulation) == 1:
+                scale1p, shift = modulation[0]
+                h = layer_norm_modulate(h, self.norm2.eps, scale=scale1p, shift=shift, act="silu")
+            else:
+                h = torch.cat([layer_norm_modulate(h[span], self.norm2.eps, scale=s, shift=t, act="silu")
+                               for span, (s, t) in zip(x.layout, modulation)])
         h = _conv.conv(h, plan, _half(c2.weight).reshape(self.hidden_channels, 27, -1), _half(c2.bias), act="silu")
         if isinstance(self.skip_connection, nn.Linear):
             sw, sb = _half(self.skip_connection.weight), _half(self.skip_connection.bias)

@@ -284,6 +284,22 @@ int hi3d_gather_conv(const void* in_dev, int64_t n_in, int32_t cin, const void* 
                      const void* residual_dev, int32_t act, int32_t dtype, void* out_dev,
                      void* stream);
 
+/* hi3d_gather_conv (fp16, no activation, no residual) into 128 output channels with the
+ * transformer res block's second norm applied to each output row before it is stored:
+ * h = conv row (fp16), then LayerNorm over its 128 channels (fp32 two-pass statistics,
+ * no affine), fp16(fp16(h * scale1p[b]) + shift[b]) and the fp16 SiLU, b = the row's
+ * batch (coords_dev[4 r], clamped to [0, batches)); bitwise hi3d_gather_conv followed by
+ * hi3d_layer_norm_act. cin in 128..512, a multiple of 64; scale1p_dev and shift_dev
+ * fp16 [batches, 128]; the same plan arguments as hi3d_gather_conv.
+ * Replaces: conv1 then norm2 * (1 + scale) + shift and SiLU of SparseResBlock3d.forward
+ * (src/sparc3d/models/transformers/sparc3d_transformer.py:137-141;
+ * src/hi3d_mac/mlx_backend/transformer.py:418-433). */
+int hi3d_gather_conv_ln_silu(const void* in_dev, int64_t n_in, int32_t cin, const void* weight_dev,
+                             const void* bias_dev, int32_t cout, int32_t kvol, const int32_t* rows_dev,
+                             const int32_t* gidx_dev, const uint32_t* tile_mask_dev, int64_t n_out,
+                             const int32_t* coords_dev, int32_t batches, const void* scale1p_dev,
+                             const void* shift_dev, float eps, void* out_dev, void* stream);
+
 /* The same convolution straight from a table [n_out, kvol], one thread per output
  * element: any channel count and F64 as well. Used for shapes the MFMA path does not
  * take (e.g. the reference's C 5->7 float64 case, tests/test_backends.py:32-50). */

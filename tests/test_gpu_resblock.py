@@ -191,3 +191,47 @@ def test_dense_linear_refuses_unsupported_shapes(cuda):
         conv.dense_linear(x, torch.zeros((64, 48), dtype=torch.float16, device=cuda))
     with pytest.raises(ValueError, match="Cin % 16"):
         conv.dense_linear(x[:, :32], torch.zeros((96, 32), dtype=torch.float16, device=cuda))
+
+
+@pytest.mark.parametrize("cin,batches,side", [(256, 1, 18), (128, 3, 14), (512, 2, 12), (192, 2, 16)])
+def test_conv_ln_silu_bitwise_equals_conv_then_norm(cuda, cin, batches, side):
+    """conv1 with norm2, each row's batch modulation and SiLU in its epilogue against the
+    convolution followed by the LayerNorm + modulate + SiLU kernel on each batch's rows:
+    bitwise equal (rows of several batch elements interleaved, so tiles mix batches)."""
+    from hi3d_amd import conv, kernels, kmap
+
+    rng = np.random.default_rng(cin + batches)
+    idx = _indices(rng, side, 0.2, batches)
+    idx = idx[rng.permutation(len(idx))]  # interleave the batch elements' rows
+    n = len(idx)
+    coords = torch.as_tensor(idx).to(cuda)
+    km = kmap.build_kernel_map(coords, [side] * 3, batches)
+    plan = km.plan()
+    x = torch.as_tensor(rng.standard_normal((n, cin)).astype(np.float16)).to(cuda)
+    w = torch.as_tensor((rng.standard_normal((128, 27, cin)) / np.sqrt(27 * cin)).astype(np.float16)).to(cuda)
+    b = torch.as_tensor(rng.normal(0, 0.1, 128).astype(np.float16)).to(cuda)
+    scale1p = torch.as_tensor((1 + 0.3 * rng.standard_normal((batches, 128))).astype(np.float16)).to(cuda)
+    shift = torch.as_tensor((0.3 * rng.standard_normal((batches, 128))).astype(np.float16)).to(cuda)
+    got = conv.conv_ln_silu(x, plan, w, b, coords, scale1p, shift, 1e-6)
+    h = conv.gather_conv(x, plan, w, b)
+    want = torch.empty_like(h)
+    for bb in range(batches):
+        sel = coords[:, 0] == bb
+        want[sel] = kernels.layer_norm_modulate(h[sel].contiguous(), 1e-6, scale=scale1p[bb], shift=shift[bb],
+                                                act="silu")
+    assert torch.equal(got, want)
+
+
+def test_conv_ln_silu_refuses_unsupported_shapes(cuda):
+    from hi3d_amd import conv, kmap
+
+    idx = _indices(np.random.default_rng(1), 8, 0.3, 1)
+    coords = torch.as_tensor(idx).to(cuda)
+    plan = kmap.build_kernel_map(coords, [8] * 3, 1).plan()
+    x = torch.zeros((len(idx), 96), dtype=torch.float16, device=cuda)
+    w = torch.zeros((128, 27, 96), dtype=torch.float16, device=cuda)
+    s = torch.ones((1, 128), dtype=torch.float16, device=cuda)
+    with pytest.raises(ValueError, match="128..512"):
+        conv.conv_ln_silu(x, plan, w, None, coords, s, s, 1e-6)
+    with pytest.raises(ValueError, match="coords"):
+        conv.conv_ln_silu(x[:, :64].repeat(1, 2), plan, w[..., :64].repeat(1, 1, 2), None, coords[:5], s, s, 1e-6)

@@ -142,6 +142,14 @@ def test_c_argument_validation_without_launch():
     rc = lib.hi3d_dense_linear(ctypes.c_void_p(24), 4, 64, fake, null, 64, null, fake, null)
     assert rc == _lib.ERR_INVALID and "aligned" in _lib.last_error()
     assert lib.hi3d_dense_linear(null, 0, 64, null, null, 64, null, null, null) == 0
+    # the convolution with the fused row norm: 128 outputs, 128..512 inputs in steps of 64
+    cln = lib.hi3d_gather_conv_ln_silu
+    for cin, cout, what in ((128, 256, "128 output"), (96, 128, "128..512"), (576, 128, "128..512")):
+        rc = cln(fake, 10, cin, fake, null, cout, 27, fake, fake, fake, 10, fake, 1, fake, fake, 1e-6, fake, null)
+        assert rc == _lib.ERR_INVALID and what in _lib.last_error()
+    rc = cln(fake, 10, 128, fake, null, 128, 27, fake, fake, fake, 10, fake, 0, fake, fake, 1e-6, fake, null)
+    assert rc == _lib.ERR_INVALID and "batches" in _lib.last_error()
+    assert cln(null, 0, 128, null, null, 128, 27, null, null, null, 0, null, 1, null, null, 1e-6, null, null) == 0
 
 
 def test_python_validation_matches_reference_errors():
