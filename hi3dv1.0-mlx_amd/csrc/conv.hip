@@ -207,11 +207,7 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a) {
     u32x4 v = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(C) + (i * BN + cc * EPC) * sizeof(T));
     const int64_t off = static_cast<int64_t>(orow) * out_row_bytes + static_cast<int64_t>(ncol) * sizeof(T);
     if (a.residual != nullptr) {
-      u32x4 r = *reinterpret_cast<const u32x4*>(a.residual + off);
-      T* pv = reinterpret_cast<T*>(&v);
-      const T* pr = reinterpret_cast<const T*>(&r);
-#pragma unroll
-      for (int e = 0; e < EPC; ++e) pv[e] = static_cast<T>(to_f32(pv[e]) + to_f32(pr[e]));
+      v = add_chunk<T>(v, *reinterpret_cast<const u32x4*>(a.residual + off));
     }
     *reinterpret_cast<u32x4*>(a.out + off) = v;
   }
@@ -497,11 +493,7 @@ __global__ __launch_bounds__(kPipeThreads) void conv_pipe_kernel(ConvArgs a) {
     u32x4 v = *reinterpret_cast<const u32x4*>(reinterpret_cast<const char*>(C) + (i * BN + cc * EPC) * sizeof(T));
     const int64_t off = static_cast<int64_t>(orow) * out_row_bytes + static_cast<int64_t>(ncol) * sizeof(T);
     if (a.residual != nullptr) {
-      u32x4 r = *reinterpret_cast<const u32x4*>(a.residual + off);
-      T* pv = reinterpret_cast<T*>(&v);
-      const T* pr = reinterpret_cast<const T*>(&r);
-#pragma unroll
-      for (int e = 0; e < EPC; ++e) pv[e] = static_cast<T>(to_f32(pv[e]) + to_f32(pr[e]));
+      v = add_chunk<T>(v, *reinterpret_cast<const u32x4*>(a.residual + off));
     }
     *reinterpret_cast<u32x4*>(a.out + off) = v;
   }
@@ -939,11 +931,7 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_ring_kernel(ConvArgs a) {
     u32x4 v = *reinterpret_cast<const u32x4*>(stg + row * ROWB + ((chunk ^ (row & (CPR - 1))) << 4));
     const int64_t off = static_cast<int64_t>(orow) * out_row_bytes + static_cast<int64_t>(cb + chunk * EPC) * ES;
     if (a.residual != nullptr) {
-      const u32x4 r = *reinterpret_cast<const u32x4*>(a.residual + off);
-      T* pv = reinterpret_cast<T*>(&v);
-      const T* pr = reinterpret_cast<const T*>(&r);
-#pragma unroll
-      for (int e = 0; e < EPC; ++e) pv[e] = static_cast<T>(to_f32(pv[e]) + to_f32(pr[e]));
+      v = add_chunk<T>(v, *reinterpret_cast<const u32x4*>(a.residual + off));
     }
     *reinterpret_cast<u32x4*>(a.out + off) = v;
   }
@@ -1540,10 +1528,7 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_wide_kernel(ConvArgs a) {
     if (!chunk_at(i, off)) continue;
     u32x4 v = *reinterpret_cast<const u32x4*>(stg + row * ROWB + ((chunk ^ (row & (CPR - 1))) << 4));
     if (a.residual != nullptr) {
-      T* pv = reinterpret_cast<T*>(&v);
-      const T* pr = reinterpret_cast<const T*>(&res[i]);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) pv[e] = static_cast<T>(to_f32(pv[e]) + to_f32(pr[e]));
+      v = add_chunk<T>(v, res[i]);
     }
     *reinterpret_cast<u32x4*>(a.out + off) = v;
   }
@@ -1839,10 +1824,7 @@ __global__ __launch_bounds__(512, 1) void conv_wide2_kernel(ConvArgs a) {
     if (!chunk_at(i, off)) continue;
     u32x4 v = *reinterpret_cast<const u32x4*>(stg + row * ROWB + ((chunk ^ (row & (CPR - 1))) << 4));
     if (a.residual != nullptr) {
-      T* pv = reinterpret_cast<T*>(&v);
-      const T* pr = reinterpret_cast<const T*>(&res[i]);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) pv[e] = static_cast<T>(to_f32(pv[e]) + to_f32(pr[e]));
+      v = add_chunk<T>(v, res[i]);
     }
     *reinterpret_cast<u32x4*>(a.out + off) = v;
   }

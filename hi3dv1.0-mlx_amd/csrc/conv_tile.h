@@ -9,6 +9,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 namespace hi3d {
 
 constexpr int kTileRows = 128;  // output rows per convolution tile
@@ -20,6 +22,25 @@ typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+
+// The residual add of the convolution epilogues on a 16-byte chunk: T(float(v) +
+// float(r)) per element. fp16 chunks add as 8 native fp16 adds (4 packed ops against 4
+// ops per element): fp32's 24 bits are at least 2 * 11 + 2, so the sum of two fp16
+// values rounded through fp32 and rounded once to fp16 agree.
+template <typename T>
+__device__ __forceinline__ u32x4 add_chunk(u32x4 v, u32x4 r) {
+  if constexpr (std::is_same_v<T, _Float16>) {
+#pragma clang fp contract(off)
+    return __builtin_bit_cast(u32x4, __builtin_bit_cast(f16x8, v) + __builtin_bit_cast(f16x8, r));
+  } else {
+    constexpr int kElems = 16 / static_cast<int>(sizeof(T));
+    T* pv = reinterpret_cast<T*>(&v);
+    const T* pr = reinterpret_cast<const T*>(&r);
+#pragma unroll
+    for (int e = 0; e < kElems; ++e) pv[e] = static_cast<T>(static_cast<float>(pv[e]) + static_cast<float>(pr[e]));
+    return v;
+  }
+}
 
 // SiLU of the convolution epilogues in fp32: x * sigmoid(x) with the sigmoid through the
 // hardware exp2 and reciprocal (v_exp_f32, v_rcp_f32; ~1 ulp each), 4 vector ops against

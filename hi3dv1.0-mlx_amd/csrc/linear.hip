@@ -133,17 +133,10 @@ __global__ __launch_bounds__(64 * S) void dense_linear_kernel(const _Float16* __
         h[e] = static_cast<_Float16>(lo[e] + bv[e]);
         h[e + 4] = static_cast<_Float16>(hi[e] + bv[e + 4]);
       }
-      if (residual != nullptr) {
-        _Float16 r[8];
-        __builtin_memcpy(r, &rv[i], 16);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) h[e] = static_cast<_Float16>(static_cast<float>(h[e]) + static_cast<float>(r[e]));
-      }
-      if (orow < n) {
-        u32x4 packed;
-        __builtin_memcpy(&packed, h, 16);
-        *reinterpret_cast<u32x4*>(out + orow * cout + c0 + ec) = packed;
-      }
+      u32x4 packed;
+      __builtin_memcpy(&packed, h, 16);
+      if (residual != nullptr) packed = add_chunk<_Float16>(packed, rv[i]);
+      if (orow < n) *reinterpret_cast<u32x4*>(out + orow * cout + c0 + ec) = packed;
     }
   }
 }
