@@ -611,7 +611,12 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_ring_kernel(ConvArgs a) {
   // the epilogue stages the whole output tile over the ring; past it lie the tile's
   // output rows, which the stores read
   static_assert(BM * BN * static_cast<int>(sizeof(T)) <= RING, "output tile must fit the ring");
-  __shared__ __attribute__((aligned(16))) char smem[RING + 3 * IDX + 256];
+  constexpr int kBiasDwords = BN * static_cast<int>(sizeof(T)) / 4;
+  constexpr int kBiasBytes = (kBiasDwords + 63) / 64 * 256;
+  // one LDS array (a second one makes the compiler wait for every direct-to-LDS load
+  // before each LDS read); the tile's bias sits at its end
+  __shared__ __attribute__((aligned(16))) char smem[RING + 3 * IDX + 256 + kBiasBytes];
+  char* const s_bias = smem + (RING + 3 * IDX + 256);
   char* const idx_ring = smem + RING;
   char* const rows_lds = idx_ring + 2 * IDX;  // the tile's output rows
   char* const idx_dummy = rows_lds + IDX;     // target of the index DMAs of stages entering no offset
@@ -622,6 +627,14 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_ring_kernel(ConvArgs a) {
   const int64_t item = xcd_remap(blockIdx.x, static_cast<int64_t>(gridDim.x));
   const int64_t tile = item / a.ny;
   const int n0 = static_cast<int>(item - tile * a.ny) * BN;
+  // the tile's bias reaches LDS by 4-byte DMAs before any stage is requested: the
+  // oldest loads, so the stage loop's constant waits still hold, and no register waits
+  // on them (the epilogue reads it after its wait for every load)
+  if (a.bias != nullptr && wave < (kBiasDwords + 63) / 64) {
+    const int d = wave * 64 + lane;
+    lds_dma4(static_cast<const char*>(a.bias) + static_cast<int64_t>(n0) * sizeof(T) + 4 * (d < kBiasDwords ? d : kBiasDwords - 1),
+             s_bias + wave * 256);
+  }
   const int kvol = a.kvol;
   uint32_t mask = 0;
 #pragma unroll
@@ -884,7 +897,7 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_ring_kernel(ConvArgs a) {
   // epilogue: each wave stages its (MB * 32) x (NB * 32) block
   wait_vmcnt<0>();
   __syncthreads();
-  const T* bias = static_cast<const T*>(a.bias);
+  const bool has_bias = a.bias != nullptr;
   constexpr int ES = static_cast<int>(sizeof(T));
   constexpr int EPC = 16 / ES;          // elements per 16-byte chunk
   constexpr int ROWB = NB * 32 * ES;    // staged row bytes
@@ -892,31 +905,41 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_ring_kernel(ConvArgs a) {
   using Quad = std::conditional_t<ES == 2, uint2, u32x4>;  // a lane's 4 consecutive channels
   char* stg = smem + wave * (MB * 32 * ROWB);
   const int cb = n0 + wn * NB * 32;
+  // convert (bias, the activation) and stage; the activation is chosen once, outside
+  // the element loops
+  auto stage_acc = [&](auto silu) {
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
+    for (int nb = 0; nb < NB; ++nb) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int j0 = nb * 32 + 8 * q + 4 * (lane >> 5);
-      float b[4];
+      for (int q = 0; q < 4; ++q) {
+        const int j0 = nb * 32 + 8 * q + 4 * (lane >> 5);
+        float b[4];
+        {
+          T bt[4];
+          __builtin_memcpy(bt, s_bias + ((cb - n0) + j0) * sizeof(T), sizeof(bt));
 #pragma unroll
-      for (int e = 0; e < 4; ++e) b[e] = bias != nullptr ? to_f32(bias[cb + j0 + e]) : 0.0f;
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb) {
-        const int row = mb * 32 + (lane & 31);
-        T h[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          float x = acc[nb][mb][4 * q + e] + b[e];
-          if (a.act == HI3D_ACT_SILU) x = silu_f32(x);
-          h[e] = static_cast<T>(x);
+          for (int e = 0; e < 4; ++e) b[e] = has_bias ? to_f32(bt[e]) : 0.0f;
         }
-        Quad packed;
-        __builtin_memcpy(&packed, h, sizeof(Quad));
-        const int byte = j0 * ES;  // 16-byte chunk byte / 16, offset byte % 16 inside it
-        *reinterpret_cast<Quad*>(stg + row * ROWB + (((byte >> 4) ^ (row & (CPR - 1))) << 4) + (byte & 15)) = packed;
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+          const int row = mb * 32 + (lane & 31);
+          T h[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float x = acc[nb][mb][4 * q + e] + b[e];
+            if constexpr (decltype(silu)::value) x = silu_f32(x);
+            h[e] = static_cast<T>(x);
+          }
+          Quad packed;
+          __builtin_memcpy(&packed, h, sizeof(Quad));
+          const int byte = j0 * ES;  // 16-byte chunk byte / 16, offset byte % 16 inside it
+          *reinterpret_cast<Quad*>(stg + row * ROWB + (((byte >> 4) ^ (row & (CPR - 1))) << 4) + (byte & 15)) = packed;
+        }
       }
     }
-  }
+  };
+  if (a.act == HI3D_ACT_SILU) stage_acc(std::true_type{});
+  else stage_acc(std::false_type{});
   wait_lgkm0();
   const int64_t out_row_bytes = static_cast<int64_t>(a.cout) * ES;
 #pragma unroll 4
@@ -1186,7 +1209,12 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_wide_kernel(ConvArgs a) {
   // stage per offset) four, two offsets ahead, so that a request has a whole stage to land
   constexpr int ISLOTS = K1 ? 4 : 2;
   constexpr int AHEAD = K1 ? 2 : 1;  // offsets between an index request and its use
-  __shared__ __attribute__((aligned(16))) char smem[NS * STAGE + (ISLOTS + 1) * IDX + 256];
+  constexpr int kBiasDwords = BN * static_cast<int>(sizeof(T)) / 4;
+  constexpr int kBiasBytes = (kBiasDwords + 63) / 64 * 256;
+  // one LDS array (a second one makes the compiler wait for every direct-to-LDS load
+  // before each LDS read); the tile's bias sits at its end
+  __shared__ __attribute__((aligned(16))) char smem[NS * STAGE + (ISLOTS + 1) * IDX + 256 + kBiasBytes];
+  char* const s_bias = smem + (NS * STAGE + (ISLOTS + 1) * IDX + 256);
   char* const idx_ring = smem + NS * STAGE;
   char* const rows_lds = idx_ring + ISLOTS * IDX;  // the tile's output rows
   char* const idx_dummy = rows_lds + IDX;     // target of the index DMA of stages entering no offset
@@ -1197,6 +1225,14 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_wide_kernel(ConvArgs a) {
   const int64_t item = xcd_remap(blockIdx.x, static_cast<int64_t>(gridDim.x));
   const int64_t tile = item / a.ny;
   const int n0 = static_cast<int>(item - tile * a.ny) * BN;
+  // the tile's bias reaches LDS by 4-byte DMAs before any stage is requested: the
+  // oldest loads, so the stage loop's constant waits still hold, and no register waits
+  // on them (the epilogue reads it after its wait for every load)
+  if (a.bias != nullptr && wave < (kBiasDwords + 63) / 64) {
+    const int d = wave * 64 + lane;
+    lds_dma4(static_cast<const char*>(a.bias) + static_cast<int64_t>(n0) * sizeof(T) + 4 * (d < kBiasDwords ? d : kBiasDwords - 1),
+             s_bias + wave * 256);
+  }
   const int kvol = a.kvol;
   uint32_t mask = 0;
 #pragma unroll
@@ -1400,7 +1436,7 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_wide_kernel(ConvArgs a) {
   // epilogue: each wave stages its 64 x (NB * 32) block
   wait_vmcnt<0>();
   __syncthreads();
-  const T* bias = static_cast<const T*>(a.bias);
+  const bool has_bias = a.bias != nullptr;
   constexpr int ROWB = NB * 64, CPR = NB * 4;
   char* stg = smem + wave * (64 * ROWB);
   const int cb = n0 + wn * NB * 32;
@@ -1426,30 +1462,40 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_wide_kernel(ConvArgs a) {
       res[i] = *reinterpret_cast<const u32x4*>(a.residual + (ok ? off : 0));
     }
   }
+  // convert (bias, the activation) and stage; the activation is chosen once, outside
+  // the element loops
+  auto stage_acc = [&](auto silu) {
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
+    for (int nb = 0; nb < NB; ++nb) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int j0 = nb * 32 + 8 * q + 4 * (lane >> 5);
-      float b[4];
+      for (int q = 0; q < 4; ++q) {
+        const int j0 = nb * 32 + 8 * q + 4 * (lane >> 5);
+        float b[4];
+        {
+          T bt[4];
+          __builtin_memcpy(bt, s_bias + ((cb - n0) + j0) * sizeof(T), sizeof(bt));
 #pragma unroll
-      for (int e = 0; e < 4; ++e) b[e] = bias != nullptr ? to_f32(bias[cb + j0 + e]) : 0.0f;
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb) {
-        const int row = mb * 32 + (lane & 31);
-        T h[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          float x = acc[nb][mb][4 * q + e] + b[e];
-          if (a.act == HI3D_ACT_SILU) x = silu_f32(x);
-          h[e] = static_cast<T>(x);
+          for (int e = 0; e < 4; ++e) b[e] = has_bias ? to_f32(bt[e]) : 0.0f;
         }
-        uint2 packed;
-        __builtin_memcpy(&packed, h, 8);
-        *reinterpret_cast<uint2*>(stg + row * ROWB + (((j0 >> 3) ^ (row & (CPR - 1))) << 4) + (j0 & 4) * 2) = packed;
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+          const int row = mb * 32 + (lane & 31);
+          T h[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float x = acc[nb][mb][4 * q + e] + b[e];
+            if constexpr (decltype(silu)::value) x = silu_f32(x);
+            h[e] = static_cast<T>(x);
+          }
+          uint2 packed;
+          __builtin_memcpy(&packed, h, 8);
+          *reinterpret_cast<uint2*>(stg + row * ROWB + (((j0 >> 3) ^ (row & (CPR - 1))) << 4) + (j0 & 4) * 2) = packed;
+        }
       }
     }
-  }
+  };
+  if (a.act == HI3D_ACT_SILU) stage_acc(std::true_type{});
+  else stage_acc(std::false_type{});
   wait_lgkm0();
   if constexpr (kLN) {
     // The res block's second norm on whole output rows (cout == BN == 128): each row's
@@ -1578,7 +1624,12 @@ __global__ __launch_bounds__(512, 1) void conv_wide2_kernel(ConvArgs a) {
   constexpr int MB = 2, NB = 4, NF = MB + NB, NM = MB * NB, LA = 4, LB = 4, L = LA + LB;
   static_assert(sizeof(T) == 2, "16-bit elements");
   static_assert(BM * BN * 2 <= NS * kW2Stage && LA * 8 * NW == BM && LB * 8 * NW == BN && L == NM, "shape");
-  __shared__ __attribute__((aligned(16))) char smem[NS * kW2Stage + 3 * kW2Idx + 256];
+  constexpr int kBiasDwords = BN * static_cast<int>(sizeof(T)) / 4;
+  constexpr int kBiasBytes = (kBiasDwords + 63) / 64 * 256;
+  // one LDS array (a second one makes the compiler wait for every direct-to-LDS load
+  // before each LDS read); the tile's bias sits at its end
+  __shared__ __attribute__((aligned(16))) char smem[NS * kW2Stage + 3 * kW2Idx + 256 + kBiasBytes];
+  char* const s_bias = smem + (NS * kW2Stage + 3 * kW2Idx + 256);
   char* const idx_ring = smem + NS * kW2Stage;
   char* const rows_lds = idx_ring + 2 * kW2Idx;  // the tile's output rows
   char* const idx_dummy = rows_lds + kW2Idx;     // target of the index DMA of stages entering no offset
@@ -1589,6 +1640,14 @@ __global__ __launch_bounds__(512, 1) void conv_wide2_kernel(ConvArgs a) {
   const int64_t item = xcd_remap(blockIdx.x, static_cast<int64_t>(gridDim.x));
   const int64_t tile = item / a.ny;
   const int n0 = static_cast<int>(item - tile * a.ny) * BN;
+  // the tile's bias reaches LDS by 4-byte DMAs before any stage is requested: the
+  // oldest loads, so the stage loop's constant waits still hold, and no register waits
+  // on them (the epilogue reads it after its wait for every load)
+  if (a.bias != nullptr && wave < (kBiasDwords + 63) / 64) {
+    const int d = wave * 64 + lane;
+    lds_dma4(static_cast<const char*>(a.bias) + static_cast<int64_t>(n0) * sizeof(T) + 4 * (d < kBiasDwords ? d : kBiasDwords - 1),
+             s_bias + wave * 256);
+  }
   const int kvol = a.kvol;
   uint32_t mask = 0;
 #pragma unroll
@@ -1765,7 +1824,7 @@ __global__ __launch_bounds__(512, 1) void conv_wide2_kernel(ConvArgs a) {
   // epilogue: each wave stages its 64 x 128 block
   wait_vmcnt<0>();
   __syncthreads();
-  const T* bias = static_cast<const T*>(a.bias);
+  const bool has_bias = a.bias != nullptr;
   constexpr int ROWB = NB * 64, CPR = NB * 4;
   char* stg = smem + wave * (64 * ROWB);
   const int cb = n0 + wn * NB * 32;
@@ -1791,30 +1850,40 @@ __global__ __launch_bounds__(512, 1) void conv_wide2_kernel(ConvArgs a) {
       res[i] = *reinterpret_cast<const u32x4*>(a.residual + (ok ? off : 0));
     }
   }
+  // convert (bias, the activation) and stage; the activation is chosen once, outside
+  // the element loops
+  auto stage_acc = [&](auto silu) {
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
+    for (int nb = 0; nb < NB; ++nb) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int j0 = nb * 32 + 8 * q + 4 * (lane >> 5);
-      float b[4];
+      for (int q = 0; q < 4; ++q) {
+        const int j0 = nb * 32 + 8 * q + 4 * (lane >> 5);
+        float b[4];
+        {
+          T bt[4];
+          __builtin_memcpy(bt, s_bias + ((cb - n0) + j0) * sizeof(T), sizeof(bt));
 #pragma unroll
-      for (int e = 0; e < 4; ++e) b[e] = bias != nullptr ? to_f32(bias[cb + j0 + e]) : 0.0f;
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb) {
-        const int row = mb * 32 + (lane & 31);
-        T h[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          float x = acc[nb][mb][4 * q + e] + b[e];
-          if (a.act == HI3D_ACT_SILU) x = silu_f32(x);
-          h[e] = static_cast<T>(x);
+          for (int e = 0; e < 4; ++e) b[e] = has_bias ? to_f32(bt[e]) : 0.0f;
         }
-        uint2 packed;
-        __builtin_memcpy(&packed, h, 8);
-        *reinterpret_cast<uint2*>(stg + row * ROWB + (((j0 >> 3) ^ (row & (CPR - 1))) << 4) + (j0 & 4) * 2) = packed;
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+          const int row = mb * 32 + (lane & 31);
+          T h[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float x = acc[nb][mb][4 * q + e] + b[e];
+            if constexpr (decltype(silu)::value) x = silu_f32(x);
+            h[e] = static_cast<T>(x);
+          }
+          uint2 packed;
+          __builtin_memcpy(&packed, h, 8);
+          *reinterpret_cast<uint2*>(stg + row * ROWB + (((j0 >> 3) ^ (row & (CPR - 1))) << 4) + (j0 & 4) * 2) = packed;
+        }
       }
     }
-  }
+  };
+  if (a.act == HI3D_ACT_SILU) stage_acc(std::true_type{});
+  else stage_acc(std::false_type{});
   wait_lgkm0();
 #pragma unroll
   for (int i = 0; i < CPR; ++i) {
@@ -2041,6 +2110,7 @@ int hi3d_gather_conv(const void* in, int64_t n_in, int32_t cin, const void* weig
   const uintptr_t align = reinterpret_cast<uintptr_t>(in) | reinterpret_cast<uintptr_t>(weight) |
                           reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(residual);
   HI3D_REQUIRE((align & 15) == 0, "feature, weight, residual and output pointers must be 16-byte aligned");
+  HI3D_REQUIRE((reinterpret_cast<uintptr_t>(bias) & 3) == 0, "the bias must be 4-byte aligned");
   ConvArgs a{};
   a.in = static_cast<const char*>(in);
   a.n_in = n_in;
@@ -2081,6 +2151,7 @@ int hi3d_gather_conv_ln_silu(const void* in, int64_t n_in, int32_t cin, const vo
                           reinterpret_cast<uintptr_t>(out) | reinterpret_cast<uintptr_t>(scale1p) |
                           reinterpret_cast<uintptr_t>(shift);
   HI3D_REQUIRE((align & 15) == 0, "feature, weight, output, scale and shift pointers must be 16-byte aligned");
+  HI3D_REQUIRE((reinterpret_cast<uintptr_t>(bias) & 3) == 0, "the bias must be 4-byte aligned");
   ConvArgs a{};
   a.in = static_cast<const char*>(in);
   a.n_in = n_in;

@@ -118,6 +118,12 @@ __device__ __forceinline__ void lds_dma16(const void* src, char* lds_wave_base) 
   __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(lds_wave_base), 16, 0, 0);
 }
 
+// 4-byte direct-to-LDS load (global_load_lds_dword): lane l's 4 bytes land at
+// lds_wave_base + 4 l.
+__device__ __forceinline__ void lds_dma4(const void* src, char* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(lds_wave_base), 4, 0, 0);
+}
+
 // XCD-aware block order: the chip deals workgroups round-robin over its 8 XCDs, so
 // block b runs on XCD b % 8. Remap so each XCD walks a contiguous range of work items
 // (neighbouring tiles share gathered rows and weights in that XCD's L2).
