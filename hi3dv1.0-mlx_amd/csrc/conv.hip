@@ -1443,24 +1443,25 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_wide_kernel(ConvArgs a) {
   const int64_t out_row_bytes = static_cast<int64_t>(a.cout) * sizeof(T);
   // chunk i of this lane: row lane / CPR + (64 / CPR) i of the wave's rows, 16-byte chunk
   // lane % CPR of its channels; false for rows past the plan or without an output row
-  auto chunk_at = [&](int i, int64_t& off) {
-    const int row = lane / CPR + (64 / CPR) * i;
-    const int tr = wm * 64 + row;
+  // the output rows of this lane's chunks, all read from LDS at once (one wait, not one
+  // per chunk)
+  int32_t orow[CPR];
+#pragma unroll
+  for (int i = 0; i < CPR; ++i) {
+    const int tr = wm * 64 + lane / CPR + (64 / CPR) * i;
     const int64_t pt = tile * SUB + tr / kTileRows;
-    const int32_t orow = pt < a.ntiles ? reinterpret_cast<const int32_t*>(rows_lds)[tr] : -1;
-    off = static_cast<int64_t>(orow) * out_row_bytes + static_cast<int64_t>(cb + (lane % CPR) * 8) * sizeof(T);
-    return orow >= 0 && orow < a.n_out;
+    orow[i] = pt < a.ntiles ? reinterpret_cast<const int32_t*>(rows_lds)[tr] : -1;
+  }
+  auto chunk_ok = [&](int i) { return orow[i] >= 0 && orow[i] < a.n_out; };
+  auto chunk_off = [&](int i) {
+    return static_cast<int64_t>(orow[i]) * out_row_bytes + static_cast<int64_t>(cb + (lane % CPR) * 8) * sizeof(T);
   };
   // the residual's chunks are requested before the accumulators are converted and
   // staged, so their latency overlaps that work instead of each group of stores
   u32x4 res[CPR];
   if (a.residual != nullptr) {
 #pragma unroll
-    for (int i = 0; i < CPR; ++i) {
-      int64_t off;
-      const bool ok = chunk_at(i, off);
-      res[i] = *reinterpret_cast<const u32x4*>(a.residual + (ok ? off : 0));
-    }
+    for (int i = 0; i < CPR; ++i) res[i] = *reinterpret_cast<const u32x4*>(a.residual + (chunk_ok(i) ? chunk_off(i) : 0));
   }
   // convert (bias, the activation) and stage; the activation is chosen once, outside
   // the element loops
@@ -1518,8 +1519,8 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_wide_kernel(ConvArgs a) {
     for (int pass = 0; pass < BM / (NW * 8); ++pass) {
       const int tr = pass * (NW * 8) + wave * 8 + (lane >> 3);  // tile row
       const int64_t pt = tile * SUB + tr / kTileRows;
-      const int32_t orow = pt < a.ntiles ? reinterpret_cast<const int32_t*>(rows_lds)[tr] : -1;
-      const bool live = orow >= 0 && orow < a.n_out;
+      const int32_t lrow = pt < a.ntiles ? reinterpret_cast<const int32_t*>(rows_lds)[tr] : -1;
+      const bool live = lrow >= 0 && lrow < a.n_out;
       const int wr = tr & 63;
       float v[2][8];
       float sum = 0.0f;
@@ -1549,7 +1550,7 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_wide_kernel(ConvArgs a) {
       sq += dpp_xor2(sq);
       sq += dpp_xor1(sq);
       const float inv = 1.0f / sqrtf(sq / c + a.ln_eps);
-      int b = live ? a.ln_coords[static_cast<int64_t>(orow) * 4] : 0;
+      int b = live ? a.ln_coords[static_cast<int64_t>(lrow) * 4] : 0;
       b = b < 0 ? 0 : (b >= a.ln_batches ? a.ln_batches - 1 : b);
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
@@ -1561,22 +1562,22 @@ __global__ __launch_bounds__(NW * 64, 1) void conv_wide_kernel(ConvArgs a) {
                       *reinterpret_cast<const f16x8*>(shift + b * BN + ch * 8));
 #pragma unroll
         for (int e = 0; e < 8; ++e) o[e] = silu_h(o[e]);
-        if (live) *reinterpret_cast<f16x8*>(a.out + (static_cast<int64_t>(orow) * BN + ch * 8) * 2) = o;
+        if (live) *reinterpret_cast<f16x8*>(a.out + (static_cast<int64_t>(lrow) * BN + ch * 8) * 2) = o;
       }
     }
     return;
   }
+  // every staged chunk is read before the first store (one LDS wait)
+  u32x4 v[CPR];
 #pragma unroll
   for (int i = 0; i < CPR; ++i) {
     const int row = lane / CPR + (64 / CPR) * i;  // 0..63 within this wave's rows
-    const int chunk = lane % CPR;
-    int64_t off;
-    if (!chunk_at(i, off)) continue;
-    u32x4 v = *reinterpret_cast<const u32x4*>(stg + row * ROWB + ((chunk ^ (row & (CPR - 1))) << 4));
-    if (a.residual != nullptr) {
-      v = add_chunk<T>(v, res[i]);
-    }
-    *reinterpret_cast<u32x4*>(a.out + off) = v;
+    v[i] = *reinterpret_cast<const u32x4*>(stg + row * ROWB + (((lane % CPR) ^ (row & (CPR - 1))) << 4));
+  }
+#pragma unroll
+  for (int i = 0; i < CPR; ++i) {
+    if (a.residual != nullptr) v[i] = add_chunk<T>(v[i], res[i]);
+    if (chunk_ok(i)) *reinterpret_cast<u32x4*>(a.out + chunk_off(i)) = v[i];
   }
 }
 
@@ -1831,24 +1832,25 @@ __global__ __launch_bounds__(512, 1) void conv_wide2_kernel(ConvArgs a) {
   const int64_t out_row_bytes = static_cast<int64_t>(a.cout) * sizeof(T);
   // chunk i of this lane: row lane / CPR + (64 / CPR) i of the wave's rows, 16-byte chunk
   // lane % CPR of its channels; false for rows past the plan or without an output row
-  auto chunk_at = [&](int i, int64_t& off) {
-    const int row = lane / CPR + (64 / CPR) * i;
-    const int tr = wm * 64 + row;
+  // the output rows of this lane's chunks, all read from LDS at once (one wait, not one
+  // per chunk)
+  int32_t orow[CPR];
+#pragma unroll
+  for (int i = 0; i < CPR; ++i) {
+    const int tr = wm * 64 + lane / CPR + (64 / CPR) * i;
     const int64_t pt = tile * SUB + tr / kTileRows;
-    const int32_t orow = pt < a.ntiles ? reinterpret_cast<const int32_t*>(rows_lds)[tr] : -1;
-    off = static_cast<int64_t>(orow) * out_row_bytes + static_cast<int64_t>(cb + (lane % CPR) * 8) * sizeof(T);
-    return orow >= 0 && orow < a.n_out;
+    orow[i] = pt < a.ntiles ? reinterpret_cast<const int32_t*>(rows_lds)[tr] : -1;
+  }
+  auto chunk_ok = [&](int i) { return orow[i] >= 0 && orow[i] < a.n_out; };
+  auto chunk_off = [&](int i) {
+    return static_cast<int64_t>(orow[i]) * out_row_bytes + static_cast<int64_t>(cb + (lane % CPR) * 8) * sizeof(T);
   };
   // the residual's chunks are requested before the accumulators are converted and
   // staged, so their latency overlaps that work instead of each group of stores
   u32x4 res[CPR];
   if (a.residual != nullptr) {
 #pragma unroll
-    for (int i = 0; i < CPR; ++i) {
-      int64_t off;
-      const bool ok = chunk_at(i, off);
-      res[i] = *reinterpret_cast<const u32x4*>(a.residual + (ok ? off : 0));
-    }
+    for (int i = 0; i < CPR; ++i) res[i] = *reinterpret_cast<const u32x4*>(a.residual + (chunk_ok(i) ? chunk_off(i) : 0));
   }
   // convert (bias, the activation) and stage; the activation is chosen once, outside
   // the element loops
@@ -1885,17 +1887,17 @@ __global__ __launch_bounds__(512, 1) void conv_wide2_kernel(ConvArgs a) {
   if (a.act == HI3D_ACT_SILU) stage_acc(std::true_type{});
   else stage_acc(std::false_type{});
   wait_lgkm0();
+  // every staged chunk is read before the first store (one LDS wait)
+  u32x4 v[CPR];
 #pragma unroll
   for (int i = 0; i < CPR; ++i) {
     const int row = lane / CPR + (64 / CPR) * i;  // 0..63 within this wave's rows
-    const int chunk = lane % CPR;
-    int64_t off;
-    if (!chunk_at(i, off)) continue;
-    u32x4 v = *reinterpret_cast<const u32x4*>(stg + row * ROWB + ((chunk ^ (row & (CPR - 1))) << 4));
-    if (a.residual != nullptr) {
-      v = add_chunk<T>(v, res[i]);
-    }
-    *reinterpret_cast<u32x4*>(a.out + off) = v;
+    v[i] = *reinterpret_cast<const u32x4*>(stg + row * ROWB + (((lane % CPR) ^ (row & (CPR - 1))) << 4));
+  }
+#pragma unroll
+  for (int i = 0; i < CPR; ++i) {
+    if (a.residual != nullptr) v[i] = add_chunk<T>(v[i], res[i]);
+    if (chunk_ok(i)) *reinterpret_cast<u32x4*>(a.out + chunk_off(i)) = v[i];
   }
 }
 
