@@ -76,13 +76,38 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def timed(fn, steps: int, warmup: int):
-    """(ms per call from host clock around `steps` calls, mean per-call ms from events)."""
+SETTLE_EACH_S = 0.3
+"""Seconds of untimed calls before each timed measurement (after its warm-up): the shader
+clock ramps under sustained load, and a few warm-up calls of a sub-millisecond kernel do
+not reach it (the C128 layer: 0.44 ms per call after 5 warm-up calls, 0.39 ms after
+2 s of calls on the same box)."""
+
+
+def settle(fn, seconds: float) -> None:
+    """Call fn repeatedly for about `seconds`, synchronising at least every 10 calls (so
+    the host never queues far ahead of the GPU) and stopping at the first call that ends
+    past the deadline (so an expensive call is not repeated ten times)."""
+    import torch
+
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end:
+        for _ in range(10):
+            fn()
+            if time.perf_counter() >= t_end:
+                break
+        torch.cuda.synchronize()
+
+
+def timed(fn, steps: int, warmup: int, settle_s: float | None = None):
+    """(ms per call from host clock around `steps` calls, mean per-call ms from events).
+    settle_s: seconds of untimed calls after the warm-up (default SETTLE_EACH_S; 0 for a
+    call that consumes its input)."""
     import torch
 
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
+    settle(fn, SETTLE_EACH_S if settle_s is None else settle_s)
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
     t0 = time.perf_counter()
@@ -105,6 +130,7 @@ def timed_batch(fn, steps: int, warmup: int) -> float:
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
+    settle(fn, SETTLE_EACH_S)
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     for _ in range(steps):
@@ -438,7 +464,7 @@ def bench_vae(steps: int, warmup: int):
                                                    torch.float16), steps, warmup)
     b_wall, b_ev = timed(lambda: vae.resnet(x, level, p, "v"), max(3, steps // 5), max(1, warmup // 2))
     pool = [x.clone() for _ in range(6)]  # each in-place call consumes its input
-    ip_wall, _ = timed(lambda: vae.resnet([pool.pop()], level, p, "v"), 5, 1)
+    ip_wall, _ = timed(lambda: vae.resnet([pool.pop()], level, p, "v"), 5, 1, settle_s=0.0)
     pairs = int((level.table < n).sum())
     return {
         "workload": "vae_resnet_c128_fp16",
@@ -663,12 +689,15 @@ WORKLOADS = ("resblock", "subm3_c128_fp16", "subm3_c64_fp32", "stride2", "w8a8",
 
 
 def main() -> int:
+    global SETTLE_EACH_S
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--settle", type=float, default=2.0,
                     help="seconds of untimed headline passes before its warm-up (clock ramp)")
+    ap.add_argument("--settle-each", type=float, default=SETTLE_EACH_S,
+                    help="seconds of untimed calls before each other timed measurement")
     ap.add_argument("--only", default="", help=f"comma-separated workloads to run, of {', '.join(WORKLOADS)}")
     ap.add_argument("--quick", action="store_true", help="headline workload only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
@@ -676,6 +705,7 @@ def main() -> int:
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (calibrates HBM byte counters) and exit")
     args = ap.parse_args()
+    SETTLE_EACH_S = max(0.0, args.settle_each)
     if args.copy_probe:
         import torch
 
