@@ -89,6 +89,27 @@ struct Grid {
   __device__ __forceinline__ int corner(int x, int y, int z) const {
     return ((x & 1) << 2) | ((y & 1) << 1) | (z & 1);
   }
+  // brick key from brick coordinates (in range)
+  __device__ __forceinline__ uint64_t brick_key(int b, int64_t bx, int64_t by, int64_t bz) const {
+    const uint64_t hx = (static_cast<uint64_t>(sx) + 1) >> 1, hy = (static_cast<uint64_t>(sy) + 1) >> 1,
+                   hz = (static_cast<uint64_t>(sz) + 1) >> 1;
+    return ((static_cast<uint64_t>(b) * hx + bx) * hy + by) * hz + bz;
+  }
+  // the 4x4x4-brick superblock (8x8x8 cells) holding a brick, packed over the quartered
+  // brick extents
+  __device__ __forceinline__ uint64_t superblock(int b, int64_t bx, int64_t by, int64_t bz) const {
+    const uint64_t qx = ((static_cast<uint64_t>(sx) + 1) / 2 + 3) >> 2,
+                   qy = ((static_cast<uint64_t>(sy) + 1) / 2 + 3) >> 2,
+                   qz = ((static_cast<uint64_t>(sz) + 1) / 2 + 3) >> 2;
+    return ((static_cast<uint64_t>(b) * qx + (bx >> 2)) * qy + (by >> 2)) * qz + (bz >> 2);
+  }
+  // home bucket of a brick: the superblock's run of 64 buckets (at a hashed, aligned
+  // start) at the brick's place in the superblock, so the words and rows of neighbouring
+  // bricks share cache lines
+  __device__ __forceinline__ uint64_t brick_home(int b, int64_t bx, int64_t by, int64_t bz, uint64_t mask) const {
+    const uint64_t local = static_cast<uint64_t>(((bx & 3) << 4) | ((by & 3) << 2) | (bz & 3));
+    return ((mix64(superblock(b, bx, by, bz)) << 6) | local) & mask;
+  }
   // voxel-slot home: the cell's corner within a run of 8 slots per brick
   __device__ __forceinline__ uint64_t home(int b, int x, int y, int z, uint64_t mask) const {
     return ((mix64(brick(b, x, y, z)) << 3) | static_cast<uint64_t>(corner(x, y, z))) & mask;
@@ -287,7 +308,8 @@ __global__ __launch_bounds__(256) void probe_kernel(const int4* __restrict__ coo
 
 // ------------------------------------------------------------- brick hash --
 // The map build's hash (hi3d_kmap_subm): one bucket per occupied 2x2x2 brick, open
-// addressing with linear probing over buckets. A bucket is one 64-bit word, the brick
+// addressing over buckets (homes grouped per 8x8x8-cell superblock, collisions by double
+// hashing; see brick_home and brick_step). A bucket is one 64-bit word, the brick
 // key shifted left by 8 with the occupancy mask of its 8 cells in the low byte, plus the
 // rows of its 8 cells (rows[8 h ..], valid where the mask bit is set, so only the words
 // are cleared per build). A row's 26 neighbours lie in 8 bricks; a lookup reads one word
@@ -301,45 +323,103 @@ struct BrickTable {
   uint64_t mask;
 };
 
-// perm (optional): rows perm[0 ..] in cell order (a negative entry stands for an
-// out-of-range row, already flagged)
-__global__ void brick_insert_kernel(const int4* __restrict__ coords, int64_t n, Grid g,
-                                    const int32_t* __restrict__ perm, BrickTable t, int32_t* __restrict__ status) {
-  int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i >= n) return;
-  if (perm != nullptr) {
-    const int32_t p = perm[i];
-    if (p < 0) return;
-    i = p;
-  }
-  const int4 c = coords[i];
-  if (!g.inside(c.x, c.y, c.z, c.w)) {
-    atomicOr(status, HI3D_MAP_RANGE);
-    return;
-  }
-  const unsigned long long bk = g.brick(c.x, c.y, c.z, c.w);
-  uint64_t h = mix64(bk) & t.mask;
-  for (uint64_t probe = 0; probe <= t.mask; ++probe) {
-    const unsigned long long prev = atomicCAS(&t.words[h], kEmptyBrick, bk << 8);
-    if (prev == kEmptyBrick || (prev >> 8) == bk) {
-      const int cn = g.corner(c.y, c.z, c.w);
-      t.rows[h * 8 + cn] = static_cast<int32_t>(i);
-      const unsigned long long old = atomicOr(&t.words[h], 1ull << cn);
-      if (old & (1ull << cn)) atomicOr(status, HI3D_MAP_DUPLICATE);
-      return;
-    }
-    h = (h + 1) & t.mask;
-  }
-  atomicOr(status, HI3D_MAP_OVERFLOW);
+// Collisions probe by double hashing: from the home on in steps of an odd stride drawn
+// from the brick key (so the probe sequence visits every bucket of the power-of-two
+// table). Linear probing from the clustered superblock runs made long chains.
+__device__ __forceinline__ uint64_t brick_step(unsigned long long bk, uint64_t mask) {
+  return (mix64(bk ^ 0x9E3779B97F4A7C15ull) | 1ull) & mask;
 }
 
-// bucket of brick bk from slot h on (h's key already known to differ), or -1
-__device__ __forceinline__ int64_t brick_find(const BrickTable& t, uint64_t h, unsigned long long bk) {
-  for (uint64_t probe = 0; probe <= t.mask; ++probe) {
+__device__ __forceinline__ unsigned long long shfl_u64(unsigned long long v, int src) {
+  const uint32_t lo = static_cast<uint32_t>(__shfl(static_cast<int>(static_cast<uint32_t>(v)), src, 64));
+  const uint32_t hi = static_cast<uint32_t>(__shfl(static_cast<int>(static_cast<uint32_t>(v >> 32)), src, 64));
+  return (static_cast<unsigned long long>(hi) << 32) | lo;
+}
+
+// perm (optional): rows perm[0 ..] in superblock order (a negative entry stands for an
+// out-of-range row, already flagged). The lanes of a wave are grouped by brick first (a
+// wave-uniform loop over its distinct bricks): one lane per brick claims or finds the
+// bucket with a CAS and ORs in the occupancy bits of all its lanes, and every lane
+// stores its row in its cell's slot. A cell set twice, inside the wave or by the
+// atomicOr's old bits, is a repeated coordinate.
+__global__ __launch_bounds__(256) void brick_insert_kernel(const int4* __restrict__ coords, int64_t n, Grid g,
+                                                           const int32_t* __restrict__ perm, BrickTable t,
+                                                           int32_t* __restrict__ status) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int lane = static_cast<int>(threadIdx.x & 63);
+  bool act = i < n;
+  int64_t row = i;
+  if (act && perm != nullptr) {
+    const int32_t pp = perm[i];
+    act = pp >= 0;
+    row = pp;
+  }
+  int4 c = act ? coords[row] : make_int4(0, 0, 0, 0);
+  if (act && !g.inside(c.x, c.y, c.z, c.w)) {
+    atomicOr(status, HI3D_MAP_RANGE);
+    act = false;
+  }
+  const unsigned long long bk = act ? g.brick(c.x, c.y, c.z, c.w) : kEmptyBrick;
+  const int cn = act ? g.corner(c.y, c.z, c.w) : 0;
+  // group the wave's lanes by brick: `leader` is the first lane of this lane's brick,
+  // `run` (at a leader) the lanes of its brick
+  unsigned long long todo = __ballot(act);
+  int leader = lane;
+  unsigned long long run = 0;
+  while (todo) {
+    const int l = __ffsll(static_cast<long long>(todo)) - 1;
+    const unsigned long long kl = shfl_u64(bk, l);
+    const unsigned long long same = __ballot(act && bk == kl) & todo;
+    if ((same >> lane) & 1ull) leader = l;
+    if (lane == l) run = same;
+    todo &= ~same;
+  }
+  unsigned long long cell[8];
+#pragma unroll
+  for (int b = 0; b < 8; ++b) cell[b] = __ballot(act && cn == b);
+  unsigned long long h = 0;
+  bool ok = true;
+  if (act && leader == lane) {
+    uint32_t bits = 0;
+    bool dup = false;
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      const unsigned long long in_run = cell[b] & run;
+      if (in_run) bits |= 1u << b;
+      if (__popcll(in_run) > 1) dup = true;
+    }
+    h = g.brick_home(c.x, c.y >> 1, c.z >> 1, c.w >> 1, t.mask);
+    const uint64_t step = brick_step(bk, t.mask);
+    ok = false;
+    for (uint64_t probe = 0; probe <= t.mask; ++probe) {
+      const unsigned long long prev = atomicCAS(&t.words[h], kEmptyBrick, bk << 8);
+      if (prev == kEmptyBrick || (prev >> 8) == bk) {
+        ok = true;
+        break;
+      }
+      h = (h + step) & t.mask;
+    }
+    if (ok) {
+      const unsigned long long old = atomicOr(&t.words[h], static_cast<unsigned long long>(bits));
+      if ((old & bits) || dup) atomicOr(status, HI3D_MAP_DUPLICATE);
+    } else {
+      atomicOr(status, HI3D_MAP_OVERFLOW);
+    }
+  }
+  h = shfl_u64(h, leader);
+  ok = __shfl(static_cast<int>(ok), leader, 64) != 0;
+  if (act && ok) t.rows[h * 8 + cn] = static_cast<int32_t>(row);
+}
+
+// bucket of brick bk past its home h0 (whose key is already known to differ), or -1
+__device__ __forceinline__ int64_t brick_find(const BrickTable& t, uint64_t h0, unsigned long long bk) {
+  const uint64_t step = brick_step(bk, t.mask);
+  uint64_t h = (h0 + step) & t.mask;
+  for (uint64_t probe = 0; probe < t.mask; ++probe) {
     const unsigned long long w = t.words[h];
     if (w == kEmptyBrick) return -1;
     if ((w >> 8) == bk) return static_cast<int64_t>(h);
-    h = (h + 1) & t.mask;
+    h = (h + step) & t.mask;
   }
   return -1;
 }
@@ -396,7 +476,7 @@ __global__ __launch_bounds__(256) void brick_probe_kernel(const int4* __restrict
         if (k != center && g.inside(c.x, x, y, z)) {
           look[u] = true;
           bk[u] = g.brick(c.x, x, y, z);
-          h[u] = mix64(bk[u]) & t.mask;
+          h[u] = g.brick_home(c.x, x >> 1, y >> 1, z >> 1, t.mask);
           cn[u] = g.corner(x, y, z);
         }
       }
@@ -414,7 +494,7 @@ __global__ __launch_bounds__(256) void brick_probe_kernel(const int4* __restrict
           hb[u] = static_cast<int64_t>(h[u]);
           m[u] = static_cast<uint32_t>(kv[u] & 0xFFu);
         } else {
-          hb[u] = brick_find(t, (h[u] + 1) & t.mask, bk[u]);
+          hb[u] = brick_find(t, h[u], bk[u]);
           if (hb[u] >= 0) m[u] = static_cast<uint32_t>(t.words[hb[u]] & 0xFFu);
         }
       }
@@ -437,6 +517,138 @@ __global__ __launch_bounds__(256) void brick_probe_kernel(const int4* __restrict
   __syncthreads();
   for (int k = threadIdx.x; k < kvol; k += blockDim.x)
     if (cnt[k]) atomicAdd(&counts[k], cnt[k]);
+}
+
+// The 3x3x3 probe: 8 lanes per row, lane l reading one of the 8 bricks that hold the
+// row's 27 cells (bit 2 of l: the upper brick along x, bit 1: y, bit 0: z), so a row
+// costs 8 bucket-word loads; each lane then resolves offsets l, l + 8, l + 16, l + 24
+// from its row's 8 (mask, bucket) pairs (lane exchanges) and loads the rows of the
+// present ones. A lane group carries kBrick3Per rows (32 rows apart), issuing their
+// loads together, so kBrick3Per word loads and up to 4 kBrick3Per row loads per lane are
+// in flight. The block's table rows are staged in LDS and written out whole. perm and
+// per as in brick_probe_kernel, over blocks of kBrick3Rows rows.
+constexpr int kBrick3Per = 4;
+constexpr int kBrick3Rows = 32 * kBrick3Per;
+
+__global__ __launch_bounds__(256) void brick_probe3_kernel(const int4* __restrict__ coords, int64_t n, Grid g,
+                                                           const int32_t* __restrict__ perm, int per, BrickTable t,
+                                                           int32_t* __restrict__ nbr, int32_t* __restrict__ counts) {
+  constexpr int P = kBrick3Per;
+  __shared__ int32_t cnt[27];
+  __shared__ int32_t stage[kBrick3Rows * 27];
+  __shared__ int32_t srow[kBrick3Rows];
+  const int64_t chunk = perm != nullptr ? static_cast<int64_t>(blockIdx.x % 8) * per + blockIdx.x / 8 : blockIdx.x;
+  const int64_t row0 = chunk * kBrick3Rows;
+  if (row0 >= n) return;  // the XCD order's spare blocks (before any barrier)
+  if (threadIdx.x < 27) cnt[threadIdx.x] = 0;
+  const int lane = threadIdx.x & 7;
+  const int slot0 = threadIdx.x >> 3;  // the group's first row in the block; rows slot0 + 32 i
+  const int group = static_cast<int>(threadIdx.x & 63) & ~7;  // the group's first lane in the wave
+  const int64_t hx = (static_cast<int64_t>(g.sx) + 1) >> 1, hy = (static_cast<int64_t>(g.sy) + 1) >> 1,
+                hz = (static_cast<int64_t>(g.sz) + 1) >> 1;
+  bool valid[P];
+  int32_t o[P];
+  int4 c[P];
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+    const int64_t r = row0 + slot0 + 32 * i;
+    valid[i] = r < n;
+    int64_t oo = valid[i] ? r : 0;
+    if (perm != nullptr && valid[i]) {
+      const int32_t pp = perm[r];
+      oo = pp >= 0 ? pp : ~pp;
+    }
+    o[i] = static_cast<int32_t>(oo);
+  }
+#pragma unroll
+  for (int i = 0; i < P; ++i) c[i] = valid[i] ? coords[o[i]] : make_int4(-1, 0, 0, 0);
+  // lowest of the row's 2 x 2 x 2 neighbour bricks along each axis, and the lane's brick
+  int64_t base_x[P], base_y[P], base_z[P];
+  uint64_t h[P];
+  unsigned long long bk[P], w[P];
+  bool in[P];
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+    base_x[i] = (static_cast<int64_t>(c[i].y) >> 1) - 1 + (c[i].y & 1);
+    base_y[i] = (static_cast<int64_t>(c[i].z) >> 1) - 1 + (c[i].z & 1);
+    base_z[i] = (static_cast<int64_t>(c[i].w) >> 1) - 1 + (c[i].w & 1);
+    const int64_t bx = base_x[i] + ((lane >> 2) & 1), by = base_y[i] + ((lane >> 1) & 1), bz = base_z[i] + (lane & 1);
+    in[i] = valid[i] && static_cast<unsigned>(c[i].x) < static_cast<unsigned>(g.batch) && bx >= 0 && bx < hx &&
+            by >= 0 && by < hy && bz >= 0 && bz < hz;
+    bk[i] = in[i] ? g.brick_key(c[i].x, bx, by, bz) : 0ull;
+    h[i] = in[i] ? g.brick_home(c[i].x, bx, by, bz, t.mask) : 0ull;
+  }
+#pragma unroll
+  for (int i = 0; i < P; ++i) w[i] = in[i] ? t.words[h[i]] : kEmptyBrick;
+  uint64_t hb[P];
+  uint32_t m[P];
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+    hb[i] = 0;
+    m[i] = 0;
+    if (w[i] != kEmptyBrick) {
+      if ((w[i] >> 8) == bk[i]) {
+        hb[i] = h[i];
+        m[i] = static_cast<uint32_t>(w[i] & 0xFFu);
+      } else {
+        const int64_t f = brick_find(t, h[i], bk[i]);
+        if (f >= 0) {
+          hb[i] = static_cast<uint64_t>(f);
+          m[i] = static_cast<uint32_t>(t.words[f] & 0xFFu);
+        }
+      }
+    }
+  }
+  const int32_t absent = static_cast<int32_t>(n);
+  int32_t found[P][4];
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int k = lane + 8 * u;  // k = 9 (dx + 1) + 3 (dy + 1) + (dz + 1)
+      const int kk = k < 27 ? k : 0;
+      const int64_t nx = static_cast<int64_t>(c[i].y) + kk / 9 - 1, ny = static_cast<int64_t>(c[i].z) + (kk / 3) % 3 - 1,
+                    nz = static_cast<int64_t>(c[i].w) + kk % 3 - 1;
+      // the neighbour's brick among the row's 8: 0 or 1 along each axis
+      const int j = static_cast<int>(
+          ((((nx >> 1) - base_x[i]) << 2) | (((ny >> 1) - base_y[i]) << 1) | ((nz >> 1) - base_z[i])) & 7);
+      const int src = group + j;
+      const uint32_t mj = static_cast<uint32_t>(__shfl(static_cast<int>(m[i]), src, 64));
+      const uint32_t hlo = static_cast<uint32_t>(__shfl(static_cast<int>(static_cast<uint32_t>(hb[i])), src, 64));
+      const uint32_t hhi = static_cast<uint32_t>(__shfl(static_cast<int>(static_cast<uint32_t>(hb[i] >> 32)), src, 64));
+      const int cn = static_cast<int>(((nx & 1) << 2) | ((ny & 1) << 1) | (nz & 1));
+      found[i][u] = absent;
+      if (valid[i] && k < 27 && k != 13 && ((mj >> cn) & 1u))
+        found[i][u] = t.rows[((static_cast<uint64_t>(hhi) << 32) | hlo) * 8 + cn];
+    }
+  }
+  __syncthreads();  // cnt cleared
+#pragma unroll
+  for (int i = 0; i < P; ++i) {
+    const int lr = slot0 + 32 * i;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int k = lane + 8 * u;
+      if (k == 13) found[i][u] = o[i];
+      const bool present = valid[i] && k < 27 && found[i][u] != absent;
+      const unsigned long long ball = __ballot(present);
+      if (k < 27) stage[lr * 27 + k] = found[i][u];
+      // lane l of the wave's first group sums offset l + 8 u over the wave's 8 rows
+      if ((threadIdx.x & 63) < 8 && k < 27) {
+        const int c8 = __popcll(ball & (0x0101010101010101ull << lane));
+        if (c8) atomicAdd(&cnt[k], c8);
+      }
+    }
+    if (lane == 0) srow[lr] = valid[i] ? o[i] : -1;
+  }
+  __syncthreads();
+  // whole rows: consecutive threads write consecutive entries of a row
+  for (int e = threadIdx.x; e < kBrick3Rows * 27; e += blockDim.x) {
+    const int rr = e / 27;
+    const int32_t orow = srow[rr];
+    if (orow >= 0) nbr[static_cast<int64_t>(orow) * 27 + (e - rr * 27)] = stage[e];
+  }
+  if (threadIdx.x < 27 && cnt[threadIdx.x]) atomicAdd(&counts[threadIdx.x], cnt[threadIdx.x]);
 }
 
 // Dense-grid variant for grids of at most kDenseMaxCells cells: one int32 cell per grid
@@ -489,6 +701,20 @@ __global__ void order_key_kernel(const int4* __restrict__ coords, int64_t n, Gri
   const int4 c = coords[i];
   const bool in = g.inside(c.x, c.y, c.z, c.w);
   keys[i] = in ? static_cast<uint32_t>(g.key(c.x, c.y, c.z, c.w) >> shift) : 0u;
+  rows[i] = in ? static_cast<int32_t>(i) : ~static_cast<int32_t>(i);
+  if (!in) atomicOr(status, HI3D_MAP_RANGE);
+}
+
+// Brick-hash order: rows by superblock (8x8x8 cells; key >> shift), so consecutive rows
+// insert into and probe the same runs of buckets.
+__global__ void superblock_key_kernel(const int4* __restrict__ coords, int64_t n, Grid g, int shift,
+                                      uint32_t* __restrict__ keys, int32_t* __restrict__ rows,
+                                      int32_t* __restrict__ status) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int4 c = coords[i];
+  const bool in = g.inside(c.x, c.y, c.z, c.w);
+  keys[i] = in ? static_cast<uint32_t>(g.superblock(c.x, c.y >> 1, c.z >> 1, c.w >> 1) >> shift) : 0u;
   rows[i] = in ? static_cast<int32_t>(i) : ~static_cast<int32_t>(i);
   if (!in) atomicOr(status, HI3D_MAP_RANGE);
 }
@@ -1132,32 +1358,36 @@ static int kmap_subm_brick(const int32_t* coords, int64_t n, Grid g, int32_t ksi
   const int4* c4 = reinterpret_cast<const int4*>(coords);
   const int32_t* perm = nullptr;
   int per = 0;
-  int64_t probe_blocks = ceil_div(n, kProbeRows);
+  int64_t probe_blocks = ceil_div(n, ksize == 3 ? kBrick3Rows : kProbeRows);
   if (brick_table_bytes(cap) > kBrickOrderMinBytes) {
     const int64_t slab = align_up(n * 4, 256);
     auto* k0 = reinterpret_cast<uint32_t*>(order);
     auto* k1 = reinterpret_cast<uint32_t*>(order + slab);
     auto* r0 = reinterpret_cast<int32_t*>(order + 2 * slab);
     auto* r1 = reinterpret_cast<int32_t*>(order + 3 * slab);
-    const uint64_t cells = static_cast<uint64_t>(g.batch) * g.sx * g.sy * g.sz;
+    const uint64_t q = static_cast<uint64_t>(g.batch) * ((((static_cast<uint64_t>(g.sx) + 1) / 2) + 3) >> 2) *
+                       ((((static_cast<uint64_t>(g.sy) + 1) / 2) + 3) >> 2) *
+                       ((((static_cast<uint64_t>(g.sz) + 1) / 2) + 3) >> 2);
     int key_bits = 1;
-    while (key_bits < 64 && (uint64_t(1) << key_bits) < cells) ++key_bits;
+    while (key_bits < 64 && (uint64_t(1) << key_bits) < q) ++key_bits;
     const int shift = key_bits > 32 ? key_bits - 32 : 0;
     const int kb = key_bits - shift;
-    hipLaunchKernelGGL(order_key_kernel, dim3(blocks), dim3(256), 0, stream, c4, n, g, shift, k0, r0, status);
-    // two radix passes over the key's top 16 bits (batch, x, y bands)
+    hipLaunchKernelGGL(superblock_key_kernel, dim3(blocks), dim3(256), 0, stream, c4, n, g, shift, k0, r0, status);
+    // radix passes over the superblock key's top 24 bits
     HI3D_HIP_CHECK(radix::sort_pairs(order + 4 * slab, radix::temp_bytes(n), k0, k1, r0, r1, n,
-                                     kb > 16 ? kb - 16 : 0, kb, stream));
+                                     kb > 24 ? kb - 24 : 0, kb, stream));
     perm = r0;
     per = static_cast<int>(ceil_div(probe_blocks, kXcds));
     probe_blocks = static_cast<int64_t>(per) * kXcds;
   }
   launch_fill<unsigned long long>(t.words, cap, kEmptyBrick, stream);
   hipLaunchKernelGGL(brick_insert_kernel, dim3(blocks), dim3(256), 0, stream, c4, n, g, perm, t, status);
-  // (one row per thread, its 8 buckets' keys, masks and rows in registers, measured
-  // slower on the config-5 shells: 1.74 against 1.60 ms for the whole build)
-  hipLaunchKernelGGL(brick_probe_kernel, dim3(static_cast<unsigned>(probe_blocks)), dim3(256), 0, stream, c4, n, g,
-                     ksize, perm, per, t, nbr, counts);
+  if (ksize == 3)
+    hipLaunchKernelGGL(brick_probe3_kernel, dim3(static_cast<unsigned>(probe_blocks)), dim3(256), 0, stream, c4, n, g,
+                       perm, per, t, nbr, counts);
+  else
+    hipLaunchKernelGGL(brick_probe_kernel, dim3(static_cast<unsigned>(probe_blocks)), dim3(256), 0, stream, c4, n, g,
+                       ksize, perm, per, t, nbr, counts);
   HI3D_LAUNCH_CHECK();
   return HI3D_OK;
 }
