@@ -103,6 +103,31 @@ struct Grid {
                    qz = ((static_cast<uint64_t>(sz) + 1) / 2 + 3) >> 2;
     return ((static_cast<uint64_t>(b) * qx + (bx >> 2)) * qy + (by >> 2)) * qz + (bz >> 2);
   }
+  // superblock-major cell key: superblock, then the brick's place in it (6 bits), then
+  // the cell's corner in the brick (3 bits)
+  __device__ __forceinline__ uint64_t sb_cell_key(int b, int x, int y, int z) const {
+    const int bx = x >> 1, by = y >> 1, bz = z >> 1;
+    return (superblock(b, bx, by, bz) << 9) |
+           static_cast<uint64_t>((((bx & 3) << 4) | ((by & 3) << 2) | (bz & 3)) << 3) |
+           static_cast<uint64_t>(corner(x, y, z));
+  }
+  // (batch, x, y, z) of a superblock-major cell key below 2^32
+  __device__ __forceinline__ int4 sb_cell_decode(uint32_t key) const {
+    const uint32_t qx = static_cast<uint32_t>((((static_cast<uint64_t>(sx) + 1) / 2) + 3) >> 2),
+                   qy = static_cast<uint32_t>((((static_cast<uint64_t>(sy) + 1) / 2) + 3) >> 2),
+                   qz = static_cast<uint32_t>((((static_cast<uint64_t>(sz) + 1) / 2) + 3) >> 2);
+    uint32_t sb = key >> 9;
+    const uint32_t pz = sb % qz;
+    sb /= qz;
+    const uint32_t py = sb % qy;
+    sb /= qy;
+    const uint32_t px = sb % qx;
+    const uint32_t b = sb / qx;
+    const uint32_t local = (key >> 3) & 63u, cn = key & 7u;
+    const uint32_t bx = (px << 2) | (local >> 4), by = (py << 2) | ((local >> 2) & 3u), bz = (pz << 2) | (local & 3u);
+    return make_int4(static_cast<int>(b), static_cast<int>((bx << 1) | (cn >> 2)),
+                     static_cast<int>((by << 1) | ((cn >> 1) & 1u)), static_cast<int>((bz << 1) | (cn & 1u)));
+  }
   // home bucket of a brick: the superblock's run of 64 buckets (at a hashed, aligned
   // start) at the brick's place in the superblock, so the words and rows of neighbouring
   // bricks share cache lines
@@ -342,19 +367,31 @@ __device__ __forceinline__ unsigned long long shfl_u64(unsigned long long v, int
 // bucket with a CAS and ORs in the occupancy bits of all its lanes, and every lane
 // stores its row in its cell's slot. A cell set twice, inside the wave or by the
 // atomicOr's old bits, is a repeated coordinate.
+// keys: the sorted superblock-major cell keys (with perm; the coordinates are decoded
+// from them), else sorted (with perm): the coordinates written in perm order here, for
+// the probe (out-of-range rows too).
 __global__ __launch_bounds__(256) void brick_insert_kernel(const int4* __restrict__ coords, int64_t n, Grid g,
-                                                           const int32_t* __restrict__ perm, BrickTable t,
-                                                           int32_t* __restrict__ status) {
+                                                           const int32_t* __restrict__ perm,
+                                                           const uint32_t* __restrict__ keys, BrickTable t,
+                                                           int4* __restrict__ sorted, int32_t* __restrict__ status) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const int lane = static_cast<int>(threadIdx.x & 63);
   bool act = i < n;
   int64_t row = i;
+  int4 c = make_int4(0, 0, 0, 0);
   if (act && perm != nullptr) {
     const int32_t pp = perm[i];
     act = pp >= 0;
     row = pp;
+    if (keys != nullptr) {
+      if (act) c = g.sb_cell_decode(keys[i]);
+    } else {
+      c = coords[pp >= 0 ? pp : ~pp];
+      sorted[i] = c;
+    }
+  } else if (act) {
+    c = coords[row];
   }
-  int4 c = act ? coords[row] : make_int4(0, 0, 0, 0);
   if (act && !g.inside(c.x, c.y, c.z, c.w)) {
     atomicOr(status, HI3D_MAP_RANGE);
     act = false;
@@ -530,8 +567,14 @@ __global__ __launch_bounds__(256) void brick_probe_kernel(const int4* __restrict
 constexpr int kBrick3Per = 4;
 constexpr int kBrick3Rows = 32 * kBrick3Per;
 
+// keys / sorted (with perm): as in brick_insert_kernel, so the coordinates load alongside
+// perm.
+// kPacked: buckets below 2^24, exchanged with their mask in one 32-bit lane move.
+template <bool kPacked>
 __global__ __launch_bounds__(256) void brick_probe3_kernel(const int4* __restrict__ coords, int64_t n, Grid g,
-                                                           const int32_t* __restrict__ perm, int per, BrickTable t,
+                                                           const int32_t* __restrict__ perm,
+                                                           const uint32_t* __restrict__ keys,
+                                                           const int4* __restrict__ sorted, int per, BrickTable t,
                                                            int32_t* __restrict__ nbr, int32_t* __restrict__ counts) {
   constexpr int P = kBrick3Per;
   __shared__ int32_t cnt[27];
@@ -554,14 +597,22 @@ __global__ __launch_bounds__(256) void brick_probe3_kernel(const int4* __restric
     const int64_t r = row0 + slot0 + 32 * i;
     valid[i] = r < n;
     int64_t oo = valid[i] ? r : 0;
+    c[i] = make_int4(-1, 0, 0, 0);
     if (perm != nullptr && valid[i]) {
       const int32_t pp = perm[r];
       oo = pp >= 0 ? pp : ~pp;
+      if (keys == nullptr)
+        c[i] = sorted[r];
+      else
+        c[i] = pp >= 0 ? g.sb_cell_decode(keys[r]) : coords[oo];
     }
     o[i] = static_cast<int32_t>(oo);
   }
+  if (perm == nullptr) {
 #pragma unroll
-  for (int i = 0; i < P; ++i) c[i] = valid[i] ? coords[o[i]] : make_int4(-1, 0, 0, 0);
+    for (int i = 0; i < P; ++i)
+      if (valid[i]) c[i] = coords[o[i]];
+  }
   // lowest of the row's 2 x 2 x 2 neighbour bricks along each axis, and the lane's brick
   int64_t base_x[P], base_y[P], base_z[P];
   uint64_t h[P];
@@ -613,13 +664,23 @@ __global__ __launch_bounds__(256) void brick_probe3_kernel(const int4* __restric
       const int j = static_cast<int>(
           ((((nx >> 1) - base_x[i]) << 2) | (((ny >> 1) - base_y[i]) << 1) | ((nz >> 1) - base_z[i])) & 7);
       const int src = group + j;
-      const uint32_t mj = static_cast<uint32_t>(__shfl(static_cast<int>(m[i]), src, 64));
-      const uint32_t hlo = static_cast<uint32_t>(__shfl(static_cast<int>(static_cast<uint32_t>(hb[i])), src, 64));
-      const uint32_t hhi = static_cast<uint32_t>(__shfl(static_cast<int>(static_cast<uint32_t>(hb[i] >> 32)), src, 64));
+      uint32_t mj;
+      uint64_t hj;
+      if constexpr (kPacked) {
+        const uint32_t v = static_cast<uint32_t>(
+            __shfl(static_cast<int>(static_cast<uint32_t>(hb[i] << 8) | m[i]), src, 64));
+        mj = v & 0xFFu;
+        hj = v >> 8;
+      } else {
+        mj = static_cast<uint32_t>(__shfl(static_cast<int>(m[i]), src, 64));
+        const uint32_t hlo = static_cast<uint32_t>(__shfl(static_cast<int>(static_cast<uint32_t>(hb[i])), src, 64));
+        const uint32_t hhi =
+            static_cast<uint32_t>(__shfl(static_cast<int>(static_cast<uint32_t>(hb[i] >> 32)), src, 64));
+        hj = (static_cast<uint64_t>(hhi) << 32) | hlo;
+      }
       const int cn = static_cast<int>(((nx & 1) << 2) | ((ny & 1) << 1) | (nz & 1));
       found[i][u] = absent;
-      if (valid[i] && k < 27 && k != 13 && ((mj >> cn) & 1u))
-        found[i][u] = t.rows[((static_cast<uint64_t>(hhi) << 32) | hlo) * 8 + cn];
+      if (valid[i] && k < 27 && k != 13 && ((mj >> cn) & 1u)) found[i][u] = t.rows[hj * 8 + cn];
     }
   }
   __syncthreads();  // cnt cleared
@@ -707,14 +768,18 @@ __global__ void order_key_kernel(const int4* __restrict__ coords, int64_t n, Gri
 
 // Brick-hash order: rows by superblock (8x8x8 cells; key >> shift), so consecutive rows
 // insert into and probe the same runs of buckets.
-__global__ void superblock_key_kernel(const int4* __restrict__ coords, int64_t n, Grid g, int shift,
+// full: the whole superblock-major cell key (below 2^32: the insert and probe decode the
+// coordinates from the sorted keys), else the superblock >> shift.
+__global__ void superblock_key_kernel(const int4* __restrict__ coords, int64_t n, Grid g, int shift, bool full,
                                       uint32_t* __restrict__ keys, int32_t* __restrict__ rows,
                                       int32_t* __restrict__ status) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= n) return;
   const int4 c = coords[i];
   const bool in = g.inside(c.x, c.y, c.z, c.w);
-  keys[i] = in ? static_cast<uint32_t>(g.superblock(c.x, c.y >> 1, c.z >> 1, c.w >> 1) >> shift) : 0u;
+  keys[i] = !in   ? 0u
+            : full ? static_cast<uint32_t>(g.sb_cell_key(c.x, c.y, c.z, c.w))
+                   : static_cast<uint32_t>(g.superblock(c.x, c.y >> 1, c.z >> 1, c.w >> 1) >> shift);
   rows[i] = in ? static_cast<int32_t>(i) : ~static_cast<int32_t>(i);
   if (!in) atomicOr(status, HI3D_MAP_RANGE);
 }
@@ -1283,7 +1348,9 @@ const char* hi3d_version(void) { return "hi3d_amd 0.1 gfx950"; }
 // Bytes of the cell-order sort that precedes a hash build: keys and rows (two slabs
 // each) and the radix sort's counts.
 static int64_t hash_order_bytes(int64_t n) {
-  return 4 * align_up(std::max<int64_t>(n, 1) * 4, 256) + radix::temp_bytes(std::max<int64_t>(n, 1));
+  // keys, rows (two of each), the radix sort's temporaries, the coordinates in order
+  return 4 * align_up(std::max<int64_t>(n, 1) * 4, 256) + align_up(radix::temp_bytes(std::max<int64_t>(n, 1)), 256) +
+         align_up(std::max<int64_t>(n, 1) * 16, 256);
 }
 
 // Bytes of a brick table of `cap` buckets: key | mask words, then 8 rows per bucket.
@@ -1357,6 +1424,8 @@ static int kmap_subm_brick(const int32_t* coords, int64_t n, Grid g, int32_t ksi
   const unsigned blocks = static_cast<unsigned>(ceil_div(n, 256));
   const int4* c4 = reinterpret_cast<const int4*>(coords);
   const int32_t* perm = nullptr;
+  int4* sorted = nullptr;
+  const uint32_t* skeys = nullptr;
   int per = 0;
   int64_t probe_blocks = ceil_div(n, ksize == 3 ? kBrick3Rows : kProbeRows);
   if (brick_table_bytes(cap) > kBrickOrderMinBytes) {
@@ -1370,21 +1439,32 @@ static int kmap_subm_brick(const int32_t* coords, int64_t n, Grid g, int32_t ksi
                        ((((static_cast<uint64_t>(g.sz) + 1) / 2) + 3) >> 2);
     int key_bits = 1;
     while (key_bits < 64 && (uint64_t(1) << key_bits) < q) ++key_bits;
-    const int shift = key_bits > 32 ? key_bits - 32 : 0;
-    const int kb = key_bits - shift;
-    hipLaunchKernelGGL(superblock_key_kernel, dim3(blocks), dim3(256), 0, stream, c4, n, g, shift, k0, r0, status);
-    // radix passes over the superblock key's top 24 bits
+    // whole cell keys when they fit 32 bits (sorted by their top 24), else the superblock's
+    // top 32 bits
+    const bool full = key_bits + 9 <= 32;
+    const int shift = full || key_bits <= 32 ? 0 : key_bits - 32;
+    const int kb = full ? key_bits + 9 : key_bits - shift;
+    hipLaunchKernelGGL(superblock_key_kernel, dim3(blocks), dim3(256), 0, stream, c4, n, g, shift, full, k0, r0,
+                       status);
     HI3D_HIP_CHECK(radix::sort_pairs(order + 4 * slab, radix::temp_bytes(n), k0, k1, r0, r1, n,
                                      kb > 24 ? kb - 24 : 0, kb, stream));
     perm = r0;
+    if (full)
+      skeys = k0;
+    else
+      sorted = reinterpret_cast<int4*>(order + 4 * slab + align_up(radix::temp_bytes(n), 256));
     per = static_cast<int>(ceil_div(probe_blocks, kXcds));
     probe_blocks = static_cast<int64_t>(per) * kXcds;
   }
   launch_fill<unsigned long long>(t.words, cap, kEmptyBrick, stream);
-  hipLaunchKernelGGL(brick_insert_kernel, dim3(blocks), dim3(256), 0, stream, c4, n, g, perm, t, status);
-  if (ksize == 3)
-    hipLaunchKernelGGL(brick_probe3_kernel, dim3(static_cast<unsigned>(probe_blocks)), dim3(256), 0, stream, c4, n, g,
-                       perm, per, t, nbr, counts);
+  hipLaunchKernelGGL(brick_insert_kernel, dim3(blocks), dim3(256), 0, stream, c4, n, g, perm, skeys, t, sorted,
+                     status);
+  if (ksize == 3 && cap <= (int64_t(1) << 24))
+    hipLaunchKernelGGL(brick_probe3_kernel<true>, dim3(static_cast<unsigned>(probe_blocks)), dim3(256), 0, stream, c4,
+                       n, g, perm, skeys, sorted, per, t, nbr, counts);
+  else if (ksize == 3)
+    hipLaunchKernelGGL(brick_probe3_kernel<false>, dim3(static_cast<unsigned>(probe_blocks)), dim3(256), 0, stream, c4,
+                       n, g, perm, skeys, sorted, per, t, nbr, counts);
   else
     hipLaunchKernelGGL(brick_probe_kernel, dim3(static_cast<unsigned>(probe_blocks)), dim3(256), 0, stream, c4, n, g,
                        ksize, perm, per, t, nbr, counts);
