@@ -613,74 +613,67 @@ __global__ __launch_bounds__(256) void brick_probe3_kernel(const int4* __restric
     for (int i = 0; i < P; ++i)
       if (valid[i]) c[i] = coords[o[i]];
   }
-  // lowest of the row's 2 x 2 x 2 neighbour bricks along each axis, and the lane's brick
-  int64_t base_x[P], base_y[P], base_z[P];
+  // the lane's brick: the lower (bit clear) or upper of the row's two neighbour bricks
+  // along each axis, from lowest = (c >> 1) - 1 + (c & 1)
+  uint32_t par[P];  // the row's coordinate parities (bit 2: x, 1: y, 0: z)
   uint64_t h[P];
   unsigned long long bk[P], w[P];
-  bool in[P];
 #pragma unroll
   for (int i = 0; i < P; ++i) {
-    base_x[i] = (static_cast<int64_t>(c[i].y) >> 1) - 1 + (c[i].y & 1);
-    base_y[i] = (static_cast<int64_t>(c[i].z) >> 1) - 1 + (c[i].z & 1);
-    base_z[i] = (static_cast<int64_t>(c[i].w) >> 1) - 1 + (c[i].w & 1);
-    const int64_t bx = base_x[i] + ((lane >> 2) & 1), by = base_y[i] + ((lane >> 1) & 1), bz = base_z[i] + (lane & 1);
-    in[i] = valid[i] && static_cast<unsigned>(c[i].x) < static_cast<unsigned>(g.batch) && bx >= 0 && bx < hx &&
-            by >= 0 && by < hy && bz >= 0 && bz < hz;
-    bk[i] = in[i] ? g.brick_key(c[i].x, bx, by, bz) : 0ull;
-    h[i] = in[i] ? g.brick_home(c[i].x, bx, by, bz, t.mask) : 0ull;
+    par[i] = static_cast<uint32_t>(((c[i].y & 1) << 2) | ((c[i].z & 1) << 1) | (c[i].w & 1));
+    const int64_t bx = (static_cast<int64_t>(c[i].y) >> 1) - 1 + (c[i].y & 1) + ((lane >> 2) & 1);
+    const int64_t by = (static_cast<int64_t>(c[i].z) >> 1) - 1 + (c[i].z & 1) + ((lane >> 1) & 1);
+    const int64_t bz = (static_cast<int64_t>(c[i].w) >> 1) - 1 + (c[i].w & 1) + (lane & 1);
+    const bool in = valid[i] && static_cast<unsigned>(c[i].x) < static_cast<unsigned>(g.batch) && bx >= 0 &&
+                    bx < hx && by >= 0 && by < hy && bz >= 0 && bz < hz;
+    bk[i] = in ? g.brick_key(c[i].x, bx, by, bz) : kEmptyBrick;
+    h[i] = in ? g.brick_home(c[i].x, bx, by, bz, t.mask) : 0ull;
   }
 #pragma unroll
-  for (int i = 0; i < P; ++i) w[i] = in[i] ? t.words[h[i]] : kEmptyBrick;
-  uint64_t hb[P];
-  uint32_t m[P];
+  for (int i = 0; i < P; ++i) w[i] = bk[i] != kEmptyBrick ? t.words[h[i]] : kEmptyBrick;
+  // the lane's brick as (bucket << 8 | occupancy), 0 when absent
+  uint64_t v[P];
 #pragma unroll
   for (int i = 0; i < P; ++i) {
-    hb[i] = 0;
-    m[i] = 0;
+    v[i] = 0;
     if (w[i] != kEmptyBrick) {
       if ((w[i] >> 8) == bk[i]) {
-        hb[i] = h[i];
-        m[i] = static_cast<uint32_t>(w[i] & 0xFFu);
+        v[i] = (h[i] << 8) | (w[i] & 0xFFu);
       } else {
         const int64_t f = brick_find(t, h[i], bk[i]);
-        if (f >= 0) {
-          hb[i] = static_cast<uint64_t>(f);
-          m[i] = static_cast<uint32_t>(t.words[f] & 0xFFu);
-        }
+        if (f >= 0) v[i] = (static_cast<uint64_t>(f) << 8) | (t.words[f] & 0xFFu);
       }
     }
+  }
+  // offsets l + 8 u: k = 9 (dx + 1) + 3 (dy + 1) + (dz + 1). Along an axis with parity p
+  // the neighbour at d lies in brick (d + 2 - p) >> 1 of the two and has parity (p + d) & 1.
+  int dx[4], dy[4], dz[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int kk = lane + 8 * u < 27 ? lane + 8 * u : 0;
+    dx[u] = kk / 9 - 1;
+    dy[u] = (kk / 3) % 3 - 1;
+    dz[u] = kk % 3 - 1;
   }
   const int32_t absent = static_cast<int32_t>(n);
   int32_t found[P][4];
 #pragma unroll
   for (int i = 0; i < P; ++i) {
+    const int px = (par[i] >> 2) & 1, py = (par[i] >> 1) & 1, pz = par[i] & 1;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const int k = lane + 8 * u;  // k = 9 (dx + 1) + 3 (dy + 1) + (dz + 1)
-      const int kk = k < 27 ? k : 0;
-      const int64_t nx = static_cast<int64_t>(c[i].y) + kk / 9 - 1, ny = static_cast<int64_t>(c[i].z) + (kk / 3) % 3 - 1,
-                    nz = static_cast<int64_t>(c[i].w) + kk % 3 - 1;
-      // the neighbour's brick among the row's 8: 0 or 1 along each axis
-      const int j = static_cast<int>(
-          ((((nx >> 1) - base_x[i]) << 2) | (((ny >> 1) - base_y[i]) << 1) | ((nz >> 1) - base_z[i])) & 7);
+      const int k = lane + 8 * u;
+      const int j = (((dx[u] + 2 - px) >> 1) << 2) | (((dy[u] + 2 - py) >> 1) << 1) | ((dz[u] + 2 - pz) >> 1);
+      const int cn = (((px + dx[u]) & 1) << 2) | (((py + dy[u]) & 1) << 1) | ((pz + dz[u]) & 1);
       const int src = group + j;
-      uint32_t mj;
-      uint64_t hj;
+      uint64_t vj;
       if constexpr (kPacked) {
-        const uint32_t v = static_cast<uint32_t>(
-            __shfl(static_cast<int>(static_cast<uint32_t>(hb[i] << 8) | m[i]), src, 64));
-        mj = v & 0xFFu;
-        hj = v >> 8;
+        vj = static_cast<uint32_t>(__shfl(static_cast<int>(static_cast<uint32_t>(v[i])), src, 64));
       } else {
-        mj = static_cast<uint32_t>(__shfl(static_cast<int>(m[i]), src, 64));
-        const uint32_t hlo = static_cast<uint32_t>(__shfl(static_cast<int>(static_cast<uint32_t>(hb[i])), src, 64));
-        const uint32_t hhi =
-            static_cast<uint32_t>(__shfl(static_cast<int>(static_cast<uint32_t>(hb[i] >> 32)), src, 64));
-        hj = (static_cast<uint64_t>(hhi) << 32) | hlo;
+        vj = shfl_u64(v[i], src);
       }
-      const int cn = static_cast<int>(((nx & 1) << 2) | ((ny & 1) << 1) | (nz & 1));
       found[i][u] = absent;
-      if (valid[i] && k < 27 && k != 13 && ((mj >> cn) & 1u)) found[i][u] = t.rows[hj * 8 + cn];
+      if (valid[i] && k < 27 && k != 13 && ((vj >> cn) & 1u)) found[i][u] = t.rows[(vj >> 8) * 8 + cn];
     }
   }
   __syncthreads();  // cnt cleared
