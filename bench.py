@@ -140,19 +140,25 @@ def timed_batch(fn, steps: int, warmup: int) -> float:
     return start.elapsed_time(end) / steps
 
 
-def dense_fresh(fn):
-    """Run a kernel-map build with a dense grid cleared inside the call (not kept)."""
+def dense_path(fn, keep: bool = True):
+    """Run a kernel-map build through the dense grid whatever the grid size (kept between
+    builds, or cleared inside the call)."""
     from hi3d_amd import kmap
 
     def run():
-        old = kmap.KMAP_DENSE_KEEP
-        kmap.KMAP_DENSE_KEEP = False
+        old = kmap.KMAP_DENSE_KEEP, kmap.KMAP_DENSE_MAX_CELLS
+        kmap.KMAP_DENSE_KEEP, kmap.KMAP_DENSE_MAX_CELLS = keep, 1 << 31
         try:
             return fn()
         finally:
-            kmap.KMAP_DENSE_KEEP = old
+            kmap.KMAP_DENSE_KEEP, kmap.KMAP_DENSE_MAX_CELLS = old
 
     return run
+
+
+def dense_fresh(fn):
+    """Run a kernel-map build with a dense grid cleared inside the call (not kept)."""
+    return dense_path(fn, keep=False)
 
 
 def bench_subm(name: str, grid: int, cin: int, cout: int, dtype, steps: int, warmup: int, seed: int = 0):
@@ -169,7 +175,8 @@ def bench_subm(name: str, grid: int, cin: int, cout: int, dtype, steps: int, war
     x = torch.as_tensor(workloads.normal((n, cin), 1.0, seed + 1, np_dtype)).to(dev)
     w = torch.as_tensor(workloads.normal((cout, 27, cin), 1.0 / np.sqrt(27 * cin), seed + 2, np_dtype)).to(dev)
     # kernel map build (hash insert + probe) and plan, timed separately
-    map_wall, map_ev = timed(lambda: kmap.build_kernel_map(coords, [grid] * 3, 1, check=False), 5, 2)
+    map_wall, _ = timed(lambda: kmap.build_kernel_map(coords, [grid] * 3, 1, check=False), 5, 2)
+    _, map_ev = timed(dense_path(lambda: kmap.build_kernel_map(coords, [grid] * 3, 1, check=False)), 5, 2)
     hash_wall, hash_ev = timed(lambda: kmap.build_kernel_map(coords, [grid] * 3, 1, capacity=0, check=False), 5, 2)
     _, fresh_ev = timed(dense_fresh(lambda: kmap.build_kernel_map(coords, [grid] * 3, 1, check=False)), 5, 2)
     km = kmap.build_kernel_map(coords, [grid] * 3, 1)
@@ -332,7 +339,8 @@ def bench_block(steps: int, warmup: int, settle_s: float = 0.0):
     n = len(idx)
     c, d = 256, 1024
     coords = torch.as_tensor(idx).to(dev)
-    map_wall, map_ev = timed(lambda: kmap.build_kernel_map(coords, [1024] * 3, 1, check=False), 3, 1)
+    map_wall, _ = timed(lambda: kmap.build_kernel_map(coords, [1024] * 3, 1, check=False), 3, 1)
+    _, map_ev = timed(dense_path(lambda: kmap.build_kernel_map(coords, [1024] * 3, 1, check=False)), 3, 1)
     hash_wall, hash_ev = timed(lambda: kmap.build_kernel_map(coords, [1024] * 3, 1, capacity=0, check=False), 3, 1)
     _, fresh_ev = timed(dense_fresh(lambda: kmap.build_kernel_map(coords, [1024] * 3, 1, check=False)), 3, 1)
     km = kmap.build_kernel_map(coords, [1024] * 3, 1)
@@ -383,6 +391,7 @@ def bench_block(steps: int, warmup: int, settle_s: float = 0.0):
         "conv_eff_tflops": conv_flops / (conv_avg * 1e-3) / 1e12,
         "ln_ms": ln_ev,
         "ln_gbs": 4.0 * n * c / (ln_ev * 1e-3) / 1e9,
+        "map_ms": map_wall,
         "map_dense_ms": map_ev,
         "map_dense_fresh_ms": fresh_ev,
         "map_hash_ms": hash_ev,
@@ -606,8 +615,9 @@ def bench_unique(steps: int, warmup: int):
 
 def bench_kmap(steps: int, warmup: int):
     """Submanifold 3x3x3 kernel-map builds on the 1024^3 residual-block shells and the
-    256^3 C128 shells: the dense grid (kept between builds, the default; and cleared
-    inside each build) and the brick hash, each checked equal to the dense table."""
+    256^3 C128 shells: the dense grid (kept between builds; and cleared inside each
+    build) and the brick hash (the default above 2^28 cells), each checked equal to the
+    dense table."""
     import torch
 
     from hi3d_amd import kmap
@@ -616,11 +626,12 @@ def bench_kmap(steps: int, warmup: int):
     out = {}
     for name, grid in (("resblock_c256_fp16", 1024), ("subm3_c128_fp16", 256)):
         coords = torch.as_tensor(coords_of(name, dev)).to(dev)
-        ref = kmap.build_kernel_map(coords, [grid] * 3, 1).table
-        dense = lambda: kmap.build_kernel_map(coords, [grid] * 3, 1, check=False)
+        build = lambda: kmap.build_kernel_map(coords, [grid] * 3, 1, check=False)
+        dense, fresh = dense_path(build), dense_fresh(build)
+        ref = dense().table
         brick = lambda: kmap.build_kernel_map(coords, [grid] * 3, 1, capacity=0, check=False)
         _, dense_ms = timed(dense, steps, warmup)
-        _, fresh_ms = timed(dense_fresh(dense), steps, warmup)
+        _, fresh_ms = timed(fresh, steps, warmup)
         _, hash_ms = timed(brick, steps, warmup)
         n = int(coords.shape[0])
         out[name] = {
@@ -631,7 +642,7 @@ def bench_kmap(steps: int, warmup: int):
             "brick_hash_ms": hash_ms,
             "brick_hash_voxels_per_s": n / (hash_ms * 1e-3),
             "hash_equal": bool(torch.equal(brick().table, ref)),
-            "dense_fresh_equal": bool(torch.equal(dense_fresh(dense)().table, ref)),
+            "dense_fresh_equal": bool(torch.equal(fresh().table, ref)),
         }
     return out
 

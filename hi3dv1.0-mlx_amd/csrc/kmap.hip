@@ -17,10 +17,13 @@
 //
 // Slots keep locality: a voxel's home slot is 8 * mix64(its 2x2x2 brick) + its corner in
 // the brick, so the eight cells of a brick share one 64-byte run of slots and a row's 26
-// neighbours fall in at most 8 such runs. With a workspace for it, the rows are first
-// sorted by the top 16 bits of their cell keys (batch, x, bands of y), and the insert and
-// the probe walk them in that order (in chunks taken XCD by XCD), so neighbouring rows
-// touch the same runs while they sit in L2.
+// neighbours fall in at most 8 such runs.
+//
+// The map build's own hash is the brick hash below (one bucket per occupied brick, homes
+// grouped per 8x8x8-cell superblock); with a workspace for it, its rows are first sorted
+// by their superblock-major cell keys and the insert and the probe walk them in that
+// order (probe chunks taken XCD by XCD), so neighbouring rows touch the same buckets while
+// they sit in L2.
 
 #include <algorithm>
 #include <cstdarg>
@@ -745,23 +748,9 @@ __global__ void cell_key_kernel(const int4* __restrict__ coords, int64_t n, Grid
   if (!in) atomicOr(status, HI3D_MAP_RANGE);
 }
 
-// Hash path's cell order: the top 32 bits of the row's cell key (the key shifted right
-// by `shift`); an out-of-range row is flagged, gets key 0 and the row id ~i.
-__global__ void order_key_kernel(const int4* __restrict__ coords, int64_t n, Grid g, int shift,
-                                 uint32_t* __restrict__ keys, int32_t* __restrict__ rows,
-                                 int32_t* __restrict__ status) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i >= n) return;
-  const int4 c = coords[i];
-  const bool in = g.inside(c.x, c.y, c.z, c.w);
-  keys[i] = in ? static_cast<uint32_t>(g.key(c.x, c.y, c.z, c.w) >> shift) : 0u;
-  rows[i] = in ? static_cast<int32_t>(i) : ~static_cast<int32_t>(i);
-  if (!in) atomicOr(status, HI3D_MAP_RANGE);
-}
-
-// Brick-hash order: rows by superblock (8x8x8 cells; key >> shift), so consecutive rows
-// insert into and probe the same runs of buckets.
-// full: the whole superblock-major cell key (below 2^32: the insert and probe decode the
+// Brick-hash order: rows by superblock (8x8x8 cells), so consecutive rows insert into and
+// probe the same runs of buckets; an out-of-range row is flagged, gets key 0 and the row
+// id ~i. full: the whole superblock-major cell key (below 2^32: the insert and probe decode the
 // coordinates from the sorted keys), else the superblock >> shift.
 __global__ void superblock_key_kernel(const int4* __restrict__ coords, int64_t n, Grid g, int shift, bool full,
                                       uint32_t* __restrict__ keys, int32_t* __restrict__ rows,
@@ -1351,7 +1340,7 @@ static int64_t brick_table_bytes(int64_t cap) { return align_up(cap * 8, 256) + 
 
 // Brick tables above this size are built and probed in cell order (below it the table
 // stays in the last-level cache and the sort costs more than it saves).
-constexpr int64_t kBrickOrderMinBytes = int64_t(64) << 20;
+constexpr int64_t kBrickOrderMinBytes = int64_t(16) << 20;
 
 int hi3d_kmap_workspace(int64_t n, int64_t capacity, int32_t key64, int64_t* bytes) {
   HI3D_REQUIRE(bytes != nullptr, "bytes_host is NULL");

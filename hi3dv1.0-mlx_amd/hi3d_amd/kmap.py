@@ -27,12 +27,14 @@ L2; larger ones group more rows of equal offset masks, so tiles run fewer absent
 shells one window 0.3775 ms against 0.3804 ms at 2^18; on the 1.1M-voxel shells one
 window C64 0.243 / C128 0.554 ms against 0.257 / 0.575 ms at 2^18; on the 4.4M-voxel
 C256 shells 2^19 is best (7.09 ms; 7.28 at 2^18, 7.22-7.25 at 2^20 .. one window)."""
-KMAP_DENSE_MAX_CELLS: int = 1 << 31
+KMAP_DENSE_MAX_CELLS: int = 1 << 28
 """Grids of at most this many cells (batch * sx * sy * sz) build their map through a
-dense grid of rows instead of the brick hash; ``0`` always hashes. The dense map is the
-faster one on every measured set (config-5 shells, 4.4M voxels at 1024^3: 0.76 ms on the
-kept grid against 1.60 ms hashed; 543k voxels at 256^3: 0.13 against 0.29 ms), so the
-hash is the path for grids above the limit (and for callers that ask for a capacity)."""
+dense grid of rows (4 bytes per cell, kept between builds) instead of the brick hash;
+``0`` always hashes. Up to 2^28 cells the dense grid is the faster map (543k voxels at
+256^3: 0.13 against 0.17 ms hashed; 1.1M at 512^3: 0.18 against 0.25 ms). Above it the
+two run at the same speed (4.4M voxels at 1024^3: 0.74 ms on the kept grid against
+0.73 ms hashed) and the grid would hold 4 GiB per 2^30 cells, against the hash's
+~110 bytes per voxel for the duration of the build, so the hash builds those maps."""
 
 KMAP_DENSE_KEEP: bool = True
 """Keep one dense grid per (device, cell count) between calls (``hi3d_kmap_subm_dense_kept``:

@@ -61,15 +61,16 @@ const char* hi3d_version(void);
  * accepted for the ABI's sake and ignored (brick keys are 64-bit). */
 int hi3d_kmap_workspace(int64_t n, int64_t capacity, int32_t key64, int64_t* bytes_host);
 
-/* Submanifold kernel map through a brick hash: every voxel claims (one 64-bit CAS) the
- * bucket of its 2x2x2 brick, keyed by the brick's packed coordinates (as
- * ((b*sx + x)*sy + y)*sz + z over the halved extents, below 2^56; open addressing, linear
- * probing over buckets), and sets its corner's bit (in the key's word) and row; the ksize^3 neighbourhood of each
- * voxel is then read bucket by bucket, writing the dense neighbour table
- * nbr_dev [n, ksize^3] (sentinel n) and per-offset non-sentinel counts counts_dev
- * [ksize^3]. Neighbours outside [0, spatial_shape) are absent. Large tables are built
- * and probed in cell order. status_dev flags DUPLICATE, RANGE and OVERFLOW (capacity
- * smaller than the occupied bricks).
+/* Submanifold kernel map through a brick hash: the voxels of each 2x2x2 brick claim (one
+ * 64-bit CAS per brick) its bucket, keyed by the brick's packed coordinates (as
+ * ((b*sx + x)*sy + y)*sz + z over the halved extents, below 2^56; open addressing, the
+ * home buckets of an 8x8x8-cell superblock's bricks one hashed run, double hashing past
+ * it), and set their corners' bits (in the key's word) and rows; the ksize^3
+ * neighbourhood of each voxel is then read bucket by bucket, writing the dense neighbour
+ * table nbr_dev [n, ksize^3] (sentinel n) and per-offset non-sentinel counts counts_dev
+ * [ksize^3]. Neighbours outside [0, spatial_shape) are absent. Tables above 16 MiB are
+ * built and probed in superblock order. status_dev flags DUPLICATE, RANGE and OVERFLOW
+ * (capacity smaller than the occupied bricks).
  * Replaces: _voxel_keys + subm_pairs (src/hi3d_mac/torch_backend/sparse_conv.py:109-149)
  * and neighbour_table (src/hi3d_mac/mlx_backend/sparse.py:29-43). */
 int hi3d_kmap_subm(const int32_t* coords_dev, int64_t n, int32_t sx, int32_t sy, int32_t sz,

@@ -145,9 +145,10 @@ def test_workload_maps_bit_exact(cuda, name):
 
 
 def test_large_shell_map_properties(cuda):
-    """The 1024^3 workload (~4.4M voxels): the whole table equals the oracle's (the
-    sort + searchsorted lookup over key-ordered rows, every row and offset), and over all
-    rows the size-independent properties: neighbour coordinates, symmetry, count
+    """The 1024^3 workload (~4.4M voxels): the whole table of the default map (the brick
+    hash at this grid size) equals the oracle's (the sort + searchsorted lookup over
+    key-ordered rows, every row and offset) and the kept dense grid's, and over all rows
+    the size-independent properties hold: neighbour coordinates, symmetry, count
     symmetry."""
     from hi3d_amd import kmap, workloads
 
@@ -158,6 +159,14 @@ def test_large_shell_map_properties(cuda):
     table = km.table
     print(f"comparing the full {n} x 27 table with the oracle", flush=True)
     assert np.array_equal(table.cpu().numpy(), okmap.neighbour_table_sorted(idx, [1024] * 3))
+    old = kmap.KMAP_DENSE_MAX_CELLS
+    try:
+        kmap.KMAP_DENSE_MAX_CELLS = 1 << 31
+        dense = kmap.build_kernel_map(coords, [1024] * 3, 1)
+    finally:
+        kmap.KMAP_DENSE_MAX_CELLS = old
+    kmap.release_dense_grids()
+    assert torch.equal(dense.table, table) and torch.equal(dense.counts, km.counts)
     offs = torch.as_tensor(okmap.kernel_offsets(3) - 1, device=cuda, dtype=torch.int32)
     present = table != n
     for k in range(27):
