@@ -328,19 +328,23 @@ _OUT_OF_RANGE = [(2, lambda n: n), (3, lambda n: 1 << 30), (3, lambda n: -(1 << 
 def test_dense_and_hash_maps_agree(cuda, ksize, batch, n_side, density):
     """The dense-grid map (rows in input order and in cell order) and the hash map give
     the same table and counts bit for bit, and equal the oracle; all flag duplicates and
-    out-of-range coordinates."""
+    out-of-range coordinates. Hash capacities: 2^16 buckets (rows in input order), 2^20
+    (a table above 16 MiB: rows in superblock order, coordinates decoded from the sorted
+    keys) and 2^25 (buckets past 2^24: the probe's 64-bit bucket exchange)."""
     from hi3d_amd import kmap
 
     rng = np.random.default_rng(n_side * 10 + batch)
     idx = _rand_indices(rng, n_side, density, batch=batch)
     t = torch.as_tensor(idx).to(cuda)
     dense = kmap.build_kernel_map(t, [n_side] * 3, batch, ksize)
-    hashed = kmap.build_kernel_map(t, [n_side] * 3, batch, ksize, capacity=1 << 16)
-    assert torch.equal(dense.table, hashed.table) and torch.equal(dense.counts, hashed.counts)
+    for cap in (1 << 16, 1 << 20, 1 << 25):
+        hashed = kmap.build_kernel_map(t, [n_side] * 3, batch, ksize, capacity=cap)
+        assert torch.equal(dense.table, hashed.table) and torch.equal(dense.counts, hashed.counts), cap
+    del hashed
     ref = okmap.neighbour_table(idx, [n_side] * 3, ksize)
     assert np.array_equal(dense.table.cpu().numpy(), ref)
     dup = torch.cat([t, t[3:4]])
-    for cap in (None, 1 << 16):
+    for cap in (None, 1 << 16, 1 << 20):
         with pytest.raises(ValueError, match="duplicate"):
             kmap.build_kernel_map(dup, [n_side] * 3, batch, ksize, capacity=cap)
         for col, value in _OUT_OF_RANGE:
@@ -371,6 +375,30 @@ def test_dense_and_hash_maps_agree(cuda, ksize, batch, n_side, density):
         assert torch.equal(kmap.build_kernel_map(t, [n_side] * 3, batch, ksize).table, dense.table)
     finally:
         kmap.KMAP_DENSE_ORDER_MIN_BYTES = old_order
+
+
+def test_hash_wide_grid_superblock_order(cuda):
+    """A grid whose superblock-major cell keys pass 32 bits (65536 x 65536 x 256): the
+    hash sorts the superblocks alone and carries the coordinates in sorted order. The
+    543k-voxel C128 shells moved to x + 40000, y + 50000 there have the neighbour table
+    of the same shells in their own 256^3 grid (the dense map), nothing crossing an edge."""
+    from hi3d_amd import kmap, workloads
+
+    idx = workloads.coords_for("subm3_c128_fp16", device=cuda)
+    coords = torch.as_tensor(idx).to(cuda)
+    ref = kmap.build_kernel_map(coords, [256] * 3, 1)
+    moved = coords.clone()
+    moved[:, 1] += 40000
+    moved[:, 2] += 50000
+    wide = kmap.build_kernel_map(moved, [65536, 65536, 256], 1)
+    assert torch.equal(wide.table, ref.table) and torch.equal(wide.counts, ref.counts)
+    dup = torch.cat([moved, moved[11:12]])
+    with pytest.raises(ValueError, match="duplicate"):
+        kmap.build_kernel_map(dup, [65536, 65536, 256], 1)
+    bad = moved.clone()
+    bad[7, 3] = 300
+    with pytest.raises(ValueError, match="outside"):
+        kmap.build_kernel_map(bad, [65536, 65536, 256], 1)
 
 
 @pytest.mark.parametrize("ordered", [True, False])
