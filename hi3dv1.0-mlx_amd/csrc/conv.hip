@@ -1637,7 +1637,11 @@ __global__ __launch_bounds__(512, 1) void conv_wide2_kernel(ConvArgs a) {
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave % WM, wn = wave / WM;
+  // Waves w and w + 4 share SIMD w % 4; they take row blocks w and w ^ 2, one from each
+  // 128-row plan tile, so that an offset present in only one plan tile still gives
+  // every SIMD one wave of MFMAs (a wave skips the offsets none of its rows has).
+  const int wn = wave / WM, wm = (wave % WM) ^ (2 * wn);
+  static_assert(WM == 4 && NW == 8, "crossed row blocks assume a 4 x 2 wave grid");
   const int64_t item = xcd_remap(blockIdx.x, static_cast<int64_t>(gridDim.x));
   const int64_t tile = item / a.ny;
   const int n0 = static_cast<int>(item - tile * a.ny) * BN;
@@ -1690,14 +1694,17 @@ __global__ __launch_bounds__(512, 1) void conv_wide2_kernel(ConvArgs a) {
 
   uint32_t rest;  // offsets after the current one of the load cursor
   int ck, ckb, cord;
+  uint32_t pres = 0;  // bit o: the wave's 64 rows have the offset of ordinal o
   const char* src[LA];
   auto enter_offset = [&]() {
     const int32_t* gi = reinterpret_cast<const int32_t*>(idx_ring + (cord & 1) * kW2Idx);
     int32_t g[LA];
 #pragma unroll
     for (int j = 0; j < LA; ++j) g[j] = gi[r0 + 8 * NW * j];
+    const int32_t gw = gi[wm * 64 + lane];
 #pragma unroll
     for (int j = 0; j < LA; ++j) src[j] = gather_src(a.in, g[j], n_in, rb, coff, zrow);
+    if (__builtin_amdgcn_ballot_w64(static_cast<uint64_t>(static_cast<uint32_t>(gw)) < n_in) != 0) pres |= 1u << cord;
   };
   auto advance = [&]() {
     if (++ckb == KB) {
@@ -1756,19 +1763,24 @@ __global__ __launch_bounds__(512, 1) void conv_wide2_kernel(ConvArgs a) {
   using I2 = std::integral_constant<int, 2>;
 
   // Stage s in slot SL. MODE 0: loads of stage s + 2 in K-group 3; 1: s = S - 2 (no
-  // loads); 2: s = S - 1 (no loads, nothing follows).
+  // loads); 2: s = S - 1 (no loads, nothing follows). A wave whose rows lack the stage's
+  // offset skips its MFMAs and the fragment reads that feed them (they would add zeros);
+  // (c_ord, c_kb) is the stage's offset ordinal and K step.
+  int c_ord = 0, c_kb = 0;
   auto stage = [&](int SL, auto modec) {
     constexpr int MODE = decltype(modec)::value;
     const int NSL = SL ^ 1;
-    auto group = [&](auto gc) {
+    const bool on = (pres >> c_ord) & 1u;
+    auto group = [&](auto gc, auto mmc, auto frc) {
       constexpr int G = decltype(gc)::value;
+      constexpr bool MM = decltype(mmc)::value, FR = decltype(frc)::value;
       wait_lgkm0();
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < NM; ++i) {
-        mma_one(gc, i);
+        if constexpr (MM) mma_one(gc, i);
         __builtin_amdgcn_sched_barrier(0);
-        if (i < NF) {
+        if (FR && i < NF) {
           if constexpr (G < 3)
             frag_one(SL, std::integral_constant<int, G + 1>{}, i);
           else if constexpr (MODE != 2)
@@ -1778,16 +1790,29 @@ __global__ __launch_bounds__(512, 1) void conv_wide2_kernel(ConvArgs a) {
         __builtin_amdgcn_sched_barrier(0);
       }
     };
-    group(G0{});
-    group(G1{});
-    group(G2{});
+    using Y = std::true_type;
+    using N = std::false_type;
+    auto group_on = [&](auto gc) {
+      if (on) group(gc, Y{}, Y{});
+      else group(gc, N{}, N{});
+    };
+    group_on(G0{});
+    group_on(G1{});
+    group_on(G2{});
     if constexpr (MODE != 2) {
       wait_vmcnt<0>();  // stage s + 1 (and the index DMA issued with it) landed
       raw_barrier();
     }
     if constexpr (MODE == 0) cursor_indices();
-    group(G3{});
+    // K-group 3 always reads the next stage's first fragments (made conditional on the
+    // next stage's offset, the kernel spilled ~570 registers)
+    if (on) group(G3{}, Y{}, Y{});
+    else group(G3{}, N{}, Y{});
     if constexpr (MODE == 0) advance();
+    if (++c_kb == KB) {
+      c_kb = 0;
+      ++c_ord;
+    }
   };
 
   if (S > 0) {  // S = taps * KB >= 2

@@ -333,6 +333,45 @@ def test_plan_choice_does_not_change_results(cuda):
     assert oconv.rel_err(halo_outs[0].float().cpu().numpy(), outs[0].float().cpu().numpy().astype(np.float64)) <= 1e-2
 
 
+@pytest.mark.parametrize("act,res", [(None, False), ("silu", True)])
+def test_wide2_offset_skips_are_exact(cuda, act, res):
+    """The 256 x 256 kernel's waves skip the MFMAs of offsets that none of their 64 rows
+    has. On a sphere shell (structured masks, so many 64-row blocks lack offsets of their
+    256-row tile) the output is bitwise the same under plans that skip different
+    (block, offset) pairs, and within the fp16 gate of float64."""
+    from hi3d_amd import conv, kmap, workloads
+
+    rng = np.random.default_rng(31)
+    idx = workloads.sphere_shell(64, 27.0, seed=3)
+    km = kmap.build_kernel_map(torch.as_tensor(idx).to(cuda), [64] * 3, 1)
+    x, w, b = _case(rng, len(idx), 256, 256, torch.float16)
+    r = torch.as_tensor(rng.standard_normal((len(idx), 256), dtype=np.float32)).half() if res else None
+    xd, wd, bd = x.to(cuda), w.to(cuda), b.to(cuda)
+    rd = r.to(cuda) if res else None
+    plans = [kmap.build_plan(km.table, km.n, coords, win)
+             for coords, win in ((km.indices, 0), (km.indices, 256), (km.indices, None), (None, 0))]
+    skipped = []
+    for p in plans:  # (64-row block, offset) pairs a wave skips under this plan
+        g = (p.gidx.reshape(p.ntiles, p.kvol, 128) < p.n_in).cpu().numpy()
+        blk = g.reshape(p.ntiles, p.kvol, 2, 64).any(3)  # [plan tile, offset, half]
+        tm = p.tile_mask.cpu().numpy().astype(np.int64)
+        pairs = np.arange(p.ntiles) // 2
+        union = np.zeros(pairs[-1] + 1, np.int64)
+        np.bitwise_or.at(union, pairs, tm)
+        bits = (union[pairs][:, None] >> np.arange(p.kvol)) & 1
+        skipped.append(int((bits[:, :, None].astype(bool) & ~blk).sum()))
+    assert min(skipped) > 0 and len(set(skipped)) > 1, skipped
+    outs = [conv.gather_conv(xd, p, wd, bd, act=act, residual=rd) for p in plans]
+    for o in outs[1:]:
+        assert torch.equal(o, outs[0])
+    ref = oconv.gather_conv_f64(x.float().numpy(), km.table.cpu().numpy(), w.float().numpy(), b.float().numpy())
+    if act == "silu":
+        ref = ref / (1.0 + np.exp(-ref))
+    if res:
+        ref = ref + r.float().numpy()
+    assert oconv.rel_err(outs[0].float().cpu().numpy(), ref) <= GATE[torch.float16]
+
+
 def test_unaligned_channels_use_simple_kernel(cuda):
     from hi3d_amd import conv, kmap
 
