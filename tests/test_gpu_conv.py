@@ -333,8 +333,9 @@ def test_plan_choice_does_not_change_results(cuda):
     assert oconv.rel_err(halo_outs[0].float().cpu().numpy(), outs[0].float().cpu().numpy().astype(np.float64)) <= 1e-2
 
 
-@pytest.mark.parametrize("act,res", [(None, False), ("silu", True)])
-def test_wide2_offset_skips_are_exact(cuda, act, res):
+@pytest.mark.parametrize("dtype,act,res", [(torch.float16, None, False), (torch.float16, "silu", True),
+                                           (torch.bfloat16, "silu", False)])
+def test_wide2_offset_skips_are_exact(cuda, dtype, act, res):
     """The 256 x 256 kernel's waves skip the MFMAs of offsets that none of their 64 rows
     has. On a sphere shell (structured masks, so many 64-row blocks lack offsets of their
     256-row tile) the output is bitwise the same under plans that skip different
@@ -344,8 +345,8 @@ def test_wide2_offset_skips_are_exact(cuda, act, res):
     rng = np.random.default_rng(31)
     idx = workloads.sphere_shell(64, 27.0, seed=3)
     km = kmap.build_kernel_map(torch.as_tensor(idx).to(cuda), [64] * 3, 1)
-    x, w, b = _case(rng, len(idx), 256, 256, torch.float16)
-    r = torch.as_tensor(rng.standard_normal((len(idx), 256), dtype=np.float32)).half() if res else None
+    x, w, b = _case(rng, len(idx), 256, 256, dtype)
+    r = torch.as_tensor(rng.standard_normal((len(idx), 256), dtype=np.float32)).to(dtype) if res else None
     xd, wd, bd = x.to(cuda), w.to(cuda), b.to(cuda)
     rd = r.to(cuda) if res else None
     plans = [kmap.build_plan(km.table, km.n, coords, win)
@@ -369,7 +370,8 @@ def test_wide2_offset_skips_are_exact(cuda, act, res):
         ref = ref / (1.0 + np.exp(-ref))
     if res:
         ref = ref + r.float().numpy()
-    assert oconv.rel_err(outs[0].float().cpu().numpy(), ref) <= GATE[torch.float16]
+    assert outs[0].dtype == dtype
+    assert oconv.rel_err(outs[0].float().cpu().numpy(), ref) <= GATE[dtype]
 
 
 def test_unaligned_channels_use_simple_kernel(cuda):
