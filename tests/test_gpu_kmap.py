@@ -377,6 +377,37 @@ def test_dense_and_hash_maps_agree(cuda, ksize, batch, n_side, density):
         kmap.KMAP_DENSE_ORDER_MIN_BYTES = old_order
 
 
+@pytest.mark.parametrize("shape,batch,ksize,density", [((13, 20, 7), 2, 3, 0.3), ((1, 9, 33), 3, 3, 0.4),
+                                                        ((17, 5, 11), 2, 5, 0.25), ((31, 2, 19), 1, 3, 0.6)])
+def test_non_cubic_odd_grids(cuda, shape, batch, ksize, density):
+    """Odd, non-cubic extents (bricks and superblocks cut by every face, a one-cell-thick
+    axis, a two-cell one) and several batch elements: the hash map at small and large
+    capacities (input order and superblock order) and the dense grid give the oracle's
+    table and counts bit for bit, voxels on every face included."""
+    from hi3d_amd import kmap
+
+    rng = np.random.default_rng(sum(shape) * 7 + batch + ksize)
+    rows = []
+    for b in range(batch):
+        xyz = np.argwhere(rng.random(shape) < density)
+        rows.append(np.concatenate([np.full((len(xyz), 1), b), xyz], 1))
+    idx = np.concatenate(rows).astype(np.int32)
+    idx = idx[rng.permutation(len(idx))]
+    t = torch.as_tensor(idx).to(cuda)
+    ref = okmap.neighbour_table(idx, list(shape), ksize)
+    ref_counts = (ref < len(idx)).sum(0)
+    dense = kmap.build_kernel_map(t, list(shape), batch, ksize)
+    assert np.array_equal(dense.table.cpu().numpy(), ref)
+    assert np.array_equal(dense.counts.cpu().numpy(), ref_counts)
+    for cap in (1 << 12, 1 << 20):
+        hashed = kmap.build_kernel_map(t, list(shape), batch, ksize, capacity=cap)
+        assert torch.equal(hashed.table, dense.table) and torch.equal(hashed.counts, dense.counts), cap
+    bad = t.clone()
+    bad[0, 1 + int(np.argmin(shape))] = min(shape)  # one cell past the thinnest axis
+    with pytest.raises(ValueError, match="outside"):
+        kmap.build_kernel_map(bad, list(shape), batch, ksize, capacity=1 << 12)
+
+
 def test_hash_wide_grid_superblock_order(cuda):
     """A grid whose superblock-major cell keys pass 32 bits (65536 x 65536 x 256): the
     hash sorts the superblocks alone and carries the coordinates in sorted order. The
